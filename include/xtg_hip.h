@@ -1,0 +1,94 @@
+/* xtg_hip: the MI355X (gfx950) kernel layer of the xtier-go decode path, behind a C ABI.
+ *
+ * One handle is one backend: one device, one in-order HIP stream, the weights it has prepared. It stands in for
+ * xtg::OpenClBackend (engine/include/xtg/opencl.h:22-63) and for the CPU kernel entry points the Dory pack calls
+ * (engine/include/xtg/kernels.h:27-49, engine/include/xtg/kv.h:21-79). Conventions follow the reference's
+ * plugin ABI (npu/xtg_npu.h:14-47): opaque handles, a NULL handle on failure, `int` return codes (0 success,
+ * -1 failure) with the message written into `err` (err_len bytes, NUL-terminated), JSON from info(). No call
+ * throws or aborts across this boundary.
+ *
+ * Device-resident calls only queue work on the backend's stream, like the OpenCL backend's in-order queue
+ * (opencl.h:16-21); xtg_hip_read() and xtg_hip_finish() wait for it. Pointers documented as "device" are
+ * addresses from xtg_hip_alloc() (or any device allocation on the same device); "host" pointers are ordinary
+ * memory. One backend is used from one thread at a time (packs/dory: one engine thread, server/runtime.h:1-3).
+ */
+#ifndef XTG_HIP_H
+#define XTG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XTG_HIP_ABI_VERSION 1
+
+typedef struct xtg_hip xtg_hip;
+typedef struct xtg_hip_kv xtg_hip_kv;
+
+/* An NVFP4 weight [n_out][k] in ModelOpt's layout: E2M1 codes two per byte (element 2j in the low nibble of byte
+ * j), one E4M3 scale per 16 inputs, one FP32 scale for the tensor; w[n][j] = e2m1 * e4m3(scale[n][j/16]) * global.
+ * Field for field the same as xtg::Nvfp4Weight (engine/include/xtg/kernels.h:13-20), so an array of those can be
+ * passed as is. codes / scales are host pointers; they key the prepared device copy (as opencl.cpp:489-492). */
+typedef struct xtg_nvfp4 {
+  const uint8_t* codes;   /* [n_out][k / 2] */
+  const uint8_t* scales;  /* [n_out][k / 16] */
+  float global;
+  int n_out, k;
+} xtg_nvfp4;
+
+enum { XTG_X_F32 = 0, XTG_X_BF16 = 1 };   /* activation element type of the device matmul */
+enum { XTG_KV_BF16 = 0, XTG_KV_FP8 = 1 }; /* xtg::KvDtype (engine/include/xtg/kv.h:18) */
+
+/* ------------------------------------------------------------------------------------------------ backend */
+
+/* Replaces OpenClBackend::OpenClBackend() (opencl.h:28). options: JSON, may be NULL or empty; keys: "device"
+ * (HIP device index, default 0). NULL on failure, the reason in err. */
+xtg_hip* xtg_hip_open(const char* options, char* err, int err_len);
+/* Replaces ~OpenClBackend (opencl.h:29): waits for queued work, frees every device buffer the backend owns. */
+void xtg_hip_close(xtg_hip* h);
+/* Replaces device_name() / weight_bytes() (opencl.h:36-37): {"abi", "device", "arch", "cus", "hbm_bytes",
+ * "weight_bytes", "weights"} as JSON. Returns the length written (without the NUL), or -1. */
+int xtg_hip_info(xtg_hip* h, char* out, int out_len);
+/* The backend's hipStream_t, for callers that time or order their own work against it. */
+void* xtg_hip_stream(xtg_hip* h);
+
+/* --------------------------------------------------------------------------------------------- NVFP4 path */
+
+/* Replaces OpenClBackend::prepare(const Nvfp4Weight&) (opencl.h:32, opencl.cpp:489-515): copy the weight to the
+ * device in the GEMV tile layout. Idempotent, keyed by w->codes. k % 16 == 0 and n_out > 0 are required. */
+int xtg_hip_prepare_nvfp4(xtg_hip* h, const xtg_nvfp4* w, char* err, int err_len);
+/* Drops the device copy prepared for `codes` (a weight whose host memory is about to be freed or reused). The
+ * reference frees its device weights only with the backend (opencl.cpp:349-353); callers that recycle host
+ * buffers need this to keep the codes-pointer key unambiguous. 0 also when nothing was prepared for it. */
+int xtg_hip_release_nvfp4(xtg_hip* h, const uint8_t* codes, char* err, int err_len);
+/* Replaces xtg::matmul_nvfp4(ThreadPool&, ws, x, m, ys) (kernels.h:27-30, kernels.cpp:84-138) and the host
+ * OpenClBackend::matmul (opencl.h:34, opencl.cpp:523-601): y_i[m][n_out_i] = x[m][k] * W_i^T for n_w weights
+ * sharing k; x and every ys[i] are host memory; synchronous. Prepares weights not seen before. m >= 1 (rows are
+ * processed 8 at a time). */
+int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* x, int m, float* const* ys,
+                         char* err, int err_len);
+/* Replaces OpenClBackend::matmul(ws, Mem x, m, Mem y, y_offset) (opencl.h:54-55, opencl.cpp:694-754): the n_w
+ * projections of the device input x ([m][k], FP32 or BF16 per x_dtype) into consecutive [m][n_out_i] blocks of
+ * the device output y starting at y_offset floats. Queued; 1 <= m <= 8, n_w <= 4 per call (the fused q/k/v/g
+ * and gate/up of the Dory sublayers). */
+int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
+                             size_t y_offset, char* err, int err_len);
+
+/* ------------------------------------------------------------------------------------- device buffers */
+
+/* Replaces OpenClBackend::alloc / release / write / read / copy / finish (opencl.h:40-45). write() is blocking
+ * (src may be reused on return), read() waits for all queued work, copy() is queued. */
+int xtg_hip_alloc(xtg_hip* h, size_t bytes, void** out, char* err, int err_len);
+void xtg_hip_release(xtg_hip* h, void* mem);
+int xtg_hip_write(xtg_hip* h, void* mem, size_t offset, const void* src, size_t bytes, char* err, int err_len);
+int xtg_hip_read(xtg_hip* h, const void* mem, size_t offset, void* dst, size_t bytes, char* err, int err_len);
+int xtg_hip_copy(xtg_hip* h, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes,
+                 char* err, int err_len);
+int xtg_hip_finish(xtg_hip* h, char* err, int err_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

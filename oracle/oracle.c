@@ -1,0 +1,647 @@
+/* CPU oracle: plain-C restatement of the reference engine's CPU kernels for the decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY -- see oracle.h. Built with the reference build's arithmetic flags
+ * (-O3 -march=x86-64-v3 -fopenmp-simd, GNU dialect so FP contraction is on), so the FP32 summation structure
+ * follows the reference's loops. Citations are reference paths.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------------------------------ formats */
+
+float xo_bf16_to_f32(uint16_t h) {
+  /* engine/include/xtg/fp.h:10-15 */
+  uint32_t bits = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t xo_f32_to_bf16(float f) {
+  /* engine/include/xtg/fp.h:18-24: round to nearest even, a NaN stays a (quiet) NaN */
+  uint32_t bits;
+  memcpy(&bits, &f, 4);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x40u);
+  bits += 0x7fffu + ((bits >> 16) & 1u);
+  return (uint16_t)(bits >> 16);
+}
+
+static float g_e4m3[256];
+static int g_e4m3_ready = 0;
+
+static void e4m3_init(void) {
+  /* engine/src/fp.cpp:12-28: bias 7, subnormal step 2^-9, 0x7f / 0xff NaN, no infinities */
+  if (g_e4m3_ready) return;
+  for (int b = 0; b < 256; ++b) {
+    int e = (b >> 3) & 15, m = b & 7;
+    float mag;
+    if ((b & 0x7f) == 0x7f)
+      mag = NAN;
+    else if (e == 0)
+      mag = (float)m * ldexpf(1.f, -9);
+    else
+      mag = (1.f + (float)m / 8.f) * ldexpf(1.f, e - 7);
+    g_e4m3[b] = (b & 0x80) ? -mag : mag;
+  }
+  g_e4m3_ready = 1;
+}
+
+__attribute__((constructor)) static void oracle_init(void) { e4m3_init(); }
+
+float xo_e4m3_to_f32(uint8_t b) { return g_e4m3[b]; }
+
+uint8_t xo_f32_to_e4m3(float f) {
+  /* engine/src/fp.cpp:30-49: the largest code not above |f| by binary search, then round to nearest even;
+   * |f| >= 448 saturates to 0x7e */
+  uint8_t sign = signbit(f) ? 0x80 : 0;
+  if (isnan(f)) return (uint8_t)(sign | 0x7f);
+  float a = fabsf(f);
+  if (a >= 448.f) return (uint8_t)(sign | 0x7e);
+  int lo = 0, hi = 0x7e;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) / 2;
+    if (g_e4m3[mid] <= a)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  if (lo < 0x7e) {
+    float d0 = a - g_e4m3[lo], d1 = g_e4m3[lo + 1] - a;
+    if (d1 < d0 || (d1 == d0 && (lo & 1))) ++lo;
+  }
+  return (uint8_t)(sign | lo);
+}
+
+uint8_t xo_e4m3_bits(float x) {
+  /* engine/src/kv.cpp:19-40: below 2^-6 count subnormal steps of 2^-9 (ties to even); above, round the FP32
+   * mantissa to 3 bits (ties to even) and rebias, capped at 0x7e */
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  uint32_t sign = (bits >> 24) & 0x80u, a = bits & 0x7fffffffu, code;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+  if (a < 0x3c800000u) {
+    float t;
+    memcpy(&t, &a, 4);
+    t *= 512.f;
+    float lo = floorf(t);
+    uint32_t steps = (uint32_t)lo;
+    float half = t - lo;
+    steps += (half > 0.5f) || (half == 0.5f && (steps & 1u));
+    code = steps;
+  } else {
+    uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+    if (code > 0x7eu) code = 0x7eu;
+  }
+  return (uint8_t)(sign | code);
+}
+
+/* engine/include/xtg/fp.h:37-39 */
+static const float kE2m1[16] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f,
+                                -0.f, -0.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f};
+float xo_e2m1(int code) { return kE2m1[code & 15]; }
+
+/* ------------------------------------------------------------------------------------------------ NVFP4 */
+
+void xo_nvfp4_row(const xo_nvfp4* w, int n, float* out) {
+  /* engine/src/kernels.cpp:34-45: the scale and the tensor scale are folded into each decoded weight */
+  const uint8_t* c = w->codes + (size_t)n * (size_t)(w->k / 2);
+  const uint8_t* s = w->scales + (size_t)n * (size_t)(w->k / 16);
+  for (int g = 0; g < w->k / 16; ++g) {
+    float sc = g_e4m3[s[g]] * w->global;
+    for (int j = 0; j < 8; ++j) {
+      uint8_t b = c[g * 8 + j];
+      out[g * 16 + 2 * j] = kE2m1[b & 15] * sc;
+      out[g * 16 + 2 * j + 1] = kE2m1[b >> 4] * sc;
+    }
+  }
+}
+
+static float dot_nvfp4(const xo_nvfp4* w, int n, const float* x) {
+  /* engine/src/kernels.cpp:48-60: per 16-input group the E2M1 products are summed in FP32, then scaled by the
+   * group's E4M3 value; the tensor scale multiplies the total */
+  const uint8_t* c = w->codes + (size_t)n * (size_t)(w->k / 2);
+  const uint8_t* s = w->scales + (size_t)n * (size_t)(w->k / 16);
+  float acc = 0.f;
+  for (int g = 0; g < w->k / 16; ++g) {
+    const uint8_t* cg = c + g * 8;
+    const float* xg = x + g * 16;
+    float part = 0.f;
+    for (int j = 0; j < 8; ++j) part += kE2m1[cg[j] & 15] * xg[2 * j] + kE2m1[cg[j] >> 4] * xg[2 * j + 1];
+    acc += part * g_e4m3[s[g]];
+  }
+  return acc * w->global;
+}
+
+/* engine/src/kernels.cpp:62-67 (a separate translation unit in the reference, hence not inlined here) */
+__attribute__((noinline)) static float dot_f32(const float* a, const float* b, int k) {
+  float s = 0.f;
+#pragma omp simd reduction(+ : s)
+  for (int j = 0; j < k; ++j) s += a[j] * b[j];
+  return s;
+}
+
+int xo_matmul_nvfp4(const xo_nvfp4* ws, int n_w, const float* x, int m, float* const* ys, int threads) {
+  /* engine/src/kernels.cpp:84-138. Several weights reading the same x form one list of rows (RowMap :69-82);
+   * which rows a thread takes changes nothing in the results, so the rows are walked weight by weight. */
+  if (n_w <= 0) return -1;
+  const int k = ws[0].k;
+  for (int i = 0; i < n_w; ++i)
+    if (ws[i].k != k || k % 16 != 0) return -1;
+  if (threads < 1) threads = 1;
+  for (int wi = 0; wi < n_w; ++wi) {
+    const xo_nvfp4* w = &ws[wi];
+    float* y = ys[wi];
+    if (m <= 2) {
+      /* decode branch (:90-114): one dot_nvfp4 per (input row, output row) */
+#pragma omp parallel for num_threads(threads) schedule(static)
+      for (int n = 0; n < w->n_out; ++n)
+        for (int i = 0; i < m; ++i) y[(size_t)i * (size_t)w->n_out + (size_t)n] = dot_nvfp4(w, n, x + (size_t)i * (size_t)k);
+    } else {
+      /* prefill branch (:116-137): the weight row decoded to FP32 (scales folded in), then dot_f32 per input row */
+#pragma omp parallel num_threads(threads)
+      {
+        float* wrow = (float*)malloc(sizeof(float) * (size_t)k);
+#pragma omp for schedule(static)
+        for (int n = 0; n < w->n_out; ++n) {
+          xo_nvfp4_row(w, n, wrow);
+          for (int i = 0; i < m; ++i)
+            y[(size_t)i * (size_t)w->n_out + (size_t)n] = dot_f32(wrow, x + (size_t)i * (size_t)k, k);
+        }
+        free(wrow);
+      }
+    }
+  }
+  return 0;
+}
+
+/* --------------------------------------------------------------------------------------------- row kernels */
+
+void xo_bf16_row(const uint16_t* table, int64_t row, int width, float* out) {
+  /* engine/src/kernels.cpp:157-160 */
+  const uint16_t* r = table + row * width;
+  for (int j = 0; j < width; ++j) out[j] = xo_bf16_to_f32(r[j]);
+}
+
+__attribute__((noinline)) static float inv_norm(const float* x, int w) {
+  /* engine/src/kernels.cpp:162-167 */
+  float s = 0.f;
+#pragma omp simd reduction(+ : s)
+  for (int j = 0; j < w; ++j) s += x[j] * x[j];
+  return 1.f / sqrtf(s + 1e-6f);
+}
+
+void xo_justnorm(float* x, int rows, int width) {
+  /* engine/src/kernels.cpp:169-175 */
+  for (int r = 0; r < rows; ++r) {
+    float* v = x + (size_t)r * (size_t)width;
+    float f = inv_norm(v, width);
+    for (int j = 0; j < width; ++j) v[j] *= f;
+  }
+}
+
+void xo_slerp_residual(float* a, const float* b, const float* lr, int rows, int width) {
+  /* engine/src/kernels.cpp:177-189 */
+  for (int r = 0; r < rows; ++r) {
+    float* va = a + (size_t)r * (size_t)width;
+    const float* vb = b + (size_t)r * (size_t)width;
+    float fa = inv_norm(va, width), fb = inv_norm(vb, width);
+    for (int j = 0; j < width; ++j) {
+      float ya = va[j] * fa, yb = vb[j] * fb;
+      va[j] = ya + lr[j] * (yb - ya);
+    }
+    float f = inv_norm(va, width);
+    for (int j = 0; j < width; ++j) va[j] *= f;
+  }
+}
+
+static void inv_freq(float theta, int d, float* f) {
+  /* engine/src/kernels.cpp:191-201: 1 / theta^(2i/d) in FP32 */
+  for (int i = 0; i < d / 2; ++i) f[i] = 1.f / powf(theta, (float)(2 * i) / (float)d);
+}
+
+void xo_rope(float* x, int rows, int heads, int head_dim, int64_t pos0, float theta) {
+  /* engine/src/kernels.cpp:203-223: NeoX half split; angle = FP32(pos) * inv_freq in FP32 */
+  const int half = head_dim / 2;
+  float* f = (float*)malloc(sizeof(float) * (size_t)half * 3);
+  float* c = f + half;
+  float* s = c + half;
+  inv_freq(theta, head_dim, f);
+  for (int r = 0; r < rows; ++r) {
+    float pos = (float)(pos0 + r);
+    for (int i = 0; i < half; ++i) {
+      float a = pos * f[i];
+      c[i] = cosf(a);
+      s[i] = sinf(a);
+    }
+    for (int h = 0; h < heads; ++h) {
+      float* v = x + ((size_t)r * (size_t)heads + (size_t)h) * (size_t)head_dim;
+      for (int i = 0; i < half; ++i) {
+        float x1 = v[i], x2 = v[i + half];
+        v[i] = x1 * c[i] - x2 * s[i];
+        v[i + half] = x2 * c[i] + x1 * s[i];
+      }
+    }
+  }
+  free(f);
+}
+
+void xo_rope_table(float* cs, int m, int head_dim, int64_t pos0, float theta) {
+  /* packs/dory/dory.cpp:1159-1171: the same FP32 angles as rope(), laid out [cos rows][sin rows] */
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    float inv = 1.f / powf(theta, (float)(2 * i) / (float)head_dim);
+    for (int r = 0; r < m; ++r) {
+      float a = (float)(pos0 + r) * inv;
+      cs[(size_t)r * (size_t)half + (size_t)i] = cosf(a);
+      cs[(size_t)(m + r) * (size_t)half + (size_t)i] = sinf(a);
+    }
+  }
+}
+
+void xo_swiglu_scaled(float* g, const float* u, const float* sg, const float* su, int rows, int w) {
+  /* engine/src/kernels.cpp:225-234 */
+  for (int r = 0; r < rows; ++r) {
+    float* gr = g + (size_t)r * (size_t)w;
+    const float* ur = u + (size_t)r * (size_t)w;
+    for (int j = 0; j < w; ++j) {
+      float z = gr[j] * sg[j];
+      gr[j] = z / (1.f + expf(-z)) * (ur[j] * su[j]);
+    }
+  }
+}
+
+void xo_qk_produce(float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0, float theta,
+                   const float* qscale) {
+  /* packs/dory/dory.cpp:482-490: RoPE on q and k, then justnorm per head, then q times the per-dimension
+   * scale over all heads (qscale has heads * head_dim entries); k is not scaled */
+  const int Q = heads * head_dim;
+  xo_rope(q, m, heads, head_dim, pos0, theta);
+  xo_rope(k, m, kv_heads, head_dim, pos0, theta);
+  xo_justnorm(q, m * heads, head_dim);
+  for (int r = 0; r < m; ++r) {
+    float* qr = q + (size_t)r * (size_t)Q;
+    for (int j = 0; j < Q; ++j) qr[j] *= qscale[j];
+  }
+  xo_justnorm(k, m * kv_heads, head_dim);
+}
+
+/* ---------------------------------------------------------------------------------------------- KV cache */
+
+struct xo_kv {
+  int kv_heads, head_dim;
+  int64_t slots;
+  int ring, dtype;
+  size_t elem;
+  uint8_t* k;
+  uint8_t* v;
+  float* ks;
+  float* vs;
+};
+
+xo_kv* xo_kv_create(int kv_heads, int head_dim, int64_t slots, int ring, int dtype) {
+  /* engine/src/kv.cpp:42-63: ring > 0 gives a ring of `ring` slots; storage [slots][kv_heads][head_dim] */
+  xo_kv* c = (xo_kv*)calloc(1, sizeof(xo_kv));
+  c->kv_heads = kv_heads;
+  c->head_dim = head_dim;
+  c->slots = ring > 0 ? ring : slots;
+  c->ring = ring > 0;
+  c->dtype = dtype;
+  c->elem = dtype == XO_KV_FP8 ? 1 : 2;
+  if (c->slots <= 0) {
+    free(c);
+    return NULL;
+  }
+  size_t n = (size_t)c->slots * (size_t)kv_heads * (size_t)head_dim;
+  c->k = (uint8_t*)calloc(n, c->elem);
+  c->v = (uint8_t*)calloc(n, c->elem);
+  if (dtype == XO_KV_FP8) {
+    c->ks = (float*)calloc((size_t)c->slots * (size_t)kv_heads, sizeof(float));
+    c->vs = (float*)calloc((size_t)c->slots * (size_t)kv_heads, sizeof(float));
+  }
+  return c;
+}
+
+void xo_kv_free(xo_kv* c) {
+  if (!c) return;
+  free(c->k);
+  free(c->v);
+  free(c->ks);
+  free(c->vs);
+  free(c);
+}
+
+int64_t xo_kv_slots(const xo_kv* c) { return c->slots; }
+const void* xo_kv_kdata(const xo_kv* c) { return c->k; }
+const void* xo_kv_vdata(const xo_kv* c) { return c->v; }
+const float* xo_kv_kscale(const xo_kv* c) { return c->ks; }
+const float* xo_kv_vscale(const xo_kv* c) { return c->vs; }
+
+int xo_kv_store(xo_kv* c, int64_t pos, int n, const float* k, const float* v) {
+  /* engine/src/kv.cpp:75-112: a ring keeps the last `slots` rows of a long call; BF16 rows rounded to nearest
+   * even; FP8 rows take a per-(position, head) scale amax / 448 and the kv.cpp rounding */
+  int64_t first = pos;
+  if (c->ring && n > c->slots) first = pos + n - c->slots;
+  if (!c->ring && pos + n > c->slots) return -1;
+  const size_t hd = (size_t)c->head_dim;
+  for (int64_t p = first; p < pos + n; ++p) {
+    int64_t slot = c->ring ? p % c->slots : p;
+    for (int h = 0; h < c->kv_heads; ++h) {
+      const float* src_k = k + ((size_t)(p - pos) * (size_t)c->kv_heads + (size_t)h) * hd;
+      const float* src_v = v + ((size_t)(p - pos) * (size_t)c->kv_heads + (size_t)h) * hd;
+      size_t idx = (size_t)slot * (size_t)c->kv_heads + (size_t)h;
+      if (c->dtype == XO_KV_BF16) {
+        uint16_t* dk = (uint16_t*)c->k + idx * hd;
+        uint16_t* dv = (uint16_t*)c->v + idx * hd;
+        for (size_t j = 0; j < hd; ++j) {
+          dk[j] = xo_f32_to_bf16(src_k[j]);
+          dv[j] = xo_f32_to_bf16(src_v[j]);
+        }
+      } else {
+        float ak = 0.f, av = 0.f;
+        for (size_t j = 0; j < hd; ++j) {
+          ak = fmaxf(ak, fabsf(src_k[j]));
+          av = fmaxf(av, fabsf(src_v[j]));
+        }
+        float sk = ak > 0.f ? ak / 448.f : 1.f, sv = av > 0.f ? av / 448.f : 1.f;
+        float ik = 1.f / sk, iv = 1.f / sv;
+        uint8_t* dk = c->k + idx * hd;
+        uint8_t* dv = c->v + idx * hd;
+        for (size_t j = 0; j < hd; ++j) {
+          dk[j] = xo_e4m3_bits(src_k[j] * ik);
+          dv[j] = xo_e4m3_bits(src_v[j] * iv);
+        }
+        c->ks[idx] = sk;
+        c->vs[idx] = sv;
+      }
+    }
+  }
+  return 0;
+}
+
+void xo_kv_load(const xo_kv* c, int h, int64_t p0, int64_t p1, float* k, float* v) {
+  /* engine/src/kv.cpp:114-138 */
+  const size_t hd = (size_t)c->head_dim;
+  for (int64_t p = p0; p < p1; ++p) {
+    int64_t slot = c->ring ? p % c->slots : p;
+    size_t idx = (size_t)slot * (size_t)c->kv_heads + (size_t)h;
+    float* ok = k + (size_t)(p - p0) * hd;
+    float* ov = v + (size_t)(p - p0) * hd;
+    if (c->dtype == XO_KV_BF16) {
+      const uint16_t* sk = (const uint16_t*)c->k + idx * hd;
+      const uint16_t* sv = (const uint16_t*)c->v + idx * hd;
+      for (size_t j = 0; j < hd; ++j) {
+        ok[j] = xo_bf16_to_f32(sk[j]);
+        ov[j] = xo_bf16_to_f32(sv[j]);
+      }
+    } else {
+      const uint8_t* sk = c->k + idx * hd;
+      const uint8_t* sv = c->v + idx * hd;
+      float fk = c->ks[idx], fv = c->vs[idx];
+      for (size_t j = 0; j < hd; ++j) {
+        ok[j] = g_e4m3[sk[j]] * fk;
+        ov[j] = g_e4m3[sv[j]] * fv;
+      }
+    }
+  }
+}
+
+/* ----------------------------------------------------------------------------------------------- attention */
+
+enum { kRows = 8, kTile = 64, kMaxGroup = 8 };   /* engine/src/kv.cpp:154-157 */
+
+static int64_t lo_of(const xo_attn_args* a, int64_t t) {
+  /* engine/src/kv.cpp:170: window > 0 -> keys t - window + 1 .. t */
+  if (a->window <= 0) return 0;
+  int64_t lo = t - a->window + 1;
+  return lo > 0 ? lo : 0;
+}
+
+int xo_attention(const xo_attn_args* a, int pool_size, int threads) {
+  /* engine/src/kv.cpp:166-286: tasks = kv_heads x blocks of 8 query rows x key splits; each task loads tiles of
+   * 64 keys (cached positions from the cache, then this call's own keys in FP32), online softmax in FP32 per
+   * (row, q head); splits are combined by their max / sum / accumulator */
+  const int group = a->heads / a->kv_heads, d = a->head_dim;
+  if (group * a->kv_heads != a->heads || group > kMaxGroup) return -1;
+  if (threads < 1) threads = 1;
+  const int64_t k_lo = lo_of(a, a->pos0), k_hi = a->pos0 + a->n_q;
+  const int64_t span = k_hi - k_lo;
+  const int qblocks = (a->n_q + kRows - 1) / kRows;
+  int splits = 1;
+  if (a->n_q <= 4 && span > 2 * kTile) {
+    int64_t want = 2 * pool_size / a->kv_heads;
+    if (want < 1) want = 1;
+    int64_t cap = (span + 1023) / 1024;
+    splits = (int)(want < cap ? want : cap);
+  }
+  if (splits < 1) splits = 1;
+  const int64_t tasks = (int64_t)a->kv_heads * qblocks * splits;
+  const size_t acc_per_task = (size_t)kRows * (size_t)group * (size_t)d;
+  float* part_m = splits > 1 ? (float*)malloc(sizeof(float) * (size_t)tasks * kRows * kMaxGroup) : NULL;
+  float* part_l = splits > 1 ? (float*)malloc(sizeof(float) * (size_t)tasks * kRows * kMaxGroup) : NULL;
+  float* accs = splits > 1 ? (float*)malloc(sizeof(float) * (size_t)tasks * acc_per_task) : NULL;
+  const float neg_inf = -INFINITY;
+
+#pragma omp parallel num_threads(threads)
+  {
+    float* kt = (float*)malloc(sizeof(float) * (size_t)kTile * (size_t)d);
+    float* vt = (float*)malloc(sizeof(float) * (size_t)kTile * (size_t)d);
+    float* acc = (float*)malloc(sizeof(float) * acc_per_task);
+    float sc[kTile];
+    float st_m[kRows][kMaxGroup], st_l[kRows][kMaxGroup];
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t task = 0; task < tasks; ++task) {
+      int s = (int)(task % splits);
+      int qb = (int)((task / splits) % qblocks);
+      int h = (int)(task / ((int64_t)splits * qblocks));
+      int i0 = qb * kRows, i1 = a->n_q < i0 + kRows ? a->n_q : i0 + kRows;
+      int64_t s0 = k_lo + span * s / splits, s1 = k_lo + span * (s + 1) / splits;
+      int64_t lo0 = lo_of(a, a->pos0 + i0);
+      int64_t r0 = s0 > lo0 ? s0 : lo0;
+      int64_t r1 = s1 < a->pos0 + i1 ? s1 : a->pos0 + i1;
+      for (int i = 0; i < kRows; ++i)
+        for (int g = 0; g < kMaxGroup; ++g) {
+          st_m[i][g] = neg_inf;
+          st_l[i][g] = 0.f;
+        }
+      memset(acc, 0, sizeof(float) * acc_per_task);
+      for (int64_t kp = r0; kp < r1; kp += kTile) {
+        int64_t kq = r1 < kp + kTile ? r1 : kp + kTile;
+        int64_t cut = a->pos0 > kp ? a->pos0 : kp;
+        if (cut > kq) cut = kq;
+        if (cut > kp) xo_kv_load(a->cache, h, kp, cut, kt, vt);
+        for (int64_t p = cut; p < kq; ++p) {
+          const size_t src = ((size_t)(p - a->pos0) * (size_t)a->kv_heads + (size_t)h) * (size_t)d;
+          memcpy(kt + (size_t)(p - kp) * (size_t)d, a->k + src, sizeof(float) * (size_t)d);
+          memcpy(vt + (size_t)(p - kp) * (size_t)d, a->v + src, sizeof(float) * (size_t)d);
+        }
+        for (int i = i0; i < i1; ++i) {
+          int64_t t = a->pos0 + i;
+          int64_t lt = lo_of(a, t);
+          int64_t j0 = kp > lt ? kp : lt, j1 = kq < t + 1 ? kq : t + 1;
+          if (j0 >= j1) continue;
+          for (int g = 0; g < group; ++g) {
+            const float* qv = a->q + ((size_t)i * (size_t)a->heads + (size_t)(h * group + g)) * (size_t)d;
+            float mx = neg_inf;
+            for (int64_t j = j0; j < j1; ++j) {
+              const float* kv = kt + (size_t)(j - kp) * (size_t)d;
+              float dot = dot_f32(qv, kv, d) * a->scale;
+              sc[j - j0] = dot;
+              mx = fmaxf(mx, dot);
+            }
+            float* m = &st_m[i - i0][g];
+            float* l = &st_l[i - i0][g];
+            float m_new = fmaxf(*m, mx);
+            float corr = *m == neg_inf ? 0.f : expf(*m - m_new);
+            float* ac = acc + ((size_t)(i - i0) * (size_t)group + (size_t)g) * (size_t)d;
+            if (corr != 1.f)
+              for (int e = 0; e < d; ++e) ac[e] *= corr;
+            *l *= corr;
+            for (int64_t j = j0; j < j1; ++j) {
+              float w = expf(sc[j - j0] - m_new);
+              *l += w;
+              const float* vv = vt + (size_t)(j - kp) * (size_t)d;
+              for (int e = 0; e < d; ++e) ac[e] += w * vv[e];
+            }
+            *m = m_new;
+          }
+        }
+      }
+      if (splits == 1) {
+        for (int i = i0; i < i1; ++i)
+          for (int g = 0; g < group; ++g) {
+            float* o = a->out + ((size_t)i * (size_t)a->heads + (size_t)(h * group + g)) * (size_t)d;
+            const float* ac = acc + ((size_t)(i - i0) * (size_t)group + (size_t)g) * (size_t)d;
+            float l = st_l[i - i0][g];
+            float inv = l > 0.f ? 1.f / l : 0.f;
+            for (int e = 0; e < d; ++e) o[e] = ac[e] * inv;
+          }
+      } else {
+        memcpy(part_m + (size_t)task * kRows * kMaxGroup, st_m, sizeof(st_m));
+        memcpy(part_l + (size_t)task * kRows * kMaxGroup, st_l, sizeof(st_l));
+        memcpy(accs + (size_t)task * acc_per_task, acc, sizeof(float) * acc_per_task);
+      }
+    }
+    free(kt);
+    free(vt);
+    free(acc);
+  }
+  if (splits > 1) {
+    /* engine/src/kv.cpp:262-285 */
+    for (int h = 0; h < a->kv_heads; ++h)
+      for (int qb = 0; qb < qblocks; ++qb) {
+        int i0 = qb * kRows, i1 = a->n_q < i0 + kRows ? a->n_q : i0 + kRows;
+        int64_t base = ((int64_t)h * qblocks + qb) * splits;
+        for (int i = i0; i < i1; ++i)
+          for (int g = 0; g < group; ++g) {
+            float mx = neg_inf;
+            for (int s = 0; s < splits; ++s)
+              mx = fmaxf(mx, part_m[(size_t)(base + s) * kRows * kMaxGroup + (size_t)(i - i0) * kMaxGroup + g]);
+            float* o = a->out + ((size_t)i * (size_t)a->heads + (size_t)(h * group + g)) * (size_t)d;
+            for (int e = 0; e < d; ++e) o[e] = 0.f;
+            float l = 0.f;
+            for (int s = 0; s < splits; ++s) {
+              size_t pi = (size_t)(base + s) * kRows * kMaxGroup + (size_t)(i - i0) * kMaxGroup + g;
+              if (part_l[pi] == 0.f) continue;
+              float w = expf(part_m[pi] - mx);
+              l += w * part_l[pi];
+              const float* ac = accs + (size_t)(base + s) * acc_per_task +
+                                ((size_t)(i - i0) * (size_t)group + (size_t)g) * (size_t)d;
+              for (int e = 0; e < d; ++e) o[e] += w * ac[e];
+            }
+            float inv = l > 0.f ? 1.f / l : 0.f;
+            for (int e = 0; e < d; ++e) o[e] *= inv;
+          }
+      }
+  }
+  free(part_m);
+  free(part_l);
+  free(accs);
+  return 0;
+}
+
+int xo_attention_slots(const xo_attn_args* a, const int64_t* slot_pos, int threads) {
+  /* npu/xtg_npu.cpp:236-258 mask semantics (slot visibility from the stored positions), evaluated with the
+   * CPU kernel's arithmetic (FP32 dot_f32 scores, online softmax over tiles of 64 keys, kv.cpp:205-245):
+   * the ring's slots in slot order, then this call's own keys in order. */
+  const int group = a->heads / a->kv_heads, d = a->head_dim;
+  if (group * a->kv_heads != a->heads || group > kMaxGroup) return -1;
+  if (threads < 1) threads = 1;
+  const int64_t slots = a->cache->slots;
+  const int64_t total = slots + a->n_q;
+  const int64_t tasks = (int64_t)a->n_q * a->heads;
+#pragma omp parallel num_threads(threads)
+  {
+    float* kt = (float*)malloc(sizeof(float) * (size_t)d);
+    float* vt = (float*)malloc(sizeof(float) * (size_t)d);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)d);
+    float* kk = (float*)malloc(sizeof(float) * (size_t)kTile * (size_t)d);
+    float* vv = (float*)malloc(sizeof(float) * (size_t)kTile * (size_t)d);
+    float sc[kTile];
+    int ok[kTile];
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t task = 0; task < tasks; ++task) {
+      int i = (int)(task / a->heads), hq = (int)(task % a->heads), h = hq / group;
+      int64_t p = a->pos0 + i;
+      const float* qv = a->q + ((size_t)i * (size_t)a->heads + (size_t)hq) * (size_t)d;
+      float m = -INFINITY, l = 0.f;
+      memset(acc, 0, sizeof(float) * (size_t)d);
+      for (int64_t t0 = 0; t0 < total; t0 += kTile) {
+        int64_t t1 = total < t0 + kTile ? total : t0 + kTile;
+        float mx = -INFINITY;
+        for (int64_t t = t0; t < t1; ++t) {
+          int see;
+          if (t < slots) {
+            int64_t q = slot_pos[t];
+            see = q >= 0 && q < a->pos0 && (a->window <= 0 || p - q < a->window);
+            if (see) {
+              xo_kv_load(a->cache, h, q, q + 1, kt, vt);
+              memcpy(kk + (size_t)(t - t0) * (size_t)d, kt, sizeof(float) * (size_t)d);
+              memcpy(vv + (size_t)(t - t0) * (size_t)d, vt, sizeof(float) * (size_t)d);
+            }
+          } else {
+            int j = (int)(t - slots);
+            see = j <= i && (a->window <= 0 || i - j < a->window);
+            if (see) {
+              const size_t src = ((size_t)j * (size_t)a->kv_heads + (size_t)h) * (size_t)d;
+              memcpy(kk + (size_t)(t - t0) * (size_t)d, a->k + src, sizeof(float) * (size_t)d);
+              memcpy(vv + (size_t)(t - t0) * (size_t)d, a->v + src, sizeof(float) * (size_t)d);
+            }
+          }
+          ok[t - t0] = see;
+          if (see) {
+            float dot = dot_f32(qv, kk + (size_t)(t - t0) * (size_t)d, d) * a->scale;
+            sc[t - t0] = dot;
+            mx = fmaxf(mx, dot);
+          }
+        }
+        if (mx == -INFINITY) continue;
+        float m_new = fmaxf(m, mx);
+        float corr = m == -INFINITY ? 0.f : expf(m - m_new);
+        if (corr != 1.f)
+          for (int e = 0; e < d; ++e) acc[e] *= corr;
+        l *= corr;
+        for (int64_t t = t0; t < t1; ++t) {
+          if (!ok[t - t0]) continue;
+          float w = expf(sc[t - t0] - m_new);
+          l += w;
+          const float* vr = vv + (size_t)(t - t0) * (size_t)d;
+          for (int e = 0; e < d; ++e) acc[e] += w * vr[e];
+        }
+        m = m_new;
+      }
+      float* o = a->out + ((size_t)i * (size_t)a->heads + (size_t)hq) * (size_t)d;
+      float inv = l > 0.f ? 1.f / l : 0.f;
+      for (int e = 0; e < d; ++e) o[e] = acc[e] * inv;
+    }
+    free(kt);
+    free(vt);
+    free(acc);
+    free(kk);
+    free(vv);
+  }
+  return 0;
+}

@@ -1,0 +1,254 @@
+"""ctypes wrappers of the CPU oracle (liboracle.so) and, where it was built, of the reference engine's own CPU
+kernels (_ref/libxtgref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker or the CPU baseline. The HIP library never uses it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libxtgref.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_I64 = ctypes.c_int64
+
+
+class Nvfp4(ctypes.Structure):
+    _fields_ = [("codes", _P), ("scales", _P), ("glob", _F), ("n_out", _I), ("k", _I)]
+
+
+class AttnArgs(ctypes.Structure):
+    """xo_attn_args / xr_attn_args (the field order of xtg::AttnArgs, engine/include/xtg/kv.h:67-78)."""
+    _fields_ = [("n_q", _I), ("pos0", _I64), ("heads", _I), ("kv_heads", _I), ("head_dim", _I), ("window", _I),
+                ("scale", _F), ("q", _P), ("k", _P), ("v", _P), ("cache", _P), ("out", _P)]
+
+
+def _load(path, sigs):
+    l = ctypes.CDLL(path)
+    for name, res, args in sigs:
+        f = getattr(l, name)
+        f.restype = res
+        f.argtypes = args
+    return l
+
+
+_ORACLE_SIGS = [
+    ("xo_bf16_to_f32", _F, [ctypes.c_uint16]),
+    ("xo_f32_to_bf16", ctypes.c_uint16, [_F]),
+    ("xo_e4m3_to_f32", _F, [ctypes.c_uint8]),
+    ("xo_f32_to_e4m3", ctypes.c_uint8, [_F]),
+    ("xo_e4m3_bits", ctypes.c_uint8, [_F]),
+    ("xo_e2m1", _F, [_I]),
+    ("xo_nvfp4_row", None, [ctypes.POINTER(Nvfp4), _I, _P]),
+    ("xo_matmul_nvfp4", _I, [ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P), _I]),
+    ("xo_bf16_row", None, [_P, _I64, _I, _P]),
+    ("xo_justnorm", None, [_P, _I, _I]),
+    ("xo_slerp_residual", None, [_P, _P, _P, _I, _I]),
+    ("xo_rope", None, [_P, _I, _I, _I, _I64, _F]),
+    ("xo_swiglu_scaled", None, [_P, _P, _P, _P, _I, _I]),
+    ("xo_rope_table", None, [_P, _I, _I, _I64, _F]),
+    ("xo_qk_produce", None, [_P, _P, _I, _I, _I, _I, _I64, _F, _P]),
+    ("xo_kv_create", _P, [_I, _I, _I64, _I, _I]),
+    ("xo_kv_free", None, [_P]),
+    ("xo_kv_slots", _I64, [_P]),
+    ("xo_kv_store", _I, [_P, _I64, _I, _P, _P]),
+    ("xo_kv_load", None, [_P, _I, _I64, _I64, _P, _P]),
+    ("xo_kv_kdata", _P, [_P]),
+    ("xo_kv_vdata", _P, [_P]),
+    ("xo_kv_kscale", _P, [_P]),
+    ("xo_kv_vscale", _P, [_P]),
+    ("xo_attention", _I, [ctypes.POINTER(AttnArgs), _I, _I]),
+    ("xo_attention_slots", _I, [ctypes.POINTER(AttnArgs), _P, _I]),
+]
+
+_REF_SIGS = [
+    ("xr_e4m3_to_f32", _F, [ctypes.c_uint8]),
+    ("xr_f32_to_e4m3", ctypes.c_uint8, [_F]),
+    ("xr_f32_to_bf16", ctypes.c_uint16, [_F]),
+    ("xr_bf16_to_f32", _F, [ctypes.c_uint16]),
+    ("xr_nvfp4_row", None, [ctypes.POINTER(Nvfp4), _I, _P]),
+    ("xr_matmul_nvfp4", _I, [ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P), _I]),
+    ("xr_justnorm", None, [_P, _I, _I]),
+    ("xr_slerp_residual", None, [_P, _P, _P, _I, _I]),
+    ("xr_rope", None, [_P, _I, _I, _I, _I64, _F]),
+    ("xr_swiglu_scaled", None, [_P, _P, _P, _P, _I, _I]),
+    ("xr_kv_create", _P, [_I, _I, _I64, _I, _I]),
+    ("xr_kv_free", None, [_P]),
+    ("xr_kv_store", _I, [_P, _I64, _I, _P, _P]),
+    ("xr_kv_load", None, [_P, _I, _I64, _I64, _P, _P]),
+    ("xr_attention", _I, [ctypes.POINTER(AttnArgs), _I]),
+]
+
+_oracle = None
+_ref = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError("oracle/liboracle.so is not built (make -C oracle)")
+        _oracle = _load(ORACLE_SO, _ORACLE_SIGS)
+    return _oracle
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        _ref = _load(REF_SO, _REF_SIGS)
+    return _ref
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _wstructs(ws):
+    arr = (Nvfp4 * len(ws))()
+    for i, (codes, scales, glob) in enumerate(ws):
+        arr[i] = Nvfp4(codes.ctypes.data, scales.ctypes.data, float(glob), codes.shape[0], codes.shape[1] * 2)
+    return arr
+
+
+def matmul_nvfp4(ws, x, threads=8, use_ref=False):
+    """ws: list of (codes, scales, global); x float32 [m][k]. Returns a list of float32 [m][n_i]."""
+    x = _f32(x)
+    m = x.shape[0]
+    for codes, scales, _ in ws:
+        assert codes.flags.c_contiguous and scales.flags.c_contiguous
+    ys = [np.empty((m, c.shape[0]), dtype=np.float32) for c, _, _ in ws]
+    yp = (_P * len(ws))(*[y.ctypes.data for y in ys])
+    st = _wstructs(ws)
+    if use_ref:
+        rc = ref().xr_matmul_nvfp4(st, len(ws), x.ctypes.data, m, yp, threads)
+    else:
+        rc = oracle().xo_matmul_nvfp4(st, len(ws), x.ctypes.data, m, yp, threads)
+    if rc != 0:
+        raise ValueError("matmul_nvfp4 rejected its arguments")
+    return ys
+
+
+def nvfp4_row(codes, scales, glob, n, use_ref=False):
+    st = _wstructs([(codes, scales, glob)])
+    out = np.empty(codes.shape[1] * 2, dtype=np.float32)
+    (ref().xr_nvfp4_row if use_ref else oracle().xo_nvfp4_row)(st, n, out.ctypes.data)
+    return out
+
+
+def justnorm(x, use_ref=False):
+    x = _f32(x).copy()
+    rows = x.shape[0] if x.ndim > 1 else 1
+    (ref().xr_justnorm if use_ref else oracle().xo_justnorm)(x.ctypes.data, rows, x.shape[-1])
+    return x
+
+
+def slerp_residual(a, b, lr, use_ref=False):
+    a = _f32(a).copy()
+    b = _f32(b)
+    lr = _f32(lr)
+    rows = a.shape[0] if a.ndim > 1 else 1
+    (ref().xr_slerp_residual if use_ref else oracle().xo_slerp_residual)(a.ctypes.data, b.ctypes.data, lr.ctypes.data,
+                                                                         rows, a.shape[-1])
+    return a
+
+
+def rope(x, heads, head_dim, pos0, theta, use_ref=False):
+    """x float32 [rows][heads][head_dim] (copied)."""
+    x = _f32(x).copy()
+    rows = x.size // (heads * head_dim)
+    (ref().xr_rope if use_ref else oracle().xo_rope)(x.ctypes.data, rows, heads, head_dim, pos0, theta)
+    return x
+
+
+def rope_table(m, head_dim, pos0, theta):
+    cs = np.empty((2 * m, head_dim // 2), dtype=np.float32)
+    oracle().xo_rope_table(cs.ctypes.data, m, head_dim, pos0, theta)
+    return cs
+
+
+def swiglu_scaled(g, u, sg, su, use_ref=False):
+    g = _f32(g).copy()
+    u = _f32(u)
+    rows = g.shape[0] if g.ndim > 1 else 1
+    (ref().xr_swiglu_scaled if use_ref else oracle().xo_swiglu_scaled)(g.ctypes.data, u.ctypes.data, _f32(sg).ctypes.data,
+                                                                       _f32(su).ctypes.data, rows, g.shape[-1])
+    return g
+
+
+def qk_produce(q, k, heads, kv_heads, head_dim, pos0, theta, qscale):
+    q = _f32(q).copy()
+    k = _f32(k).copy()
+    m = q.size // (heads * head_dim)
+    oracle().xo_qk_produce(q.ctypes.data, k.ctypes.data, m, heads, kv_heads, head_dim, pos0, theta,
+                           _f32(qscale).ctypes.data)
+    return q, k
+
+
+class KvCache:
+    """The oracle's (or the reference's) KvCache: kv.h:21-62."""
+
+    def __init__(self, kv_heads, head_dim, slots, ring=0, fp8=False, use_ref=False):
+        self.use_ref = use_ref
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+        self.slots = ring if ring > 0 else slots
+        self.ring = ring
+        if use_ref:
+            self.h = ref().xr_kv_create(kv_heads, head_dim, slots, ring, 1 if fp8 else 0)
+        else:
+            self.h = oracle().xo_kv_create(kv_heads, head_dim, slots, ring, 1 if fp8 else 0)
+        if not self.h:
+            raise ValueError("KV cache creation failed")
+
+    def __del__(self):
+        try:
+            if self.h:
+                (ref().xr_kv_free if self.use_ref else oracle().xo_kv_free)(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+    def store(self, pos, k, v):
+        k = _f32(k)
+        v = _f32(v)
+        n = k.shape[0]
+        f = ref().xr_kv_store if self.use_ref else oracle().xo_kv_store
+        if f(self.h, pos, n, k.ctypes.data, v.ctypes.data) != 0:
+            raise ValueError("KV cache full")
+
+    def load(self, h, p0, p1):
+        k = np.empty((p1 - p0, self.head_dim), dtype=np.float32)
+        v = np.empty_like(k)
+        (ref().xr_kv_load if self.use_ref else oracle().xo_kv_load)(self.h, h, p0, p1, k.ctypes.data, v.ctypes.data)
+        return k, v
+
+
+def attention(q, k, v, cache, pos0, heads, kv_heads, head_dim, window=0, scale=None, pool_size=8, threads=8,
+              slot_pos=None):
+    """q [n_q][heads][d], k / v [n_q][kv_heads][d] float32; returns out [n_q][heads][d]. With slot_pos (int64 per
+    ring slot) the ring mask is taken from the stored positions (xo_attention_slots)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    n_q = q.shape[0]
+    out = np.empty((n_q, heads, head_dim), dtype=np.float32)
+    sc = float(scale) if scale is not None else float(np.float32(1) / np.sqrt(np.float32(head_dim)))
+    a = AttnArgs(n_q, pos0, heads, kv_heads, head_dim, window, sc, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                 cache.h, out.ctypes.data)
+    if cache.use_ref:
+        rc = ref().xr_attention(ctypes.byref(a), pool_size)
+    elif slot_pos is not None:
+        sp = np.ascontiguousarray(slot_pos, dtype=np.int64)
+        rc = oracle().xo_attention_slots(ctypes.byref(a), sp.ctypes.data, threads)
+    else:
+        rc = oracle().xo_attention(ctypes.byref(a), pool_size, threads)
+    if rc != 0:
+        raise ValueError("attention rejected its arguments")
+    return out

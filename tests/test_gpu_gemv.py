@@ -1,0 +1,145 @@
+"""GPU parity of the NVFP4 GEMV / skinny GEMM (include/xtg_hip.h xtg_hip_matmul_nvfp4*) against the oracle's
+matmul_nvfp4 (engine/src/kernels.cpp:84-138) on the same seeded inputs.
+
+Bars: rel-L2 <= 1e-5 against the oracle; max |err| / RMS <= 3e-5 against the FP64 closed form (the reference's
+own device bar, tests/opencl_test.cpp:57). Shapes: the reference unit test's fused 70x256 + 33x256, ragged row
+counts, K not a multiple of 128, and the config shapes (3072x3072, QKV 5120, gate/up 2x8192, down K=8192) at
+M in {1, 2, 4, 8}.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(np.asarray(y, np.float64) - ref) / np.linalg.norm(ref))
+
+
+def err_over_rms(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref)) / np.sqrt(np.mean(ref ** 2)))
+
+
+def kt_weight(rng, n, k):
+    codes = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    scales = (0x20 + rng.integers(0, 0x30, size=(n, k // 16))).astype(np.uint8)
+    return codes, scales, 0.37
+
+
+@pytest.mark.parametrize("m", [1, 2, 7, 8, 13])
+def test_unit_shapes_host_call(hip, pkg, orc, wl, m):
+    """tests/kernels_test.cpp:57-87 shapes through the host-synchronous entry (rows > 8 run in passes of 8)."""
+    rng = np.random.default_rng(42 + m)
+    a, b = kt_weight(rng, 70, 256), kt_weight(rng, 33, 256)
+    x = rng.uniform(-1, 1, size=(m, 256)).astype(np.float32)
+    ys = hip.matmul([pkg.Weight(*a), pkg.Weight(*b)], x)
+    refs = orc.matmul_nvfp4([a, b], x)
+    for y, r, w in zip(ys, refs, (a, b)):
+        assert rel_l2(y, r) <= 1e-5
+        exact = x.astype(np.float64) @ wl.decode_nvfp4(*w).astype(np.float64).T
+        assert err_over_rms(y, exact) <= 3e-5
+
+
+@pytest.mark.parametrize("n,k", [(1, 16), (17, 48), (40, 272), (129, 1040)])
+def test_ragged_shapes(hip, pkg, orc, n, k):
+    """Row counts that do not fill a 16-row block, K a multiple of 16 but not of 32 or 128."""
+    rng = np.random.default_rng(n * 1000 + k)
+    w = kt_weight(rng, n, k)
+    for m in (1, 3, 8):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        (y,) = hip.matmul([pkg.Weight(*w)], x)
+        (r,) = orc.matmul_nvfp4([w], x)
+        assert rel_l2(y, r) <= 1e-5, (m, n, k)
+
+
+def test_zero_and_extreme_scales(hip, pkg, orc):
+    """Zero scales (code 0x00), the largest scale 448 (0x7e) and the smallest subnormal 2^-9 (0x01)."""
+    rng = np.random.default_rng(9)
+    n, k = 64, 512
+    codes = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    scales = rng.choice(np.array([0x00, 0x01, 0x07, 0x38, 0x7E, 0x40], np.uint8), size=(n, k // 16))
+    x = rng.standard_normal((4, k)).astype(np.float32)
+    (y,) = hip.matmul([pkg.Weight(codes, scales, 1.0)], x)
+    (r,) = orc.matmul_nvfp4([(codes, scales, 1.0)], x)
+    assert rel_l2(y, r) <= 1e-5
+
+
+def test_activation_scale_extremes(hip, pkg, orc):
+    """Rows of very different magnitude (1e-30 .. 1e30): each row is brought into f16 range on its own."""
+    rng = np.random.default_rng(10)
+    w = kt_weight(rng, 48, 256)
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    x[0] *= 1e-30
+    x[1] *= 1e30
+    x[2, 5] = 3e4
+    (y,) = hip.matmul([pkg.Weight(*w)], x)
+    (r,) = orc.matmul_nvfp4([w], x)
+    for i in range(4):
+        assert rel_l2(y[i], r[i]) <= 1e-5, i
+
+
+SHAPES = [(3072, 3072), (5120, 3072), (16384, 3072), (3072, 8192)]
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_config_shapes_device_bf16(hip, pkg, orc, wl, n, k, m):
+    """The config weights and BF16 unit rows through the device entry, x given as BF16."""
+    rng = np.random.default_rng(n + k + m)
+    w = wl.nvfp4_weight(rng, n, k)
+    xb = wl.unit_rows_bf16(rng, m, k)
+    x32 = wl.bf16_to_f32(xb)
+    dx = hip.array(xb)
+    dy = hip.array(shape=(m, n))
+    hip.matmul_dev([pkg.Weight(*w)], dx, pkg.X_BF16, m, dy)
+    y = dy.numpy()
+    dx.free()
+    dy.free()
+    (r,) = orc.matmul_nvfp4([w], x32)
+    assert rel_l2(y, r) <= 1e-5
+    if m in (1, 8) and n <= 5120:
+        exact = x32.astype(np.float64) @ wl.decode_nvfp4(*w).astype(np.float64).T
+        assert err_over_rms(y, exact) <= 3e-5
+
+
+def test_fused_gate_up_device_f32(hip, pkg, orc, wl):
+    """gate/up as one fused call (the MLP's two projections into consecutive [m][n] blocks), FP32 x."""
+    rng = np.random.default_rng(77)
+    g = wl.nvfp4_weight(rng, 8192, 3072)
+    u = wl.nvfp4_weight(rng, 8192, 3072)
+    m = 8
+    x = rng.standard_normal((m, 3072)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    dx = hip.array(x)
+    dy = hip.array(np.full(16 + 2 * m * 8192, np.nan, dtype=np.float32))
+    hip.matmul_dev([pkg.Weight(*g), pkg.Weight(*u)], dx, pkg.X_F32, m, dy, y_offset=16)
+    y = dy.numpy()
+    dx.free()
+    dy.free()
+    assert np.isnan(y[:16]).all()   # nothing written before y_offset
+    rg, ru = orc.matmul_nvfp4([g, u], x)
+    assert rel_l2(y[16:16 + m * 8192].reshape(m, 8192), rg) <= 1e-5
+    assert rel_l2(y[16 + m * 8192:].reshape(m, 8192), ru) <= 1e-5
+
+
+def test_fused_qkvg_four_weights(hip, pkg, orc, wl):
+    """q / k / v / g of the attention sublayer (4096 + 1024 + 1024 + 4096 rows) in one launch."""
+    rng = np.random.default_rng(78)
+    ws = [wl.nvfp4_weight(rng, n, 3072) for n in (4096, 1024, 1024, 4096)]
+    x = rng.standard_normal((3, 3072)).astype(np.float32)
+    ys = hip.matmul([pkg.Weight(*w) for w in ws], x)
+    refs = orc.matmul_nvfp4(ws, x)
+    for y, r in zip(ys, refs):
+        assert rel_l2(y, r) <= 1e-5
+
+
+def test_errors_are_reported(hip, pkg):
+    rng = np.random.default_rng(1)
+    a = kt_weight(rng, 8, 256)
+    b = kt_weight(rng, 8, 128)
+    with pytest.raises(pkg.XtgError, match="widths differ"):
+        hip.matmul([pkg.Weight(*a), pkg.Weight(*b)], np.zeros((1, 256), np.float32))
+    with pytest.raises(pkg.XtgError, match="rows"):
+        hip.matmul_dev([pkg.Weight(*a)], 0, pkg.X_F32, 9, 0)

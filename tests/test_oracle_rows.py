@@ -1,0 +1,104 @@
+"""Row kernels of the oracle (engine/src/kernels.cpp:162-234) and the Q/K producer composition
+(packs/dory/dory.cpp:482-490), pinned by mathematical invariants (unit norms, RoPE as a norm-preserving rotation
+that reduces to the identity at position 0, closed-form SwiGLU in FP64) and by golden vectors from the
+compiled reference."""
+import math
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_justnorm_unit_norm(orc):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((4, 3072)).astype(np.float32) * 3
+    y = orc.justnorm(x)
+    np.testing.assert_allclose(np.linalg.norm(y.astype(np.float64), axis=1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(y, x / np.sqrt((x.astype(np.float64) ** 2).sum(1, keepdims=True) + 1e-6), rtol=2e-6,
+                               atol=1e-9)
+
+
+def test_slerp_endpoints(orc):
+    """lr = 0 gives justnorm(a); lr = 1 gives justnorm(b); the result is always unit norm."""
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((2, 512)).astype(np.float32)
+    b = rng.standard_normal((2, 512)).astype(np.float32)
+    np.testing.assert_allclose(orc.slerp_residual(a, b, np.zeros(512, np.float32)), orc.justnorm(a), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(orc.slerp_residual(a, b, np.ones(512, np.float32)), orc.justnorm(b), rtol=1e-5, atol=1e-7)
+    y = orc.slerp_residual(a, b, rng.uniform(0, 1, 512).astype(np.float32))
+    np.testing.assert_allclose(np.linalg.norm(y.astype(np.float64), axis=1), 1.0, rtol=1e-6)
+
+
+def test_rope_rotation(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 4, 128)).astype(np.float32)
+    np.testing.assert_array_equal(orc.rope(x, 4, 128, 0, 1e6)[0], x[0])   # position 0: angle 0
+    y = orc.rope(x, 4, 128, 40000, 1e6)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+    # NeoX pairing (i, i + 64) with angle pos * theta^(-2i/d), checked in FP64 against FP32 angles
+    half = 64
+    # powf is correctly rounded here: the FP64 power rounded to FP32 (the exponent 2i/128 is exact in FP32)
+    inv = np.array([np.float32(1) / np.float32(math.pow(1e6, 2 * i / 128)) for i in range(half)], dtype=np.float32)
+    ang = (np.float32(40001) * inv).astype(np.float32).astype(np.float64)
+    x1, x2 = x[1, :, :half].astype(np.float64), x[1, :, half:].astype(np.float64)
+    ref = np.concatenate([x1 * np.cos(ang) - x2 * np.sin(ang), x2 * np.cos(ang) + x1 * np.sin(ang)], axis=-1)
+    np.testing.assert_allclose(y[1], ref, atol=2e-6)
+
+
+def test_rope_table_matches_rope(orc):
+    cs = orc.rope_table(3, 128, 40000, 1e6)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 1, 128)).astype(np.float32)
+    y = orc.rope(x, 1, 128, 40000, 1e6)
+    c, s = cs[:3], cs[3:]
+    ref = np.concatenate([x[:, 0, :64] * c - x[:, 0, 64:] * s, x[:, 0, 64:] * c + x[:, 0, :64] * s], axis=-1)
+    # the oracle (like the reference build) contracts x1 * c - x2 * s into an FMA: equal to rounding
+    np.testing.assert_allclose(y[:, 0], ref.astype(np.float32), rtol=0, atol=1e-6)
+
+
+def test_swiglu_closed_form(orc):
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((2, 256)).astype(np.float32)
+    u = rng.standard_normal((2, 256)).astype(np.float32)
+    sg = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    su = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    z = g.astype(np.float64) * sg
+    ref = z / (1 + np.exp(-z)) * (u.astype(np.float64) * su)
+    np.testing.assert_allclose(orc.swiglu_scaled(g, u, sg, su), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_qk_produce(orc):
+    """RoPE then per-head norm then q * qscale; k normalised and not scaled."""
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((2, 32, 128)).astype(np.float32)
+    k = rng.standard_normal((2, 8, 128)).astype(np.float32)
+    qs = rng.uniform(0.5, 1.5, 32 * 128).astype(np.float32)
+    qo, ko = orc.qk_produce(q, k, 32, 8, 128, 40000, 1e6, qs)
+    rq = orc.justnorm(orc.rope(q, 32, 128, 40000, 1e6).reshape(-1, 128)).reshape(2, 32 * 128) * qs
+    rk = orc.justnorm(orc.rope(k, 8, 128, 40000, 1e6).reshape(-1, 128)).reshape(2, 8, 128)
+    np.testing.assert_array_equal(qo.reshape(2, -1), rq)
+    np.testing.assert_array_equal(ko, rk)
+    np.testing.assert_allclose(np.linalg.norm(ko, axis=-1), 1.0, rtol=1e-6)
+
+
+def test_rows_golden(orc):
+    d = np.load(os.path.join(GOLDEN, "rows.npz"))
+    tol = dict(rtol=0, atol=1e-6)
+    np.testing.assert_allclose(orc.justnorm(d["x"]), d["justnorm"], **tol)
+    np.testing.assert_allclose(orc.slerp_residual(d["x"], d["b"], d["lr"]), d["slerp"], **tol)
+    np.testing.assert_allclose(orc.rope(d["qk"], 5, 128, 40000, 1e6), d["rope"], **tol)
+    np.testing.assert_allclose(orc.swiglu_scaled(d["g"], d["u"], d["sg"], d["su"]), d["swiglu"], **tol)
+
+
+@pytest.mark.skipif(not __import__("oracle").ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_rows_vs_reference_bitwise(orc):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5, 3072)).astype(np.float32)
+    b = rng.standard_normal((5, 3072)).astype(np.float32)
+    lr = rng.uniform(0, 0.2, 3072).astype(np.float32)
+    np.testing.assert_array_equal(orc.justnorm(x), orc.justnorm(x, use_ref=True))
+    np.testing.assert_array_equal(orc.slerp_residual(x, b, lr), orc.slerp_residual(x, b, lr, use_ref=True))
+    qk = rng.standard_normal((8, 40, 128)).astype(np.float32)
+    np.testing.assert_array_equal(orc.rope(qk, 40, 128, 39999, 1e6), orc.rope(qk, 40, 128, 39999, 1e6, use_ref=True))

@@ -1,0 +1,241 @@
+"""ctypes binding of libxtg_hip.so, the gfx950 kernel layer behind include/xtg_hip.h.
+
+The binding is a thin mirror of the C ABI for tests, benchmarks and Python callers. It has no CPU fallback:
+when the library is not built, every call raises.
+"""
+import ctypes
+import json
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libxtg_hip.so")
+
+X_F32, X_BF16 = 0, 1
+KV_BF16, KV_FP8 = 0, 1
+
+# Every function the header declares, with its ctypes signature: (name, restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_ERR = [ctypes.c_char_p, _I]
+
+
+class Nvfp4(ctypes.Structure):
+    """xtg_nvfp4 (same fields as xtg::Nvfp4Weight, engine/include/xtg/kernels.h:13-20)."""
+    _fields_ = [("codes", _P), ("scales", _P), ("glob", ctypes.c_float), ("n_out", _I), ("k", _I)]
+
+
+SIGNATURES = [
+    ("xtg_hip_open", _P, [ctypes.c_char_p] + _ERR),
+    ("xtg_hip_close", None, [_P]),
+    ("xtg_hip_info", _I, [_P, ctypes.c_char_p, _I]),
+    ("xtg_hip_stream", _P, [_P]),
+    ("xtg_hip_prepare_nvfp4", _I, [_P, ctypes.POINTER(Nvfp4)] + _ERR),
+    ("xtg_hip_release_nvfp4", _I, [_P, _P] + _ERR),
+    ("xtg_hip_matmul_nvfp4", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P)] + _ERR),
+    ("xtg_hip_matmul_nvfp4_dev", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _I, _P, _SZ] + _ERR),
+    ("xtg_hip_alloc", _I, [_P, _SZ, ctypes.POINTER(_P)] + _ERR),
+    ("xtg_hip_release", None, [_P, _P]),
+    ("xtg_hip_write", _I, [_P, _P, _SZ, _P, _SZ] + _ERR),
+    ("xtg_hip_read", _I, [_P, _P, _SZ, _P, _SZ] + _ERR),
+    ("xtg_hip_copy", _I, [_P, _P, _SZ, _P, _SZ, _SZ] + _ERR),
+    ("xtg_hip_finish", _I, [_P] + _ERR),
+]
+
+_lib = None
+
+
+class XtgError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library; raises when it is not built (there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise XtgError("libxtg_hip.so is not built (run __graft_entry__.build() or xtier-go_amd/build.py)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _errbuf():
+    return ctypes.create_string_buffer(2048)
+
+
+def _check(rc, err):
+    if rc != 0:
+        raise XtgError(err.value.decode(errors="replace"))
+
+
+def _ptr(a):
+    """Address of a numpy array or a torch tensor (device or host), or an int."""
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()   # torch.Tensor
+
+
+class Weight:
+    """An NVFP4 weight held in host memory: codes [n][k/2] u8, scales [n][k/16] u8 (E4M3), global f32."""
+
+    def __init__(self, codes, scales, glob=1.0):
+        self.codes = np.ascontiguousarray(codes, dtype=np.uint8)
+        self.scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        self.glob = float(glob)
+        self.n_out = self.codes.shape[0]
+        self.k = self.codes.shape[1] * 2
+        assert self.scales.shape == (self.n_out, self.k // 16)
+
+    def struct(self):
+        return Nvfp4(self.codes.ctypes.data, self.scales.ctypes.data, self.glob, self.n_out, self.k)
+
+
+def _structs(ws):
+    arr = (Nvfp4 * len(ws))()
+    for i, w in enumerate(ws):
+        arr[i] = w.struct()
+    return arr
+
+
+class HipBackend:
+    """One xtg_hip handle (a device, its stream and prepared weights)."""
+
+    def __init__(self, device=0):
+        err = _errbuf()
+        self.h = lib().xtg_hip_open(json.dumps({"device": device}).encode(), err, len(err))
+        if not self.h:
+            raise XtgError(err.value.decode(errors="replace"))
+        # Prepared weights are keyed by the address of their codes (as in the reference); every Weight passed in
+        # is kept alive here so that no later array can reuse an address that still names a prepared copy.
+        self._weights = {}
+
+    def close(self):
+        if self.h:
+            lib().xtg_hip_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self):
+        buf = ctypes.create_string_buffer(4096)
+        n = lib().xtg_hip_info(self.h, buf, len(buf))
+        if n < 0:
+            raise XtgError("info failed")
+        return json.loads(buf.value.decode())
+
+    @property
+    def stream(self):
+        return lib().xtg_hip_stream(self.h)
+
+    def _hold(self, ws):
+        for w in ws:
+            self._weights.setdefault(w.codes.ctypes.data, w)
+        return _structs(ws)
+
+    def prepare(self, w):
+        err = _errbuf()
+        arr = self._hold([w])
+        _check(lib().xtg_hip_prepare_nvfp4(self.h, arr, err, len(err)), err)
+
+    def release_weight(self, w):
+        """Drop the device copy of w (and let its host arrays go)."""
+        err = _errbuf()
+        key = w.codes.ctypes.data
+        _check(lib().xtg_hip_release_nvfp4(self.h, key, err, len(err)), err)
+        self._weights.pop(key, None)
+
+    def matmul(self, ws, x):
+        """Host-synchronous matmul_nvfp4: x float32 [m][k] -> list of float32 [m][n_i]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m = x.shape[0]
+        ys = [np.empty((m, w.n_out), dtype=np.float32) for w in ws]
+        yp = (_P * len(ws))(*[y.ctypes.data for y in ys])
+        err = _errbuf()
+        _check(lib().xtg_hip_matmul_nvfp4(self.h, self._hold(ws), len(ws), x.ctypes.data, m, yp, err, len(err)), err)
+        return ys
+
+    def matmul_dev(self, ws, x, x_dtype, m, y, y_offset=0):
+        """Queued device matmul: x, y are device addresses (ints or torch tensors)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_matmul_nvfp4_dev(self.h, self._hold(ws), len(ws), _ptr(x), x_dtype, m, _ptr(y), y_offset,
+                                              err, len(err)), err)
+
+    def alloc(self, nbytes):
+        err = _errbuf()
+        out = _P()
+        _check(lib().xtg_hip_alloc(self.h, nbytes, ctypes.byref(out), err, len(err)), err)
+        return out.value
+
+    def release(self, mem):
+        lib().xtg_hip_release(self.h, mem)
+
+    def write(self, mem, src, offset=0):
+        src = np.ascontiguousarray(src)
+        err = _errbuf()
+        _check(lib().xtg_hip_write(self.h, _ptr(mem), offset, src.ctypes.data, src.nbytes, err, len(err)), err)
+
+    def read(self, mem, dst, offset=0):
+        err = _errbuf()
+        _check(lib().xtg_hip_read(self.h, _ptr(mem), offset, dst.ctypes.data, dst.nbytes, err, len(err)), err)
+        return dst
+
+    def copy(self, src, dst, nbytes, src_offset=0, dst_offset=0):
+        err = _errbuf()
+        _check(lib().xtg_hip_copy(self.h, _ptr(src), src_offset, _ptr(dst), dst_offset, nbytes, err, len(err)), err)
+
+    def finish(self):
+        err = _errbuf()
+        _check(lib().xtg_hip_finish(self.h, err, len(err)), err)
+
+    def array(self, a=None, shape=None, dtype=np.float32):
+        """A device buffer owned by this backend, filled from the numpy array a (or left unset)."""
+        return DeviceArray(self, a, shape, dtype)
+
+
+class DeviceArray:
+    """Device memory from xtg_hip_alloc with a numpy shape and dtype (the library's own buffers, so no other
+    HIP runtime is involved)."""
+
+    def __init__(self, backend, a=None, shape=None, dtype=np.float32):
+        self.b = backend
+        if a is not None:
+            a = np.ascontiguousarray(a)
+            shape, dtype = a.shape, a.dtype
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = backend.alloc(max(self.nbytes, 4))
+        if a is not None:
+            backend.write(self.ptr, a)
+
+    def data_ptr(self):
+        return self.ptr
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes
+        self.b.write(self.ptr, a)
+
+    def numpy(self):
+        out = np.empty(self.shape, dtype=self.dtype)
+        return self.b.read(self.ptr, out)
+
+    def free(self):
+        if self.ptr:
+            self.b.release(self.ptr)
+            self.ptr = None

@@ -1,0 +1,146 @@
+// The C ABI of include/xtg_hip.h: every entry point catches what the backend throws and returns -1 (or NULL)
+// with the message in err, as the reference's plugin ABI does (npu/xtg_npu.cpp:517-526, server/capi.cpp:23-35).
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+
+#include "backend.hpp"
+#include "common.hpp"
+#include "xtg_hip.h"
+
+struct xtg_hip {
+  std::unique_ptr<xtg::hip::Backend> b;
+};
+
+namespace {
+void put_err(char* err, int err_len, const char* msg) {
+  if (err && err_len > 0) {
+    std::snprintf(err, size_t(err_len), "%s", msg);
+  }
+}
+
+template <class F>
+int guarded(char* err, int err_len, F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    put_err(err, err_len, e.what());
+  } catch (...) {
+    put_err(err, err_len, "unknown error");
+  }
+  return -1;
+}
+
+int option_int(const char* json, const char* key, int def) {
+  if (!json) return def;
+  std::string s(json), k = std::string("\"") + key + "\"";
+  size_t p = s.find(k);
+  if (p == std::string::npos) return def;
+  p = s.find(':', p + k.size());
+  if (p == std::string::npos) return def;
+  return std::atoi(s.c_str() + p + 1);
+}
+}  // namespace
+
+extern "C" {
+
+xtg_hip* xtg_hip_open(const char* options, char* err, int err_len) {
+  xtg_hip* h = nullptr;
+  int rc = guarded(err, err_len, [&] {
+    auto b = std::make_unique<xtg::hip::Backend>(option_int(options, "device", 0));
+    h = new xtg_hip{std::move(b)};
+  });
+  return rc == 0 ? h : nullptr;
+}
+
+void xtg_hip_close(xtg_hip* h) {
+  try {
+    delete h;
+  } catch (...) {
+  }
+}
+
+int xtg_hip_info(xtg_hip* h, char* out, int out_len) {
+  if (!h) return -1;
+  std::string s;
+  if (guarded(nullptr, 0, [&] { s = h->b->info_json(); }) != 0) return -1;
+  if (out && out_len > 0) std::snprintf(out, size_t(out_len), "%s", s.c_str());
+  return int(s.size());
+}
+
+void* xtg_hip_stream(xtg_hip* h) { return h ? static_cast<void*>(h->b->stream()) : nullptr; }
+
+int xtg_hip_prepare_nvfp4(xtg_hip* h, const xtg_nvfp4* w, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && w, "prepare: NULL handle or weight");
+    h->b->prepare(*w);
+  });
+}
+
+int xtg_hip_release_nvfp4(xtg_hip* h, const uint8_t* codes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "release_nvfp4: NULL handle");
+    h->b->release_weight(codes);
+  });
+}
+
+int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* x, int m, float* const* ys, char* err,
+                         int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && ws && ys, "matmul: NULL argument");
+    h->b->matmul(ws, n_w, x, m, ys);
+  });
+}
+
+int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
+                             size_t y_offset, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && ws, "matmul: NULL argument");
+    h->b->matmul_dev(ws, n_w, x, x_dtype, m, y, y_offset);
+  });
+}
+
+int xtg_hip_alloc(xtg_hip* h, size_t bytes, void** out, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && out, "alloc: NULL argument");
+    *out = h->b->alloc(bytes);
+  });
+}
+
+void xtg_hip_release(xtg_hip* h, void* mem) {
+  if (h) guarded(nullptr, 0, [&] { h->b->release(mem); });
+}
+
+int xtg_hip_write(xtg_hip* h, void* mem, size_t offset, const void* src, size_t bytes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && mem && (src || !bytes), "write: NULL argument");
+    h->b->write(mem, offset, src, bytes);
+  });
+}
+
+int xtg_hip_read(xtg_hip* h, const void* mem, size_t offset, void* dst, size_t bytes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && mem && (dst || !bytes), "read: NULL argument");
+    h->b->read(mem, offset, dst, bytes);
+  });
+}
+
+int xtg_hip_copy(xtg_hip* h, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes, char* err,
+                 int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && src && dst, "copy: NULL argument");
+    h->b->copy(src, src_offset, dst, dst_offset, bytes);
+  });
+}
+
+int xtg_hip_finish(xtg_hip* h, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "finish: NULL handle");
+    h->b->finish();
+  });
+}
+
+}  // extern "C"

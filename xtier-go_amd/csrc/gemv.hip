@@ -1,0 +1,333 @@
+// NVFP4 GEMV / skinny GEMM for 1..8 activation rows on gfx950 matrix cores.
+//
+// Semantics: y[m][n] = global * sum_g e4m3(scale[n][g]) * sum_{j in group g} e2m1(code[n][j]) * x[m][j]
+// (engine/src/kernels.cpp:48-60 and :116-137; the two CPU branches differ only in FP32 rounding order).
+//
+// Design (MI355X, bandwidth-bound at M <= 8):
+//  - Each wave owns R row-blocks of 16 rows and T k-tiles of 128 inputs; a work-group stacks S waves along k and
+//    adds their partials in LDS in a fixed order (deterministic, no atomics). Weights stream as one 16-byte load
+//    per lane per tile (a wave reads a contiguous 1 KiB) plus one 2-byte scale load.
+//  - Dequantisation is exact and in registers: FP4 -> f16 pairs by v_cvt_scalef32_pk_f16_fp4 (unit scale; the
+//    instruction's own scale uses only the exponent), then v_pk_mul_f16 by the E4M3 group scale, which f16 holds
+//    exactly; E2M1 x E4M3 products (at most 6 significant bits, 2^-10 .. 2688) are exact in f16.
+//  - v_mfma_f32_16x16x32_f16 does the products with FP32 accumulation. The operand's 16 columns carry the high
+//    and the low f16 part of up to 8 activation rows (each row first scaled by a power of two), so the FP32
+//    activations keep ~22 significant bits at no extra matrix-core cost.
+//  - Output: column j and j + 8 of the accumulator are added, times global and the row's 2^-s.
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace xtg::hip {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out) {
+  const int nb = (n + kTileRows - 1) / kTileRows, kt = (k + kTileK - 1) / kTileK;
+  out.assign(size_t(nb) * size_t(kt) * kTileBytes, 0);
+  const size_t row_c = size_t(k) / 2, row_s = size_t(k) / 16;
+  for (int rb = 0; rb < nb; ++rb)
+    for (int t = 0; t < kt; ++t) {
+      uint8_t* tile = out.data() + (size_t(rb) * size_t(kt) + size_t(t)) * kTileBytes;
+      for (int l = 0; l < 64; ++l) {
+        const int row = rb * kTileRows + (l & 15);
+        const int k0 = t * kTileK + 32 * (l >> 4);   // the lane's first input
+        if (row >= n || k0 >= k) continue;
+        const int nk = std::min(32, k - k0);         // 16 or 32: k is a multiple of 16
+        std::memcpy(tile + 16 * l, codes + size_t(row) * row_c + size_t(k0 / 2), size_t(nk / 2));
+        std::memcpy(tile + 1024 + 2 * l, scales + size_t(row) * row_s + size_t(k0 / 16), size_t(nk / 16));
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------- activation operand
+
+__device__ inline float load_x(const void* x, int x_dtype, size_t i) {
+  if (x_dtype == kXBF16) {
+    const uint32_t b = uint32_t(static_cast<const uint16_t*>(x)[i]) << 16;
+    return __uint_as_float(b);
+  }
+  return static_cast<const float*>(x)[i];
+}
+
+// One work-group per operand column pair (j, 8 + j), j < 8: row j's largest magnitude picks the power of two
+// 2^s that brings it to [2^14, 2^15); the scaled row is split into f16 high and low parts written in MFMA B
+// operand order. Rows j >= m are written as zeros.
+__global__ void __launch_bounds__(256) prep_x_kernel(const void* __restrict__ x, int x_dtype, int m, int k, int kt,
+                                                     f16x8* __restrict__ xop, float* __restrict__ xinv) {
+  __shared__ float red[256];
+  const int j = blockIdx.x, tid = threadIdx.x;
+  const bool live = j < m;
+  float mx = 0.f;
+  if (live)
+    for (int i = tid; i < k; i += 256) mx = fmaxf(mx, fabsf(load_x(x, x_dtype, size_t(j) * size_t(k) + size_t(i))));
+  red[tid] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  mx = red[0];
+  int e = 0;
+  if (mx > 0.f && mx <= FLT_MAX) e = 14 - ilogbf(mx);
+  e = std::min(120, std::max(-120, e));
+  const float up = ldexpf(1.f, e);
+  if (tid == 0) xinv[j] = ldexpf(1.f, -e);
+  for (int c = tid; c < kt * 16; c += 256) {   // chunk c: inputs 8c .. 8c + 7
+    const int k0 = c * 8;
+    f16x8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = (live && k0 + i < k) ? load_x(x, x_dtype, size_t(j) * size_t(k) + size_t(k0 + i)) * up : 0.f;
+      const _Float16 h = (_Float16)v;
+      hi[i] = h;
+      lo[i] = (_Float16)(v - (float)h);
+    }
+    // within k-tile c / 16: chunk w = 4 g + t holds inputs 32 g + 8 t .. +8 (lane group g of MFMA t)
+    const int w = c & 15, g = w >> 2, t = w & 3;
+    const size_t base = (size_t(c >> 4) * 4 + size_t(t)) * 64;
+    xop[base + size_t(g * 16 + j)] = hi;
+    xop[base + size_t(g * 16 + 8 + j)] = lo;
+  }
+}
+
+void launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream) {
+  XTG_CHECK(m >= 1 && m <= kMaxRows, "prep_x: %d rows (1..%d)", m, kMaxRows);
+  const int kt = (k + kTileK - 1) / kTileK;
+  hipLaunchKernelGGL(prep_x_kernel, dim3(kMaxRows), dim3(256), 0, stream, x, x_dtype, m, k, kt,
+                     static_cast<f16x8*>(xop), xinv);
+  HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------------------ GEMV
+
+struct GemvArgs {
+  const uint8_t* tiles[4];
+  int nb[4];
+  int n[4];
+  float global[4];
+  long long y_off[4];
+  int wg_end[4];   // cumulative work-group counts per weight
+  int nw;
+  int kt;
+  int m;
+  const uint4* xop;
+  const float* xinv;
+  float* y;
+};
+
+__device__ inline f16x8 dequant8(uint32_t word, f16x2 s) {
+  const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 0) * s;
+  const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 1) * s;
+  const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 2) * s;
+  const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 3) * s;
+  f16x8 a;
+  a[0] = p0[0];
+  a[1] = p0[1];
+  a[2] = p1[0];
+  a[3] = p1[1];
+  a[4] = p2[0];
+  a[5] = p2[1];
+  a[6] = p3[0];
+  a[7] = p3[1];
+  return a;
+}
+
+__device__ inline f16x2 scale_pair(uint32_t sbits, int which) {
+  const _Float16 s = (_Float16)(which ? __builtin_amdgcn_cvt_f32_fp8(sbits, 1) : __builtin_amdgcn_cvt_f32_fp8(sbits, 0));
+  f16x2 r;
+  r[0] = s;
+  r[1] = s;
+  return r;
+}
+
+// Output of one accumulator fragment: lane (g, j), j < 8, holds rows 4 g .. 4 g + 3 of the row-block for
+// activation row j.
+__device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int j, f32x4 v) {
+  if (j >= a.m) return;
+  const int n = a.n[wi];
+  const int n0 = rb * kTileRows + 4 * g;
+  const float f = a.global[wi] * a.xinv[j];
+  float* yp = a.y + a.y_off[wi] + (long long)j * n;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (n0 + e < n) yp[n0 + e] = v[e] * f;
+}
+
+template <int R, int T, int MAXT>
+__global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
+  extern __shared__ f32x4 red[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  int wi = 0;
+  while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+  const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * R;
+  const int nb = a.nb[wi], KT = a.kt;
+  const uint8_t* __restrict__ tiles = a.tiles[wi];
+  const int kt0 = wave * T;
+
+  // every load of the wave first (T k-tiles of activations, R x T weight tiles), then the math
+  uint4 xb[T][4];
+  uint4 cw[T][R];
+  uint32_t sw[T][R];
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    const int kt = kt0 + u;
+    const bool ok = kt < KT;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xb[u][t] = ok ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(lane)] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool ok2 = ok && rb0 + r < nb;
+      const uint8_t* tile = tiles + (size_t(rb0 + r) * size_t(KT) + size_t(kt)) * kTileBytes;
+      cw[u][r] = ok2 ? *reinterpret_cast<const uint4*>(tile + 16 * lane) : make_uint4(0, 0, 0, 0);
+      sw[u][r] = ok2 ? uint32_t(*reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane)) : 0u;
+    }
+  }
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const f16x2 s0 = scale_pair(sw[u][r], 0), s1 = scale_pair(sw[u][r], 1);
+      const uint32_t words[4] = {cw[u][r].x, cw[u][r].y, cw[u][r].z, cw[u][r].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f16x8 A = dequant8(words[t], t < 2 ? s0 : s1);
+        const f16x8 B = __builtin_bit_cast(f16x8, xb[u][t]);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[r], 0, 0, 0);
+      }
+    }
+  }
+  const int g = lane >> 4, j = lane & 15;
+  if (S == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f32x4 v = acc[r];
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = __shfl_xor(v[e], 8);
+      if (j < 8 && rb0 + r < nb) store_rows(a, wi, rb0 + r, g, j, v + o);
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
+    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7, ln = gg * 16 + jj;
+    if (rb0 + r >= nb) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < S; ++w) sum += red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 8];
+    store_rows(a, wi, rb0 + r, gg, jj, sum);
+  }
+}
+
+namespace {
+using GemvFn = void (*)(const GemvArgs);
+
+template <int R, int T>
+GemvFn pick_fn(int threads) {
+  if (threads <= 512) return gemv_kernel<R, T, 512>;
+  return gemv_kernel<R, T, 1024>;
+}
+
+GemvFn gemv_fn(int r, int t, int threads) {
+#define XTG_CASE(R, T) \
+  if (r == R && t == T) return pick_fn<R, T>(threads);
+  XTG_CASE(1, 1) XTG_CASE(1, 2) XTG_CASE(1, 3) XTG_CASE(1, 4) XTG_CASE(1, 6) XTG_CASE(1, 8)
+  XTG_CASE(2, 1) XTG_CASE(2, 2) XTG_CASE(2, 3) XTG_CASE(2, 4) XTG_CASE(2, 6)
+  XTG_CASE(4, 1) XTG_CASE(4, 2) XTG_CASE(4, 3)
+#undef XTG_CASE
+  return nullptr;
+}
+
+bool shape_ok(int r, int t, int s) {
+  if (s < 1 || s > 16) return false;
+  if (r * t > 12) return false;
+  if (s > 8 && r * t > 4) return false;   // 1024-thread groups get 128 VGPRs per lane
+  return gemv_fn(r, t, s * 64) != nullptr;
+}
+}  // namespace
+
+GemvShape gemv_shape(int /*unused*/, int kt, const int* nbs, int nw) {
+  if (const char* env = std::getenv("XTG_GEMV_SHAPE")) {   // "R,T": a fixed shape for experiments
+    int r = 0, t = 0;
+    if (std::sscanf(env, "%d,%d", &r, &t) == 2) {
+      const int s = (kt + t - 1) / t;
+      if (shape_ok(r, t, s)) return {r, t, s};
+    }
+  }
+  // Enough waves to cover the chip (256 CUs x 8), then as much work per wave as possible (more loads in
+  // flight per wave, more reuse of the activation operand across row-blocks).
+  GemvShape best{1, 1, std::min(16, kt)};
+  long best_waves = -1, best_rt = 0;
+  for (int r : {4, 2, 1})
+    for (int t : {8, 6, 4, 3, 2, 1}) {
+      const int s = (kt + t - 1) / t;
+      if (!shape_ok(r, t, s)) continue;
+      long wgs = 0;
+      for (int i = 0; i < nw; ++i) wgs += (nbs[i] + r - 1) / r;
+      const long waves = wgs * s;
+      const bool full = waves >= 2048, best_full = best_waves >= 2048;
+      bool take;
+      if (full != best_full)
+        take = full;
+      else if (full)
+        take = r * t > best_rt || (r * t == best_rt && waves < best_waves);
+      else
+        take = waves > best_waves;
+      if (take) {
+        best = {r, t, s};
+        best_waves = waves;
+        best_rt = r * t;
+      }
+    }
+  return best;
+}
+
+void launch_gemv(const GemvCall& c, hipStream_t stream) {
+  XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
+  XTG_CHECK(c.m >= 1 && c.m <= kMaxRows, "gemv: %d rows (1..%d)", c.m, kMaxRows);
+  GemvArgs a{};
+  const int kt = c.w[0]->kt;
+  int nbs[4];
+  for (int i = 0; i < c.nw; ++i) {
+    XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
+    nbs[i] = c.w[i]->nb;
+  }
+  const GemvShape sh = gemv_shape(0, kt, nbs, c.nw);
+  int wgs = 0;
+  for (int i = 0; i < c.nw; ++i) {
+    a.tiles[i] = c.w[i]->tiles;
+    a.nb[i] = c.w[i]->nb;
+    a.n[i] = c.w[i]->n;
+    a.global[i] = c.w[i]->global;
+    a.y_off[i] = (long long)c.y_off[i];
+    wgs += (c.w[i]->nb + sh.r - 1) / sh.r;
+    a.wg_end[i] = wgs;
+  }
+  for (int i = c.nw; i < 4; ++i) a.wg_end[i] = wgs;
+  a.nw = c.nw;
+  a.kt = kt;
+  a.m = c.m;
+  a.xop = static_cast<const uint4*>(c.xop);
+  a.xinv = c.xinv;
+  a.y = c.y;
+  const int threads = sh.s * 64;
+  GemvFn fn = gemv_fn(sh.r, sh.t, threads);
+  XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d", sh.r, sh.t);
+  const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * 64 * sizeof(f32x4) : 0;
+  hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace xtg::hip

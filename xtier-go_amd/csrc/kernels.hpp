@@ -1,0 +1,55 @@
+// Host-side launchers of the gfx950 kernels (the kernels themselves live in the .hip files).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace xtg::hip {
+
+// ---- NVFP4 GEMV / skinny GEMM (gemv.hip) ----
+//
+// Device weight layout: tiles of 16 rows x 128 inputs, 1152 bytes each, row-block major ([rb][kt]):
+//   bytes    0..1023: lane l's 16 bytes at 16 l = the codes of row rb*16 + (l & 15), inputs
+//                     kt*128 + 32 (l >> 4) .. +32 (the original bytes, low nibble = even input)
+//   bytes 1024..1151: lane l's 2 bytes at 1024 + 2 l = that row's two E4M3 scales for those 32 inputs
+// Rows past n_out and inputs past k are zero codes with zero scales.
+constexpr int kTileRows = 16, kTileK = 128, kTileBytes = 1152;
+
+struct PackedNvfp4 {
+  uint8_t* tiles = nullptr;   // device
+  size_t bytes = 0;
+  int n = 0, k = 0, nb = 0, kt = 0;
+  float global = 1.f;
+};
+
+// Host repack of [n][k/2] codes and [n][k/16] scales into the tile layout above.
+void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out);
+
+// The MFMA operand form of the activations: [kt][4][64 lanes][8 f16] (4096 bytes per k-tile). Column j < 8 of
+// the operand is the high f16 part of row j scaled by 2^s_j, column 8 + j the low part; xinv[j] = 2^-s_j.
+inline size_t xop_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 4096; }
+constexpr int kMaxRows = 8;
+
+enum XDtype { kXF32 = 0, kXBF16 = 1 };
+void launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream);
+
+struct GemvCall {
+  const PackedNvfp4* w[4] = {nullptr, nullptr, nullptr, nullptr};
+  int nw = 0;
+  size_t y_off[4] = {0, 0, 0, 0};   // floats from y
+  float* y = nullptr;
+  int m = 0;
+  const void* xop = nullptr;
+  const float* xinv = nullptr;
+};
+// The launch shape: R row-blocks and T k-tiles per wave, S waves per work-group along k.
+struct GemvShape {
+  int r = 1, t = 1, s = 1;
+};
+GemvShape gemv_shape(int nb_total_for_r1, int kt, const int* nbs, int nw);
+void launch_gemv(const GemvCall& c, hipStream_t stream);
+
+}  // namespace xtg::hip
