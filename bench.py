@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the NVFP4 skinny-GEMM hot path on one MI355X.
+
+Workload (one step): the three projection shapes of one synthetic 4B-shaped layer -- QKV (N=5120, K=3072),
+fused gate/up (2 x N=8192, K=3072, one launch) and down (N=3072, K=8192) -- each at M=1 (decode) and at M=8
+(the speculative-verify batch): 6 calls, each = activation-operand prep + the GEMV kernel. Weights follow the
+BASELINE distributions (uniform E2M1 codes, |N(0,1)|*0.05 E4M3 scales, tensor scale 1.0); activations are unit
+BF16 rows. Consecutive calls read different copies of their weights, rotating over >= 1 GiB, so every launch
+streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed from HIP graphs (one per
+rotation phase), so host launch cost does not set the pace.
+
+value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
+roofline: the GEMV kernel alone. For each (shape, rows) a graph of one GEMV launch per weight copy on a prepared
+operand is replayed between two HIP events on the backend's stream; achieved = algorithmic bytes of those
+launches / their time, against the 8 TB/s HBM peak.
+cpu_baseline: the reference engine's own CPU matmul_nvfp4 (oracle/_ref, compiled from the reference sources)
+on the same shapes and inputs on this host's cores, or the oracle restatement when that library is absent.
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "xtier-go_amd")
+HBM_PEAK_GBS = 8000.0
+METRIC = "NVFP4 GEMV HBM GB/s (%peak) at M=1/8; synthetic 4B decode tok/s @4K/8K/32K"
+
+# name, weights (n, k) fused in one call
+SHAPES = [("qkv5120", [(5120, 3072)]), ("gateup2x8192", [(8192, 3072), (8192, 3072)]), ("down3072x8192", [(3072, 8192)])]
+ROWS = (1, 8)
+
+
+def load_package():
+    if "xtier_go_amd" in sys.modules:
+        return sys.modules["xtier_go_amd"]
+    spec = importlib.util.spec_from_file_location("xtier_go_amd", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["xtier_go_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def call_bytes(ws, m):
+    """Algorithmic HBM bytes of one call: codes + scales + tensor scale per weight, BF16 x once, FP32 y."""
+    k = ws[0][1]
+    return sum(n * k // 2 + n * k // 16 + 4 for n, _ in ws) + 2 * m * k + 4 * m * sum(n for n, _ in ws)
+
+
+def cpu_baseline(base, xs, seconds):
+    """The reference's CPU matmul_nvfp4 (or the oracle) over the step's 6 calls, until `seconds` have passed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    use_ref = orc.ref_available()
+    threads = os.cpu_count() or 1
+    ws_by = {name: [(w.codes, w.scales, w.glob) for w in base[name]] for name, _ in SHAPES}
+    calls = [(name, m) for m in ROWS for name, _ in SHAPES]
+    orc.matmul_nvfp4(ws_by[calls[0][0]], xs[calls[0]], threads=threads, use_ref=use_ref)   # warm-up
+    done, nbytes, t0 = 0, 0, time.perf_counter()
+    while True:
+        for name, m in calls:
+            orc.matmul_nvfp4(ws_by[name], xs[(name, m)], threads=threads, use_ref=use_ref)
+            nbytes += call_bytes(dict(SHAPES)[name], m)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(nbytes / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d passes over the step's 6 calls (QKV 5120, gate/up 2x8192, down 3072x8192 at M=1 and M=8, "
+                      "same weights and inputs, one weight copy), %.1f s on %d threads" % (done, el, threads)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate over (0: enough for 1 GiB)")
+    ap.add_argument("--roofline-reps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the kernels are one GPU's share of a "
+              "sharded layer); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = load_package()
+    import xtier_go_amd.workloads as wl
+
+    rng = np.random.default_rng(20261201)
+    base = {name: [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes] for name, shapes in SHAPES}
+    set_bytes = sum(w.codes.nbytes + w.scales.nbytes for ws in base.values() for w in ws)
+    copies = args.copies or max(2, -(-(1 << 30) // set_bytes) + 1)
+    log("weight set %.1f MB, %d copies (%.2f GiB)" % (set_bytes / 1e6, copies, copies * set_bytes / 2 ** 30))
+
+    hip = pkg.HipBackend(0)
+    info = hip.info()
+    log("device %s, %d CUs" % (info["arch"], info["cus"]))
+    sets = []
+    for _ in range(copies):
+        s = {name: [pkg.Weight(w.codes.copy(), w.scales.copy(), w.glob) for w in ws] for name, ws in base.items()}
+        for ws in s.values():
+            for w in ws:
+                hip.prepare(w)
+        sets.append(s)
+    log("prepared %d weight copies (%.2f GB on the device)" % (copies, hip.info()["weight_bytes"] / 1e9))
+
+    xs, dx, ops = {}, {}, {}
+    for name, shapes in SHAPES:
+        k = shapes[0][1]
+        xb = wl.unit_rows_bf16(rng, 8, k)
+        for m in ROWS:
+            xs[(name, m)] = wl.bf16_to_f32(xb[:m])
+            dx[(name, m)] = hip.array(xb[:m])
+            ops[(name, m)] = hip.array(shape=(hip.x_operand_bytes(k),), dtype=np.uint8)
+            hip.prep_x(dx[(name, m)], pkg.X_BF16, m, k, ops[(name, m)])
+    dy = hip.array(shape=(8 * 16384 + 64,))
+    calls = [(name, m) for m in ROWS for name, _ in SHAPES]
+    step_bytes = sum(call_bytes(dict(SHAPES)[name], m) for name, m in calls)
+
+    # one graph per rotation phase p: call i of the step reads copy (6 p + i) mod copies
+    for name, m in calls:   # size the scratch before capturing
+        hip.matmul_dev(sets[0][name], dx[(name, m)], pkg.X_BF16, m, dy)
+    hip.finish()
+    phases = []
+    for p in range(copies):
+        hip.graph_begin()
+        for i, (name, m) in enumerate(calls):
+            hip.matmul_dev(sets[(len(calls) * p + i) % copies][name], dx[(name, m)], pkg.X_BF16, m, dy)
+        phases.append(hip.graph_end("step_phase%d" % p))
+
+    for s in range(args.warmup):
+        hip.graph_launch(phases[s % copies])
+    hip.finish()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        hip.graph_launch(phases[s % copies])
+    hip.finish()
+    el = time.perf_counter() - t0
+    ms_per_step = el / args.steps * 1e3
+    value = step_bytes / (el / args.steps) / 1e9
+    log("timed %d steps: %.4f ms/step, %.1f GB/s whole-step (%.1f%% of HBM peak)"
+        % (args.steps, ms_per_step, value, value / HBM_PEAK_GBS * 100))
+
+    # roofline: GEMV-only graphs (one launch per weight copy on a prepared operand), timed by events
+    per_call = {}
+    gemv_graphs = {}
+    for name, m in calls:
+        hip.graph_begin()
+        for c in range(copies):
+            hip.matmul_op(sets[c][name], ops[(name, m)], m, dy)
+        gemv_graphs[(name, m)] = hip.graph_end("gemv_%s_m%d" % (name, m))
+    for g in gemv_graphs.values():   # warm
+        hip.graph_launch(g)
+    hip.finish()
+    hip.profile(True)
+    for _ in range(args.roofline_reps):
+        for g in gemv_graphs.values():
+            hip.graph_launch(g)
+    rep = hip.profile_report()
+    hip.profile(False)
+    tot_bytes, tot_s = 0, 0.0
+    for name, m in calls:
+        t = rep["gemv_%s_m%d" % (name, m)]
+        launches = t["calls"] * copies
+        us = t["ms"] * 1e3 / launches
+        b = call_bytes(dict(SHAPES)[name], m)
+        per_call["%s_m%d" % (name, m)] = {"us_per_launch": round(us, 3), "bytes": b, "gbs": round(b / us / 1e3, 1),
+                                          "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        tot_bytes += b * launches
+        tot_s += t["ms"] / 1e3
+    achieved = tot_bytes / tot_s / 1e9
+    by_m = {}
+    for m in ROWS:
+        keys = ["%s_m%d" % (name, m) for name, _ in SHAPES]
+        by_m["m%d" % m] = round(sum(per_call[k]["bytes"] for k in keys) /
+                                sum(per_call[k]["us_per_launch"] for k in keys) / 1e3, 1)
+    log("GEMV kernel: %.1f GB/s (%.1f%% of HBM peak) averaged over the 6 shapes; M=1 %.1f, M=8 %.1f GB/s"
+        % (achieved, achieved / HBM_PEAK_GBS * 100, by_m["m1"], by_m["m8"]))
+    for k, v in per_call.items():
+        log("  %-22s %7.3f us  %7.1f GB/s" % (k, v["us_per_launch"], v["gbs"]))
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(base, xs, args.cpu_seconds)
+        log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "NVFP4 skinny GEMM over one 4B-shaped layer's projections: QKV N=5120 K=3072, fused gate/up "
+                        "2x8192 K=3072, down N=3072 K=8192, each at M=1 and M=8 (6 calls per step, prep + GEMV each; "
+                        "BF16 unit-row activations, FP32 out); weights rotated over %d copies (%.2f GiB) so each "
+                        "call reads HBM; steps replayed from HIP graphs" % (copies, copies * set_bytes / 2 ** 30),
+            "step_bytes": step_bytes,
+            "gemv_gbs_by_rows": by_m,
+            "per_call": per_call,
+        },
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    hip.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -76,6 +76,15 @@ int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* 
 int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
                              size_t y_offset, char* err, int err_len);
 
+/* The device matmul in its two steps, for callers that reuse one activation operand or produce it themselves
+ * (no counterpart in the reference, whose kernels read FP32 x directly): xtg_hip_x_operand_bytes(k) bytes of
+ * device memory hold the matrix-core form of up to 8 rows of x; xtg_hip_prep_x fills it (queued) and
+ * xtg_hip_matmul_nvfp4_op runs the projections on it with the same output convention as the call above. */
+size_t xtg_hip_x_operand_bytes(int k);
+int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* op, char* err, int err_len);
+int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* op, int m, float* y, size_t y_offset,
+                            char* err, int err_len);
+
 /* ------------------------------------------------------------------------------------- device buffers */
 
 /* Replaces OpenClBackend::alloc / release / write / read / copy / finish (opencl.h:40-45). write() is blocking
@@ -87,6 +96,29 @@ int xtg_hip_read(xtg_hip* h, const void* mem, size_t offset, void* dst, size_t b
 int xtg_hip_copy(xtg_hip* h, const void* src, size_t src_offset, void* dst, size_t dst_offset, size_t bytes,
                  char* err, int err_len);
 int xtg_hip_finish(xtg_hip* h, char* err, int err_len);
+
+/* ------------------------------------------------------------------------------------------------- graphs */
+
+/* No counterpart in the reference (its OpenCL queue replays nothing): HIP graphs over the backend's stream, the
+ * survey's graph_begin / end / replay. Every device call queued between begin and end is captured into one graph
+ * instead of running; launch replays it on the stream. Weights must be prepared and scratch sized before the
+ * capture (run the calls once first); blocking calls fail during a capture. `name` (may be NULL) is the graph's
+ * entry in the profile report, where a profiled replay is timed as a whole. */
+typedef struct xtg_hip_graph xtg_hip_graph;
+int xtg_hip_graph_begin(xtg_hip* h, char* err, int err_len);
+int xtg_hip_graph_end(xtg_hip* h, const char* name, xtg_hip_graph** out, char* err, int err_len);
+int xtg_hip_graph_launch(xtg_hip* h, xtg_hip_graph* g, char* err, int err_len);
+void xtg_hip_graph_destroy(xtg_hip* h, xtg_hip_graph* g);
+
+/* ---------------------------------------------------------------------------------------------- profiling */
+
+/* Replaces the XTG_GPU_PROFILE switch of the OpenCL backend (opencl.cpp:293-315, :391-392): with enable != 0
+ * every kernel the backend queues is bracketed by two events on its stream. */
+int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len);
+/* Waits for queued work and writes {"kernels": {name: {"calls": n, "ms": total}}} for the launches recorded since
+ * the last report (names as rocprof prints them, without the namespace), then starts over. Returns the length
+ * (without the NUL), or -1. */
+int xtg_hip_profile_report(xtg_hip* h, char* out, int out_len);
 
 #ifdef __cplusplus
 }

@@ -36,12 +36,21 @@ SIGNATURES = [
     ("xtg_hip_release_nvfp4", _I, [_P, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P)] + _ERR),
     ("xtg_hip_matmul_nvfp4_dev", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _I, _P, _SZ] + _ERR),
+    ("xtg_hip_x_operand_bytes", _SZ, [_I]),
+    ("xtg_hip_prep_x", _I, [_P, _P, _I, _I, _I, _P] + _ERR),
+    ("xtg_hip_matmul_nvfp4_op", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _P, _SZ] + _ERR),
     ("xtg_hip_alloc", _I, [_P, _SZ, ctypes.POINTER(_P)] + _ERR),
     ("xtg_hip_release", None, [_P, _P]),
     ("xtg_hip_write", _I, [_P, _P, _SZ, _P, _SZ] + _ERR),
     ("xtg_hip_read", _I, [_P, _P, _SZ, _P, _SZ] + _ERR),
     ("xtg_hip_copy", _I, [_P, _P, _SZ, _P, _SZ, _SZ] + _ERR),
     ("xtg_hip_finish", _I, [_P] + _ERR),
+    ("xtg_hip_graph_begin", _I, [_P] + _ERR),
+    ("xtg_hip_graph_end", _I, [_P, ctypes.c_char_p, ctypes.POINTER(_P)] + _ERR),
+    ("xtg_hip_graph_launch", _I, [_P, _P] + _ERR),
+    ("xtg_hip_graph_destroy", None, [_P, _P]),
+    ("xtg_hip_profile", _I, [_P, _I] + _ERR),
+    ("xtg_hip_profile_report", _I, [_P, ctypes.c_char_p, _I]),
 ]
 
 _lib = None
@@ -175,6 +184,21 @@ class HipBackend:
         _check(lib().xtg_hip_matmul_nvfp4_dev(self.h, self._hold(ws), len(ws), _ptr(x), x_dtype, m, _ptr(y), y_offset,
                                               err, len(err)), err)
 
+    @staticmethod
+    def x_operand_bytes(k):
+        return lib().xtg_hip_x_operand_bytes(k)
+
+    def prep_x(self, x, x_dtype, m, k, op):
+        """Queued: the matrix-core operand of x ([m][k] on the device) into the device buffer op."""
+        err = _errbuf()
+        _check(lib().xtg_hip_prep_x(self.h, _ptr(x), x_dtype, m, k, _ptr(op), err, len(err)), err)
+
+    def matmul_op(self, ws, op, m, y, y_offset=0):
+        """Queued: the projections of a prepared operand into y (as matmul_dev)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_matmul_nvfp4_op(self.h, self._hold(ws), len(ws), _ptr(op), m, _ptr(y), y_offset, err,
+                                             len(err)), err)
+
     def alloc(self, nbytes):
         err = _errbuf()
         out = _P()
@@ -201,6 +225,36 @@ class HipBackend:
     def finish(self):
         err = _errbuf()
         _check(lib().xtg_hip_finish(self.h, err, len(err)), err)
+
+    def graph_begin(self):
+        err = _errbuf()
+        _check(lib().xtg_hip_graph_begin(self.h, err, len(err)), err)
+
+    def graph_end(self, name=None):
+        """The captured graph (an opaque handle for graph_launch / graph_destroy)."""
+        err = _errbuf()
+        g = _P()
+        _check(lib().xtg_hip_graph_end(self.h, name.encode() if name else None, ctypes.byref(g), err, len(err)), err)
+        return g.value
+
+    def graph_launch(self, g):
+        err = _errbuf()
+        _check(lib().xtg_hip_graph_launch(self.h, g, err, len(err)), err)
+
+    def graph_destroy(self, g):
+        lib().xtg_hip_graph_destroy(self.h, g)
+
+    def profile(self, enable=True):
+        err = _errbuf()
+        _check(lib().xtg_hip_profile(self.h, 1 if enable else 0, err, len(err)), err)
+
+    def profile_report(self):
+        """{kernel name: {"calls": n, "ms": total}} since the last report (waits for queued work)."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        n = lib().xtg_hip_profile_report(self.h, buf, len(buf))
+        if n < 0 or n >= len(buf):
+            raise XtgError("profile report failed")
+        return json.loads(buf.value.decode())["kernels"]
 
     def array(self, a=None, shape=None, dtype=np.float32):
         """A device buffer owned by this backend, filled from the numpy array a (or left unset)."""

@@ -18,16 +18,29 @@ Backend::Backend(int device) : device_(device) {
 Backend::~Backend() {
   // teardown: errors cannot be reported from a destructor; every release is still attempted
   (void)hipSetDevice(device_);
+  if (capturing_) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(stream_, &g);
+    if (g) (void)hipGraphDestroy(g);
+  }
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.first);
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {xop_, xinv_, hx_, hy_})
+  for (void* p : {op_, hx_, hy_})
     if (p) (void)hipFree(p);
+  for (const Pending& p : pending_) {
+    (void)hipEventDestroy(p.a);
+    (void)hipEventDestroy(p.b);
+  }
+  for (hipEvent_t e : free_events_) (void)hipEventDestroy(e);
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
 void Backend::ensure(void*& buf, size_t& size, size_t need) {
   if (size >= need) return;
+  XTG_CHECK(!capturing_, "scratch of %zu bytes needed during graph capture (run the calls once before capturing)",
+            need);
   if (buf) {
     HIP_CHECK(hipStreamSynchronize(stream_));   // queued work may still read the old buffer
     HIP_CHECK(hipFree(buf));
@@ -47,6 +60,7 @@ const PackedNvfp4& Backend::prepare(const xtg_nvfp4& w) {
     return it->second;
   }
   XTG_CHECK(w.n_out > 0 && w.k > 0 && w.k % 16 == 0, "prepare: invalid NVFP4 shape %dx%d (k %% 16 == 0)", w.n_out, w.k);
+  XTG_CHECK(!capturing_, "prepare: weights must be prepared before a graph capture");
   std::vector<uint8_t> host;
   pack_nvfp4_tiles(w.codes, w.scales, w.n_out, w.k, host);
   PackedNvfp4 p;
@@ -63,6 +77,7 @@ const PackedNvfp4& Backend::prepare(const xtg_nvfp4& w) {
 }
 
 void Backend::release_weight(const uint8_t* codes) {
+  XTG_CHECK(!capturing_, "release_nvfp4: not during a graph capture");
   auto it = weights_.find(codes);
   if (it == weights_.end()) return;
   HIP_CHECK(hipStreamSynchronize(stream_));   // queued launches may still read it
@@ -73,9 +88,24 @@ void Backend::release_weight(const uint8_t* codes) {
 
 void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off) {
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
+  const int k = ws[0].k;
+  ensure(op_, op_size_, op_bytes(k));
+  prep_x(x, x_dtype, m, k, op_);
+  matmul_op(ws, nw, op_, m, y, y_off);
+}
+
+void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op) {
   XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul: %d rows (1..%d per device call)", m, kMaxRows);
   XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul: unknown activation type %d", x_dtype);
-  XTG_CHECK(x && y, "matmul: NULL input or output");
+  XTG_CHECK(x && op, "prep_x: NULL input or operand");
+  float* xinv = reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(k));
+  timed([&] { return launch_prep_x(x, x_dtype, m, k, op, xinv, stream_); });
+}
+
+void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off) {
+  XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
+  XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul: %d rows (1..%d per device call)", m, kMaxRows);
+  XTG_CHECK(op && y, "matmul: NULL operand or output");
   const int k = ws[0].k;
   GemvCall c;
   c.nw = nw;
@@ -86,18 +116,93 @@ void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype
     c.y_off[i] = off;
     off += size_t(m) * size_t(ws[i].n_out);
   }
-  ensure(xop_, xop_size_, xop_bytes(k));
-  ensure(xinv_, xinv_size_, kMaxRows * sizeof(float));
-  launch_prep_x(x, x_dtype, m, k, xop_, static_cast<float*>(xinv_), stream_);
   c.y = y;
   c.m = m;
-  c.xop = xop_;
-  c.xinv = static_cast<const float*>(xinv_);
-  launch_gemv(c, stream_);
+  c.xop = op;
+  c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
+  timed([&] { return launch_gemv(c, stream_); });
+}
+
+hipEvent_t Backend::event() {
+  if (!free_events_.empty()) {
+    hipEvent_t e = free_events_.back();
+    free_events_.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  HIP_CHECK(hipEventCreate(&e));
+  return e;
+}
+
+void Backend::set_profile(bool on) {
+  XTG_CHECK(!capturing_, "profile: not during graph capture");
+  if (!on && profile_) profile_report();   // settle what was recorded
+  profile_ = on;
+}
+
+void Backend::graph_begin() {
+  XTG_CHECK(!capturing_, "graph_begin: a capture is already open");
+  XTG_CHECK(!profile_, "graph_begin: profiling is on (events cannot be timed inside a graph)");
+  HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+  capturing_ = true;
+}
+
+hipGraphExec_t Backend::graph_end(const std::string& name) {
+  XTG_CHECK(capturing_, "graph_end: no capture open");
+  capturing_ = false;
+  hipGraph_t g = nullptr;
+  HIP_CHECK(hipStreamEndCapture(stream_, &g));
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) fail("hipGraphInstantiate failed: %s", hipGetErrorString(e));
+  graphs_[exec] = name.empty() ? strf("graph#%zu", graphs_.size()) : name;
+  return exec;
+}
+
+void Backend::graph_launch(hipGraphExec_t g) {
+  auto it = graphs_.find(g);
+  XTG_CHECK(it != graphs_.end(), "graph_launch: unknown graph");
+  XTG_CHECK(!capturing_, "graph_launch: not during a capture");
+  timed([&] {
+    HIP_CHECK(hipGraphLaunch(g, stream_));
+    return it->second;
+  });
+}
+
+void Backend::graph_destroy(hipGraphExec_t g) {
+  auto it = graphs_.find(g);
+  if (it == graphs_.end()) return;
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipGraphExecDestroy(g));
+  graphs_.erase(it);
+}
+
+std::string Backend::profile_report() {
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  for (const Pending& p : pending_) {
+    float ms = 0;
+    HIP_CHECK(hipEventElapsedTime(&ms, p.a, p.b));
+    auto it = std::find_if(totals_.begin(), totals_.end(), [&](const auto& t) { return t.first == p.name; });
+    if (it == totals_.end()) it = totals_.insert(totals_.end(), {p.name, Total{}});
+    it->second.calls += 1;
+    it->second.ms += ms;
+    free_events_.push_back(p.a);
+    free_events_.push_back(p.b);
+  }
+  pending_.clear();
+  std::string s = "{\"kernels\": {";
+  for (size_t i = 0; i < totals_.size(); ++i)
+    s += strf("%s\"%s\": {\"calls\": %ld, \"ms\": %.6f}", i ? ", " : "", totals_[i].first.c_str(),
+              totals_[i].second.calls, totals_[i].second.ms);
+  s += "}}";
+  totals_.clear();
+  return s;
 }
 
 void Backend::matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* const* ys) {
   XTG_CHECK(nw >= 1 && m >= 1 && x, "matmul: %d weights, %d rows", nw, m);
+  XTG_CHECK(!capturing_, "matmul: the host-synchronous call cannot be captured (use the device call)");
   const int k = ws[0].k;
   for (int i = 0; i < nw; ++i) XTG_CHECK(ws[i].k == k && k % 16 == 0, "matmul: input widths differ (%d, %d)", ws[i].k, k);
   // more than four weights: groups of four, each group one fused launch
@@ -135,6 +240,7 @@ void* Backend::alloc(size_t bytes) {
 
 void Backend::release(void* p) {
   if (!p) return;
+  XTG_CHECK(!capturing_, "release: not during a graph capture");
   auto it = allocs_.find(p);
   XTG_CHECK(it != allocs_.end(), "release: %p was not allocated by this backend", p);
   HIP_CHECK(hipStreamSynchronize(stream_));
@@ -143,12 +249,14 @@ void Backend::release(void* p) {
 }
 
 void Backend::write(void* dst, size_t offset, const void* src, size_t bytes) {
+  XTG_CHECK(!capturing_, "write: blocking copies cannot be captured");
   if (!bytes) return;
   HIP_CHECK(hipMemcpyAsync(static_cast<char*>(dst) + offset, src, bytes, hipMemcpyHostToDevice, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 void Backend::read(const void* src, size_t offset, void* dst, size_t bytes) {
+  XTG_CHECK(!capturing_, "read: blocking copies cannot be captured");
   if (bytes)
     HIP_CHECK(hipMemcpyAsync(dst, static_cast<const char*>(src) + offset, bytes, hipMemcpyDeviceToHost, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));
@@ -160,7 +268,10 @@ void Backend::copy(const void* src, size_t src_off, void* dst, size_t dst_off, s
                            hipMemcpyDeviceToDevice, stream_));
 }
 
-void Backend::finish() { HIP_CHECK(hipStreamSynchronize(stream_)); }
+void Backend::finish() {
+  XTG_CHECK(!capturing_, "finish: not during a graph capture");
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
 
 std::string Backend::info_json() const {
   hipDeviceProp_t p;

@@ -11,6 +11,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "common.hpp"
 #include "kernels.hpp"
 #include "xtg_hip.h"
 
@@ -30,6 +31,10 @@ class Backend {
   void matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* const* ys);
   // opencl.h:54-55 device matmul into consecutive [m][n_i] blocks from y_off
   void matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off);
+  // the two halves of matmul_dev: the activation operand ([xop][8 row scales], op_bytes(k)) and the GEMV on it
+  static size_t op_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
+  void prep_x(const void* x, int x_dtype, int m, int k, void* op);
+  void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off);
 
   // opencl.h:40-45
   void* alloc(size_t bytes);
@@ -44,18 +49,58 @@ class Backend {
   std::string info_json() const;
   size_t weight_bytes() const { return weight_bytes_; }
 
+  // Per-kernel device time (the reference's XTG_GPU_PROFILE, opencl.cpp:293-315): with profiling on, every
+  // launch is bracketed by two events on the stream; report() waits, sums the durations per kernel name and
+  // starts over.
+  void set_profile(bool on);
+  std::string profile_report();
+
+  // HIP graphs over the backend's stream: begin/end capture every launch queued in between into one graph,
+  // launch() replays it. Scratch buffers must already be large enough (run the calls once before capturing).
+  void graph_begin();
+  hipGraphExec_t graph_end(const std::string& name);   // name: the graph's entry in the profile report
+  void graph_launch(hipGraphExec_t g);
+  void graph_destroy(hipGraphExec_t g);
+  bool capturing() const { return capturing_; }
+  // Runs fn, which queues one kernel and returns its name, between two profile events when profiling is on.
+  template <class F>
+  void timed(F&& fn) {
+    if (!profile_) {
+      fn();
+      return;
+    }
+    hipEvent_t a = event(), b = event();
+    HIP_CHECK(hipEventRecord(a, stream_));
+    std::string name = fn();
+    HIP_CHECK(hipEventRecord(b, stream_));
+    pending_.push_back({name, a, b});
+  }
+
  private:
   void ensure(void*& buf, size_t& size, size_t need);
+  hipEvent_t event();
+  struct Pending {
+    std::string name;
+    hipEvent_t a, b;
+  };
+  bool profile_ = false;
+  bool capturing_ = false;
+  std::unordered_map<hipGraphExec_t, std::string> graphs_;
+  std::vector<Pending> pending_;
+  std::vector<hipEvent_t> free_events_;
+  struct Total {
+    long calls = 0;
+    double ms = 0;
+  };
+  std::vector<std::pair<std::string, Total>> totals_;
   int device_ = 0;
   hipStream_t stream_ = nullptr;
   std::unordered_map<const uint8_t*, PackedNvfp4> weights_;
   std::unordered_set<void*> allocs_;
   size_t weight_bytes_ = 0;
   // scratch (grown on demand, owned): activation operand, its row scales, host-call staging
-  void* xop_ = nullptr;
-  size_t xop_size_ = 0;
-  void* xinv_ = nullptr;
-  size_t xinv_size_ = 0;
+  void* op_ = nullptr;
+  size_t op_size_ = 0;
   void* hx_ = nullptr;
   size_t hx_size_ = 0;
   void* hy_ = nullptr;

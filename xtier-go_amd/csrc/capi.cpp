@@ -103,6 +103,23 @@ int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const voi
   });
 }
 
+size_t xtg_hip_x_operand_bytes(int k) { return k > 0 ? xtg::hip::Backend::op_bytes(k) : 0; }
+
+int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* op, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "prep_x: NULL handle");
+    h->b->prep_x(x, x_dtype, m, k, op);
+  });
+}
+
+int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* op, int m, float* y, size_t y_offset,
+                            char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && ws, "matmul: NULL argument");
+    h->b->matmul_op(ws, n_w, op, m, y, y_offset);
+  });
+}
+
 int xtg_hip_alloc(xtg_hip* h, size_t bytes, void** out, char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h && out, "alloc: NULL argument");
@@ -134,6 +151,46 @@ int xtg_hip_copy(xtg_hip* h, const void* src, size_t src_offset, void* dst, size
     XTG_CHECK(h && src && dst, "copy: NULL argument");
     h->b->copy(src, src_offset, dst, dst_offset, bytes);
   });
+}
+
+int xtg_hip_graph_begin(xtg_hip* h, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "graph_begin: NULL handle");
+    h->b->graph_begin();
+  });
+}
+
+int xtg_hip_graph_end(xtg_hip* h, const char* name, xtg_hip_graph** out, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && out, "graph_end: NULL argument");
+    *out = reinterpret_cast<xtg_hip_graph*>(h->b->graph_end(name ? name : ""));
+  });
+}
+
+int xtg_hip_graph_launch(xtg_hip* h, xtg_hip_graph* g, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && g, "graph_launch: NULL argument");
+    h->b->graph_launch(reinterpret_cast<hipGraphExec_t>(g));
+  });
+}
+
+void xtg_hip_graph_destroy(xtg_hip* h, xtg_hip_graph* g) {
+  if (h && g) guarded(nullptr, 0, [&] { h->b->graph_destroy(reinterpret_cast<hipGraphExec_t>(g)); });
+}
+
+int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "profile: NULL handle");
+    h->b->set_profile(enable != 0);
+  });
+}
+
+int xtg_hip_profile_report(xtg_hip* h, char* out, int out_len) {
+  if (!h) return -1;
+  std::string s;
+  if (guarded(nullptr, 0, [&] { s = h->b->profile_report(); }) != 0) return -1;
+  if (out && out_len > 0) std::snprintf(out, size_t(out_len), "%s", s.c_str());
+  return int(s.size());
 }
 
 int xtg_hip_finish(xtg_hip* h, char* err, int err_len) {

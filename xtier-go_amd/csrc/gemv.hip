@@ -57,53 +57,106 @@ __device__ inline float load_x(const void* x, int x_dtype, size_t i) {
   return static_cast<const float*>(x)[i];
 }
 
-// One work-group per operand column pair (j, 8 + j), j < 8: row j's largest magnitude picks the power of two
-// 2^s that brings it to [2^14, 2^15); the scaled row is split into f16 high and low parts written in MFMA B
-// operand order. Rows j >= m are written as zeros.
-__global__ void __launch_bounds__(256) prep_x_kernel(const void* __restrict__ x, int x_dtype, int m, int k, int kt,
-                                                     f16x8* __restrict__ xop, float* __restrict__ xinv) {
-  __shared__ float red[256];
-  const int j = blockIdx.x, tid = threadIdx.x;
-  const bool live = j < m;
-  float mx = 0.f;
-  if (live)
-    for (int i = tid; i < k; i += 256) mx = fmaxf(mx, fabsf(load_x(x, x_dtype, size_t(j) * size_t(k) + size_t(i))));
-  red[tid] = mx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
+// Eight consecutive inputs of row j from chunk c (inputs 8c .. 8c + 7); zeros past k (k is a multiple of 16, so
+// a chunk is either whole or past the end).
+__device__ inline void load_chunk(const void* x, int x_dtype, int j, int k, int c, float v[8]) {
+  const int k0 = c * 8;
+  if (k0 >= k) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    return;
   }
+  const size_t base = size_t(j) * size_t(k) + size_t(k0);
+  if (x_dtype == kXBF16) {
+    const uint4 b = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base);
+    const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + base);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+}
+
+// Row j's chunk c as the f16 high and low parts of x * 2^e, stored where MFMA lane (g, j) / (g, 8 + j) of
+// k-tile c / 16 reads them: chunk w = 4 g + t of a tile holds inputs 32 g + 8 t .. +8 (lane group g, MFMA t).
+__device__ inline void store_chunk(f16x8* xop, int j, int c, const float v[8], float up) {
+  f16x8 hi, lo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float s = v[i] * up;
+    const _Float16 h = (_Float16)s;
+    hi[i] = h;
+    lo[i] = (_Float16)(s - (float)h);
+  }
+  const int w = c & 15, g = w >> 2, t = w & 3;
+  const size_t base = (size_t(c >> 4) * 4 + size_t(t)) * 64;
+  xop[base + size_t(g * 16 + j)] = hi;
+  xop[base + size_t(g * 16 + 8 + j)] = lo;
+}
+
+// One work-group per activation row j < m: the row's largest magnitude picks the power of two 2^e that brings it
+// to [2^14, 2^15); the scaled row is split into f16 high and low parts in MFMA B-operand order (columns j and
+// 8 + j). Rows up to 8192 wide make one read of x (chunks held in registers); wider rows read x twice. Columns of
+// rows >= m are not written: the GEMV never loads them.
+constexpr int kPrepThreads = 256, kPrepChunks = 4;
+__global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __restrict__ x, int x_dtype, int k, int kt,
+                                                              f16x8* __restrict__ xop, float* __restrict__ xinv) {
+  __shared__ float red[kPrepThreads / 64];
+  const int j = blockIdx.x, tid = threadIdx.x;
+  const int chunks = kt * 16;
+  float v[kPrepChunks][8];
+  float mx = 0.f;
+#pragma unroll
+  for (int u = 0; u < kPrepChunks; ++u) {
+    const int c = tid + u * kPrepThreads;
+    load_chunk(x, x_dtype, j, k, c < chunks ? c : chunks, v[u]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
+  }
+  for (int c = tid + kPrepChunks * kPrepThreads; c < chunks; c += kPrepThreads) {
+    float w[8];
+    load_chunk(x, x_dtype, j, k, c, w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(w[i]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
   mx = red[0];
+#pragma unroll
+  for (int i = 1; i < kPrepThreads / 64; ++i) mx = fmaxf(mx, red[i]);
   int e = 0;
   if (mx > 0.f && mx <= FLT_MAX) e = 14 - ilogbf(mx);
   e = std::min(120, std::max(-120, e));
   const float up = ldexpf(1.f, e);
   if (tid == 0) xinv[j] = ldexpf(1.f, -e);
-  for (int c = tid; c < kt * 16; c += 256) {   // chunk c: inputs 8c .. 8c + 7
-    const int k0 = c * 8;
-    f16x8 hi, lo;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = (live && k0 + i < k) ? load_x(x, x_dtype, size_t(j) * size_t(k) + size_t(k0 + i)) * up : 0.f;
-      const _Float16 h = (_Float16)v;
-      hi[i] = h;
-      lo[i] = (_Float16)(v - (float)h);
-    }
-    // within k-tile c / 16: chunk w = 4 g + t holds inputs 32 g + 8 t .. +8 (lane group g of MFMA t)
-    const int w = c & 15, g = w >> 2, t = w & 3;
-    const size_t base = (size_t(c >> 4) * 4 + size_t(t)) * 64;
-    xop[base + size_t(g * 16 + j)] = hi;
-    xop[base + size_t(g * 16 + 8 + j)] = lo;
+  for (int u = 0; u < kPrepChunks; ++u) {
+    const int c = tid + u * kPrepThreads;
+    if (c < chunks) store_chunk(xop, j, c, v[u], up);
+  }
+  for (int c = tid + kPrepChunks * kPrepThreads; c < chunks; c += kPrepThreads) {
+    float w[8];
+    load_chunk(x, x_dtype, j, k, c, w);
+    store_chunk(xop, j, c, w, up);
   }
 }
 
-void launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream) {
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream) {
   XTG_CHECK(m >= 1 && m <= kMaxRows, "prep_x: %d rows (1..%d)", m, kMaxRows);
+  XTG_CHECK(k > 0 && k % 16 == 0, "prep_x: width %d (a multiple of 16)", k);
+  XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, "prep_x: activations at %p are not 16-byte aligned", x);
   const int kt = (k + kTileK - 1) / kTileK;
-  hipLaunchKernelGGL(prep_x_kernel, dim3(kMaxRows), dim3(256), 0, stream, x, x_dtype, m, k, kt,
+  hipLaunchKernelGGL(prep_x_kernel, dim3(unsigned(m)), dim3(kPrepThreads), 0, stream, x, x_dtype, k, kt,
                      static_cast<f16x8*>(xop), xinv);
   HIP_CHECK(hipGetLastError());
+  return "prep_x_kernel";
 }
 
 // ------------------------------------------------------------------------------------------------------ GEMV
@@ -172,7 +225,10 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   const uint8_t* __restrict__ tiles = a.tiles[wi];
   const int kt0 = wave * T;
 
-  // every load of the wave first (T k-tiles of activations, R x T weight tiles), then the math
+  // every load of the wave first (T k-tiles of activations, R x T weight tiles), then the math; operand columns
+  // of absent activation rows are not loaded (their accumulator columns are never stored)
+  const int col = lane & 15;
+  const bool live_col = (col < 8 ? col : col - 8) < a.m;
   uint4 xb[T][4];
   uint4 cw[T][R];
   uint32_t sw[T][R];
@@ -181,7 +237,8 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     const int kt = kt0 + u;
     const bool ok = kt < KT;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xb[u][t] = ok ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(lane)] : make_uint4(0, 0, 0, 0);
+    for (int t = 0; t < 4; ++t)
+      xb[u][t] = ok && live_col ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(lane)] : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool ok2 = ok && rb0 + r < nb;
@@ -258,7 +315,7 @@ bool shape_ok(int r, int t, int s) {
 }
 }  // namespace
 
-GemvShape gemv_shape(int /*unused*/, int kt, const int* nbs, int nw) {
+GemvShape gemv_shape(int kt, const int* nbs, int nw) {
   if (const char* env = std::getenv("XTG_GEMV_SHAPE")) {   // "R,T": a fixed shape for experiments
     int r = 0, t = 0;
     if (std::sscanf(env, "%d,%d", &r, &t) == 2) {
@@ -294,7 +351,7 @@ GemvShape gemv_shape(int /*unused*/, int kt, const int* nbs, int nw) {
   return best;
 }
 
-void launch_gemv(const GemvCall& c, hipStream_t stream) {
+std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
   XTG_CHECK(c.m >= 1 && c.m <= kMaxRows, "gemv: %d rows (1..%d)", c.m, kMaxRows);
   GemvArgs a{};
@@ -304,7 +361,7 @@ void launch_gemv(const GemvCall& c, hipStream_t stream) {
     XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
     nbs[i] = c.w[i]->nb;
   }
-  const GemvShape sh = gemv_shape(0, kt, nbs, c.nw);
+  const GemvShape sh = gemv_shape(kt, nbs, c.nw);
   int wgs = 0;
   for (int i = 0; i < c.nw; ++i) {
     a.tiles[i] = c.w[i]->tiles;
@@ -328,6 +385,7 @@ void launch_gemv(const GemvCall& c, hipStream_t stream) {
   const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * 64 * sizeof(f32x4) : 0;
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
+  return strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, threads <= 512 ? 512 : 1024);
 }
 
 }  // namespace xtg::hip

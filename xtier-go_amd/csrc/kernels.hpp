@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <string>
 #include <vector>
 
 namespace xtg::hip {
@@ -34,7 +35,8 @@ inline size_t xop_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 4096
 constexpr int kMaxRows = 8;
 
 enum XDtype { kXF32 = 0, kXBF16 = 1 };
-void launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream);
+// Launchers return the kernel's name (as rocprof prints it, without the namespace) for the profiler.
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream);
 
 struct GemvCall {
   const PackedNvfp4* w[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -49,7 +51,7 @@ struct GemvCall {
 struct GemvShape {
   int r = 1, t = 1, s = 1;
 };
-GemvShape gemv_shape(int nb_total_for_r1, int kt, const int* nbs, int nw);
-void launch_gemv(const GemvCall& c, hipStream_t stream);
+GemvShape gemv_shape(int kt, const int* nbs, int nw);
+std::string launch_gemv(const GemvCall& c, hipStream_t stream);
 
 }  // namespace xtg::hip
