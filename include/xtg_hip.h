@@ -85,6 +85,76 @@ int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* o
 int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* op, int m, float* y, size_t y_offset,
                             char* err, int err_len);
 
+/* ------------------------------------------------------------------------------------------- KV caches */
+
+/* Replaces xtg::KvCache(kv_heads, head_dim, slots, ring, dtype) (kv.h:24, kv.cpp:42-63): ring > 0 makes a ring of
+ * `ring` slots (slot = position mod ring), else a linear cache of `slots` positions, in device memory. BF16 only
+ * (dtype XTG_KV_BF16). Every slot starts empty. NULL on failure. */
+xtg_hip_kv* xtg_hip_kv_create(xtg_hip* h, int kv_heads, int head_dim, int64_t slots, int ring, int dtype, char* err,
+                              int err_len);
+void xtg_hip_kv_destroy(xtg_hip* h, xtg_hip_kv* kv);
+/* Replaces KvCache::store (kv.h:35, kv.cpp:75-112): rows of positions pos .. pos + n - 1 from device FP32 k, v
+ * [n][kv_heads][head_dim], rounded to BF16 (nearest even); a ring keeps the last `ring` rows; queued. A linear
+ * cache refuses positions beyond its capacity ("KV cache full"). */
+int xtg_hip_kv_store(xtg_hip* h, xtg_hip_kv* kv, int64_t pos, int n, const float* k, const float* v, char* err,
+                     int err_len);
+/* Replaces KvCache::load (kv.h:37, kv.cpp:114-138): FP32 K and V rows of head `head` for positions p0 .. p1 - 1
+ * into host k, v [p1 - p0][head_dim]; waits for queued work. */
+int xtg_hip_kv_load(xtg_hip* h, const xtg_hip_kv* kv, int head, int64_t p0, int64_t p1, float* k, float* v, char* err,
+                    int err_len);
+/* Replaces KvCache::save / restore / release (kv.h:45-48): the whole cache (K, V and slot positions) as
+ * xtg_hip_kv_bytes() host bytes and back; release empties every slot. */
+int64_t xtg_hip_kv_bytes(xtg_hip* h, const xtg_hip_kv* kv);
+int xtg_hip_kv_save(xtg_hip* h, const xtg_hip_kv* kv, void* out, size_t bytes, char* err, int err_len);
+int xtg_hip_kv_restore(xtg_hip* h, xtg_hip_kv* kv, const void* in, size_t bytes, char* err, int err_len);
+int xtg_hip_kv_release(xtg_hip* h, xtg_hip_kv* kv, char* err, int err_len);
+
+/* ------------------------------------------------------------------------------------------- attention */
+
+/* xtg::AttnArgs (kv.h:67-78), field for field, with device pointers and a device cache. */
+typedef struct xtg_attn_args {
+  int n_q;
+  int64_t pos0;
+  int heads, kv_heads, head_dim;
+  int window;
+  float scale;
+  const float* q;   /* [n_q][heads][head_dim] */
+  const float* k;   /* [n_q][kv_heads][head_dim]: this call's keys, FP32, not yet stored */
+  const float* v;
+  const xtg_hip_kv* cache;
+  float* out;       /* [n_q][heads][head_dim] */
+} xtg_attn_args;
+/* Replaces xtg::attention(ThreadPool&, const AttnArgs&) (kv.h:79, kv.cpp:166-286): causal GQA attention of the
+ * call's n_q rows over the cached positions before pos0 plus the call's own keys; window > 0 limits a row at t to
+ * keys t - window + 1 .. t. The cache is read only; which slots a row sees is decided from the positions stored
+ * in them (for a ring: npu/xtg_npu.cpp:236-258). Queued. head_dim 64 or 128, at most 8 q heads per KV head. */
+int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len);
+
+/* ----------------------------------------------------------------------------------------- row kernels */
+
+/* The Q/K producer of an attention sublayer (packs/dory/dory.cpp:482-490; the OpenCL rope_norm, dory.cpp:728-746):
+ * NeoX RoPE of q [m][heads][head_dim] and k [m][kv_heads][head_dim] at positions pos0 + row (inv_freq as
+ * engine/src/kernels.cpp:191-201), justnorm per head, then q times qscale [heads * head_dim] (NULL: no scale);
+ * in place, queued. */
+int xtg_hip_qk_rope_norm(xtg_hip* h, float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0,
+                         float theta, const float* qscale, char* err, int err_len);
+/* xtg::slerp_residual (kernels.h:43, kernels.cpp:177-189; OpenCL slerp dory.cpp:680-696): x = justnorm(ya + lr *
+ * (yb - ya)), ya = justnorm(x), yb = justnorm(o), per row of width; in place, queued. */
+int xtg_hip_slerp_residual(xtg_hip* h, float* x, const float* o, const float* lr, int rows, int width, char* err,
+                           int err_len);
+/* swiglu_scaled then justnorm (kernels.h:48, kernels.cpp:225-234, dory.cpp:474-475; OpenCL swiglu_norm
+ * dory.cpp:698-711): g = justnorm(silu(g * sg) * (u * su)); in place, queued. */
+int xtg_hip_swiglu_norm(xtg_hip* h, float* g, const float* u, const float* sg, const float* su, int rows, int width,
+                        char* err, int err_len);
+/* The attention output gate (dory.cpp:510-515; OpenCL gate_norm dory.cpp:713-726): att = justnorm(att *
+ * sigmoid(gate * gs)) over each row; in place, queued. */
+int xtg_hip_gate_norm(xtg_hip* h, float* att, const float* gate, const float* gs, int rows, int width, char* err,
+                      int err_len);
+/* The loop entry / exit norms (dory.cpp:532-541; OpenCL add_norm dory.cpp:669-678): out = justnorm(a + b), or
+ * justnorm(a) when b is NULL; out may be a; queued. */
+int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int rows, int width, char* err,
+                     int err_len);
+
 /* ------------------------------------------------------------------------------------- device buffers */
 
 /* Replaces OpenClBackend::alloc / release / write / read / copy / finish (opencl.h:40-45). write() is blocking

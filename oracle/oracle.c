@@ -274,6 +274,23 @@ void xo_swiglu_scaled(float* g, const float* u, const float* sg, const float* su
   }
 }
 
+void xo_gate_norm(float* att, const float* gate, const float* gs, int rows, int width) {
+  /* packs/dory/dory.cpp:510-515: sigmoid output gate, then a norm over all heads */
+  for (int r = 0; r < rows; ++r) {
+    float* ar = att + (size_t)r * (size_t)width;
+    const float* gr = gate + (size_t)r * (size_t)width;
+    for (int j = 0; j < width; ++j) ar[j] *= 1.f / (1.f + expf(-gr[j] * gs[j]));
+  }
+  xo_justnorm(att, rows, width);
+}
+
+void xo_add_norm(const float* a, const float* b, float* out, int rows, int width) {
+  /* packs/dory/dory.cpp:532-541: loop entry x = justnorm(state + input); loop exit state = justnorm(x) */
+  const size_t n = (size_t)rows * (size_t)width;
+  for (size_t i = 0; i < n; ++i) out[i] = b ? a[i] + b[i] : a[i];
+  xo_justnorm(out, rows, width);
+}
+
 void xo_qk_produce(float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0, float theta,
                    const float* qscale) {
   /* packs/dory/dory.cpp:482-490: RoPE on q and k, then justnorm per head, then q times the per-dimension

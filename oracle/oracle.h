@@ -52,6 +52,12 @@ void xo_swiglu_scaled(float* g, const float* u, const float* sg, const float* su
  * cs[m + r][i] = sin, for rows at pos0 + r. */
 void xo_rope_table(float* cs, int m, int head_dim, int64_t pos0, float theta);
 
+/* --- sublayer compositions of packs/dory/dory.cpp --- */
+/* :510-515: att[r][j] *= 1 / (1 + exp(-gate[r][j] * gs[j])), then justnorm of each row */
+void xo_gate_norm(float* att, const float* gate, const float* gs, int rows, int width);
+/* :532-541: out = justnorm(a + b) (b non-NULL) or justnorm(a); out may alias a */
+void xo_add_norm(const float* a, const float* b, float* out, int rows, int width);
+
 /* --- Q/K producer: packs/dory/dory.cpp:481-490 (RoPE q and k, justnorm per head, q *= qscale) --- */
 void xo_qk_produce(float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0, float theta,
                    const float* qscale);

@@ -54,6 +54,8 @@ _ORACLE_SIGS = [
     ("xo_swiglu_scaled", None, [_P, _P, _P, _P, _I, _I]),
     ("xo_rope_table", None, [_P, _I, _I, _I64, _F]),
     ("xo_qk_produce", None, [_P, _P, _I, _I, _I, _I, _I64, _F, _P]),
+    ("xo_gate_norm", None, [_P, _P, _P, _I, _I]),
+    ("xo_add_norm", None, [_P, _P, _P, _I, _I]),
     ("xo_kv_create", _P, [_I, _I, _I64, _I, _I]),
     ("xo_kv_free", None, [_P]),
     ("xo_kv_slots", _I64, [_P]),
@@ -183,6 +185,22 @@ def swiglu_scaled(g, u, sg, su, use_ref=False):
     (ref().xr_swiglu_scaled if use_ref else oracle().xo_swiglu_scaled)(g.ctypes.data, u.ctypes.data, _f32(sg).ctypes.data,
                                                                        _f32(su).ctypes.data, rows, g.shape[-1])
     return g
+
+
+def gate_norm(att, gate, gs):
+    att = _f32(att).copy()
+    rows = att.shape[0] if att.ndim > 1 else 1
+    oracle().xo_gate_norm(att.ctypes.data, _f32(gate).ctypes.data, _f32(gs).ctypes.data, rows, att.shape[-1])
+    return att
+
+
+def add_norm(a, b=None):
+    a = _f32(a)
+    out = np.empty_like(a)
+    rows = a.shape[0] if a.ndim > 1 else 1
+    oracle().xo_add_norm(a.ctypes.data, _f32(b).ctypes.data if b is not None else None, out.ctypes.data, rows,
+                         a.shape[-1])
+    return out
 
 
 def qk_produce(q, k, heads, kv_heads, head_dim, pos0, theta, qscale):

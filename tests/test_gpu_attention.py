@@ -1,0 +1,214 @@
+"""GPU parity of the device KV cache (xtg_hip_kv_*) and decode attention (xtg_hip_attention) against the oracle's
+KvCache + attention (engine/src/kv.cpp:75-286) and ring mask (npu/xtg_npu.cpp:236-258), on the same seeded inputs.
+
+Bars: KV store / load bit-exact (BF16 round to nearest even); attention rel-L2 <= 1e-5 against the oracle and
+max |err| <= 2e-5 against an FP64 softmax of exactly what the cache holds (tests/kernels_test.cpp:103-183's bar);
+for the sharp cases (scores up to ~20) rel-L2 <= 5e-5 against the oracle, whose own FP32 error is of that order.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(np.asarray(y, np.float64) - ref) / np.linalg.norm(ref))
+
+
+def bf16_round(a):
+    b = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = ((b + np.uint32(0x7FFF) + ((b >> 16) & 1)) >> 16).astype(np.uint32) << 16
+    return r.view(np.float32).reshape(np.shape(a))
+
+
+def naive(q, Kc, Vc, pos0, heads, kvh, window, scale):
+    """FP64 softmax attention over explicit rows Kc / Vc [positions][kvh][d] (tests/kernels_test.cpp:104-130)."""
+    n_q, d = q.shape[0], q.shape[2]
+    g = heads // kvh
+    out = np.zeros((n_q, heads, d))
+    for i in range(n_q):
+        t = pos0 + i
+        lo = max(0, t - window + 1) if window > 0 else 0
+        for h in range(heads):
+            s = Kc[lo:t + 1, h // g].astype(np.float64) @ q[i, h].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ Vc[lo:t + 1, h // g].astype(np.float64)
+    return out
+
+
+def run_case(hip, orc, cached, n_q, window, heads, kvh, d, scale, rng, ring=None, qmul=1.0, unit=False):
+    total = cached + n_q
+    if unit:
+        K = rng.standard_normal((total, kvh, d)).astype(np.float32)
+        K /= np.linalg.norm(K, axis=-1, keepdims=True)
+        V = rng.standard_normal((total, kvh, d)).astype(np.float32)
+        V /= np.linalg.norm(V, axis=-1, keepdims=True)
+        q = rng.standard_normal((n_q, heads, d)).astype(np.float32)
+        q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    else:
+        K = rng.uniform(-1, 1, (total, kvh, d)).astype(np.float32)
+        V = rng.uniform(-1, 1, (total, kvh, d)).astype(np.float32)
+        q = rng.uniform(-1, 1, (n_q, heads, d)).astype(np.float32)
+    q = (q * np.float32(qmul)).astype(np.float32)
+    ring = ring if ring is not None else (window if window > 0 else 0)
+    oc = orc.KvCache(kvh, d, total + 8, ring=ring)
+    dc = hip.kv_cache(kvh, d, total + 8, ring=ring)
+    for p in range(0, cached, 50):
+        n = min(50, cached - p)
+        oc.store(p, K[p:p + n], V[p:p + n])
+        dc.store_host(p, K[p:p + n], V[p:p + n])
+    ref = orc.attention(q, K[cached:], V[cached:], oc, cached, heads, kvh, d, window=window, scale=scale, pool_size=4)
+    dq, dk, dv = hip.array(q), hip.array(K[cached:]), hip.array(V[cached:])
+    dout = hip.array(shape=q.shape)
+    hip.attention(dc, dq, dk, dv, dout, n_q, cached, heads, window=window, scale=scale)
+    out = dout.numpy()
+    for a in (dq, dk, dv, dout):
+        a.free()
+    Kc, Vc = bf16_round(K), bf16_round(V)
+    Kc[cached:], Vc[cached:] = K[cached:], V[cached:]
+    sc = scale if scale is not None else float(np.float32(1) / np.sqrt(np.float32(d)))
+    exact = naive(q, Kc, Vc, cached, heads, kvh, window, sc) if cached * n_q <= 400000 else None
+    dc.destroy()
+    return out, ref, exact
+
+
+# tests/kernels_test.cpp:139-141 (BF16 cache; the FP8 cases run with a BF16 cache here, FP8 being a later row)
+KT = [(300, 1, 0), (5000, 1, 0), (300, 1, 64), (100, 37, 0), (100, 37, 16), (0, 20, 0), (900, 3, 128)]
+
+
+@pytest.mark.parametrize("cached,n_q,window", KT)
+def test_reference_unit_cases(hip, orc, cached, n_q, window):
+    rng = np.random.default_rng(42 + cached + n_q + window)
+    out, ref, exact = run_case(hip, orc, cached, n_q, window, 8, 2, 64, 0.7, rng)
+    assert rel_l2(out, ref) <= 1e-5
+    if exact is not None:
+        assert np.max(np.abs(out - exact)) < 2e-5
+
+
+@pytest.mark.parametrize("ctx", [4096, 8192, 32768])
+@pytest.mark.parametrize("n_q", [1, 8])
+def test_decode_global_cache(hip, orc, ctx, n_q):
+    """Config 2: 32 q / 8 KV heads of 128, unit-norm K / V / q, BF16 cache of ctx positions, 1 or 8 new rows."""
+    rng = np.random.default_rng(ctx + n_q)
+    out, ref, _ = run_case(hip, orc, ctx, n_q, 0, 32, 8, 128, None, rng, unit=True)
+    assert rel_l2(out, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("qmul", [60.0, 250.0])
+def test_decode_sharp_softmax(hip, orc, qmul):
+    """Peaked softmax (q scaled so that scores reach tens): the three-term q split keeps FP32-level scores."""
+    rng = np.random.default_rng(int(qmul))
+    out, ref, exact = run_case(hip, orc, 600, 8, 0, 32, 8, 128, None, rng, unit=True, qmul=qmul)
+    assert rel_l2(out, ref) <= 5e-5
+    err_gpu = rel_l2(out, exact)
+    err_cpu = rel_l2(ref, exact)
+    assert err_gpu <= max(3 * err_cpu, 1e-5), (err_gpu, err_cpu)
+
+
+@pytest.mark.parametrize("window", [1024, 1088])
+def test_ring_wrapped_config3(hip, orc, wl, window):
+    """Config 3: a 1088-slot ring after 40000 positions (holding 38912..39999), 8 rows at 40000..40007, q and k
+    produced by RoPE (theta 1e6) -> per-head norm -> q * qscale ~ U(0.5, 1.5); the mask is rebuilt from the stored
+    slot positions. Compared with the oracle's position form and its slot form."""
+    rng = np.random.default_rng(window)
+    heads, kvh, d, ring, pos0, n_q = 32, 8, 128, 1088, 40000, 8
+    Kr = wl.unit_heads(rng, (ring, kvh), d)
+    Vr = wl.unit_heads(rng, (ring, kvh), d)
+    first = pos0 - ring
+    oc = orc.KvCache(kvh, d, 0, ring=ring)
+    dc = hip.kv_cache(kvh, d, 0, ring=ring)
+    oc.store(first, Kr, Vr)
+    dc.store_host(first, Kr, Vr)
+    slot_pos = np.full(ring, -1, np.int64)
+    for p in range(first, pos0):
+        slot_pos[p % ring] = p
+    q = rng.standard_normal((n_q, heads, d)).astype(np.float32)
+    k = rng.standard_normal((n_q, kvh, d)).astype(np.float32)
+    v = wl.unit_heads(rng, (n_q, kvh), d)
+    qscale = rng.uniform(0.5, 1.5, heads * d).astype(np.float32)
+    qo, ko = orc.qk_produce(q, k, heads, kvh, d, pos0, 1e6, qscale)
+    ref = orc.attention(qo, ko, v, oc, pos0, heads, kvh, d, window=window, pool_size=4)
+    ref_slots = orc.attention(qo, ko, v, oc, pos0, heads, kvh, d, window=window, slot_pos=slot_pos)
+    dq, dk, dv = hip.array(q), hip.array(k), hip.array(v)
+    dqs = hip.array(qscale)
+    dout = hip.array(shape=(n_q, heads, d))
+    hip.qk_rope_norm(dq, dk, n_q, heads, kvh, d, pos0, 1e6, dqs)
+    hip.attention(dc, dq, dk, dv, dout, n_q, pos0, heads, window=window)
+    out = dout.numpy()
+    qg, kg = dq.numpy(), dk.numpy()
+    for a in (dq, dk, dv, dqs, dout):
+        a.free()
+    dc.destroy()
+    assert rel_l2(qg, qo) <= 1e-6 and rel_l2(kg, ko) <= 1e-6
+    assert rel_l2(out, ref) <= 1e-5
+    assert rel_l2(out, ref_slots) <= 1e-5
+
+
+def test_kv_store_load_roundtrip(hip, orc):
+    """Store in chunks (linear and ring), load back: the BF16 bits the oracle's cache returns, exactly."""
+    rng = np.random.default_rng(5)
+    kvh, d = 8, 128
+    K = rng.standard_normal((700, kvh, d)).astype(np.float32)
+    V = rng.standard_normal((700, kvh, d)).astype(np.float32)
+    for ring in (0, 96):
+        oc = orc.KvCache(kvh, d, 800, ring=ring)
+        dc = hip.kv_cache(kvh, d, 800, ring=ring)
+        for p in range(0, 700, 70):
+            oc.store(p, K[p:p + 70], V[p:p + 70])
+            dc.store_host(p, K[p:p + 70], V[p:p + 70])
+        lo = 700 - 96 if ring else 0
+        for h in (0, 3, 7):
+            ok, ov = oc.load(h, lo, 700)
+            gk, gv = dc.load(h, lo, 700)
+            np.testing.assert_array_equal(gk, ok)
+            np.testing.assert_array_equal(gv, ov)
+        dc.destroy()
+
+
+def test_kv_ring_long_store_keeps_last(hip, orc):
+    """A store longer than the ring keeps its last `slots` rows (engine/src/kv.cpp:75-80)."""
+    rng = np.random.default_rng(6)
+    K = rng.standard_normal((300, 2, 64)).astype(np.float32)
+    V = rng.standard_normal((300, 2, 64)).astype(np.float32)
+    dc = hip.kv_cache(2, 64, 0, ring=64)
+    dc.store_host(0, K, V)
+    gk, gv = dc.load(1, 236, 300)
+    np.testing.assert_array_equal(gk, bf16_round(K[236:, 1]))
+    np.testing.assert_array_equal(gv, bf16_round(V[236:, 1]))
+    dc.destroy()
+
+
+def test_kv_save_restore_release(hip, orc):
+    rng = np.random.default_rng(7)
+    kvh, d = 2, 64
+    K = rng.standard_normal((64, kvh, d)).astype(np.float32)
+    V = rng.standard_normal((64, kvh, d)).astype(np.float32)
+    dc = hip.kv_cache(kvh, d, 0, ring=40)
+    dc.store_host(0, K[:40], V[:40])
+    snap = dc.save()
+    dc.store_host(40, K[40:], V[40:])
+    dc.restore(snap)
+    gk, _ = dc.load(0, 0, 40)
+    np.testing.assert_array_equal(gk, bf16_round(K[:40, 0]))
+    dc.release()
+    q = rng.standard_normal((1, 4, d)).astype(np.float32)
+    dq, dk, dv = hip.array(q), hip.array(K[:1]), hip.array(V[:1])
+    dout = hip.array(shape=(1, 4, d))
+    hip.attention(dc, dq, dk, dv, dout, 1, 40, 4)   # released: only the call's own key is visible
+    out = dout.numpy()
+    np.testing.assert_allclose(out[0], np.repeat(V[:1, :, :], 2, axis=1)[0], rtol=0, atol=1e-6)
+    for a in (dq, dk, dv, dout):
+        a.free()
+    dc.destroy()
+
+
+def test_errors(hip, pkg):
+    with pytest.raises(pkg.XtgError, match="KV cache full"):
+        dc = hip.kv_cache(2, 64, 32)
+        try:
+            dc.store_host(30, np.zeros((4, 2, 64), np.float32), np.zeros((4, 2, 64), np.float32))
+        finally:
+            dc.destroy()
+    with pytest.raises(pkg.XtgError, match="head_dim"):
+        hip.kv_cache(2, 96, 32)

@@ -1,0 +1,82 @@
+"""GPU parity of the decode-step row kernels against the oracle (engine/src/kernels.cpp:162-234,
+packs/dory/dory.cpp:474-475, :482-490, :510-515, :532-541). Bar: rel-L2 <= 1e-6 (single FP32 row passes)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(np.asarray(y, np.float64) - ref) / np.linalg.norm(ref))
+
+
+@pytest.mark.parametrize("m,pos0", [(1, 0), (1, 4095), (8, 40000), (3, 123456)])
+def test_qk_rope_norm(hip, orc, m, pos0):
+    rng = np.random.default_rng(m + pos0)
+    heads, kvh, d = 32, 8, 128
+    q = rng.standard_normal((m, heads, d)).astype(np.float32)
+    k = rng.standard_normal((m, kvh, d)).astype(np.float32)
+    qs = rng.uniform(0.5, 1.5, heads * d).astype(np.float32)
+    qo, ko = orc.qk_produce(q, k, heads, kvh, d, pos0, 1e6, qs)
+    dq, dk, ds = hip.array(q), hip.array(k), hip.array(qs)
+    hip.qk_rope_norm(dq, dk, m, heads, kvh, d, pos0, 1e6, ds)
+    assert rel_l2(dq.numpy(), qo) <= 1e-6
+    assert rel_l2(dk.numpy(), ko) <= 1e-6
+    # no scale: q only normalised
+    dq2 = hip.array(q)
+    hip.qk_rope_norm(dq2, dk, m, heads, kvh, d, pos0, 1e4, None)
+    qo2, _ = orc.qk_produce(q, k, heads, kvh, d, pos0, 1e4, np.ones(heads * d, np.float32))
+    assert rel_l2(dq2.numpy(), qo2) <= 1e-6
+    for a in (dq, dk, ds, dq2):
+        a.free()
+
+
+@pytest.mark.parametrize("rows,w", [(1, 3072), (8, 3072), (2, 4096)])
+def test_slerp(hip, orc, rows, w):
+    rng = np.random.default_rng(rows * w)
+    x = rng.standard_normal((rows, w)).astype(np.float32)
+    o = rng.standard_normal((rows, w)).astype(np.float32)
+    lr = np.abs(rng.standard_normal(w)).astype(np.float32) * 0.05
+    dx, do, dl = hip.array(x), hip.array(o), hip.array(lr)
+    hip.slerp_residual(dx, do, dl, rows, w)
+    assert rel_l2(dx.numpy(), orc.slerp_residual(x, o, lr)) <= 1e-6
+    for a in (dx, do, dl):
+        a.free()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_swiglu_norm(hip, orc, rows):
+    rng = np.random.default_rng(rows)
+    w = 8192
+    g = rng.standard_normal((rows, w)).astype(np.float32)
+    u = rng.standard_normal((rows, w)).astype(np.float32)
+    sg = rng.uniform(0.5, 1.5, w).astype(np.float32) * 50
+    su = rng.uniform(0.5, 1.5, w).astype(np.float32) * 50
+    dg, du, dsg, dsu = hip.array(g), hip.array(u), hip.array(sg), hip.array(su)
+    hip.swiglu_norm(dg, du, dsg, dsu, rows, w)
+    ref = orc.justnorm(orc.swiglu_scaled(g, u, sg, su))
+    assert rel_l2(dg.numpy(), ref) <= 1e-6
+    for a in (dg, du, dsg, dsu):
+        a.free()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_gate_and_add_norm(hip, orc, rows):
+    rng = np.random.default_rng(10 + rows)
+    w = 4096
+    att = rng.standard_normal((rows, w)).astype(np.float32)
+    gate = rng.standard_normal((rows, w)).astype(np.float32)
+    gs = rng.uniform(0.5, 1.5, w).astype(np.float32) * 8
+    da, dgt, dgs = hip.array(att), hip.array(gate), hip.array(gs)
+    hip.gate_norm(da, dgt, dgs, rows, w)
+    assert rel_l2(da.numpy(), orc.gate_norm(att, gate, gs)) <= 1e-6
+    a = rng.standard_normal((rows, 3072)).astype(np.float32)
+    b = rng.standard_normal((rows, 3072)).astype(np.float32)
+    dx, dy, dz = hip.array(a), hip.array(b), hip.array(shape=(rows, 3072))
+    hip.add_norm(dx, dy, dz, rows, 3072)
+    assert rel_l2(dz.numpy(), orc.add_norm(a, b)) <= 1e-6
+    hip.add_norm(dx, None, dx, rows, 3072)   # in place, no addend
+    assert rel_l2(dx.numpy(), orc.add_norm(a)) <= 1e-6
+    for arr in (da, dgt, dgs, dx, dy, dz):
+        arr.free()

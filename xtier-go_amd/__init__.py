@@ -27,6 +27,16 @@ class Nvfp4(ctypes.Structure):
     _fields_ = [("codes", _P), ("scales", _P), ("glob", ctypes.c_float), ("n_out", _I), ("k", _I)]
 
 
+class AttnArgs(ctypes.Structure):
+    """xtg_attn_args (the fields of xtg::AttnArgs, engine/include/xtg/kv.h:67-78)."""
+    _fields_ = [("n_q", _I), ("pos0", ctypes.c_int64), ("heads", _I), ("kv_heads", _I), ("head_dim", _I),
+                ("window", _I), ("scale", ctypes.c_float), ("q", _P), ("k", _P), ("v", _P), ("cache", _P),
+                ("out", _P)]
+
+
+_F = ctypes.c_float
+_I64 = ctypes.c_int64
+
 SIGNATURES = [
     ("xtg_hip_open", _P, [ctypes.c_char_p] + _ERR),
     ("xtg_hip_close", None, [_P]),
@@ -36,6 +46,20 @@ SIGNATURES = [
     ("xtg_hip_release_nvfp4", _I, [_P, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P)] + _ERR),
     ("xtg_hip_matmul_nvfp4_dev", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _I, _P, _SZ] + _ERR),
+    ("xtg_hip_kv_create", _P, [_P, _I, _I, _I64, _I, _I] + _ERR),
+    ("xtg_hip_kv_destroy", None, [_P, _P]),
+    ("xtg_hip_kv_store", _I, [_P, _P, _I64, _I, _P, _P] + _ERR),
+    ("xtg_hip_kv_load", _I, [_P, _P, _I, _I64, _I64, _P, _P] + _ERR),
+    ("xtg_hip_kv_bytes", _I64, [_P, _P]),
+    ("xtg_hip_kv_save", _I, [_P, _P, _P, _SZ] + _ERR),
+    ("xtg_hip_kv_restore", _I, [_P, _P, _P, _SZ] + _ERR),
+    ("xtg_hip_kv_release", _I, [_P, _P] + _ERR),
+    ("xtg_hip_attention", _I, [_P, ctypes.POINTER(AttnArgs)] + _ERR),
+    ("xtg_hip_qk_rope_norm", _I, [_P, _P, _P, _I, _I, _I, _I, _I64, _F, _P] + _ERR),
+    ("xtg_hip_slerp_residual", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
+    ("xtg_hip_swiglu_norm", _I, [_P, _P, _P, _P, _P, _I, _I] + _ERR),
+    ("xtg_hip_gate_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
+    ("xtg_hip_add_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_x_operand_bytes", _SZ, [_I]),
     ("xtg_hip_prep_x", _I, [_P, _P, _I, _I, _I, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4_op", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _P, _SZ] + _ERR),
@@ -259,6 +283,100 @@ class HipBackend:
     def array(self, a=None, shape=None, dtype=np.float32):
         """A device buffer owned by this backend, filled from the numpy array a (or left unset)."""
         return DeviceArray(self, a, shape, dtype)
+
+    # ---- KV caches and attention (engine/include/xtg/kv.h)
+    def kv_cache(self, kv_heads, head_dim, slots, ring=0, dtype=KV_BF16):
+        return KvCache(self, kv_heads, head_dim, slots, ring, dtype)
+
+    def attention(self, cache, q, k, v, out, n_q, pos0, heads, window=0, scale=None):
+        """Queued device attention: q, k, v, out device buffers as xtg::AttnArgs."""
+        sc = float(np.float32(1) / np.sqrt(np.float32(cache.head_dim))) if scale is None else float(scale)
+        a = AttnArgs(n_q, pos0, heads, cache.kv_heads, cache.head_dim, window, sc, _ptr(q), _ptr(k), _ptr(v), cache.h,
+                     _ptr(out))
+        err = _errbuf()
+        _check(lib().xtg_hip_attention(self.h, ctypes.byref(a), err, len(err)), err)
+
+    # ---- row kernels (queued, device buffers)
+    def qk_rope_norm(self, q, k, m, heads, kv_heads, head_dim, pos0, theta, qscale=None):
+        err = _errbuf()
+        _check(lib().xtg_hip_qk_rope_norm(self.h, _ptr(q), _ptr(k), m, heads, kv_heads, head_dim, pos0, theta,
+                                          _ptr(qscale), err, len(err)), err)
+
+    def slerp_residual(self, x, o, lr, rows, width):
+        err = _errbuf()
+        _check(lib().xtg_hip_slerp_residual(self.h, _ptr(x), _ptr(o), _ptr(lr), rows, width, err, len(err)), err)
+
+    def swiglu_norm(self, g, u, sg, su, rows, width):
+        err = _errbuf()
+        _check(lib().xtg_hip_swiglu_norm(self.h, _ptr(g), _ptr(u), _ptr(sg), _ptr(su), rows, width, err, len(err)),
+               err)
+
+    def gate_norm(self, att, gate, gs, rows, width):
+        err = _errbuf()
+        _check(lib().xtg_hip_gate_norm(self.h, _ptr(att), _ptr(gate), _ptr(gs), rows, width, err, len(err)), err)
+
+    def add_norm(self, a, b, out, rows, width):
+        err = _errbuf()
+        _check(lib().xtg_hip_add_norm(self.h, _ptr(a), _ptr(b), _ptr(out), rows, width, err, len(err)), err)
+
+
+class KvCache:
+    """A device KV cache (xtg_hip_kv): store from device rows, load to host, save / restore / release."""
+
+    def __init__(self, backend, kv_heads, head_dim, slots, ring=0, dtype=KV_BF16):
+        self.b = backend
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+        self.slots = ring if ring > 0 else slots
+        self.ring = ring
+        err = _errbuf()
+        self.h = lib().xtg_hip_kv_create(backend.h, kv_heads, head_dim, slots, ring, dtype, err, len(err))
+        if not self.h:
+            raise XtgError(err.value.decode(errors="replace"))
+
+    def destroy(self):
+        if self.h and self.b.h:
+            lib().xtg_hip_kv_destroy(self.b.h, self.h)
+        self.h = None
+
+    def store(self, pos, n, k, v):
+        """Rows pos .. pos + n - 1 from device FP32 k, v [n][kv_heads][head_dim] (queued)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_store(self.b.h, self.h, pos, n, _ptr(k), _ptr(v), err, len(err)), err)
+
+    def store_host(self, pos, k, v):
+        """Convenience: upload FP32 host rows, then store them."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        dk, dv = self.b.array(k), self.b.array(v)
+        self.store(pos, k.shape[0], dk, dv)
+        self.b.finish()
+        dk.free()
+        dv.free()
+
+    def load(self, head, p0, p1):
+        k = np.empty((p1 - p0, self.head_dim), dtype=np.float32)
+        v = np.empty_like(k)
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_load(self.b.h, self.h, head, p0, p1, k.ctypes.data, v.ctypes.data, err, len(err)), err)
+        return k, v
+
+    def nbytes(self):
+        return lib().xtg_hip_kv_bytes(self.b.h, self.h)
+
+    def save(self):
+        out = np.empty(self.nbytes(), dtype=np.uint8)
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_save(self.b.h, self.h, out.ctypes.data, out.nbytes, err, len(err)), err)
+        return out
+
+    def restore(self, blob):
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_restore(self.b.h, self.h, blob.ctypes.data, blob.nbytes, err, len(err)), err)
+
+    def release(self):
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_release(self.b.h, self.h, err, len(err)), err)
 
 
 class DeviceArray:

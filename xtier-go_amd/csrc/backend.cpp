@@ -1,7 +1,9 @@
 #include "backend.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
+#include <memory>
 
 #include "common.hpp"
 
@@ -27,8 +29,15 @@ Backend::~Backend() {
   for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.first);
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, hx_, hy_})
+  for (void* p : {op_, hx_, hy_, part_})
     if (p) (void)hipFree(p);
+  for (DevKv* c : kvs_) {
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    (void)hipFree(c->slot_pos);
+    delete c;
+  }
+  for (auto& f : inv_freq_) (void)hipFree(f.second);
   for (const Pending& p : pending_) {
     (void)hipEventDestroy(p.a);
     (void)hipEventDestroy(p.b);
@@ -121,6 +130,185 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
   c.xop = op;
   c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
   timed([&] { return launch_gemv(c, stream_); });
+}
+
+// ------------------------------------------------------------------------------------------------- KV caches
+
+DevKv* Backend::kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype) {
+  XTG_CHECK(!capturing_, "kv_create: not during a graph capture");
+  XTG_CHECK(dtype == XTG_KV_BF16, "kv_create: only BF16 caches are implemented on the device");
+  XTG_CHECK(head_dim == 64 || head_dim == 128, "kv_create: head_dim %d (64 or 128)", head_dim);
+  XTG_CHECK(kv_heads > 0, "kv_create: %d KV heads", kv_heads);
+  const long long n = ring > 0 ? ring : slots;   // kv.cpp:42-44: ring > 0 gives a ring of `ring` slots
+  XTG_CHECK(n > 0 && n < (1LL << 30), "kv_create: %lld slots", n);
+  auto c = std::make_unique<DevKv>();
+  c->kv_heads = kv_heads;
+  c->head_dim = head_dim;
+  c->slots = n;
+  c->slots_pad = int((n + 31) / 32 * 32);
+  c->ring = ring > 0;
+  const size_t elems = size_t(kv_heads) * size_t(c->slots_pad) * size_t(head_dim);
+  HIP_CHECK(hipMalloc(&c->k, elems * 2));
+  HIP_CHECK(hipMalloc(&c->v, elems * 2));
+  HIP_CHECK(hipMalloc(&c->slot_pos, size_t(c->slots_pad) * sizeof(int)));
+  HIP_CHECK(hipMemsetAsync(c->k, 0, elems * 2, stream_));
+  HIP_CHECK(hipMemsetAsync(c->v, 0, elems * 2, stream_));
+  HIP_CHECK(hipMemsetAsync(c->slot_pos, 0xff, size_t(c->slots_pad) * sizeof(int), stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  DevKv* p = c.release();
+  kvs_.insert(p);
+  return p;
+}
+
+void Backend::kv_destroy(DevKv* c) {
+  auto it = kvs_.find(c);
+  if (it == kvs_.end()) return;
+  XTG_CHECK(!capturing_, "kv_destroy: not during a graph capture");
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipFree(c->k));
+  HIP_CHECK(hipFree(c->v));
+  HIP_CHECK(hipFree(c->slot_pos));
+  kvs_.erase(it);
+  delete c;
+}
+
+void Backend::kv_store(DevKv* c, long long pos, int n, const float* k, const float* v) {
+  XTG_CHECK(kvs_.count(c), "kv_store: unknown cache");
+  XTG_CHECK(n >= 0 && pos >= 0, "kv_store: %d rows at %lld", n, pos);
+  // kv.cpp:78: a linear cache holds positions below its capacity
+  XTG_CHECK(c->ring || pos + n <= c->slots, "KV cache full: position %lld of %lld", pos + n, c->slots);
+  XTG_CHECK(pos + n < (1LL << 31), "kv_store: position %lld beyond the 32-bit slot positions", pos + n);
+  if (n == 0) return;
+  XTG_CHECK(k && v, "kv_store: NULL rows");
+  timed([&] {
+    launch_kv_store(*c, pos, n, k, v, stream_);
+    return std::string("kv_store_kernel");
+  });
+}
+
+void Backend::kv_load(const DevKv* c, int h, long long p0, long long p1, float* k, float* v) {
+  XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "kv_load: unknown cache");
+  XTG_CHECK(!capturing_, "kv_load: not during a graph capture");
+  XTG_CHECK(h >= 0 && h < c->kv_heads && p0 >= 0 && p0 <= p1, "kv_load: head %d, positions %lld..%lld", h, p0, p1);
+  XTG_CHECK(c->ring || p1 <= c->slots, "kv_load: position %lld beyond the cache", p1);
+  const int d = c->head_dim;
+  const size_t elems = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(d);
+  std::vector<uint16_t> hk(elems), hv(elems);
+  HIP_CHECK(hipMemcpyAsync(hk.data(), c->k, elems * 2, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipMemcpyAsync(hv.data(), c->v, elems * 2, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  for (long long p = p0; p < p1; ++p) {
+    const int slot = int(c->ring ? p % c->slots : p);
+    for (int j = 0; j < d; ++j) {
+      const uint32_t kb = uint32_t(hk[kv_k_index(h, slot, j, c->slots_pad, d)]) << 16;
+      const uint32_t vb = uint32_t(hv[kv_v_index(h, slot, j, c->slots_pad, d)]) << 16;
+      std::memcpy(k + size_t(p - p0) * size_t(d) + size_t(j), &kb, 4);
+      std::memcpy(v + size_t(p - p0) * size_t(d) + size_t(j), &vb, 4);
+    }
+  }
+}
+
+size_t Backend::kv_bytes(const DevKv* c) const {
+  return size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 4 + size_t(c->slots_pad) * sizeof(int);
+}
+
+void Backend::kv_save(const DevKv* c, void* out, size_t bytes) {
+  XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "kv_save: unknown cache");
+  XTG_CHECK(!capturing_, "kv_save: not during a graph capture");
+  XTG_CHECK(bytes == kv_bytes(c), "kv_save: %zu bytes for a cache of %zu", bytes, kv_bytes(c));
+  const size_t half = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 2;
+  char* o = static_cast<char*>(out);
+  HIP_CHECK(hipMemcpyAsync(o, c->k, half, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipMemcpyAsync(o + half, c->v, half, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipMemcpyAsync(o + 2 * half, c->slot_pos, size_t(c->slots_pad) * sizeof(int), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void Backend::kv_restore(DevKv* c, const void* in, size_t bytes) {
+  XTG_CHECK(kvs_.count(c), "kv_restore: unknown cache");
+  XTG_CHECK(!capturing_, "kv_restore: not during a graph capture");
+  XTG_CHECK(bytes == kv_bytes(c), "KV snapshot of %zu bytes for a cache of %zu", bytes, kv_bytes(c));
+  const size_t half = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 2;
+  const char* s = static_cast<const char*>(in);
+  HIP_CHECK(hipMemcpyAsync(c->k, s, half, hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(c->v, s + half, half, hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(c->slot_pos, s + 2 * half, size_t(c->slots_pad) * sizeof(int), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void Backend::kv_release(DevKv* c) {
+  XTG_CHECK(kvs_.count(c), "kv_release: unknown cache");
+  XTG_CHECK(!capturing_, "kv_release: not during a graph capture");
+  const size_t elems = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim);
+  HIP_CHECK(hipMemsetAsync(c->k, 0, elems * 2, stream_));
+  HIP_CHECK(hipMemsetAsync(c->v, 0, elems * 2, stream_));
+  HIP_CHECK(hipMemsetAsync(c->slot_pos, 0xff, size_t(c->slots_pad) * sizeof(int), stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
+                        const float* k, const float* v, float* out) {
+  XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "attention: unknown cache");
+  XTG_CHECK(n_q >= 1 && pos0 >= 0, "attention: %d rows at %lld", n_q, pos0);
+  XTG_CHECK(q && k && v && out, "attention: NULL argument");
+  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v)})
+    XTG_CHECK(reinterpret_cast<uintptr_t>(p) % 16 == 0, "attention: inputs must be 16-byte aligned");
+  ensure(part_, part_size_, attn_part_floats_max(*c, n_q, heads, pos0, window) * sizeof(float));
+  const int d = c->head_dim, rows = attn_rows_per_block(heads / c->kv_heads);
+  for (int r0 = 0; r0 < n_q; r0 += rows) {
+    const int nr = std::min(rows, n_q - r0);
+    const AttnPlan p = attn_plan(*c, nr, heads, pos0, window);
+    XTG_CHECK(attn_part_floats(c->kv_heads, p.splits, p.qb * 16, d) * sizeof(float) <= part_size_,
+              "attention: partial buffer too small");
+    const size_t off = size_t(r0) * size_t(heads) * size_t(d);
+    timed([&] {
+      return launch_attn_decode(*c, p, q + off, k, v, nr, r0, n_q, heads, pos0, window, scale,
+                                static_cast<float*>(part_), stream_);
+    });
+    timed([&] { return launch_attn_merge(*c, p, nr, heads, static_cast<const float*>(part_), out + off, stream_); });
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- row kernels
+
+const float* Backend::inv_freq(float theta, int d) {
+  for (auto& f : inv_freq_)
+    if (f.first.first == theta && f.first.second == d) return f.second;
+  XTG_CHECK(!capturing_, "rope: the table for theta %g, head_dim %d must exist before a graph capture", theta, d);
+  std::vector<float> h(size_t(d / 2));
+  for (int i = 0; i < d / 2; ++i) h[size_t(i)] = 1.f / std::pow(theta, float(2 * i) / float(d));
+  float* p = nullptr;
+  HIP_CHECK(hipMalloc(&p, h.size() * sizeof(float)));
+  HIP_CHECK(hipMemcpy(p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
+  inv_freq_.push_back({{theta, d}, p});
+  return p;
+}
+
+void Backend::qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
+                           const float* qscale) {
+  XTG_CHECK(q && k && m >= 1, "rope: NULL argument or %d rows", m);
+  const float* f = inv_freq(theta, d);
+  timed([&] { return launch_qk_rope_norm(q, k, m, heads, kv_heads, d, pos0, f, qscale, stream_); });
+}
+
+void Backend::slerp_norm(float* x, const float* o, const float* lr, int rows, int w) {
+  XTG_CHECK(x && o && lr && rows >= 1 && w >= 1, "slerp: bad arguments");
+  timed([&] { return launch_slerp_norm(x, o, lr, rows, w, stream_); });
+}
+
+void Backend::swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w) {
+  XTG_CHECK(g && u && sg && su && rows >= 1 && w >= 1, "swiglu: bad arguments");
+  timed([&] { return launch_swiglu_norm(g, u, sg, su, rows, w, stream_); });
+}
+
+void Backend::gate_norm(float* a, const float* gate, const float* gs, int rows, int w) {
+  XTG_CHECK(a && gate && gs && rows >= 1 && w >= 1, "gate_norm: bad arguments");
+  timed([&] { return launch_gate_norm(a, gate, gs, rows, w, stream_); });
+}
+
+void Backend::add_norm(const float* a, const float* b, float* out, int rows, int w) {
+  XTG_CHECK(a && out && rows >= 1 && w >= 1, "add_norm: bad arguments");
+  timed([&] { return launch_add_norm(a, b, out, rows, w, stream_); });
 }
 
 hipEvent_t Backend::event() {

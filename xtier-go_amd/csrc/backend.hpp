@@ -11,8 +11,10 @@
 #include <unordered_set>
 #include <vector>
 
+#include "attention.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "rows.hpp"
 #include "xtg_hip.h"
 
 namespace xtg::hip {
@@ -35,6 +37,28 @@ class Backend {
   static size_t op_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
   void prep_x(const void* x, int x_dtype, int m, int k, void* op);
   void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off);
+
+  // KV caches (xtg::KvCache, kv.h:21-62): device storage, host-side load / save for tests and snapshots
+  DevKv* kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype);
+  void kv_destroy(DevKv* c);
+  void kv_store(DevKv* c, long long pos, int n, const float* k, const float* v);            // device k, v
+  void kv_load(const DevKv* c, int h, long long p0, long long p1, float* k, float* v);      // host k, v
+  size_t kv_bytes(const DevKv* c) const;
+  void kv_save(const DevKv* c, void* out, size_t bytes);
+  void kv_restore(DevKv* c, const void* in, size_t bytes);
+  void kv_release(DevKv* c);
+  // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
+  void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
+                 const float* k, const float* v, float* out);
+  // the row kernels of the decode step (rows.hip); device memory
+  void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
+                    const float* qscale);
+  void slerp_norm(float* x, const float* o, const float* lr, int rows, int w);
+  void swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w);
+  void gate_norm(float* a, const float* gate, const float* gs, int rows, int w);
+  void add_norm(const float* a, const float* b, float* out, int rows, int w);
+  // 1 / theta^(2i/d) in FP32 computed on the host as engine/src/kernels.cpp:191-201 does, kept on the device
+  const float* inv_freq(float theta, int d);
 
   // opencl.h:40-45
   void* alloc(size_t bytes);
@@ -101,6 +125,10 @@ class Backend {
   // scratch (grown on demand, owned): activation operand, its row scales, host-call staging
   void* op_ = nullptr;
   size_t op_size_ = 0;
+  void* part_ = nullptr;   // attention split partials
+  size_t part_size_ = 0;
+  std::unordered_set<DevKv*> kvs_;
+  std::vector<std::pair<std::pair<float, int>, float*>> inv_freq_;
   void* hx_ = nullptr;
   size_t hx_size_ = 0;
   void* hy_ = nullptr;

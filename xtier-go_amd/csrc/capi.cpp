@@ -103,6 +103,113 @@ int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const voi
   });
 }
 
+xtg_hip_kv* xtg_hip_kv_create(xtg_hip* h, int kv_heads, int head_dim, int64_t slots, int ring, int dtype, char* err,
+                              int err_len) {
+  xtg::hip::DevKv* c = nullptr;
+  int rc = guarded(err, err_len, [&] {
+    XTG_CHECK(h, "kv_create: NULL handle");
+    c = h->b->kv_create(kv_heads, head_dim, slots, ring, dtype);
+  });
+  return rc == 0 ? reinterpret_cast<xtg_hip_kv*>(c) : nullptr;
+}
+
+void xtg_hip_kv_destroy(xtg_hip* h, xtg_hip_kv* kv) {
+  if (h && kv) guarded(nullptr, 0, [&] { h->b->kv_destroy(reinterpret_cast<xtg::hip::DevKv*>(kv)); });
+}
+
+int xtg_hip_kv_store(xtg_hip* h, xtg_hip_kv* kv, int64_t pos, int n, const float* k, const float* v, char* err,
+                     int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && kv, "kv_store: NULL argument");
+    h->b->kv_store(reinterpret_cast<xtg::hip::DevKv*>(kv), pos, n, k, v);
+  });
+}
+
+int xtg_hip_kv_load(xtg_hip* h, const xtg_hip_kv* kv, int head, int64_t p0, int64_t p1, float* k, float* v, char* err,
+                    int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && kv && k && v, "kv_load: NULL argument");
+    h->b->kv_load(reinterpret_cast<const xtg::hip::DevKv*>(kv), head, p0, p1, k, v);
+  });
+}
+
+int64_t xtg_hip_kv_bytes(xtg_hip* h, const xtg_hip_kv* kv) {
+  if (!h || !kv) return -1;
+  return int64_t(h->b->kv_bytes(reinterpret_cast<const xtg::hip::DevKv*>(kv)));
+}
+
+int xtg_hip_kv_save(xtg_hip* h, const xtg_hip_kv* kv, void* out, size_t bytes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && kv && out, "kv_save: NULL argument");
+    h->b->kv_save(reinterpret_cast<const xtg::hip::DevKv*>(kv), out, bytes);
+  });
+}
+
+int xtg_hip_kv_restore(xtg_hip* h, xtg_hip_kv* kv, const void* in, size_t bytes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && kv && in, "kv_restore: NULL argument");
+    h->b->kv_restore(reinterpret_cast<xtg::hip::DevKv*>(kv), in, bytes);
+  });
+}
+
+int xtg_hip_kv_release(xtg_hip* h, xtg_hip_kv* kv, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && kv, "kv_release: NULL argument");
+    h->b->kv_release(reinterpret_cast<xtg::hip::DevKv*>(kv));
+  });
+}
+
+int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && a && a->cache, "attention: NULL argument");
+    const auto* c = reinterpret_cast<const xtg::hip::DevKv*>(a->cache);
+    XTG_CHECK(a->kv_heads == c->kv_heads && a->head_dim == c->head_dim,
+              "attention: %d KV heads of %d for a cache of %d of %d", a->kv_heads, a->head_dim, c->kv_heads,
+              c->head_dim);
+    h->b->attention(c, a->n_q, a->pos0, a->heads, a->window, a->scale, a->q, a->k, a->v, a->out);
+  });
+}
+
+int xtg_hip_qk_rope_norm(xtg_hip* h, float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0,
+                         float theta, const float* qscale, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "rope: NULL handle");
+    h->b->qk_rope_norm(q, k, m, heads, kv_heads, head_dim, pos0, theta, qscale);
+  });
+}
+
+int xtg_hip_slerp_residual(xtg_hip* h, float* x, const float* o, const float* lr, int rows, int width, char* err,
+                           int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "slerp: NULL handle");
+    h->b->slerp_norm(x, o, lr, rows, width);
+  });
+}
+
+int xtg_hip_swiglu_norm(xtg_hip* h, float* g, const float* u, const float* sg, const float* su, int rows, int width,
+                        char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "swiglu: NULL handle");
+    h->b->swiglu_norm(g, u, sg, su, rows, width);
+  });
+}
+
+int xtg_hip_gate_norm(xtg_hip* h, float* att, const float* gate, const float* gs, int rows, int width, char* err,
+                      int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "gate_norm: NULL handle");
+    h->b->gate_norm(att, gate, gs, rows, width);
+  });
+}
+
+int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int rows, int width, char* err,
+                     int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "add_norm: NULL handle");
+    h->b->add_norm(a, b, out, rows, width);
+  });
+}
+
 size_t xtg_hip_x_operand_bytes(int k) { return k > 0 ? xtg::hip::Backend::op_bytes(k) : 0; }
 
 int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* op, char* err, int err_len) {
