@@ -155,6 +155,47 @@ int xtg_hip_gate_norm(xtg_hip* h, float* att, const float* gate, const float* gs
 int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int rows, int width, char* err,
                      int err_len);
 
+/* ----------------------------------------------------------------------------------- Dory decode step */
+
+/* The looped-nGPT model's sublayer kinds (packs/dory/dory.cpp:38) and shape (dory.cpp:45-56). */
+enum { XTG_DORY_MLP = 0, XTG_DORY_SLIDING = 1, XTG_DORY_FULL = 2 };
+typedef struct xtg_dory_config {
+  int hidden, ffn, heads, kv_heads, head_dim, vocab;
+  int n_in, n_rec, n_out, loops;   /* input / recurrent / output sublayers; recurrent passes (per_loop caches) */
+  int window, ring_slots;          /* sliding window and the ring size of a sliding sublayer's cache */
+  int64_t context;                 /* capacity of a full-attention cache */
+  float theta_sliding, theta_full; /* RoPE theta per kind */
+} xtg_dory_config;
+/* One physical sublayer (dory.cpp:332-364) with the scale vectors already folded as the model constructor does
+ * (qscale = (sqk * sqrt(d) / init_range)^2, gscale likewise, sg / su times sqrt(hidden), lr = |alpha * alpha_init /
+ * init_range|). Weights are host NVFP4 tensors (prepared to the device by create), vectors host FP32. */
+typedef struct xtg_dory_layer {
+  int kind;
+  xtg_nvfp4 q, k, v, g, o;      /* attention */
+  xtg_nvfp4 gate, up, down;     /* MLP */
+  const float* qscale;          /* [heads * head_dim] */
+  const float* gscale;          /* [heads * head_dim] */
+  const float* sg;              /* [ffn] */
+  const float* su;              /* [ffn] */
+  const float* lr;              /* [hidden] */
+} xtg_dory_layer;
+typedef struct xtg_hip_dory xtg_hip_dory;
+/* Replaces the DoryModel constructor's weight preparation (dory.cpp:365-371) and the GpuDorySession constructor
+ * (dory.cpp:1043-1084): prepares every weight and the NVFP4 LM head [vocab][hidden], uploads the vectors and
+ * logit_scale [vocab], creates the caches (BF16; sliding sublayers: rings of ring_slots). NULL on failure. The
+ * host weights must stay alive and unchanged while the session exists (they key the prepared copies). */
+xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xtg_dory_layer* layers,
+                                  const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len);
+void xtg_hip_dory_destroy(xtg_hip_dory* d);
+/* Replaces GpuDorySession::run_chunk + the head of forward (dory.cpp:1150-1214; CPU dory.cpp:520-578) for one
+ * chunk of m <= 8 rows: from the hidden rows x [m][hidden] (device, the embedding rows) at positions pos0 ..
+ * pos0 + m - 1 to logits [m][vocab] (device, times logit_scale); each attention sublayer's cache gains the chunk's
+ * keys. Queued: capturable into a graph (xtg_hip_graph_*) once the call has run. */
+int xtg_hip_dory_forward(xtg_hip_dory* d, const float* x, int m, int64_t pos0, float* logits, char* err, int err_len);
+/* The cache of attention sublayer `attn` (counted over attention sublayers) for loop `inst`, e.g. to fill a
+ * context with xtg_hip_kv_store. NULL when there is none. */
+xtg_hip_kv* xtg_hip_dory_cache(xtg_hip_dory* d, int attn, int inst);
+
 /* ------------------------------------------------------------------------------------- device buffers */
 
 /* Replaces OpenClBackend::alloc / release / write / read / copy / finish (opencl.h:40-45). write() is blocking

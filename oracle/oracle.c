@@ -662,3 +662,152 @@ int xo_attention_slots(const xo_attn_args* a, const int64_t* slot_pos, int threa
   }
   return 0;
 }
+
+/* -------------------------------------------------------------------------------------------- decode step */
+
+struct xo_dory {
+  xo_dory_config c;
+  const xo_dory_layer* layers;
+  const xo_nvfp4* head;
+  const float* logit_scale;
+  int n_layers, n_attn;
+  int* attn_of;    /* per sublayer: its attention index, or -1 */
+  xo_kv** caches;  /* [n_attn][loops] (instance 0 only for non-recurrent sublayers) */
+};
+
+static int xo_recurrent(const xo_dory* d, int l) { return l >= d->c.n_in && l < d->c.n_in + d->c.n_rec; }
+
+xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, const xo_nvfp4* head,
+                        const float* logit_scale) {
+  /* the session's caches: packs/dory/dory.cpp:436-447 (per_loop: one cache per loop for recurrent sublayers) */
+  xo_dory* d = (xo_dory*)calloc(1, sizeof(xo_dory));
+  d->c = *c;
+  d->layers = layers;
+  d->head = head;
+  d->logit_scale = logit_scale;
+  d->n_layers = c->n_in + c->n_rec + c->n_out;
+  d->attn_of = (int*)malloc(sizeof(int) * (size_t)d->n_layers);
+  for (int l = 0; l < d->n_layers; ++l) d->attn_of[l] = layers[l].kind == XO_MLP ? -1 : d->n_attn++;
+  d->caches = (xo_kv**)calloc((size_t)d->n_attn * (size_t)c->loops, sizeof(xo_kv*));
+  for (int l = 0; l < d->n_layers; ++l) {
+    if (d->attn_of[l] < 0) continue;
+    int inst = xo_recurrent(d, l) ? c->loops : 1;
+    for (int i = 0; i < inst; ++i)
+      d->caches[(size_t)d->attn_of[l] * (size_t)c->loops + (size_t)i] =
+          xo_kv_create(c->kv_heads, c->head_dim, c->context, layers[l].kind == XO_SLIDING ? c->ring_slots : 0,
+                       XO_KV_BF16);
+  }
+  return d;
+}
+
+void xo_dory_free(xo_dory* d) {
+  if (!d) return;
+  for (int i = 0; i < d->n_attn * d->c.loops; ++i) xo_kv_free(d->caches[i]);
+  free(d->caches);
+  free(d->attn_of);
+  free(d);
+}
+
+xo_kv* xo_dory_cache(xo_dory* d, int attn, int inst) {
+  if (attn < 0 || attn >= d->n_attn || inst < 0 || inst >= d->c.loops) return NULL;
+  return d->caches[(size_t)attn * (size_t)d->c.loops + (size_t)inst];
+}
+
+typedef struct {
+  float *mg, *mu, *hq, *hk, *hv, *hg, *ha, *ho;
+} xo_scratch;
+
+static void xo_sublayer(xo_dory* d, int l, float* x, int m, int64_t pos0, int inst, int store, xo_scratch* s,
+                        int threads) {
+  /* packs/dory/dory.cpp:467-518 */
+  const xo_dory_config* c = &d->c;
+  const xo_dory_layer* L = &d->layers[l];
+  const int H = c->hidden, Q = c->heads * c->head_dim;
+  if (L->kind == XO_MLP) {
+    xo_nvfp4 gu[2] = {L->gate, L->up};
+    float* ys[2] = {s->mg, s->mu};
+    xo_matmul_nvfp4(gu, 2, x, m, ys, threads);
+    xo_swiglu_scaled(s->mg, s->mu, L->sg, L->su, m, c->ffn);
+    xo_justnorm(s->mg, m, c->ffn);
+    float* yo[1] = {s->ho};
+    xo_matmul_nvfp4(&L->down, 1, s->mg, m, yo, threads);
+    xo_slerp_residual(x, s->ho, L->lr, m, H);
+    return;
+  }
+  xo_nvfp4 qkvg[4] = {L->q, L->k, L->v, L->g};
+  float* ys[4] = {s->hq, s->hk, s->hv, s->hg};
+  xo_matmul_nvfp4(qkvg, 4, x, m, ys, threads);
+  const float theta = L->kind == XO_SLIDING ? c->theta_sliding : c->theta_full;
+  xo_qk_produce(s->hq, s->hk, m, c->heads, c->kv_heads, c->head_dim, pos0, theta, L->qscale);
+  xo_kv* cache = xo_dory_cache(d, d->attn_of[l], inst);
+  xo_attn_args a;
+  a.n_q = m;
+  a.pos0 = pos0;
+  a.heads = c->heads;
+  a.kv_heads = c->kv_heads;
+  a.head_dim = c->head_dim;
+  a.window = L->kind == XO_SLIDING ? c->window : 0;
+  a.scale = 1.f / sqrtf((float)c->head_dim);
+  a.q = s->hq;
+  a.k = s->hk;
+  a.v = s->hv;
+  a.cache = cache;
+  a.out = s->ha;
+  xo_attention(&a, threads, threads);
+  if (store) xo_kv_store(cache, pos0, m, s->hk, s->hv);
+  xo_gate_norm(s->ha, s->hg, L->gscale, m, Q);
+  float* yo[1] = {s->ho};
+  xo_matmul_nvfp4(&L->o, 1, s->ha, m, yo, threads);
+  xo_slerp_residual(x, s->ho, L->lr, m, H);
+}
+
+int xo_dory_forward(xo_dory* d, const float* x, int m, int64_t pos0, float* logits, int threads) {
+  /* packs/dory/dory.cpp:520-544 (run_chunk after the embedding rows) and :566-576 (head, logit scale) */
+  const xo_dory_config* c = &d->c;
+  const int H = c->hidden, Q = c->heads * c->head_dim, KV = c->kv_heads * c->head_dim;
+  const size_t n = (size_t)m * (size_t)H;
+  xo_scratch s;
+  s.mg = (float*)malloc(sizeof(float) * (size_t)m * (size_t)c->ffn);
+  s.mu = (float*)malloc(sizeof(float) * (size_t)m * (size_t)c->ffn);
+  s.hq = (float*)malloc(sizeof(float) * (size_t)m * (size_t)Q);
+  s.hk = (float*)malloc(sizeof(float) * (size_t)m * (size_t)KV);
+  s.hv = (float*)malloc(sizeof(float) * (size_t)m * (size_t)KV);
+  s.hg = (float*)malloc(sizeof(float) * (size_t)m * (size_t)Q);
+  s.ha = (float*)malloc(sizeof(float) * (size_t)m * (size_t)Q);
+  s.ho = (float*)malloc(sizeof(float) * n);
+  float* xs = (float*)malloc(sizeof(float) * n);
+  float* input = (float*)malloc(sizeof(float) * n);
+  float* state = (float*)malloc(sizeof(float) * n);
+  memcpy(xs, x, sizeof(float) * n);
+  int l = 0;
+  for (; l < c->n_in; ++l) xo_sublayer(d, l, xs, m, pos0, 0, 1, &s, threads);
+  memcpy(input, xs, sizeof(float) * n);
+  memcpy(state, xs, sizeof(float) * n);
+  for (int i = 0; i < c->loops; ++i) {
+    for (size_t j = 0; j < n; ++j) xs[j] = state[j] + input[j];
+    xo_justnorm(xs, m, H);
+    for (int r = c->n_in; r < c->n_in + c->n_rec; ++r) xo_sublayer(d, r, xs, m, pos0, i, 1, &s, threads);
+    memcpy(state, xs, sizeof(float) * n);
+    xo_justnorm(state, m, H);
+  }
+  memcpy(xs, state, sizeof(float) * n);
+  for (l = c->n_in + c->n_rec; l < d->n_layers; ++l) xo_sublayer(d, l, xs, m, pos0, 0, 1, &s, threads);
+  float* yl[1] = {logits};
+  xo_matmul_nvfp4(d->head, 1, xs, m, yl, threads);
+  for (int r = 0; r < m; ++r) {
+    float* lg = logits + (size_t)r * (size_t)c->vocab;
+    for (int j = 0; j < c->vocab; ++j) lg[j] *= d->logit_scale[j];
+  }
+  free(s.mg);
+  free(s.mu);
+  free(s.hq);
+  free(s.hk);
+  free(s.hv);
+  free(s.hg);
+  free(s.ha);
+  free(s.ho);
+  free(xs);
+  free(input);
+  free(state);
+  return 0;
+}

@@ -98,6 +98,37 @@ int xo_attention(const xo_attn_args* a, int pool_size, int threads);
  * softmax over tiles of 64 slots. */
 int xo_attention_slots(const xo_attn_args* a, const int64_t* slot_pos, int threads);
 
+/* --- the Dory decode step: packs/dory/dory.cpp:467-578 --- */
+enum { XO_MLP = 0, XO_SLIDING = 1, XO_FULL = 2 };   /* dory.cpp:38 */
+typedef struct xo_dory_layer {
+  int kind;
+  xo_nvfp4 q, k, v, g, o;          /* attention sublayer */
+  xo_nvfp4 gate, up, down;         /* MLP sublayer */
+  const float* qscale;             /* [heads * head_dim], folded as dory.cpp:354-357 */
+  const float* gscale;             /* [heads * head_dim] */
+  const float* sg;                 /* [ffn], folded (dory.cpp:342-345) */
+  const float* su;
+  const float* lr;                 /* [hidden], |alpha * scale| (dory.cpp:363) */
+} xo_dory_layer;
+typedef struct xo_dory_config {
+  int hidden, ffn, heads, kv_heads, head_dim, vocab;
+  int n_in, n_rec, n_out, loops;   /* input / recurrent / output sublayers; recurrent passes */
+  int window, ring_slots;          /* sliding window and its ring size */
+  int64_t context;                 /* linear cache capacity */
+  float theta_sliding, theta_full;
+} xo_dory_config;
+typedef struct xo_dory xo_dory;
+/* Layers and vectors are borrowed (they must outlive the model); per_loop KV mode: a recurrent attention sublayer
+ * keeps one cache per loop (dory.cpp:436-447). */
+xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, const xo_nvfp4* head,
+                        const float* logit_scale);
+void xo_dory_free(xo_dory* d);
+/* The cache of attention sublayer `attn` (counted over attention sublayers), loop instance `inst`. */
+xo_kv* xo_dory_cache(xo_dory* d, int attn, int inst);
+/* dory.cpp:520-544 run_chunk from the hidden rows x [m][hidden] (the embedding rows) at positions pos0 .., then the
+ * head for every row times logit_scale (dory.cpp:566-576): logits [m][vocab]; the caches gain the chunk's keys. */
+int xo_dory_forward(xo_dory* d, const float* x, int m, int64_t pos0, float* logits, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,19 @@ class AttnArgs(ctypes.Structure):
                 ("scale", _F), ("q", _P), ("k", _P), ("v", _P), ("cache", _P), ("out", _P)]
 
 
+class DoryConfig(ctypes.Structure):
+    """xo_dory_config."""
+    _fields_ = [(n, _I) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "n_in", "n_rec", "n_out",
+                                  "loops", "window", "ring_slots")] + \
+               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F)]
+
+
+class DoryLayer(ctypes.Structure):
+    """xo_dory_layer."""
+    _fields_ = [("kind", _I)] + [(n, Nvfp4) for n in ("q", "k", "v", "g", "o", "gate", "up", "down")] + \
+               [(n, _P) for n in ("qscale", "gscale", "sg", "su", "lr")]
+
+
 def _load(path, sigs):
     l = ctypes.CDLL(path)
     for name, res, args in sigs:
@@ -67,6 +80,10 @@ _ORACLE_SIGS = [
     ("xo_kv_vscale", _P, [_P]),
     ("xo_attention", _I, [ctypes.POINTER(AttnArgs), _I, _I]),
     ("xo_attention_slots", _I, [ctypes.POINTER(AttnArgs), _P, _I]),
+    ("xo_dory_create", _P, [ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4), _P]),
+    ("xo_dory_free", None, [_P]),
+    ("xo_dory_cache", _P, [_P, _I, _I]),
+    ("xo_dory_forward", _I, [_P, _P, _I, _I64, _P, _I]),
 ]
 
 _REF_SIGS = [
@@ -229,9 +246,9 @@ class KvCache:
 
     def __del__(self):
         try:
-            if self.h:
+            if self.h and not getattr(self, "_borrowed", False):
                 (ref().xr_kv_free if self.use_ref else oracle().xo_kv_free)(self.h)
-                self.h = None
+            self.h = None
         except Exception:
             pass
 
@@ -270,3 +287,39 @@ def attention(q, k, v, cache, pos0, heads, kv_heads, head_dim, window=0, scale=N
     if rc != 0:
         raise ValueError("attention rejected its arguments")
     return out
+
+
+class Dory:
+    """The oracle's decode step (packs/dory/dory.cpp:467-578) over DoryWeights (xtier-go_amd/workloads.py)."""
+
+    def __init__(self, weights, wl):
+        self.w = weights
+        cfg, layers, head = wl.dory_structs(weights, Nvfp4, DoryLayer, DoryConfig)
+        self._keep = (cfg, layers, head)
+        self.h = oracle().xo_dory_create(ctypes.byref(cfg), layers, ctypes.byref(head), weights.logit_scale.ctypes.data)
+
+    def __del__(self):
+        try:
+            if self.h:
+                oracle().xo_dory_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+    def forward(self, x, pos0, threads=8):
+        """x float32 [m][hidden] -> logits float32 [m][vocab]."""
+        x = _f32(x)
+        m = x.shape[0]
+        out = np.empty((m, self.w.cfg["vocab"]), dtype=np.float32)
+        oracle().xo_dory_forward(self.h, x.ctypes.data, m, pos0, out.ctypes.data, threads)
+        return out
+
+    def cache(self, attn, inst=0):
+        """The KvCache of attention sublayer `attn`, loop `inst` (owned by the model)."""
+        c = KvCache.__new__(KvCache)
+        c.use_ref = False
+        c.kv_heads, c.head_dim = self.w.cfg["kv_heads"], self.w.cfg["head_dim"]
+        c.h = oracle().xo_dory_cache(self.h, attn, inst)
+        c.slots, c.ring = None, None
+        c._borrowed = True
+        return c

@@ -37,6 +37,20 @@ class AttnArgs(ctypes.Structure):
 _F = ctypes.c_float
 _I64 = ctypes.c_int64
 
+
+class DoryConfig(ctypes.Structure):
+    """xtg_dory_config."""
+    _fields_ = [(n, _I) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "n_in", "n_rec", "n_out",
+                                  "loops", "window", "ring_slots")] + \
+               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F)]
+
+
+class DoryLayer(ctypes.Structure):
+    """xtg_dory_layer."""
+    _fields_ = [("kind", _I)] + [(n, Nvfp4) for n in ("q", "k", "v", "g", "o", "gate", "up", "down")] + \
+               [(n, _P) for n in ("qscale", "gscale", "sg", "su", "lr")]
+
+
 SIGNATURES = [
     ("xtg_hip_open", _P, [ctypes.c_char_p] + _ERR),
     ("xtg_hip_close", None, [_P]),
@@ -60,6 +74,11 @@ SIGNATURES = [
     ("xtg_hip_swiglu_norm", _I, [_P, _P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_gate_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_add_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
+    ("xtg_hip_dory_create", _P, [_P, ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4),
+                                 _P] + _ERR),
+    ("xtg_hip_dory_destroy", None, [_P]),
+    ("xtg_hip_dory_forward", _I, [_P, _P, _I, _I64, _P] + _ERR),
+    ("xtg_hip_dory_cache", _P, [_P, _I, _I]),
     ("xtg_hip_x_operand_bytes", _SZ, [_I]),
     ("xtg_hip_prep_x", _I, [_P, _P, _I, _I, _I, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4_op", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _P, _SZ] + _ERR),
@@ -296,6 +315,11 @@ class HipBackend:
         err = _errbuf()
         _check(lib().xtg_hip_attention(self.h, ctypes.byref(a), err, len(err)), err)
 
+    # ---- the Dory decode step
+    def dory(self, weights):
+        """A decode session over DoryWeights (xtier_go_amd.workloads); the weights stay referenced by it."""
+        return DorySession(self, weights)
+
     # ---- row kernels (queued, device buffers)
     def qk_rope_norm(self, q, k, m, heads, kv_heads, head_dim, pos0, theta, qscale=None):
         err = _errbuf()
@@ -320,6 +344,40 @@ class HipBackend:
         _check(lib().xtg_hip_add_norm(self.h, _ptr(a), _ptr(b), _ptr(out), rows, width, err, len(err)), err)
 
 
+class DorySession:
+    """xtg_hip_dory: forward(x, m, pos0, logits) on device buffers; cache(attn, inst) for filling contexts."""
+
+    def __init__(self, backend, weights):
+        import xtier_go_amd.workloads as wl
+        self.b = backend
+        self.w = weights
+        cfg, layers, head = wl.dory_structs(weights, Nvfp4, DoryLayer, DoryConfig)
+        self._keep = (cfg, layers, head)
+        err = _errbuf()
+        self.h = lib().xtg_hip_dory_create(backend.h, ctypes.byref(cfg), layers, ctypes.byref(head),
+                                           weights.logit_scale.ctypes.data, err, len(err))
+        if not self.h:
+            raise XtgError(err.value.decode(errors="replace"))
+
+    def destroy(self):
+        if self.h:
+            lib().xtg_hip_dory_destroy(self.h)
+            self.h = None
+
+    def forward(self, x, m, pos0, logits):
+        err = _errbuf()
+        _check(lib().xtg_hip_dory_forward(self.h, _ptr(x), m, pos0, _ptr(logits), err, len(err)), err)
+
+    def cache(self, attn, inst=0):
+        h = lib().xtg_hip_dory_cache(self.h, attn, inst)
+        if not h:
+            raise XtgError("no cache %d / %d" % (attn, inst))
+        c = KvCache.__new__(KvCache)
+        c.b, c.h, c.owned = self.b, h, False
+        c.kv_heads, c.head_dim = self.w.cfg["kv_heads"], self.w.cfg["head_dim"]
+        return c
+
+
 class KvCache:
     """A device KV cache (xtg_hip_kv): store from device rows, load to host, save / restore / release."""
 
@@ -328,13 +386,14 @@ class KvCache:
         self.kv_heads, self.head_dim = kv_heads, head_dim
         self.slots = ring if ring > 0 else slots
         self.ring = ring
+        self.owned = True
         err = _errbuf()
         self.h = lib().xtg_hip_kv_create(backend.h, kv_heads, head_dim, slots, ring, dtype, err, len(err))
         if not self.h:
             raise XtgError(err.value.decode(errors="replace"))
 
     def destroy(self):
-        if self.h and self.b.h:
+        if self.h and self.b.h and self.owned:
             lib().xtg_hip_kv_destroy(self.b.h, self.h)
         self.h = None
 

@@ -111,8 +111,10 @@ void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op) {
   timed([&] { return launch_prep_x(x, x_dtype, m, k, op, xinv, stream_); });
 }
 
-void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off) {
+void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
+                        const float* col_scale) {
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
+  XTG_CHECK(!col_scale || nw == 1, "matmul: a column scale applies to a single weight");
   XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul: %d rows (1..%d per device call)", m, kMaxRows);
   XTG_CHECK(op && y, "matmul: NULL operand or output");
   const int k = ws[0].k;
@@ -129,6 +131,7 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
   c.m = m;
   c.xop = op;
   c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
+  c.col_scale[0] = col_scale;
   timed([&] { return launch_gemv(c, stream_); });
 }
 

@@ -36,7 +36,8 @@ class Backend {
   // the two halves of matmul_dev: the activation operand ([xop][8 row scales], op_bytes(k)) and the GEMV on it
   static size_t op_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
   void prep_x(const void* x, int x_dtype, int m, int k, void* op);
-  void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off);
+  void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
+                 const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]
 
   // KV caches (xtg::KvCache, kv.h:21-62): device storage, host-side load / save for tests and snapshots
   DevKv* kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype);

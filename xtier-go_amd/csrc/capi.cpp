@@ -8,6 +8,7 @@
 
 #include "backend.hpp"
 #include "common.hpp"
+#include "dory.hpp"
 #include "xtg_hip.h"
 
 struct xtg_hip {
@@ -208,6 +209,42 @@ int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int
     XTG_CHECK(h, "add_norm: NULL handle");
     h->b->add_norm(a, b, out, rows, width);
   });
+}
+
+struct xtg_hip_dory {
+  xtg_hip* h;
+  std::unique_ptr<xtg::hip::DorySession> s;
+};
+
+xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xtg_dory_layer* layers,
+                                  const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len) {
+  xtg_hip_dory* d = nullptr;
+  int rc = guarded(err, err_len, [&] {
+    XTG_CHECK(h && c && layers && head && logit_scale, "dory_create: NULL argument");
+    auto s = std::make_unique<xtg::hip::DorySession>(*h->b, *c, layers, *head, logit_scale);
+    d = new xtg_hip_dory{h, std::move(s)};
+  });
+  return rc == 0 ? d : nullptr;
+}
+
+void xtg_hip_dory_destroy(xtg_hip_dory* d) {
+  try {
+    delete d;
+  } catch (...) {
+  }
+}
+
+int xtg_hip_dory_forward(xtg_hip_dory* d, const float* x, int m, int64_t pos0, float* logits, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(d && x && logits, "dory_forward: NULL argument");
+    d->s->forward(x, m, pos0, logits);
+  });
+}
+
+xtg_hip_kv* xtg_hip_dory_cache(xtg_hip_dory* d, int attn, int inst) {
+  xtg::hip::DevKv* c = nullptr;
+  if (!d || guarded(nullptr, 0, [&] { c = d->s->cache(attn, inst); }) != 0) return nullptr;
+  return reinterpret_cast<xtg_hip_kv*>(c);
 }
 
 size_t xtg_hip_x_operand_bytes(int k) { return k > 0 ? xtg::hip::Backend::op_bytes(k) : 0; }

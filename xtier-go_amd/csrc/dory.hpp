@@ -1,0 +1,59 @@
+// The looped-nGPT (Dory) decode step on the HIP backend: the composition of packs/dory/dory.cpp:467-578
+// (DorySession::sublayer / run_chunk / forward; the OpenCL GpuDorySession, dory.cpp:1108-1214) over the gfx950
+// kernels. Weights are prepared once; every forward call queues its kernels on the backend's stream, so a step
+// can be captured into one HIP graph.
+#pragma once
+
+#include <vector>
+
+#include "backend.hpp"
+#include "xtg_hip.h"
+
+namespace xtg::hip {
+
+class DorySession {
+ public:
+  DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_layer* layers, const xtg_nvfp4& head,
+              const float* logit_scale);
+  ~DorySession();
+  DorySession(const DorySession&) = delete;
+  DorySession& operator=(const DorySession&) = delete;
+
+  // run_chunk from the hidden rows x [m][hidden] (device; the embedding rows) at positions pos0 .. pos0 + m - 1,
+  // then the LM head times logit_scale into logits [m][vocab] (device). m <= 8. The caches gain the chunk's keys.
+  void forward(const float* x, int m, long long pos0, float* logits);
+  DevKv* cache(int attn, int inst);
+  Backend& backend() { return b_; }
+  int n_attn() const { return n_attn_; }
+
+ private:
+  struct Layer {
+    xtg_dory_layer w;   // weight descriptors (host pointers key the prepared device copies)
+    int attn = -1;
+    bool recurrent = false;
+    float* qscale = nullptr;   // device copies of the per-layer vectors
+    float* gscale = nullptr;
+    float* sg = nullptr;
+    float* su = nullptr;
+    float* lr = nullptr;
+  };
+  void sublayer(Layer& L, int m, long long pos0, int inst);
+  float* upload(const float* v, size_t n);
+
+  Backend& b_;
+  xtg_dory_config c_;
+  std::vector<Layer> layers_;
+  xtg_nvfp4 head_;
+  float* logit_scale_ = nullptr;
+  int n_attn_ = 0;
+  std::vector<DevKv*> caches_;   // [attn][loops]
+  std::vector<void*> owned_;     // device vectors and scratch
+  // scratch for up to 8 rows
+  float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *att_ = nullptr, *gu_ = nullptr,
+        *o_ = nullptr;
+  void* op_h_ = nullptr;   // activation operand for K = hidden
+  void* op_q_ = nullptr;   // for K = heads * head_dim (o_proj)
+  void* op_f_ = nullptr;   // for K = ffn (down)
+};
+
+}  // namespace xtg::hip

@@ -167,6 +167,7 @@ struct GemvArgs {
   int n[4];
   float global[4];
   long long y_off[4];
+  const float* col_scale[4];   // optional per-output-column factor (the LM head's logit scale)
   int wg_end[4];   // cumulative work-group counts per weight
   int nw;
   int kt;
@@ -209,9 +210,10 @@ __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int 
   const int n0 = rb * kTileRows + 4 * g;
   const float f = a.global[wi] * a.xinv[j];
   float* yp = a.y + a.y_off[wi] + (long long)j * n;
+  const float* cs = a.col_scale[wi];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    if (n0 + e < n) yp[n0 + e] = v[e] * f;
+    if (n0 + e < n) yp[n0 + e] = cs ? (v[e] * f) * cs[n0 + e] : v[e] * f;
 }
 
 template <int R, int T, int MAXT>
@@ -369,6 +371,7 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
     a.n[i] = c.w[i]->n;
     a.global[i] = c.w[i]->global;
     a.y_off[i] = (long long)c.y_off[i];
+    a.col_scale[i] = c.col_scale[i];
     wgs += (c.w[i]->nb + sh.r - 1) / sh.r;
     a.wg_end[i] = wgs;
   }

@@ -42,6 +42,7 @@ struct GemvCall {
   const PackedNvfp4* w[4] = {nullptr, nullptr, nullptr, nullptr};
   int nw = 0;
   size_t y_off[4] = {0, 0, 0, 0};   // floats from y
+  const float* col_scale[4] = {nullptr, nullptr, nullptr, nullptr};   // optional per-column factors (device)
   float* y = nullptr;
   int m = 0;
   const void* xop = nullptr;

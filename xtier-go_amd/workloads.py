@@ -31,21 +31,34 @@ E2M1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -
 
 
 def f32_to_e4m3(x):
-    """FP32 -> E4M3 codes: the largest code not above |x|, then nearest even; |x| >= 448 saturates to 0x7e."""
-    x = np.asarray(x, dtype=np.float32)
-    sign = np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
-    a = np.abs(x)
-    pos = E4M3[:0x7F]   # codes 0x00 .. 0x7e, increasing
-    lo = np.searchsorted(pos, a, side="right") - 1
-    lo = np.clip(lo, 0, 0x7E)
-    nxt = np.minimum(lo + 1, 0x7E)
-    d0 = (a - pos[lo]).astype(np.float32)
-    d1 = (pos[nxt] - a).astype(np.float32)
-    up = (lo < 0x7E) & ((d1 < d0) | ((d1 == d0) & ((lo & 1) == 1)))
-    code = (lo + up).astype(np.uint8)
-    code = np.where(a >= 448.0, 0x7E, code).astype(np.uint8)
-    code = np.where(np.isnan(x), 0x7F, code).astype(np.uint8)
-    return (code | sign).astype(np.uint8)
+    """FP32 -> E4M3 codes, round to nearest even, |x| >= 448 saturating to 0x7e, NaN to 0x7f (with the sign).
+
+    Below 2^-6 the result counts subnormal steps of 2^-9 (ties to even); above, the FP32 significand is rounded to
+    3 bits (ties to even) and rebiased -- the same codes as the nearest-even table search, done on the bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    bits = x.view(np.uint32)
+    sign = ((bits >> 24) & np.uint32(0x80)).astype(np.uint8)
+    a = bits & np.uint32(0x7FFFFFFF)
+    small = a < np.uint32(0x3C800000)
+    # normal range (a >= 2^-6): round the significand to 3 bits, nearest even, rebias 127 -> 7
+    code = (a >> 20) & np.uint32(1)
+    code += a
+    code += np.uint32(0x7FFFF)
+    code >>= 20                                   # exponent (8 bits) and 3 significand bits
+    code -= np.uint32(120 << 3)                   # rebias; wraps for small a, which is replaced below
+    np.minimum(code, np.uint32(0x7E), out=code)
+    if small.any():
+        # subnormal range: steps of 2^-9, nearest even
+        t = a[small].view(np.float32) * np.float32(512.0)
+        lo = np.floor(t)
+        half = t - lo
+        steps = lo.astype(np.uint32)
+        steps += (half > 0.5) | ((half == 0.5) & ((steps & np.uint32(1)) == 1))
+        code[small] = steps
+    code[a > np.uint32(0x7F800000)] = 0x7F          # NaN (above the saturation test, which NaN fails)
+    out = code.astype(np.uint8)
+    out |= sign
+    return out
 
 
 def f32_to_bf16(x):
@@ -99,6 +112,106 @@ def unit_heads(rng, shape, head_dim):
 def gemv_bytes(n, k, m):
     """Algorithmic HBM bytes of one NVFP4 GEMV call: codes + scales + tensor scale + BF16 x + FP32 y."""
     return n * k // 2 + n * k // 16 + 4 + 2 * m * k + 4 * m * n
+
+
+# ------------------------------------------------------------------------------------- synthetic Dory model
+
+MLP, SLIDING, FULL = 0, 1, 2
+
+# The 4B-shaped decode configuration: d_model 3072, 32 q / 8 KV heads of 128, FFN 8192 (SwiGLU), 4 input / 40
+# recurrent / 4 output sublayers alternating attention and MLP (24 + 24), one loop, every fourth attention
+# sublayer global and the others sliding (window 1024 in a 1088-slot ring), vocab 131072 with an NVFP4 head.
+DORY_4B = dict(hidden=3072, ffn=8192, heads=32, kv_heads=8, head_dim=128, vocab=131072, n_in=4, n_rec=40, n_out=4,
+               loops=1, window=1024, ring_slots=1088, theta_sliding=1e6, theta_full=1e6)
+# A small model with the same structure for parity tests (two loops exercise the per-loop caches).
+DORY_TINY = dict(hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, n_in=2, n_rec=4, n_out=2,
+                 loops=2, window=48, ring_slots=64, theta_sliding=1e4, theta_full=1e6)
+
+
+def dory_kinds(cfg):
+    """Sublayer kinds: attention and MLP alternate (attention first); every fourth attention sublayer is global."""
+    n = cfg["n_in"] + cfg["n_rec"] + cfg["n_out"]
+    kinds, a = [], 0
+    for l in range(n):
+        if l % 2 == 0:
+            kinds.append(FULL if a % 4 == 3 else SLIDING)
+            a += 1
+        else:
+            kinds.append(MLP)
+    return kinds
+
+
+class DoryWeights:
+    """Random-init weights of a Dory-shaped model with the scale vectors already folded (as the reference's model
+    constructor leaves them): NVFP4 projections with the BASELINE distributions; qscale, gscale ~ U(0.5, 1.5);
+    sg, su ~ U(5, 15) (so silu sees arguments of order one); lr ~ U(0.02, 0.1); logit_scale ~ U(0.5, 1.5)."""
+
+    def __init__(self, cfg, seed=0, context=4096, workers=8):
+        import concurrent.futures
+        self.cfg = dict(cfg)
+        self.cfg["context"] = int(context)
+        H, F = cfg["hidden"], cfg["ffn"]
+        Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
+        self.kinds = dory_kinds(cfg)
+
+        def layer(i):   # every sublayer (and the head, i = len) draws from its own stream of the seed
+            rng = np.random.default_rng([seed, i])
+            if i == len(self.kinds):
+                return nvfp4_weight(rng, cfg["vocab"], H), rng.uniform(0.5, 1.5, cfg["vocab"]).astype(np.float32)
+            kind = self.kinds[i]
+            L = {"kind": kind, "lr": rng.uniform(0.02, 0.1, H).astype(np.float32)}
+            if kind == MLP:
+                L["gate"] = nvfp4_weight(rng, F, H)
+                L["up"] = nvfp4_weight(rng, F, H)
+                L["down"] = nvfp4_weight(rng, H, F)
+                L["sg"] = rng.uniform(5, 15, F).astype(np.float32)
+                L["su"] = rng.uniform(5, 15, F).astype(np.float32)
+            else:
+                for name, n in (("q", Q), ("k", KV), ("v", KV), ("g", Q)):
+                    L[name] = nvfp4_weight(rng, n, H)
+                L["o"] = nvfp4_weight(rng, H, Q)
+                L["qscale"] = rng.uniform(0.5, 1.5, Q).astype(np.float32)
+                L["gscale"] = rng.uniform(0.5, 1.5, Q).astype(np.float32)
+            return L
+
+        with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as ex:
+            parts = list(ex.map(layer, range(len(self.kinds) + 1)))
+        self.layers = parts[:-1]
+        self.head, self.logit_scale = parts[-1]
+
+    def n_attn(self):
+        return sum(1 for k in self.kinds if k != MLP)
+
+    def weight_bytes(self):
+        b = self.head[0].nbytes + self.head[1].nbytes
+        for L in self.layers:
+            for name in ("q", "k", "v", "g", "o", "gate", "up", "down"):
+                if name in L:
+                    b += L[name][0].nbytes + L[name][1].nbytes
+        return b
+
+
+def dory_structs(w, nvfp4_type, layer_type, config_type):
+    """ctypes views (config, layer array, head) of DoryWeights for a C ABI with the xtg_dory_* layouts."""
+    def nv(t):
+        codes, scales, glob = t
+        return nvfp4_type(codes.ctypes.data, scales.ctypes.data, glob, codes.shape[0], codes.shape[1] * 2)
+
+    zero = nvfp4_type(None, None, 1.0, 0, 0)
+    arr = (layer_type * len(w.layers))()
+    for i, L in enumerate(w.layers):
+        s = layer_type()
+        s.kind = L["kind"]
+        for name in ("q", "k", "v", "g", "o", "gate", "up", "down"):
+            setattr(s, name, nv(L[name]) if name in L else zero)
+        for name in ("qscale", "gscale", "sg", "su", "lr"):
+            setattr(s, name, L[name].ctypes.data if name in L else None)
+        arr[i] = s
+    c = w.cfg
+    cfg = config_type(c["hidden"], c["ffn"], c["heads"], c["kv_heads"], c["head_dim"], c["vocab"], c["n_in"],
+                      c["n_rec"], c["n_out"], c["loops"], c["window"], c["ring_slots"], c["context"],
+                      c["theta_sliding"], c["theta_full"])
+    return cfg, arr, nv(w.head)
 
 
 # The projection shapes of one synthetic 4B-shaped layer (d_model 3072, 32 q / 8 KV heads of 128, FFN 8192).
