@@ -80,6 +80,106 @@ def cpu_baseline(base, xs, seconds):
                       "same weights and inputs, one weight copy), %.1f s on %d threads" % (done, el, threads)}
 
 
+def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
+    """Config 4: the synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
+    row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
+    synthetic context of unit-norm K / V rows; a replay re-decodes position ctx, so every replay is the same step."""
+    ctx_max = max(contexts)
+    t0 = time.perf_counter()
+    w = wl.DoryWeights(wl.DORY_4B, seed=11, context=ctx_max + 64)
+    log("decode: 4B-shaped model %.2f GB of NVFP4 weights generated in %.1f s" % (w.weight_bytes() / 1e9,
+                                                                                time.perf_counter() - t0))
+    t0 = time.perf_counter()
+    dev = hip.dory(w)
+    log("decode: weights prepared on the device in %.1f s" % (time.perf_counter() - t0))
+    c = w.cfg
+    kvh, d, ring, H, V = c["kv_heads"], c["head_dim"], c["ring_slots"], c["hidden"], c["vocab"]
+    rng = np.random.default_rng(12)
+    K = wl.unit_heads(rng, (ctx_max, kvh), d)
+    Vv = wl.unit_heads(rng, (ctx_max, kvh), d)
+    dK, dV = hip.array(K), hip.array(Vv)
+    row = kvh * d * 4
+    x = rng.standard_normal((8, H)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    dx = hip.array(x)
+    dl = hip.array(shape=(8, V))
+    attn = [a for a, k in enumerate(k for k in w.kinds if k != wl.MLP)]
+    kinds = [k for k in w.kinds if k != wl.MLP]
+    for a, kind in zip(attn, kinds):   # global caches: positions 0 .. ctx_max - 1 once
+        if kind == wl.FULL:
+            dev.cache(a).store(0, ctx_max, dK, dV)
+    kv_step = {}
+    results = {}
+    for ctx in contexts:
+        for a, kind in zip(attn, kinds):   # rings: the 1088 positions before ctx
+            if kind == wl.SLIDING:
+                dev.cache(a).store(ctx - ring, ring, dK.ptr + (ctx - ring) * row, dV.ptr + (ctx - ring) * row)
+        hip.finish()
+        n_full = kinds.count(wl.FULL)
+        kv_step[ctx] = (n_full * ctx + (len(kinds) - n_full) * min(ring, c["window"])) * kvh * d * 2 * 2
+        res = {}
+        for m in (1, 8):
+            dev.forward(dx, m, ctx, dl)   # eager once (scratch sized), then capture
+            hip.finish()
+            hip.graph_begin()
+            dev.forward(dx, m, ctx, dl)
+            g = hip.graph_end("dory_step_ctx%d_m%d" % (ctx, m))
+            for _ in range(3):
+                hip.graph_launch(g)
+            hip.finish()
+            t = time.perf_counter()
+            for _ in range(reps):
+                hip.graph_launch(g)
+            hip.finish()
+            ms = (time.perf_counter() - t) / reps * 1e3
+            hip.graph_destroy(g)
+            step_bytes = w.weight_bytes() + kv_step[ctx]
+            res["m%d" % m] = {"ms_per_step": round(ms, 4), "rows_per_s": round(m * 1e3 / ms, 1),
+                              "hbm_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1)}
+        res["tok_s"] = res["m1"]["rows_per_s"]
+        res["step_bytes_m1"] = w.weight_bytes() + kv_step[ctx]
+        results["ctx%d" % ctx] = res
+        log("decode ctx %5d: M=1 %.3f ms/token (%.0f tok/s, %.0f GB/s), M=8 verify %.3f ms/step (%.0f rows/s)"
+            % (ctx, res["m1"]["ms_per_step"], res["tok_s"], res["m1"]["hbm_gbs"], res["m8"]["ms_per_step"],
+               res["m8"]["rows_per_s"]))
+    # per-kernel breakdown of one eager step at the largest context (events around every launch)
+    hip.profile(True)
+    dev.forward(dx, 1, ctx_max, dl)
+    rep = hip.profile_report()
+    hip.profile(False)
+    kernels = {k: {"calls": v["calls"], "us": round(v["ms"] * 1e3, 1)} for k, v in
+               sorted(rep.items(), key=lambda kv: -kv[1]["ms"])}
+    results["kernels_ctx%d_m1_eager" % ctx_max] = kernels
+    cpu = None
+    if cpu_seconds > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        ctx = min(contexts)
+        ref = orc.Dory(w, wl)
+        a_i = 0
+        for a, kind in zip(attn, kinds):
+            lo = 0 if kind == wl.FULL else ctx - ring
+            ref.cache(a).store(lo, K[lo:ctx], Vv[lo:ctx])
+        threads = os.cpu_count() or 1
+        ref.forward(x[:1], ctx, threads=threads)
+        n, t = 0, time.perf_counter()
+        while time.perf_counter() - t < cpu_seconds or n == 0:
+            ref.forward(x[:1], ctx, threads=threads)
+            n += 1
+        el = (time.perf_counter() - t) / n
+        cpu = {"tok_s": round(1 / el, 3), "ms_per_token": round(el * 1e3, 2), "cores": threads, "kind": "port",
+               "sample": "%d decode steps (M=1) of the oracle's composition at a %d context" % (n, ctx)}
+        log("decode CPU (oracle, %d threads): %.2f tok/s at %d context" % (threads, cpu["tok_s"], ctx))
+        del ref
+    for a in (dK, dV, dx, dl):
+        a.free()
+    dev.destroy()
+    results["cpu"] = cpu
+    results["model"] = ("looped nGPT, d_model 3072, 32 q / 8 KV heads of 128, FFN 8192, 4/40/4 sublayers (24 attention: "
+                        "6 global + 18 sliding 1024 in 1088-slot rings; 24 MLP), 1 loop, NVFP4 head over 131072")
+    return results
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,6 +189,9 @@ def main():
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-contexts", default="4096,8192,32768")
+    ap.add_argument("--decode-reps", type=int, default=50)
+    ap.add_argument("--no-decode", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels are one GPU's share of a "
@@ -196,6 +299,16 @@ def main():
         cpu = cpu_baseline(base, xs, args.cpu_seconds)
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
+    decode = None
+    if not args.no_decode:
+        for name in list(base):   # the projection bench's weights are no longer needed
+            for s in sets:
+                for w in s[name]:
+                    hip.release_weight(w)
+        sets.clear()
+        contexts = [int(v) for v in args.decode_contexts.split(",") if v]
+        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2)
+
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -221,6 +334,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     hip.close()
     print(json.dumps(out), flush=True)
