@@ -3,9 +3,8 @@
 // Semantics (engine/src/kv.cpp:166-286, npu/xtg_npu.cpp:236-258): query row i of this call (position pos0 + i)
 // attends, for each of its q heads, to the cached keys whose stored position q satisfies 0 <= q < pos0 and
 // (window <= 0 or pos0 + i - q < window), and to this call's own keys j <= i (with i - j < window); FP32 softmax of
-// scale * q.k; the cache is read only. For a linear cache the stored position of slot s is s; for a ring it is
-// whatever position was last written there (the slot-position array), so the mask is rebuilt from slot
-// positions on every call.
+// scale * q.k. For a linear cache the stored position of slot s is s; for a ring it is whatever position was last
+// written there (the slot-position array), so the mask is rebuilt from slot positions on every call.
 //
 // Device cache layout (head-major, in matrix-core operand order, slots padded to a multiple of 32):
 //   K: per head, per block of 16 slots, per 32-wide chunk c of head_dim: 64 lanes x 8 BF16, lane (g, i) holding
@@ -14,18 +13,27 @@
 //      dim 16 dd + i of slots {4 g .. 4 g + 3, 16 + 4 g .. 16 + 4 g + 3}: the A operand (dims x keys) of the P.V
 //      product whose B operand (keys x queries) is exactly what each lane holds of the score tile's accumulator.
 //   slot_pos: int32 per slot, -1 = never written.
-// Scores: S^T = K Q^T with the q vectors (times scale) split into three BF16 terms (about 24 significant bits, so
-// sharp softmaxes keep FP32-level scores); K is BF16 and exact. P.V with P split into two BF16 terms. The q heads
-// sharing a KV head and the query rows are stacked as MFMA columns (q-col = row * group + head), so every K and V
-// byte is read once per KV head. This call's own keys (FP32, not yet stored) are added in FP32 on the vector ALUs.
-// Flash decoding: a work-group of 4 waves per (KV head, split of the key tiles); the waves' online-softmax states
-// are merged in LDS into one partial (max, sum, accumulator) per q-col, and attn_merge_kernel combines the splits.
+//
+// Work (flash decoding, partials laid out as AttnPlan says):
+//   attn_scan_kernel: a work-group of 4 waves per (KV head, split of the key tiles). Scores S^T = K Q^T with the q
+//     vectors (times scale) split into three BF16 terms (about 24 significant bits, so sharp softmaxes keep
+//     FP32-level scores); K is BF16 and exact. P.V with P split into two BF16 terms. The q heads sharing a KV head
+//     and the query rows are stacked as MFMA columns (q-col = row * group + head), so every K and V byte is read
+//     once per KV head. Each wave streams its tiles with the next tile's loads in flight; the waves' states are
+//     merged in LDS into one partial per q-col.
+//   Own keys (FP32, not rounded to the cache's BF16): one wave per q-col on the vector ALUs, in attn_own_kernel or
+//     inside the decode step's producer (qk_produce_kernel), as one more partial.
+//   attn_merge_kernel / attn_gate_kernel: one work-group per query row merges its partials (kv.cpp:262-285);
+//     the gate variant applies the decode step's sigmoid gate and norm and writes the o-projection's operand.
 #include <algorithm>
 #include <cfloat>
+#include <climits>
 #include <cmath>
+#include <cstdlib>
 
 #include "attention.hpp"
 #include "common.hpp"
+#include "rowops.hpp"
 
 namespace xtg::hip {
 
@@ -98,221 +106,218 @@ void launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const
   HIP_CHECK(hipGetLastError());
 }
 
-// -------------------------------------------------------------------------------------------------- attention
 
-struct AttnKernelArgs {
-  const float* q;         // [n_rows][heads][d]: rows row0 .. row0 + n_rows - 1 of the call
-  const float* k;         // [n_own][kv_heads][d] all of this call's keys (positions pos0 .. pos0 + n_own - 1)
-  const float* v;
-  const uint4* ck;        // cache, operand layout
+// ------------------------------------------------------------------------------------------------------- scan
+
+struct ScanArgs {
+  const float* q;          // the block's rows [n_rows][heads][d]
+  const uint4* ck;         // cache, operand layout
   const uint4* cv;
   const int* slot_pos;
-  float* part;            // [kv_heads][splits][qcols][2 + d]
-  int n_rows, row0, n_own, heads, kv_heads, group, window, splits, slots_pad;
-  int tile_lo, tiles;     // the key tiles to scan: tile_lo .. tile_lo + tiles - 1
-  long long pos0;
-  float scale;
+  float* acc;              // the block's partials: record (h, s, c) at (h * splits1 + s) * qpad + c
+  float* ml;
+  int n_rows, row0, heads, group, window, splits, splits1, qpad, slots_pad;
+  int tile_lo, tiles;      // the key tiles to scan: tile_lo .. tile_lo + tiles - 1
+  int pos0;                // positions are below 2^31 (the slot-position array is int32)
+  float scale2;            // scale * log2(e)
 };
 
-__device__ inline bf16x8 bf16x8_of(const float v[8]) {
-  bf16x8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(v[e]));
-  return r;
-}
+// FP32 -> BF16 on the vector ALU (v_cvt_pk_bf16_f32, round to nearest even) and back (exact).
+__device__ inline __bf16 to_bf16(float x) { return (__bf16)x; }
+__device__ inline float of_bf16(__bf16 b) { return (float)b; }
 
 // x = t0 + t1 + t2 + O(2^-24 |x|), each term the BF16 rounding of what is left.
 __device__ inline void split3(const float x[8], bf16x8& t0, bf16x8& t1, bf16x8& t2) {
-  float a[8], b[8], c[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    a[e] = bf16_bits_to_f32(f32_to_bf16_bits(x[e]));
-    const float r = x[e] - a[e];
-    b[e] = bf16_bits_to_f32(f32_to_bf16_bits(r));
-    c[e] = r - b[e];
+    const __bf16 a = to_bf16(x[e]);
+    const float r = x[e] - of_bf16(a);
+    const __bf16 b = to_bf16(r);
+    t0[e] = a;
+    t1[e] = b;
+    t2[e] = to_bf16(r - of_bf16(b));
   }
-  t0 = bf16x8_of(a);
-  t1 = bf16x8_of(b);
-  t2 = bf16x8_of(c);
+}
+
+// Softmax weights run in the base-2 domain: scores are q.k * scale * log2(e) and every partial's max is in those
+// units, so each weight is one v_exp_f32 (exp2(-inf) = 0).
+constexpr float kLog2e = 1.44269504088896341f;
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One 32-slot tile of a KV head as a wave holds it: K as two 16-slot A operands per 32-dim chunk, V as one A
+// operand per 16-dim block, and the slot positions of the lane's 8 keys.
+template <int D>
+struct KvTile {
+  uint4 k[2][D / 32];
+  uint4 v[D / 16];
+  int4 p0, p1;
+};
+
+template <int D>
+__device__ inline void load_tile(KvTile<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
+                                 const int* __restrict__ slot_pos, int t, int lane) {
+  constexpr int NC = D / 32, ND = D / 16;
+  const size_t ktile = size_t(2 * NC) * 64, vtile = size_t(ND) * 64;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) T.k[b][c] = kb[size_t(t) * ktile + size_t(b * NC + c) * 64 + size_t(lane)];
+#pragma unroll
+  for (int dd = 0; dd < ND; ++dd) T.v[dd] = vb[size_t(t) * vtile + size_t(dd) * 64 + size_t(lane)];
+  const int g = lane >> 4;
+  T.p0 = *reinterpret_cast<const int4*>(slot_pos + t * kTile + 4 * g);
+  T.p1 = *reinterpret_cast<const int4*>(slot_pos + t * kTile + 16 + 4 * g);
+}
+
+// The online-softmax state of the lane's column in each q-block (the same in the 4 lanes of a column).
+template <int D, int QB>
+struct ScanState {
+  float m[QB], l[QB];
+  f32x4 acc[QB][D / 16];
+};
+
+// One tile for every q-block: scores (three MFMA terms), mask, online softmax, P.V (two terms). lo[qb]: the
+// lane's column sees stored positions lo .. pos0 - 1 (INT_MAX for a column with no query).
+template <int D, int QB>
+__device__ inline void scan_tile(const KvTile<D>& T, const bf16x8 (&qop)[QB][D / 32][3], const int (&lo)[QB],
+                                 ScanState<D, QB>& st, int pos0) {
+  constexpr int NC = D / 32, ND = D / 16;
+  const int kpos[8] = {T.p0.x, T.p0.y, T.p0.z, T.p0.w, T.p1.x, T.p1.y, T.p1.z, T.p1.w};
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    f32x4 s[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      s[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8 A = __builtin_bit_cast(bf16x8, T.k[b][c]);
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+          s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, qop[qb][c][term], s[b], 0, 0, 0);
+      }
+    }
+    // mask, then the column's max over its 4 lanes x 8 keys
+    float sc[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sc[e] = kpos[e] >= lo[qb] && kpos[e] < pos0 ? s[e >> 2][e & 3] : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = xor32_max(xor16_max(mx));
+    // No branch on visibility: every lane takes part in the swaps and matrix ops below. A column with nothing
+    // visible yet keeps max -inf, sum 0 and a zero accumulator (reference max 0: weights exp2(-inf) = 0).
+    const float m_new = fmaxf(st.m[qb], mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = exp2_fast(st.m[qb] - m_ref);
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = exp2_fast(sc[e] - m_ref);
+      ps += p[e];
+    }
+    ps = xor32_sum(xor16_sum(ps));
+    st.l[qb] = st.l[qb] * corr + ps;
+    st.m[qb] = m_new;
+    bf16x8 phi, plo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 h = to_bf16(p[e]);
+      phi[e] = h;
+      plo[e] = to_bf16(p[e] - of_bf16(h));
+    }
+    if (__ballot(corr != 1.f)) {   // some column's max moved: rescale (skipped once the maxima settle)
+#pragma unroll
+      for (int dd = 0; dd < ND; ++dd) st.acc[qb][dd] *= corr;
+    }
+#pragma unroll
+    for (int dd = 0; dd < ND; ++dd) {
+      const bf16x8 A = __builtin_bit_cast(bf16x8, T.v[dd]);
+      st.acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, phi, st.acc[qb][dd], 0, 0, 0);
+      st.acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, plo, st.acc[qb][dd], 0, 0, 0);
+    }
+  }
 }
 
 template <int D, int QB>
-__global__ void __launch_bounds__(kWaves * 64) attn_decode_kernel(const AttnKernelArgs a) {
-  constexpr int NC = D / 32;   // 32-dim chunks (QK^T contraction)
-  constexpr int ND = D / 16;   // 16-dim blocks (P.V rows)
+__global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a) {
+  constexpr int NC = D / 32, ND = D / 16;
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int kvh = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
   const int qcols = a.n_rows * a.group;
 
-  // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale, three terms
+  // this split's tiles (at least one: splits <= tiles), dealt to the waves round-robin; the first tile's loads go
+  // out before the q operands are built, and every later tile's while the previous one is worked on (an index
+  // past the split's end loads its last tile again and is not used)
+  const int t_begin = a.tile_lo + int((long long)a.tiles * split / a.splits);
+  const int t_end = a.tile_lo + int((long long)a.tiles * (split + 1) / a.splits);
+  const int t_last = t_end - 1;
+  const uint4* kbase = a.ck + size_t(kvh) * size_t(a.slots_pad / kTile) * size_t(2 * NC) * 64;
+  const uint4* vbase = a.cv + size_t(kvh) * size_t(a.slots_pad / kTile) * size_t(ND) * 64;
+  int t = t_begin + wave;
+  KvTile<D> A, B;
+  load_tile<D>(A, kbase, vbase, a.slot_pos, min(t, t_last), lane);
+
+  // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale * log2(e),
+  // three terms. lo: the first stored position the column sees.
   bf16x8 qop[QB][NC][3];
-  int qrow[QB];
-  bool qlive[QB];
+  int lo[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qc = qb * 16 + j;
-    qlive[qb] = qc < qcols;
-    qrow[qb] = qlive[qb] ? qc / a.group : 0;
-    const float* qp = a.q + (size_t(qrow[qb]) * size_t(a.heads) + size_t(kvh * a.group + (qlive[qb] ? qc % a.group : 0))) * D;
+    const bool live = qc < qcols;
+    const int qrow = live ? qc / a.group : 0;
+    const int qpos = a.pos0 + a.row0 + qrow;
+    lo[qb] = !live ? INT_MAX : (a.window > 0 ? max(0, qpos - a.window + 1) : 0);
+    const float* qp = a.q + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (live ? qc % a.group : 0))) * D;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float x[8];
-      if (qlive[qb]) {
-        const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
-        const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
-        x[0] = u.x, x[1] = u.y, x[2] = u.z, x[3] = u.w, x[4] = w.x, x[5] = w.y, x[6] = w.z, x[7] = w.w;
+      const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
+      const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
+      float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= a.scale;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = 0.f;
-      }
+      for (int e = 0; e < 8; ++e) x[e] = live ? x[e] * a.scale2 : 0.f;
       split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
     }
   }
 
-  // online-softmax state of the lane's column in each q-block (the same in the 4 lanes of a column)
-  float m[QB], l[QB];
-  f32x4 acc[QB][ND];
+  ScanState<D, QB> st;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    m[qb] = -INFINITY;
-    l[qb] = 0.f;
+    st.m[qb] = -INFINITY;
+    st.l[qb] = 0.f;
 #pragma unroll
-    for (int dd = 0; dd < ND; ++dd) acc[qb][dd] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dd = 0; dd < ND; ++dd) st.acc[qb][dd] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  while (t < t_end) {
+    load_tile<D>(B, kbase, vbase, a.slot_pos, min(t + kWaves, t_last), lane);
+    scan_tile<D, QB>(A, qop, lo, st, a.pos0);
+    t += kWaves;
+    if (t >= t_end) break;
+    load_tile<D>(A, kbase, vbase, a.slot_pos, min(t + kWaves, t_last), lane);
+    scan_tile<D, QB>(B, qop, lo, st, a.pos0);
+    t += kWaves;
   }
 
-  // this split's tiles, dealt to the waves round-robin
-  const int t_begin = a.tile_lo + int((long long)a.tiles * split / a.splits);
-  const int t_end = a.tile_lo + int((long long)a.tiles * (split + 1) / a.splits);
-  const size_t ktile = size_t(2 * NC) * 64, vtile = size_t(ND) * 64;   // uint4 per tile
-  const uint4* kbase = a.ck + size_t(kvh) * size_t(a.slots_pad / kTile) * ktile;
-  const uint4* vbase = a.cv + size_t(kvh) * size_t(a.slots_pad / kTile) * vtile;
-  for (int t = t_begin + wave; t < t_end; t += kWaves) {
-    uint4 kop[2][NC], vop[ND];
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) kop[b][c] = kbase[size_t(t) * ktile + size_t(b * NC + c) * 64 + size_t(lane)];
-#pragma unroll
-    for (int dd = 0; dd < ND; ++dd) vop[dd] = vbase[size_t(t) * vtile + size_t(dd) * 64 + size_t(lane)];
-    const int4 p0 = *reinterpret_cast<const int4*>(a.slot_pos + t * kTile + 4 * g);
-    const int4 p1 = *reinterpret_cast<const int4*>(a.slot_pos + t * kTile + 16 + 4 * g);
-    const int kpos[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      f32x4 s[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        s[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const bf16x8 A = __builtin_bit_cast(bf16x8, kop[b][c]);
-#pragma unroll
-          for (int term = 0; term < 3; ++term)
-            s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, qop[qb][c][term], s[b], 0, 0, 0);
-        }
-      }
-      // mask, tile max over the lane's 8 keys and the column's 4 lanes
-      const long long qpos = a.pos0 + a.row0 + qrow[qb];
-      float sc[8];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int kp = kpos[e];
-        const bool see = qlive[qb] && kp >= 0 && kp < a.pos0 && (a.window <= 0 || qpos - kp < a.window);
-        sc[e] = see ? s[e >> 2][e & 3] : -INFINITY;
-        mx = fmaxf(mx, sc[e]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // No branch on visibility: every lane takes part in the shuffles and matrix ops below. A column with
-      // nothing visible yet keeps max -inf, sum 0 and a zero accumulator (correction 1, probabilities 0).
-      const float m_new = fmaxf(m[qb], mx);
-      const float corr = m[qb] == -INFINITY ? (m_new == -INFINITY ? 1.f : 0.f) : expf(m[qb] - m_new);
-      float p[8], ps = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = sc[e] == -INFINITY ? 0.f : expf(sc[e] - m_new);
-        ps += p[e];
-      }
-      ps += __shfl_xor(ps, 16);
-      ps += __shfl_xor(ps, 32);
-      l[qb] = l[qb] * corr + ps;
-      m[qb] = m_new;
-      bf16x8 phi, plo;
-      {
-        float hi[8], lo[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          hi[e] = bf16_bits_to_f32(f32_to_bf16_bits(p[e]));
-          lo[e] = p[e] - hi[e];
-        }
-        phi = bf16x8_of(hi);
-        plo = bf16x8_of(lo);
-      }
-#pragma unroll
-      for (int dd = 0; dd < ND; ++dd) {
-        acc[qb][dd] *= corr;
-        const bf16x8 A = __builtin_bit_cast(bf16x8, vop[dd]);
-        acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, phi, acc[qb][dd], 0, 0, 0);
-        acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, plo, acc[qb][dd], 0, 0, 0);
-      }
-    }
-  }
-
-  // this call's own keys, in FP32: the last split's first wave
-  if (split == a.splits - 1 && wave == 0) {
-    for (int jj = 0; jj < a.n_own; ++jj) {
-      const float* kr = a.k + (size_t(jj) * size_t(a.kv_heads) + size_t(kvh)) * D;
-      const float* vr = a.v + (size_t(jj) * size_t(a.kv_heads) + size_t(kvh)) * D;
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const int qc = qb * 16 + j;
-        const int hg = qlive[qb] ? qc % a.group : 0;
-        const float* qp = a.q + (size_t(qrow[qb]) * size_t(a.heads) + size_t(kvh * a.group + hg)) * D;
-        float dot = 0.f;
-        for (int e = 0; e < D / 4; ++e) dot += qp[g * (D / 4) + e] * kr[g * (D / 4) + e];
-        dot += __shfl_xor(dot, 16);
-        dot += __shfl_xor(dot, 32);
-        const int i = a.row0 + qrow[qb];   // the row's index in the call: it sees own keys jj <= i
-        const bool see = qlive[qb] && jj <= i && (a.window <= 0 || i - jj < a.window);
-        const float sc = see ? dot * a.scale : -INFINITY;
-        const float m_new = fmaxf(m[qb], sc);
-        const float corr = m[qb] == -INFINITY ? (m_new == -INFINITY ? 1.f : 0.f) : expf(m[qb] - m_new);
-        const float pw = see ? expf(sc - m_new) : 0.f;
-        l[qb] = l[qb] * corr + pw;
-        m[qb] = m_new;
-#pragma unroll
-        for (int dd = 0; dd < ND; ++dd) {
-          const float4 vv = *reinterpret_cast<const float4*>(vr + 16 * dd + 4 * g);
-          acc[qb][dd][0] = acc[qb][dd][0] * corr + pw * vv.x;
-          acc[qb][dd][1] = acc[qb][dd][1] * corr + pw * vv.y;
-          acc[qb][dd][2] = acc[qb][dd][2] * corr + pw * vv.z;
-          acc[qb][dd][3] = acc[qb][dd][3] * corr + pw * vv.w;
-        }
-      }
-    }
-  }
-
-  // merge the 4 waves' states in LDS: [wave][qb][2 + D][16 cols] ... laid out as ml: [wave][qb][2][16], then
-  // accumulators [wave][qb][dd][64 lanes][4]
+  // merge the 4 waves' states in LDS: (max, sum) as [wave][qb][2][16 cols], then accumulators
+  // [wave][qb][dd][64 lanes][4]
   float* ml = lds;
   float* accs = lds + kWaves * QB * 2 * 16;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     if (g == 0) {
-      ml[((wave * QB + qb) * 2 + 0) * 16 + j] = m[qb];
-      ml[((wave * QB + qb) * 2 + 1) * 16 + j] = l[qb];
+      ml[((wave * QB + qb) * 2 + 0) * 16 + j] = st.m[qb];
+      ml[((wave * QB + qb) * 2 + 1) * 16 + j] = st.l[qb];
     }
 #pragma unroll
     for (int dd = 0; dd < ND; ++dd)
-      *reinterpret_cast<f32x4*>(accs + ((size_t(wave * QB + qb) * ND + dd) * 64 + lane) * 4) = acc[qb][dd];
+      *reinterpret_cast<f32x4*>(accs + ((size_t(wave * QB + qb) * ND + dd) * 64 + lane) * 4) = st.acc[qb][dd];
   }
   __syncthreads();
-  // wave w finishes q-block w (and w + 4, ...): partial (max, sum, accumulator[D]) of each live q-col
+  // wave w finishes q-block w: the partial (max, sum, accumulator[D]) of each live q-col
   for (int qb = wave; qb < QB; qb += kWaves) {
     const int qc = qb * 16 + j;
     float M = -INFINITY;
@@ -320,69 +325,379 @@ __global__ void __launch_bounds__(kWaves * 64) attn_decode_kernel(const AttnKern
     float L = 0.f, f[kWaves];
     for (int w = 0; w < kWaves; ++w) {
       const float mw = ml[((w * QB + qb) * 2 + 0) * 16 + j];
-      f[w] = mw == -INFINITY ? 0.f : expf(mw - M);
+      f[w] = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
       L += f[w] * ml[((w * QB + qb) * 2 + 1) * 16 + j];
     }
     if (qc >= qcols) continue;
-    float* out = a.part + ((size_t(kvh) * a.splits + split) * size_t(QB * 16) + size_t(qc)) * (2 + D);
-    if (g == 0) {
-      out[0] = M;
-      out[1] = L;
-    }
+    const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(split)) * size_t(a.qpad) + size_t(qc);
+    if (g == 0) *reinterpret_cast<float2*>(a.ml + rec * 2) = make_float2(M, L);
     for (int dd = 0; dd < ND; ++dd) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < kWaves; ++w)
         s += f[w] * *reinterpret_cast<const f32x4*>(accs + ((size_t(w * QB + qb) * ND + dd) * 64 + lane) * 4);
-      *reinterpret_cast<f32x4*>(out + 2 + 16 * dd + 4 * g) = s;
+      *reinterpret_cast<f32x4*>(a.acc + rec * D + 16 * dd + 4 * g) = s;
     }
   }
 }
 
-// One work-group (D threads) per (row, q head): the splits' partials into out[row][head][:]
-// (engine/src/kv.cpp:262-285; a split with no visible key has max -inf and sum 0 and is skipped).
-__global__ void attn_merge_kernel(const float* __restrict__ part, float* __restrict__ out, int heads, int group,
-                                  int splits, int qcols_pad, int d) {
-  const int row = blockIdx.x / heads, h = blockIdx.x % heads, t = threadIdx.x;
-  const int kvh = h / group, qc = row * group + h % group;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s)
-    M = fmaxf(M, part[((size_t(kvh) * splits + s) * size_t(qcols_pad) + size_t(qc)) * (2 + d)]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float* p = part + ((size_t(kvh) * splits + s) * size_t(qcols_pad) + size_t(qc)) * (2 + d);
-    if (p[1] == 0.f || p[0] == -INFINITY) continue;
-    const float w = expf(p[0] - M);
-    L += w * p[1];
-    acc += w * p[2 + t];
+// --------------------------------------------------------------------------------------------------- own keys
+
+// The online-softmax state of one q-col over own keys j0 .. j1 - 1 (kv.cpp:214-243 with this call's FP32 rows),
+// held by one wave: lane l < D / 2 holds dims l and l + D / 2 of the q vector (qa, qb; zero in the other lanes)
+// and of the output (a0, a1); key / value rows at kb + j * stride, vb + j * stride. Keys go in batches of 8 whose
+// loads are all issued first (indices clamped into the rows, so no load sits behind a branch); scores are in the
+// base-2 domain (scale2 = scale * log2 e).
+template <int D>
+__device__ inline void own_state(float qa, float qb, const float* kb, const float* vb, size_t stride, int j0, int j1,
+                                 float scale2, float& M, float& L, float& a0, float& a1) {
+  const int l = (threadIdx.x & 63) & (D / 2 - 1);
+  for (int jb = j0; jb < j1; jb += 8) {
+    float k0[8], k1[8], v0[8], v1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t r = size_t(min(jb + u, j1 - 1)) * stride;
+      k0[u] = kb[r + l];
+      k1[u] = kb[r + l + D / 2];
+      v0[u] = vb[r + l];
+      v1[u] = vb[r + l + D / 2];
+    }
+    float s[8], bm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      s[u] = wave_sum(qa * k0[u] + qb * k1[u]) * scale2;
+      if (jb + u < j1) bm = fmaxf(bm, s[u]);
+    }
+    const float mn = fmaxf(M, bm);   // finite: the batch holds at least one key
+    const float corr = exp2_fast(M - mn);
+    L *= corr;
+    a0 *= corr;
+    a1 *= corr;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float w = jb + u < j1 ? exp2_fast(s[u] - mn) : 0.f;
+      L += w;
+      a0 += w * v0[u];
+      a1 += w * v1[u];
+    }
+    M = mn;
   }
-  out[(size_t(row) * heads + h) * d + t] = L > 0.f ? acc / L : 0.f;
 }
 
-namespace {
-using AttnFn = void (*)(const AttnKernelArgs);
-AttnFn attn_fn(int d, int qb) {
-#define XTG_CASE(D, Q) \
-  if (d == D && qb == Q) return attn_decode_kernel<D, Q>;
-  XTG_CASE(64, 1) XTG_CASE(64, 2) XTG_CASE(64, 3) XTG_CASE(64, 4)
-  XTG_CASE(128, 1) XTG_CASE(128, 2) XTG_CASE(128, 3) XTG_CASE(128, 4)
-#undef XTG_CASE
-  return nullptr;
+__device__ inline void write_partial(float* acc, float* ml, size_t rec, int d, float M, float L, float a0, float a1) {
+  const int l = threadIdx.x & 63;
+  if (l == 0) *reinterpret_cast<float2*>(ml + rec * 2) = make_float2(M, L);
+  if (l < d / 2) {
+    acc[rec * d + l] = a0;
+    acc[rec * d + l + d / 2] = a1;
+  }
 }
-}  // namespace
 
-size_t attn_part_floats(int kv_heads, int splits, int qcols_pad, int d) {
-  return size_t(kv_heads) * size_t(splits) * size_t(qcols_pad) * size_t(2 + d);
+// One work-group per KV head for one block of query rows: wave w takes q-cols w, w + 4, ...
+template <int D>
+__global__ void __launch_bounds__(kWaves * 64) attn_own_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                               const float* __restrict__ v, int n_rows, int row0,
+                                                               int n_own, int heads, int kv_heads, int group,
+                                                               int window, float scale, float* __restrict__ acc,
+                                                               float* __restrict__ ml, int splits, int splits1,
+                                                               int qpad) {
+  const int kvh = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int c = wave; c < n_rows * group; c += kWaves) {
+    const int r = c / group, hg = c % group, i = row0 + r;
+    const float* qp = q + (size_t(r) * size_t(heads) + size_t(kvh * group + hg)) * D;
+    const int l = lane & (D / 2 - 1);
+    const float qa = lane < D / 2 ? qp[l] : 0.f, qb = lane < D / 2 ? qp[l + D / 2] : 0.f;
+    const int j0 = window > 0 ? max(0, i - window + 1) : 0, j1 = min(i + 1, n_own);
+    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+    own_state<D>(qa, qb, k + size_t(kvh) * D, v + size_t(kvh) * D, size_t(kv_heads) * D, j0, j1, scale * kLog2e, M,
+                 L, a0, a1);
+    write_partial(acc, ml, (size_t(kvh) * size_t(splits1) + size_t(splits)) * size_t(qpad) + size_t(c), D, M, L, a0,
+                  a1);
+  }
 }
+
+// -------------------------------------------------------------------------------------------------- producer
+
+constexpr int kProdRows = 8, kProdGroup = 8;
+constexpr int kProdVecs = (kProdRows * (kProdGroup + 1) + kWaves - 1) / kWaves;   // vectors per wave, at most
+
+struct ProduceArgs {
+  float* q;                // [m][heads][d], processed in place
+  float* k;                // [m][kv_heads][d], processed in place
+  const float* v;
+  int m, heads, kv_heads, group, window, rpb, splits, splits1, qpad, store;
+  long long pos0;
+  float scale;
+  const float* inv_freq;   // [d / 2]
+  const float* qscale;     // [heads * d] or NULL
+  uint16_t* ck;
+  uint16_t* cv;
+  int* slot_pos;
+  long long slots;
+  int ring, slots_pad;
+  float* acc;              // partials of the whole call
+  float* ml;
+  size_t blk_records;      // records per row block
+};
+
+// One work-group per KV head: RoPE + justnorm of its q heads and its k row for every row of the call, v copied,
+// the processed rows kept in LDS; then the own-key partial of every q-col.
+template <int D>
+__global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceArgs a) {
+  constexpr int HALF = D / 2;
+  __shared__ float sq[kProdRows * kProdGroup * D], sk[kProdRows * D], sv[kProdRows * D];
+  __shared__ float scos[kProdRows * HALF], ssin[kProdRows * HALF];
+  const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool on = lane < HALF;
+  const int nq = a.m * a.group, nv = nq + a.m;
+
+  // every load first, each at an index clamped into its buffer (no load behind a branch): the wave's q / k pairs
+  // (lane l: dims l, l + d/2), their q scales, the rows' inverse frequencies and v
+  const int l = lane & (HALF - 1);
+  float x1[kProdVecs], x2[kProdVecs], s1[kProdVecs], s2[kProdVecs];
+#pragma unroll
+  for (int it = 0; it < kProdVecs; ++it) {
+    const int idx = min(wave + it * kWaves, nv - 1);
+    const bool is_q = idx < nq;
+    const int h = kvh * a.group + (is_q ? idx % a.group : 0);
+    const float* p = is_q ? a.q + (size_t(idx / a.group) * size_t(a.heads) + size_t(h)) * D
+                          : a.k + (size_t(idx - nq) * size_t(a.kv_heads) + size_t(kvh)) * D;
+    x1[it] = p[l];
+    x2[it] = p[l + HALF];
+    s1[it] = s2[it] = 1.f;
+    if (a.qscale && is_q) {
+      s1[it] = a.qscale[size_t(h) * D + l];
+      s2[it] = a.qscale[size_t(h) * D + l + HALF];
+    }
+  }
+  constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
+  constexpr int kVals = (kProdRows * D + kWaves * 64 - 1) / (kWaves * 64);
+  float fr[kAngles], vv[kVals];
+#pragma unroll
+  for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[min(tid + u * kWaves * 64, a.m * HALF - 1) % HALF];
+#pragma unroll
+  for (int u = 0; u < kVals; ++u) {
+    const int e = min(tid + u * kWaves * 64, a.m * D - 1);
+    vv[u] = a.v[(size_t(e / D) * size_t(a.kv_heads) + size_t(kvh)) * D + size_t(e % D)];
+  }
+  // the rows' rotation angles FP32(pos0 + r) * inv_freq[i] (engine/src/kernels.cpp:203-222), v into LDS and
+  // the cache
+#pragma unroll
+  for (int u = 0; u < kAngles; ++u) {
+    const int e = tid + u * kWaves * 64;
+    if (e < a.m * HALF) {
+      const float ang = float(a.pos0 + e / HALF) * fr[u];
+      scos[e] = cosf(ang);
+      ssin[e] = sinf(ang);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kVals; ++u) {
+    const int e = tid + u * kWaves * 64;
+    if (e < a.m * D) {
+      sv[e] = vv[u];
+      if (a.store) {
+        const long long p = a.pos0 + e / D;
+        const int slot = int(a.ring ? p % a.slots : p);
+        a.cv[v_index(kvh, slot, e % D, a.slots_pad, D)] = f32_to_bf16_bits(vv[u]);
+      }
+    }
+  }
+  if (a.store && kvh == 0 && tid < a.m) {
+    const long long p = a.pos0 + tid;
+    a.slot_pos[a.ring ? p % a.slots : p] = int(p);
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int it = 0; it < kProdVecs; ++it) {
+    const int idx = wave + it * kWaves;
+    if (idx >= nv) break;   // uniform over the wave
+    const int r = idx < nq ? idx / a.group : idx - nq;
+    float o1 = 0.f, o2 = 0.f;
+    if (on) {
+      const float c = scos[r * HALF + lane], s = ssin[r * HALF + lane];
+      o1 = x1[it] * c - x2[it] * s;
+      o2 = x2[it] * c + x1[it] * s;
+    }
+    const float f = inv_norm_of(wave_sum(o1 * o1 + o2 * o2));
+    o1 *= f;
+    o2 *= f;
+    if (on && idx < nq) {   // q: times qscale, back in place and into LDS
+      o1 *= s1[it];
+      o2 *= s2[it];
+      float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + idx % a.group)) * D;
+      p[lane] = o1;
+      p[lane + HALF] = o2;
+      sq[idx * D + lane] = o1;
+      sq[idx * D + lane + HALF] = o2;
+    } else if (on) {   // k: back in place (a store after the scan reads it there) and into LDS
+      float* p = a.k + (size_t(r) * size_t(a.kv_heads) + size_t(kvh)) * D;
+      p[lane] = o1;
+      p[lane + HALF] = o2;
+      sk[r * D + lane] = o1;
+      sk[r * D + lane + HALF] = o2;
+      if (a.store) {
+        const long long p = a.pos0 + r;
+        const int slot = int(a.ring ? p % a.slots : p);
+        a.ck[k_index(kvh, slot, lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
+        a.ck[k_index(kvh, slot, lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
+      }
+    }
+  }
+  __syncthreads();
+
+  // own keys: q-col c = r * group + hg of row r sees keys j <= r within the window
+  for (int c = wave; c < nq; c += kWaves) {
+    const int r = c / a.group, hg = c % a.group;
+    const float qa = on ? sq[c * D + l] : 0.f, qb = on ? sq[c * D + l + HALF] : 0.f;
+    const int j0 = a.window > 0 ? max(0, r - a.window + 1) : 0;
+    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+    own_state<D>(qa, qb, sk, sv, D, j0, r + 1, a.scale * kLog2e, M, L, a0, a1);
+    const int blk = r / a.rpb, qc = (r % a.rpb) * a.group + hg;
+    const size_t rec = size_t(blk) * a.blk_records + (size_t(kvh) * size_t(a.splits1) + size_t(a.splits)) * size_t(a.qpad) +
+                       size_t(qc);
+    write_partial(a.acc, a.ml, rec, D, M, L, a0, a1);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------ merge
+
+constexpr int kMergeThreads = 512;
+
+// The merged output of one q-col for 8 dims dd .. dd + 7 over its S1 records rec0 + s * qpad (kv.cpp:262-285:
+// splits with a zero sum are skipped, weights 2^(m_s - max) with the maxima in base-2 units, the sum's reciprocal
+// applied last). The running
+// maximum is updated once per batch of B records, whose loads are all in flight together.
+template <int D, int B>
+__device__ inline void merge8(const float* __restrict__ acc, const float* __restrict__ ml, size_t rec0, int qpad,
+                              int S1, int dd, float out[8]) {
+  float M = -INFINITY, L = 0.f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.f;
+  for (int s0 = 0; s0 < S1; s0 += B) {
+    float2 w2[B];
+    float4 x0[B], x1[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      w2[u] = make_float2(-INFINITY, 0.f);
+      x0[u] = x1[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (s0 + u < S1) {
+        const size_t rec = rec0 + size_t(s0 + u) * size_t(qpad);
+        w2[u] = *reinterpret_cast<const float2*>(ml + rec * 2);
+        x0[u] = *reinterpret_cast<const float4*>(acc + rec * D + dd);
+        x1[u] = *reinterpret_cast<const float4*>(acc + rec * D + dd + 4);
+      }
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (w2[u].y != 0.f) bm = fmaxf(bm, w2[u].x);
+    const float mn = fmaxf(M, bm);
+    if (mn == -INFINITY) continue;
+    const float corr = exp2_fast(M - mn);   // M = -inf: 0
+    L *= corr;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= corr;
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (w2[u].y != 0.f) {
+        const float w = exp2_fast(w2[u].x - mn);
+        L += w * w2[u].y;
+        o[0] += w * x0[u].x, o[1] += w * x0[u].y, o[2] += w * x0[u].z, o[3] += w * x0[u].w;
+        o[4] += w * x1[u].x, o[5] += w * x1[u].y, o[6] += w * x1[u].z, o[7] += w * x1[u].w;
+      }
+    M = mn;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = o[e] * inv;
+}
+
+struct MergeArgs {
+  const float* acc;
+  const float* ml;
+  int heads, group, rpb, kv_heads, splits1, qpad;
+};
+
+// Chunk c (dims 8c .. 8c + 7 of the row's heads * D outputs) of query row `row`.
+template <int D, int B>
+__device__ inline void merge_chunk(const MergeArgs& a, int row, int c, float out[8]) {
+  const int e0 = 8 * c, h = e0 / D, dd = e0 % D;
+  const int blk = row / a.rpb, qc = (row % a.rpb) * a.group + h % a.group;
+  const size_t rec0 = ((size_t(blk) * size_t(a.kv_heads) + size_t(h / a.group)) * size_t(a.splits1)) * size_t(a.qpad) +
+                      size_t(qc);
+  merge8<D, B>(a.acc, a.ml, rec0, a.qpad, a.splits1, dd, out);
+}
+
+// One work-group per query row: out[row][heads][D].
+template <int D>
+__global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(const MergeArgs a, float* __restrict__ out) {
+  const int row = blockIdx.x, Q = a.heads * D;
+  for (int c = threadIdx.x; c < Q / 8; c += kMergeThreads) {
+    float o[8];
+    merge_chunk<D, 12>(a, row, c, o);
+    float* p = out + size_t(row) * Q + 8 * c;
+    *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+// One work-group per row of the decode step: merge, a * sigmoid(g * gs), justnorm over the row (dory.cpp:509-515),
+// then the FP32 row (out, optional) and the o-projection's operand (optional).
+template <int D, int U>
+__global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArgs a, const float* __restrict__ g,
+                                                                   const float* __restrict__ gs, int vec,
+                                                                   float* __restrict__ out, f16x8* __restrict__ xop,
+                                                                   float* __restrict__ xinv) {
+  __shared__ float red[2 * kMergeThreads / 64];
+  const int row = blockIdx.x, Q = a.heads * D;
+  float gv[U][8], sv[U][8], t[U][8];
+  load_row<kMergeThreads, U>(g + size_t(row) * Q, Q, vec, gv);
+  load_row<kMergeThreads, U>(gs, Q, vec, sv);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = int(threadIdx.x) + u * kMergeThreads;
+    if (8 * c < Q) {
+      merge_chunk<D, (U == 1 ? 12 : 16 / (2 * U))>(a, row, c, t[u]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[u][e] = 0.f;
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      t[u][e] = t[u][e] * (1.f / (1.f + expf(-gv[u][e] * sv[u][e])));
+      s += t[u][e] * t[u][e];
+    }
+  const float f = inv_norm_of(block_sum<kMergeThreads>(s, red));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[u][e] *= f;
+  if (out) store_row<kMergeThreads, U>(out + size_t(row) * Q, Q, vec, t);
+  if (xop) emit_operand<kMergeThreads, U>(t, Q, row, xop, xinv, red);
+}
+
+// ------------------------------------------------------------------------------------------------------- plan
 
 AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window) {
   XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "attention: head_dim %d (64 or 128)", c.head_dim);
   XTG_CHECK(heads % c.kv_heads == 0, "attention: %d heads over %d KV heads", heads, c.kv_heads);
   const int group = heads / c.kv_heads;
   XTG_CHECK(group <= 8, "attention: %d query heads per KV head (at most 8)", group);
-  XTG_CHECK(n_q >= 1 && n_q * group <= 64, "attention: %d rows x %d heads per KV head (at most 64 columns)", n_q, group);
+  XTG_CHECK(n_q >= 1, "attention: %d query rows", n_q);
+  XTG_CHECK(pos0 >= 0 && pos0 + n_q < (1LL << 31), "attention: positions %lld + %d beyond the 32-bit slot positions",
+            pos0, n_q);
   AttnPlan p;
   p.group = group;
-  p.qb = (n_q * group + 15) / 16;
+  p.kv_heads = c.kv_heads;
+  p.d = c.head_dim;
+  p.rpb = std::max(1, 32 / group);
+  p.blocks = (n_q + p.rpb - 1) / p.rpb;
+  p.qpad = (std::min(n_q, p.rpb) * group + 15) / 16 * 16;
   if (c.ring) {   // any slot may hold a visible position: scan the whole ring
     p.tile_lo = 0;
     p.tiles = c.slots_pad / kTile;
@@ -393,74 +708,204 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
     p.tile_lo = int(lo / kTile);
     p.tiles = hi > lo ? int((hi + kTile - 1) / kTile - lo / kTile) : 0;
   }
-  // about 512 work-groups over the KV heads, at least one tile per wave where there is work
-  const int want = std::max(1, 512 / c.kv_heads);
-  p.splits = std::max(1, std::min(want, (p.tiles + kWaves - 1) / kWaves));
-  p.splits = std::min(p.splits, 128);
+  // about 256 work-groups over the KV heads (one per CU), at least two tiles per wave, at most one split per tile
+  // (XTG_ATTN_SPLITS=n fixes the count, for experiments)
+  if (p.tiles > 0) {
+    const int want = std::max(1, 256 / c.kv_heads);
+    p.splits = std::max(1, std::min(want, (p.tiles + 2 * kWaves - 1) / (2 * kWaves)));
+    if (const char* env = std::getenv("XTG_ATTN_SPLITS")) p.splits = std::max(1, std::atoi(env));
+    p.splits = std::min(p.splits, p.tiles);
+  } else {
+    p.splits = 0;
+  }
   return p;
 }
 
-int attn_rows_per_block(int group) { return std::max(1, 32 / group); }
+// ------------------------------------------------------------------------------------------------- launchers
 
-size_t attn_part_floats_max(const DevKv& c, int n_q, int heads, long long pos0, int window) {
-  const int rows = std::min(n_q, attn_rows_per_block(heads / c.kv_heads));
-  const AttnPlan p = attn_plan(c, rows, heads, pos0, window);
-  return attn_part_floats(c.kv_heads, p.splits, p.qb * 16, c.head_dim);
+namespace {
+
+using ScanFn = void (*)(const ScanArgs);
+ScanFn scan_fn(int d, int qb) {
+#define XTG_CASE(D, Q) \
+  if (d == D && qb == Q) return attn_scan_kernel<D, Q>;
+  XTG_CASE(64, 1) XTG_CASE(64, 2) XTG_CASE(128, 1) XTG_CASE(128, 2)
+#undef XTG_CASE
+  return nullptr;
 }
 
-std::string launch_attn_decode(const DevKv& c, const AttnPlan& p, const float* q, const float* k, const float* v,
-                               int n_rows, int row0, int n_own, int heads, long long pos0, int window, float scale,
-                               float* part, hipStream_t stream) {
-  AttnKernelArgs a{};
-  a.q = q;
-  a.k = k;
-  a.v = v;
+// The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks (gfx950
+// has 160 KiB per CU): raise the kernel's limit once.
+void allow_lds(ScanFn fn, size_t lds) {
+  if (lds <= 65536) return;
+  static thread_local ScanFn raised[4] = {};
+  for (ScanFn f : raised)
+    if (f == fn) return;
+  HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(lds)));
+  for (ScanFn& f : raised)
+    if (!f) {
+      f = fn;
+      return;
+    }
+}
+
+size_t blk_records(const AttnPlan& p) { return size_t(p.kv_heads) * size_t(p.splits + 1) * size_t(p.qpad); }
+float* part_acc(const AttnPlan& p, float* part, int b) { return part + size_t(b) * blk_records(p) * size_t(p.d); }
+float* part_ml(const AttnPlan& p, float* part, int b) {
+  return part + p.records() * size_t(p.d) + size_t(b) * blk_records(p) * 2;
+}
+
+MergeArgs merge_args(const AttnPlan& p, int heads, const float* part) {
+  MergeArgs a;
+  a.acc = part;
+  a.ml = part + p.records() * size_t(p.d);
+  a.heads = heads;
+  a.group = p.group;
+  a.rpb = p.rpb;
+  a.kv_heads = p.kv_heads;
+  a.splits1 = p.splits + 1;
+  a.qpad = p.qpad;
+  return a;
+}
+
+int block_rows(const AttnPlan& p, int n_q, int b) {
+  XTG_CHECK(b >= 0 && b < p.blocks, "attention: block %d of %d", b, p.blocks);
+  return std::min(p.rpb, n_q - b * p.rpb);
+}
+
+}  // namespace
+
+std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const float* q, int n_q, int heads,
+                             long long pos0, int window, float scale, float* part, hipStream_t stream) {
+  XTG_CHECK(p.splits >= 1 && p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
+  const int nr = block_rows(p, n_q, b);
+  ScanArgs a{};
+  a.q = q + size_t(b) * size_t(p.rpb) * size_t(heads) * size_t(p.d);
   a.ck = reinterpret_cast<const uint4*>(c.k);
   a.cv = reinterpret_cast<const uint4*>(c.v);
   a.slot_pos = c.slot_pos;
-  a.part = part;
-  a.n_rows = n_rows;
-  a.row0 = row0;
-  a.n_own = n_own;
+  a.acc = part_acc(p, part, b);
+  a.ml = part_ml(p, part, b);
+  a.n_rows = nr;
+  a.row0 = b * p.rpb;
+  a.heads = heads;
+  a.group = p.group;
+  a.window = window;
+  a.splits = p.splits;
+  a.splits1 = p.splits + 1;
+  a.qpad = p.qpad;
+  a.slots_pad = c.slots_pad;
+  a.tile_lo = p.tile_lo;
+  a.tiles = p.tiles;
+  a.pos0 = int(pos0);
+  a.scale2 = scale * kLog2e;
+  const int qb = (nr * p.group + 15) / 16;
+  ScanFn fn = scan_fn(c.head_dim, qb);
+  XTG_CHECK(fn != nullptr, "attention: no kernel for head_dim %d and %d column blocks", c.head_dim, qb);
+  const int nd = c.head_dim / 16;
+  const size_t lds = (size_t(kWaves) * qb * 2 * 16 + size_t(kWaves) * qb * nd * 64 * 4) * sizeof(float);
+  allow_lds(fn, lds);
+  hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits)), dim3(kWaves * 64), lds, stream, a);
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_scan_kernel<%d, %d>", c.head_dim, qb);
+}
+
+std::string launch_attn_own(const AttnPlan& p, int b, const float* q, const float* k, const float* v, int n_q,
+                            int heads, int window, float scale, float* part, hipStream_t stream) {
+  const int nr = block_rows(p, n_q, b);
+  const float* qb = q + size_t(b) * size_t(p.rpb) * size_t(heads) * size_t(p.d);
+  float* acc = part_acc(p, part, b);
+  float* ml = part_ml(p, part, b);
+  const dim3 grid{unsigned(p.kv_heads)}, block{unsigned(kWaves * 64)};
+  if (p.d == 64)
+    hipLaunchKernelGGL(attn_own_kernel<64>, grid, block, 0, stream, qb, k, v, nr, b * p.rpb, n_q, heads, p.kv_heads,
+                       p.group, window, scale, acc, ml, p.splits, p.splits + 1, p.qpad);
+  else
+    hipLaunchKernelGGL(attn_own_kernel<128>, grid, block, 0, stream, qb, k, v, nr, b * p.rpb, n_q, heads, p.kv_heads,
+                       p.group, window, scale, acc, ml, p.splits, p.splits + 1, p.qpad);
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_own_kernel<%d>", p.d);
+}
+
+std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
+                              hipStream_t stream) {
+  const MergeArgs a = merge_args(p, heads, part);
+  if (p.d == 64)
+    hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(unsigned(n_q)), dim3(kMergeThreads), 0, stream, a, out);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(unsigned(n_q)), dim3(kMergeThreads), 0, stream, a, out);
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_merge_kernel<%d>", p.d);
+}
+
+std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float* k, const float* v, int m,
+                              int heads, long long pos0, int window, float scale, const float* inv_freq,
+                              const float* qscale, bool store, float* part, hipStream_t stream) {
+  XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
+  XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
+  XTG_CHECK(!store || !c.ring || c.slots >= m, "producer: %d rows into a %lld-slot ring", m, c.slots);
+  ProduceArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.m = m;
   a.heads = heads;
   a.kv_heads = c.kv_heads;
   a.group = p.group;
   a.window = window;
+  a.rpb = p.rpb;
   a.splits = p.splits;
-  a.slots_pad = c.slots_pad;
-  a.tile_lo = p.tile_lo;
-  a.tiles = p.tiles;
+  a.splits1 = p.splits + 1;
+  a.qpad = p.qpad;
+  a.store = store ? 1 : 0;
   a.pos0 = pos0;
   a.scale = scale;
-  AttnFn fn = attn_fn(c.head_dim, p.qb);
-  XTG_CHECK(fn != nullptr, "attention: no kernel for head_dim %d and %d column blocks", c.head_dim, p.qb);
-  const int nd = c.head_dim / 16;
-  const size_t lds = (size_t(kWaves) * p.qb * 2 * 16 + size_t(kWaves) * p.qb * nd * 64 * 4) * sizeof(float);
-  if (lds > 65536) {   // the wave merge needs more than the default 64 KiB of LDS (gfx950 has 160 KiB)
-    static thread_local AttnFn raised[8] = {};
-    bool done = false;
-    for (AttnFn f : raised) done |= f == fn;
-    if (!done) {
-      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    int(lds)));
-      for (AttnFn& f : raised)
-        if (!f) {
-          f = fn;
-          break;
-        }
-    }
-  }
-  hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits)), dim3(kWaves * 64), lds, stream, a);
+  a.inv_freq = inv_freq;
+  a.qscale = qscale;
+  a.ck = c.k;
+  a.cv = c.v;
+  a.slot_pos = c.slot_pos;
+  a.slots = c.slots;
+  a.ring = c.ring ? 1 : 0;
+  a.slots_pad = c.slots_pad;
+  a.acc = part;
+  a.ml = part + p.records() * size_t(p.d);
+  a.blk_records = blk_records(p);
+  if (c.head_dim == 64)
+    hipLaunchKernelGGL(qk_produce_kernel<64>, dim3(unsigned(c.kv_heads)), dim3(kWaves * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL(qk_produce_kernel<128>, dim3(unsigned(c.kv_heads)), dim3(kWaves * 64), 0, stream, a);
   HIP_CHECK(hipGetLastError());
-  return strf("attn_decode_kernel<%d, %d>", c.head_dim, p.qb);
+  return strf("qk_produce_kernel<%d>", c.head_dim);
 }
 
-std::string launch_attn_merge(const DevKv& c, const AttnPlan& p, int n_rows, int heads, const float* part, float* out,
-                              hipStream_t stream) {
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(unsigned(n_rows * heads)), dim3(unsigned(c.head_dim)), 0, stream, part,
-                     out, heads, p.group, p.splits, p.qb * 16, c.head_dim);
+std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,
+                             float* out, void* op, hipStream_t stream) {
+  const MergeArgs a = merge_args(p, heads, part);
+  const int Q = heads * p.d;
+  f16x8* xop = nullptr;
+  float* xinv = nullptr;
+  if (op) {
+    XTG_CHECK(m <= kMaxRows, "attention gate: %d rows for an operand", m);
+    xop = static_cast<f16x8*>(op);
+    xinv = reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(Q));
+  }
+  auto al = [](const void* x) { return !x || reinterpret_cast<uintptr_t>(x) % 16 == 0; };
+  const int vec = al(g) && al(gs) && al(out) ? 1 : 0;
+  const int chunks = Q / 8;
+  const dim3 grid{unsigned(m)}, block{unsigned(kMergeThreads)};
+  int u = 0;
+#define XTG_GATE(D, U)                                                                                      \
+  if (p.d == D && chunks <= U * kMergeThreads && !u) {                                                      \
+    hipLaunchKernelGGL((attn_gate_kernel<D, U>), grid, block, 0, stream, a, g, gs, vec, out, xop, xinv);    \
+    u = U;                                                                                                  \
+  }
+  XTG_GATE(64, 1) XTG_GATE(64, 2) XTG_GATE(64, 4) XTG_GATE(128, 1) XTG_GATE(128, 2) XTG_GATE(128, 4)
+#undef XTG_GATE
+  XTG_CHECK(u != 0, "attention gate: %d heads of %d", heads, p.d);
   HIP_CHECK(hipGetLastError());
-  return "attn_merge_kernel";
+  return strf("attn_gate_kernel<%d, %d>", p.d, u);
 }
 
 }  // namespace xtg::hip

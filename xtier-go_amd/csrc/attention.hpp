@@ -29,23 +29,42 @@ size_t kv_v_index(int h, int slot, int dim, int slots_pad, int d);
 // `slots` rows.
 void launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const float* v, hipStream_t stream);
 
+// How one attention call (n_q query rows at pos0) is cut up. Query rows go in blocks of rpb rows (at most 32
+// (row, head) columns per KV head); each block's key tiles go to `splits` work-groups per KV head, plus one more
+// partial per (block, KV head) for this call's own keys. Partials: acc [blocks][kv_heads][splits + 1][qpad][d]
+// then (max, sum) [blocks][kv_heads][splits + 1][qpad][2]; q-col (row r of the block, head g of the group) is
+// r * group + g.
 struct AttnPlan {
-  int group = 1, qb = 1;         // q heads per KV head; 16-column blocks of (row, head) pairs
-  int tile_lo = 0, tiles = 0;    // the 32-slot tiles to scan
-  int splits = 1;                // work-groups per KV head
+  int group = 1;               // q heads per KV head
+  int rpb = 1, blocks = 1;     // rows per block, blocks
+  int qpad = 16;               // q-cols per block, padded to 16
+  int tile_lo = 0, tiles = 0;  // the 32-slot tiles to scan
+  int splits = 0;              // work-groups per KV head over the tiles (0: no cached key is visible)
+  int kv_heads = 1, d = 64;
+  size_t records() const { return size_t(blocks) * size_t(kv_heads) * size_t(splits + 1) * size_t(qpad); }
+  size_t part_floats() const { return records() * size_t(d + 2); }
 };
-AttnPlan attn_plan(const DevKv& c, int n_rows, int heads, long long pos0, int window);
-size_t attn_part_floats(int kv_heads, int splits, int qcols_pad, int d);
-// Query rows per launch (at most 32 (row, head) columns per KV head) and the partial buffer a call needs.
-int attn_rows_per_block(int group);
-size_t attn_part_floats_max(const DevKv& c, int n_q, int heads, long long pos0, int window);
-// One block of n_rows <= attn_rows_per_block query rows (rows row0 .. row0 + n_rows - 1 of a call with n_own new
-// rows; device q / k / v as xtg::AttnArgs, engine/include/xtg/kv.h:67-78): the split partials into part, then
-// their merge into out (the block's rows). Launchers return the kernel name.
-std::string launch_attn_decode(const DevKv& c, const AttnPlan& p, const float* q, const float* k, const float* v,
-                               int n_rows, int row0, int n_own, int heads, long long pos0, int window, float scale,
-                               float* part, hipStream_t stream);
-std::string launch_attn_merge(const DevKv& c, const AttnPlan& p, int n_rows, int heads, const float* part, float* out,
+AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window);
+
+// Per block b (rows b * rpb .. of the call; device q / k / v as xtg::AttnArgs, engine/include/xtg/kv.h:67-78):
+// the own-key partials and the split partials. Then the merge of every row into out [n_q][heads][d].
+std::string launch_attn_own(const AttnPlan& p, int b, const float* q, const float* k, const float* v, int n_q,
+                            int heads, int window, float scale, float* part, hipStream_t stream);
+std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const float* q, int n_q, int heads,
+                             long long pos0, int window, float scale, float* part, hipStream_t stream);
+std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
                               hipStream_t stream);
+
+// The decode step's producer (packs/dory/dory.cpp:482-490 and the cache store of :507): in one launch per
+// call (m <= 8 rows), RoPE + justnorm of q and k (q *= qscale; both written back in place), the own-key partials
+// from the FP32 rows, and -- when store is set -- k, v stored into the cache. Storing before the scan is exact
+// when no key the scan should see is overwritten: a linear cache, or a ring of at least window + m - 1 slots.
+std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float* k, const float* v, int m,
+                              int heads, long long pos0, int window, float scale, const float* inv_freq,
+                              const float* qscale, bool store, float* part, hipStream_t stream);
+// The decode step's finish (dory.cpp:509-515): every row's merge, times sigmoid(g * gscale), justnorm over the
+// heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).
+std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,
+                             float* out, void* op, hipStream_t stream);
 
 }  // namespace xtg::hip

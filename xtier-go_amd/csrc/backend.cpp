@@ -254,22 +254,48 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
   XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "attention: unknown cache");
   XTG_CHECK(n_q >= 1 && pos0 >= 0, "attention: %d rows at %lld", n_q, pos0);
   XTG_CHECK(q && k && v && out, "attention: NULL argument");
-  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v)})
-    XTG_CHECK(reinterpret_cast<uintptr_t>(p) % 16 == 0, "attention: inputs must be 16-byte aligned");
-  ensure(part_, part_size_, attn_part_floats_max(*c, n_q, heads, pos0, window) * sizeof(float));
-  const int d = c->head_dim, rows = attn_rows_per_block(heads / c->kv_heads);
-  for (int r0 = 0; r0 < n_q; r0 += rows) {
-    const int nr = std::min(rows, n_q - r0);
-    const AttnPlan p = attn_plan(*c, nr, heads, pos0, window);
-    XTG_CHECK(attn_part_floats(c->kv_heads, p.splits, p.qb * 16, d) * sizeof(float) <= part_size_,
-              "attention: partial buffer too small");
-    const size_t off = size_t(r0) * size_t(heads) * size_t(d);
-    timed([&] {
-      return launch_attn_decode(*c, p, q + off, k, v, nr, r0, n_q, heads, pos0, window, scale,
-                                static_cast<float*>(part_), stream_);
-    });
-    timed([&] { return launch_attn_merge(*c, p, nr, heads, static_cast<const float*>(part_), out + off, stream_); });
+  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
+                        static_cast<const void*>(out)})
+    XTG_CHECK(reinterpret_cast<uintptr_t>(p) % 16 == 0, "attention: arguments must be 16-byte aligned");
+  const AttnPlan p = attn_plan(*c, n_q, heads, pos0, window);
+  ensure(part_, part_size_, p.part_floats() * sizeof(float));
+  float* part = static_cast<float*>(part_);
+  for (int b = 0; b < p.blocks; ++b) {
+    timed([&] { return launch_attn_own(p, b, q, k, v, n_q, heads, window, scale, part, stream_); });
+    if (p.splits > 0)
+      timed([&] { return launch_attn_scan(*c, p, b, q, n_q, heads, pos0, window, scale, part, stream_); });
   }
+  timed([&] { return launch_attn_merge(p, n_q, heads, part, out, stream_); });
+}
+
+void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
+                        float* k, const float* v, const float* qscale, const float* g, const float* gscale,
+                        float* out, void* op) {
+  XTG_CHECK(kvs_.count(c), "attention step: unknown cache");
+  XTG_CHECK(m >= 1 && pos0 >= 0, "attention step: %d rows at %lld", m, pos0);
+  XTG_CHECK(pos0 + m < (1LL << 31), "attention step: position %lld beyond the 32-bit slot positions", pos0 + m);
+  XTG_CHECK(c->ring || pos0 + m <= c->slots, "attention step: context full (%lld + %d > %lld slots)", pos0, m,
+            c->slots);
+  XTG_CHECK(q && k && v && g && gscale, "attention step: NULL argument");
+  const AttnPlan p = attn_plan(*c, m, heads, pos0, window);
+  ensure(part_, part_size_, p.part_floats() * sizeof(float));
+  float* part = static_cast<float*>(part_);
+  const float* f = inv_freq(theta, c->head_dim);
+  // storing before the scan hides nothing the scan should see: a linear cache's new slots are masked as
+  // positions >= pos0, and a ring of window + m - 1 slots or more only drops positions outside every row's window
+  const bool store_first = !c->ring || (window > 0 && c->slots >= (long long)window + m - 1);
+  timed([&] {
+    return launch_qk_produce(*c, p, q, k, v, m, heads, pos0, window, scale, f, qscale, store_first, part, stream_);
+  });
+  if (p.splits > 0)
+    for (int b = 0; b < p.blocks; ++b)
+      timed([&] { return launch_attn_scan(*c, p, b, q, m, heads, pos0, window, scale, part, stream_); });
+  if (!store_first)
+    timed([&] {
+      launch_kv_store(*c, pos0, m, k, v, stream_);
+      return std::string("kv_store_kernel");
+    });
+  timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
 
 // ---------------------------------------------------------------------------------------------- row kernels
@@ -294,24 +320,25 @@ void Backend::qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, i
   timed([&] { return launch_qk_rope_norm(q, k, m, heads, kv_heads, d, pos0, f, qscale, stream_); });
 }
 
-void Backend::slerp_norm(float* x, const float* o, const float* lr, int rows, int w) {
+void Backend::slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op) {
   XTG_CHECK(x && o && lr && rows >= 1 && w >= 1, "slerp: bad arguments");
-  timed([&] { return launch_slerp_norm(x, o, lr, rows, w, stream_); });
+  timed([&] { return launch_slerp_norm(x, o, lr, rows, w, op, stream_); });
 }
 
-void Backend::swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w) {
+void Backend::swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
+                          float* out, void* op) {
   XTG_CHECK(g && u && sg && su && rows >= 1 && w >= 1, "swiglu: bad arguments");
-  timed([&] { return launch_swiglu_norm(g, u, sg, su, rows, w, stream_); });
+  timed([&] { return launch_swiglu_norm(g, u, sg, su, rows, w, out, op, stream_); });
 }
 
-void Backend::gate_norm(float* a, const float* gate, const float* gs, int rows, int w) {
+void Backend::gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op) {
   XTG_CHECK(a && gate && gs && rows >= 1 && w >= 1, "gate_norm: bad arguments");
-  timed([&] { return launch_gate_norm(a, gate, gs, rows, w, stream_); });
+  timed([&] { return launch_gate_norm(a, gate, gs, rows, w, out, op, stream_); });
 }
 
-void Backend::add_norm(const float* a, const float* b, float* out, int rows, int w) {
+void Backend::add_norm(const float* a, const float* b, float* out, int rows, int w, void* op) {
   XTG_CHECK(a && out && rows >= 1 && w >= 1, "add_norm: bad arguments");
-  timed([&] { return launch_add_norm(a, b, out, rows, w, stream_); });
+  timed([&] { return launch_add_norm(a, b, out, rows, w, op, stream_); });
 }
 
 hipEvent_t Backend::event() {

@@ -28,6 +28,7 @@ class Backend {
 
   // opencl.h:32 prepare(): idempotent, keyed by w.codes
   const PackedNvfp4& prepare(const xtg_nvfp4& w);
+  bool has_weight(const uint8_t* codes) const { return weights_.count(codes) != 0; }
   void release_weight(const uint8_t* codes);
   // opencl.h:34 host matmul: upload, compute, read back (8 rows per pass)
   void matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* const* ys);
@@ -51,13 +52,22 @@ class Backend {
   // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
-  // the row kernels of the decode step (rows.hip); device memory
+  // The attention half of a decode-step sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
+  // k / v [m][kv_heads][d], g [m][heads * d]: RoPE + norms of q and k (both rewritten), the attention over the cache
+  // and this call's keys, the store of k / v into the cache, then out (optional) and op (optional, the
+  // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)).
+  void attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
+                 float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
+                 void* op);
+  // the row kernels of the decode step (rows.hip); device memory. op (optional): also write the result rows as a
+  // GEMV operand of op_bytes(w) bytes.
   void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
                     const float* qscale);
-  void slerp_norm(float* x, const float* o, const float* lr, int rows, int w);
-  void swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w);
-  void gate_norm(float* a, const float* gate, const float* gs, int rows, int w);
-  void add_norm(const float* a, const float* b, float* out, int rows, int w);
+  void slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op = nullptr);
+  void swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w, float* out,
+                   void* op = nullptr);
+  void gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op = nullptr);
+  void add_norm(const float* a, const float* b, float* out, int rows, int w, void* op = nullptr);
   // 1 / theta^(2i/d) in FP32 computed on the host as engine/src/kernels.cpp:191-201 does, kept on the device
   const float* inv_freq(float theta, int d);
 

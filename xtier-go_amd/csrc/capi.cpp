@@ -191,7 +191,7 @@ int xtg_hip_swiglu_norm(xtg_hip* h, float* g, const float* u, const float* sg, c
                         char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h, "swiglu: NULL handle");
-    h->b->swiglu_norm(g, u, sg, su, rows, width);
+    h->b->swiglu_norm(g, u, sg, su, rows, width, g);
   });
 }
 
@@ -199,7 +199,7 @@ int xtg_hip_gate_norm(xtg_hip* h, float* att, const float* gate, const float* gs
                       int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h, "gate_norm: NULL handle");
-    h->b->gate_norm(att, gate, gs, rows, width);
+    h->b->gate_norm(att, gate, gs, rows, width, att);
   });
 }
 

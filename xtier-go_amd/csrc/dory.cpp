@@ -18,9 +18,25 @@ float* DorySession::upload(const float* v, size_t n) {
   return p;
 }
 
+void DorySession::prepare(const xtg_nvfp4& w) {
+  const bool fresh = w.codes && !b_.has_weight(w.codes);
+  b_.prepare(w);
+  if (fresh) prepared_.push_back(w.codes);
+}
+
 DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_layer* layers, const xtg_nvfp4& head,
                          const float* logit_scale)
     : b_(b), c_(c), head_(head) {
+  try {
+    build(layers, logit_scale);
+  } catch (...) {
+    release_all();
+    throw;
+  }
+}
+
+void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) {
+  const xtg_dory_config& c = c_;
   const int n_layers = c.n_in + c.n_rec + c.n_out;
   XTG_CHECK(n_layers > 0 && c.loops >= 1, "dory: %d sublayers, %d loops", n_layers, c.loops);
   XTG_CHECK(c.heads % c.kv_heads == 0 && c.head_dim % 2 == 0, "dory: unsupported attention shape");
@@ -32,14 +48,14 @@ DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_la
     L.recurrent = l >= c.n_in && l < c.n_in + c.n_rec;
     L.lr = upload(L.w.lr, size_t(H));
     if (L.w.kind == XTG_DORY_MLP) {
-      for (const xtg_nvfp4* w : {&L.w.gate, &L.w.up, &L.w.down}) b_.prepare(*w);
+      for (const xtg_nvfp4* w : {&L.w.gate, &L.w.up, &L.w.down}) prepare(*w);
       XTG_CHECK(L.w.gate.n_out == F && L.w.up.n_out == F && L.w.gate.k == H && L.w.down.k == F && L.w.down.n_out == H,
                 "dory: MLP sublayer %d has the wrong shapes", l);
       L.sg = upload(L.w.sg, size_t(F));
       L.su = upload(L.w.su, size_t(F));
     } else {
       XTG_CHECK(L.w.kind == XTG_DORY_SLIDING || L.w.kind == XTG_DORY_FULL, "dory: sublayer %d kind %d", l, L.w.kind);
-      for (const xtg_nvfp4* w : {&L.w.q, &L.w.k, &L.w.v, &L.w.g, &L.w.o}) b_.prepare(*w);
+      for (const xtg_nvfp4* w : {&L.w.q, &L.w.k, &L.w.v, &L.w.g, &L.w.o}) prepare(*w);
       XTG_CHECK(L.w.q.n_out == Q && L.w.k.n_out == KV && L.w.v.n_out == KV && L.w.g.n_out == Q && L.w.q.k == H &&
                     L.w.o.k == Q && L.w.o.n_out == H,
                 "dory: attention sublayer %d has the wrong shapes", l);
@@ -55,7 +71,7 @@ DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_la
       b_.inv_freq(L.w.kind == XTG_DORY_SLIDING ? c.theta_sliding : c.theta_full, c.head_dim);
     }
   }
-  b_.prepare(head_);
+  prepare(head_);
   XTG_CHECK(head_.k == H && head_.n_out == c.vocab, "dory: LM head %dx%d for hidden %d, vocab %d", head_.n_out,
             head_.k, H, c.vocab);
   logit_scale_ = upload(logit_scale, size_t(c.vocab));
@@ -69,7 +85,6 @@ DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_la
   input_ = scratch(R * H);
   state_ = scratch(R * H);
   proj_ = scratch(R * size_t(2 * Q + 2 * KV));
-  att_ = scratch(R * Q);
   gu_ = scratch(R * 2 * size_t(F));
   o_ = scratch(R * H);
   for (auto* op : {&op_h_, &op_q_, &op_f_}) {
@@ -79,14 +94,20 @@ DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_la
   }
 }
 
-DorySession::~DorySession() {
+void DorySession::release_all() {
   try {
     for (DevKv* c : caches_)
       if (c) b_.kv_destroy(c);
     for (void* p : owned_) b_.release(p);
+    for (const uint8_t* codes : prepared_) b_.release_weight(codes);
   } catch (...) {
   }
+  caches_.clear();
+  owned_.clear();
+  prepared_.clear();
 }
+
+DorySession::~DorySession() { release_all(); }
 
 DevKv* DorySession::cache(int attn, int inst) {
   XTG_CHECK(attn >= 0 && attn < n_attn_ && inst >= 0 && inst < c_.loops, "dory: no cache %d / %d", attn, inst);
@@ -96,36 +117,28 @@ DevKv* DorySession::cache(int attn, int inst) {
 }
 
 void DorySession::sublayer(Layer& L, int m, long long pos0, int inst) {
-  // packs/dory/dory.cpp:467-518
+  // packs/dory/dory.cpp:467-518; x's GEMV operand is in op_h_ on entry and on exit
   const int H = c_.hidden, Q = c_.heads * c_.head_dim, KV = c_.kv_heads * c_.head_dim, F = c_.ffn;
   if (L.w.kind == XTG_DORY_MLP) {
     const xtg_nvfp4 gu[2] = {L.w.gate, L.w.up};
-    b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
-    b_.matmul_op(gu, 2, op_h_, m, gu_, 0);                            // gate rows [m][F], then up rows [m][F]
-    b_.swiglu_norm(gu_, gu_ + size_t(m) * F, L.sg, L.su, m, F);      // justnorm(silu(g sg) (u su))
-    b_.prep_x(gu_, XTG_X_F32, m, F, op_f_);
+    b_.matmul_op(gu, 2, op_h_, m, gu_, 0);                                      // gate rows [m][F], then up rows
+    b_.swiglu_norm(gu_, gu_ + size_t(m) * F, L.sg, L.su, m, F, nullptr, op_f_);  // justnorm(silu(g sg) (u su))
     b_.matmul_op(&L.w.down, 1, op_f_, m, o_, 0);
-    b_.slerp_norm(x_, o_, L.lr, m, H);
+    b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
     return;
   }
   const xtg_nvfp4 qkvg[4] = {L.w.q, L.w.k, L.w.v, L.w.g};
-  b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
   b_.matmul_op(qkvg, 4, op_h_, m, proj_, 0);   // q [m][Q] | k [m][KV] | v [m][KV] | g [m][Q]
   float* q = proj_;
   float* k = proj_ + size_t(m) * Q;
   float* v = k + size_t(m) * KV;
   float* g = v + size_t(m) * KV;
   const bool sliding = L.w.kind == XTG_DORY_SLIDING;
-  b_.qk_rope_norm(q, k, m, c_.heads, c_.kv_heads, c_.head_dim, pos0, sliding ? c_.theta_sliding : c_.theta_full,
-                  L.qscale);
-  DevKv* cache = this->cache(L.attn, inst);
   const float scale = 1.f / std::sqrt(float(c_.head_dim));
-  b_.attention(cache, m, pos0, c_.heads, sliding ? c_.window : 0, scale, q, k, v, att_);
-  b_.kv_store(cache, pos0, m, k, v);   // after the attention: the cache is read only during it
-  b_.gate_norm(att_, g, L.gscale, m, Q);
-  b_.prep_x(att_, XTG_X_F32, m, Q, op_q_);
+  b_.attn_step(this->cache(L.attn, inst), m, pos0, c_.heads, sliding ? c_.window : 0, scale,
+               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_);
   b_.matmul_op(&L.w.o, 1, op_q_, m, o_, 0);
-  b_.slerp_norm(x_, o_, L.lr, m, H);
+  b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
 }
 
 void DorySession::forward(const float* x, int m, long long pos0, float* logits) {
@@ -136,18 +149,19 @@ void DorySession::forward(const float* x, int m, long long pos0, float* logits) 
   const int H = c_.hidden;
   const size_t bytes = size_t(m) * H * sizeof(float);
   b_.copy(x, 0, x_, 0, bytes);
+  b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
   size_t l = 0;
   for (; l < size_t(c_.n_in); ++l) sublayer(layers_[l], m, pos0, 0);
   b_.copy(x_, 0, input_, 0, bytes);
   b_.copy(x_, 0, state_, 0, bytes);
   for (int i = 0; i < c_.loops; ++i) {
-    b_.add_norm(state_, input_, x_, m, H);   // loop entry: x = justnorm(state + input)
+    b_.add_norm(state_, input_, x_, m, H, op_h_);   // loop entry: x = justnorm(state + input)
     for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r) sublayer(layers_[r], m, pos0, i);
-    b_.add_norm(x_, nullptr, state_, m, H);  // loop exit: state = justnorm(x)
+    // loop exit: state = justnorm(x); after the last loop x = state, whose operand the next projection reads
+    b_.add_norm(x_, nullptr, state_, m, H, i == c_.loops - 1 ? op_h_ : nullptr);
   }
   b_.copy(state_, 0, x_, 0, bytes);
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0);
-  b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
   b_.matmul_op(&head_, 1, op_h_, m, logits, 0, logit_scale_);
 }
 

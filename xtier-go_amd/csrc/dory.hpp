@@ -39,6 +39,9 @@ class DorySession {
   };
   void sublayer(Layer& L, int m, long long pos0, int inst);
   float* upload(const float* v, size_t n);
+  void build(const xtg_dory_layer* layers, const float* logit_scale);
+  void prepare(const xtg_nvfp4& w);
+  void release_all();
 
   Backend& b_;
   xtg_dory_config c_;
@@ -48,12 +51,17 @@ class DorySession {
   int n_attn_ = 0;
   std::vector<DevKv*> caches_;   // [attn][loops]
   std::vector<void*> owned_;     // device vectors and scratch
+  // weights this session prepared (their device copies go with it: the host arrays that key them may be freed
+  // and their addresses reused once the session is gone)
+  std::vector<const uint8_t*> prepared_;
   // scratch for up to 8 rows
-  float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *att_ = nullptr, *gu_ = nullptr,
+  float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
         *o_ = nullptr;
-  void* op_h_ = nullptr;   // activation operand for K = hidden
-  void* op_q_ = nullptr;   // for K = heads * head_dim (o_proj)
-  void* op_f_ = nullptr;   // for K = ffn (down)
+  // GEMV operands, each written by the kernel that produces its rows: x's (K = hidden; by the slerp / loop norms
+  // or, for the first sublayer, prep_x), the gated attention's (K = heads * head_dim), the SwiGLU's (K = ffn)
+  void* op_h_ = nullptr;
+  void* op_q_ = nullptr;
+  void* op_f_ = nullptr;
 };
 
 }  // namespace xtg::hip

@@ -12,8 +12,11 @@
 //    exactly; E2M1 x E4M3 products (at most 6 significant bits, 2^-10 .. 2688) are exact in f16.
 //  - v_mfma_f32_16x16x32_f16 does the products with FP32 accumulation. The operand's 16 columns carry the high
 //    and the low f16 part of up to 8 activation rows (each row first scaled by a power of two), so the FP32
-//    activations keep ~22 significant bits at no extra matrix-core cost.
-//  - Output: column j and j + 8 of the accumulator are added, times global and the row's 2^-s.
+//    activations keep ~22 significant bits at no extra matrix-core cost. Lane (g, c) loads column c's entry
+//    4 c + g, so at small m the live columns are a few contiguous lines per MFMA step.
+//  - Weights stream with nontemporal loads (read once per call; kept out of the caches' way).
+//  - Output: columns 2 r and 2 r + 1 of the accumulator (neighbour lanes) are added, times global and row r's
+//    2^-s.
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
@@ -22,11 +25,12 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "rowops.hpp"
 
 namespace xtg::hip {
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out) {
@@ -82,23 +86,6 @@ __device__ inline void load_chunk(const void* x, int x_dtype, int j, int k, int 
   }
 }
 
-// Row j's chunk c as the f16 high and low parts of x * 2^e, stored where MFMA lane (g, j) / (g, 8 + j) of
-// k-tile c / 16 reads them: chunk w = 4 g + t of a tile holds inputs 32 g + 8 t .. +8 (lane group g, MFMA t).
-__device__ inline void store_chunk(f16x8* xop, int j, int c, const float v[8], float up) {
-  f16x8 hi, lo;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float s = v[i] * up;
-    const _Float16 h = (_Float16)s;
-    hi[i] = h;
-    lo[i] = (_Float16)(s - (float)h);
-  }
-  const int w = c & 15, g = w >> 2, t = w & 3;
-  const size_t base = (size_t(c >> 4) * 4 + size_t(t)) * 64;
-  xop[base + size_t(g * 16 + j)] = hi;
-  xop[base + size_t(g * 16 + 8 + j)] = lo;
-}
-
 // One work-group per activation row j < m: the row's largest magnitude picks the power of two 2^e that brings it
 // to [2^14, 2^15); the scaled row is split into f16 high and low parts in MFMA B-operand order (columns j and
 // 8 + j). Rows up to 8192 wide make one read of x (chunks held in registers); wider rows read x twice. Columns of
@@ -131,9 +118,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __rest
   mx = red[0];
 #pragma unroll
   for (int i = 1; i < kPrepThreads / 64; ++i) mx = fmaxf(mx, red[i]);
-  int e = 0;
-  if (mx > 0.f && mx <= FLT_MAX) e = 14 - ilogbf(mx);
-  e = std::min(120, std::max(-120, e));
+  const int e = operand_exponent(mx);
   const float up = ldexpf(1.f, e);
   if (tid == 0) xinv[j] = ldexpf(1.f, -e);
 #pragma unroll
@@ -202,8 +187,8 @@ __device__ inline f16x2 scale_pair(uint32_t sbits, int which) {
   return r;
 }
 
-// Output of one accumulator fragment: lane (g, j), j < 8, holds rows 4 g .. 4 g + 3 of the row-block for
-// activation row j.
+// Output of one accumulator fragment: for activation row j, rows 4 g .. 4 g + 3 of the row-block (high and low
+// columns already added).
 __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int j, f32x4 v) {
   if (j >= a.m) return;
   const int n = a.n[wi];
@@ -229,8 +214,9 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
 
   // every load of the wave first (T k-tiles of activations, R x T weight tiles), then the math; operand columns
   // of absent activation rows are not loaded (their accumulator columns are never stored)
-  const int col = lane & 15;
-  const bool live_col = (col < 8 ? col : col - 8) < a.m;
+  const int col = lane & 15, grp = lane >> 4;
+  const bool live_col = (col >> 1) < a.m;
+  const int entry = 4 * col + grp;
   uint4 xb[T][4];
   uint4 cw[T][R];
   uint32_t sw[T][R];
@@ -240,13 +226,19 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     const bool ok = kt < KT;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      xb[u][t] = ok && live_col ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(lane)] : make_uint4(0, 0, 0, 0);
+      xb[u][t] = ok && live_col ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(entry)] : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool ok2 = ok && rb0 + r < nb;
       const uint8_t* tile = tiles + (size_t(rb0 + r) * size_t(KT) + size_t(kt)) * kTileBytes;
-      cw[u][r] = ok2 ? *reinterpret_cast<const uint4*>(tile + 16 * lane) : make_uint4(0, 0, 0, 0);
-      sw[u][r] = ok2 ? uint32_t(*reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane)) : 0u;
+      if (ok2) {
+        const u32x4 c4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + 16 * lane));
+        cw[u][r] = make_uint4(c4[0], c4[1], c4[2], c4[3]);
+        sw[u][r] = uint32_t(__builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane)));
+      } else {
+        cw[u][r] = make_uint4(0, 0, 0, 0);
+        sw[u][r] = 0u;
+      }
     }
   }
   f32x4 acc[R];
@@ -266,15 +258,13 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
       }
     }
   }
-  const int g = lane >> 4, j = lane & 15;
   if (S == 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       f32x4 v = acc[r];
-      f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = __shfl_xor(v[e], 8);
-      if (j < 8 && rb0 + r < nb) store_rows(a, wi, rb0 + r, g, j, v + o);
+      for (int e = 0; e < 4; ++e) v[e] += dpp<kDppXor1>(v[e]);   // high + low column of the row
+      if ((col & 1) == 0 && rb0 + r < nb) store_rows(a, wi, rb0 + r, grp, col >> 1, v);
     }
     return;
   }
@@ -282,10 +272,10 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
   __syncthreads();
   for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
-    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7, ln = gg * 16 + jj;
+    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7, ln = gg * 16 + 2 * jj;
     if (rb0 + r >= nb) continue;
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < S; ++w) sum += red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 8];
+    for (int w = 0; w < S; ++w) sum += red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 1];
     store_rows(a, wi, rb0 + r, gg, jj, sum);
   }
 }

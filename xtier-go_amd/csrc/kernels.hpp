@@ -29,8 +29,10 @@ struct PackedNvfp4 {
 // Host repack of [n][k/2] codes and [n][k/16] scales into the tile layout above.
 void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out);
 
-// The MFMA operand form of the activations: [kt][4][64 lanes][8 f16] (4096 bytes per k-tile). Column j < 8 of
-// the operand is the high f16 part of row j scaled by 2^s_j, column 8 + j the low part; xinv[j] = 2^-s_j.
+// The MFMA operand form of the activations: [kt][4 steps][64 entries][8 f16] (4096 bytes per k-tile). Operand
+// column 2 r is the high f16 part of row r scaled by 2^s_r, column 2 r + 1 the low part; xinv[r] = 2^-s_r. Entry
+// 4 c + g of step t holds column c's inputs 32 g + 8 t .. +8 of the k-tile, so the live columns of m rows fill the
+// first 128 m bytes of every step (one cache line per step at m = 1).
 inline size_t xop_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 4096; }
 constexpr int kMaxRows = 8;
 

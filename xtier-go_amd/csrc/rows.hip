@@ -1,4 +1,5 @@
-// Row kernels of the Dory decode step: the fused Q/K producer and the nGPT norms around the projections.
+// Row kernels of the Dory decode step: the Q/K producer of the reference's host path and the nGPT norms around
+// the projections.
 //
 // Semantics (FP32 throughout; justnorm(x) = x / sqrt(sum x^2 + 1e-6), engine/src/kernels.cpp:162-175):
 //   qk_rope_norm: NeoX RoPE of q and k at positions pos0 + row, then justnorm per head, then q *= qscale (per
@@ -9,36 +10,19 @@
 //   swiglu_norm:  g = justnorm(silu(g * sg) * (u * su)) (kernels.cpp:225-234 then justnorm, dory.cpp:474-475)
 //   gate_norm:    a = justnorm(a * sigmoid(g * gs)) over all heads (dory.cpp:510-515)
 //   add_norm:     out = justnorm(a + b), or justnorm(a) without b (dory.cpp:532-541)
-// One work-group per row (per (row, head) for the producer); sums are wave reductions then one LDS step.
+// The norms run one work-group of 512 threads per row with the whole row in registers (one read of each input,
+// the sums as block reductions), and can also write the row as the next projection's GEMV operand (the f16
+// high / low split prep_x_kernel makes), so no separate operand pass runs between a norm and its projection.
 #include <cmath>
 
 #include "common.hpp"
+#include "rowops.hpp"
 #include "rows.hpp"
 
 namespace xtg::hip {
 
-constexpr int kRowThreads = 256;
-
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-// Sum over the work-group (kRowThreads threads); every thread gets the total. red holds kRowThreads / 64 floats.
-__device__ inline float group_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();   // red may still be read from a previous call
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kRowThreads / 64; ++i) s += red[i];
-  return s;
-}
-
-__device__ inline float inv_norm_of(float sumsq) { return 1.f / sqrtf(sumsq + 1e-6f); }
+constexpr int kNormThreads = 512;
+constexpr int kNormRed = 2 * kNormThreads / 64;
 
 // One wave per (row, head): thread i holds the pair (i, i + d/2); d <= 128.
 __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q, float* __restrict__ k, int m,
@@ -72,73 +56,169 @@ __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q,
   }
 }
 
-__global__ void __launch_bounds__(kRowThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
-                                                                  const float* __restrict__ lr, int w) {
-  __shared__ float red[kRowThreads / 64];
+// The normalised row t * f: written to out (if any) and as operand row j (if any).
+template <int U>
+__device__ inline void finish_row(float (&t)[U][8], float sumsq, int w, bool vec, float* out, f16x8* xop, float* xinv,
+                                  float* red) {
+  const float f = inv_norm_of(block_sum<kNormThreads>(sumsq, red));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[u][e] *= f;
+  if (out) store_row<kNormThreads, U>(out, w, vec, t);
+  if (xop) emit_operand<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, red);
+}
+
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
+                                                                   const float* __restrict__ lr, int w, int vec,
+                                                                   f16x8* __restrict__ xop, float* __restrict__ xinv) {
+  __shared__ float red[kNormRed];
   float* xr = x + size_t(blockIdx.x) * w;
-  const float* orow = o + size_t(blockIdx.x) * w;
+  float a[U][8], b[U][8], l[U][8];
+  load_row<kNormThreads, U>(xr, w, vec, a);
+  load_row<kNormThreads, U>(o + size_t(blockIdx.x) * w, w, vec, b);
+  load_row<kNormThreads, U>(lr, w, vec, l);
   float sa = 0.f, sb = 0.f;
-  for (int j = threadIdx.x; j < w; j += kRowThreads) {
-    sa += xr[j] * xr[j];
-    sb += orow[j] * orow[j];
-  }
-  const float fa = inv_norm_of(group_sum(sa, red)), fb = inv_norm_of(group_sum(sb, red));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sa += a[u][e] * a[u][e];
+      sb += b[u][e] * b[u][e];
+    }
+  block_sum2<kNormThreads>(sa, sb, red);
+  const float fa = inv_norm_of(sa), fb = inv_norm_of(sb);
   float s = 0.f;
-  for (int j = threadIdx.x; j < w; j += kRowThreads) {
-    const float ya = xr[j] * fa, yb = orow[j] * fb, t = ya + lr[j] * (yb - ya);
-    xr[j] = t;
-    s += t * t;
-  }
-  const float f = inv_norm_of(group_sum(s, red));
-  for (int j = threadIdx.x; j < w; j += kRowThreads) xr[j] *= f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float ya = a[u][e] * fa, yb = b[u][e] * fb;
+      a[u][e] = ya + l[u][e] * (yb - ya);
+      s += a[u][e] * a[u][e];
+    }
+  finish_row<U>(a, s, w, vec, xr, xop, xinv, red);
 }
 
-__global__ void __launch_bounds__(kRowThreads) swiglu_norm_kernel(float* __restrict__ g, const float* __restrict__ u,
-                                                                   const float* __restrict__ sg,
-                                                                   const float* __restrict__ su, int w) {
-  __shared__ float red[kRowThreads / 64];
-  float* gr = g + size_t(blockIdx.x) * w;
-  const float* ur = u + size_t(blockIdx.x) * w;
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* g,
+                                                                    const float* __restrict__ u_,
+                                                                    const float* __restrict__ sg,
+                                                                    const float* __restrict__ su, int w, int vec,
+                                                                    float* out, f16x8* __restrict__ xop,
+                                                                    float* __restrict__ xinv) {
+  __shared__ float red[kNormRed];
+  float a[U][8], b[U][8], s1[U][8], s2[U][8];
+  load_row<kNormThreads, U>(g + size_t(blockIdx.x) * w, w, vec, a);
+  load_row<kNormThreads, U>(u_ + size_t(blockIdx.x) * w, w, vec, b);
+  load_row<kNormThreads, U>(sg, w, vec, s1);
+  load_row<kNormThreads, U>(su, w, vec, s2);
   float s = 0.f;
-  for (int j = threadIdx.x; j < w; j += kRowThreads) {
-    const float z = gr[j] * sg[j];
-    const float t = z / (1.f + expf(-z)) * (ur[j] * su[j]);
-    gr[j] = t;
-    s += t * t;
-  }
-  const float f = inv_norm_of(group_sum(s, red));
-  for (int j = threadIdx.x; j < w; j += kRowThreads) gr[j] *= f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = a[u][e] * s1[u][e];
+      a[u][e] = z / (1.f + expf(-z)) * (b[u][e] * s2[u][e]);
+      s += a[u][e] * a[u][e];
+    }
+  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, red);
 }
 
-__global__ void __launch_bounds__(kRowThreads) gate_norm_kernel(float* __restrict__ a, const float* __restrict__ gate,
-                                                                 const float* __restrict__ gs, int w) {
-  __shared__ float red[kRowThreads / 64];
-  float* ar = a + size_t(blockIdx.x) * w;
-  const float* gr = gate + size_t(blockIdx.x) * w;
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) gate_norm_kernel(const float* a_,
+                                                                  const float* __restrict__ gate,
+                                                                  const float* __restrict__ gs, int w, int vec,
+                                                                  float* out, f16x8* __restrict__ xop,
+                                                                  float* __restrict__ xinv) {
+  __shared__ float red[kNormRed];
+  float a[U][8], g[U][8], sc[U][8];
+  load_row<kNormThreads, U>(a_ + size_t(blockIdx.x) * w, w, vec, a);
+  load_row<kNormThreads, U>(gate + size_t(blockIdx.x) * w, w, vec, g);
+  load_row<kNormThreads, U>(gs, w, vec, sc);
   float s = 0.f;
-  for (int j = threadIdx.x; j < w; j += kRowThreads) {
-    const float t = ar[j] * (1.f / (1.f + expf(-gr[j] * gs[j])));
-    ar[j] = t;
-    s += t * t;
-  }
-  const float f = inv_norm_of(group_sum(s, red));
-  for (int j = threadIdx.x; j < w; j += kRowThreads) ar[j] *= f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[u][e] = a[u][e] * (1.f / (1.f + expf(-g[u][e] * sc[u][e])));
+      s += a[u][e] * a[u][e];
+    }
+  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, red);
 }
 
-__global__ void __launch_bounds__(kRowThreads) add_norm_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                                float* __restrict__ out, int w) {
-  __shared__ float red[kRowThreads / 64];
-  const float* ar = a + size_t(blockIdx.x) * w;
-  const float* br = b ? b + size_t(blockIdx.x) * w : nullptr;
-  float* orow = out + size_t(blockIdx.x) * w;
-  float s = 0.f;
-  for (int j = threadIdx.x; j < w; j += kRowThreads) {
-    const float t = ar[j] + (br ? br[j] : 0.f);
-    s += t * t;
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_, const float* __restrict__ b_,
+                                                                 float* out,
+                                                                 int w, int vec, f16x8* __restrict__ xop,
+                                                                 float* __restrict__ xinv) {
+  __shared__ float red[kNormRed];
+  float a[U][8], b[U][8];
+  load_row<kNormThreads, U>(a_ + size_t(blockIdx.x) * w, w, vec, a);
+  if (b_) {
+    load_row<kNormThreads, U>(b_ + size_t(blockIdx.x) * w, w, vec, b);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[u][e] += b[u][e];
   }
-  const float f = inv_norm_of(group_sum(s, red));
-  for (int j = threadIdx.x; j < w; j += kRowThreads) orow[j] = (ar[j] + (br ? br[j] : 0.f)) * f;
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += a[u][e] * a[u][e];
+  finish_row<U>(a, s, w, vec, out + size_t(blockIdx.x) * w, xop, xinv, red);
 }
+
+// ------------------------------------------------------------------------------------------------ launchers
+
+namespace {
+
+// Chunks of 8 per thread for a row of w floats: 1, 2, 4 or 8 (rows up to 32768 wide).
+int norm_chunks(int w) {
+  const int chunks = (w + 7) / 8;
+  for (int u : {1, 2, 4, 8})
+    if (chunks <= u * kNormThreads) return u;
+  fail("row kernels: width %d above %d", w, 8 * 8 * kNormThreads);
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// vec: whole chunks of every row may be read as float4s
+bool rows_vec(int w, std::initializer_list<const void*> ptrs) {
+  if (w % 4 != 0) return false;
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+struct Operand {
+  f16x8* xop = nullptr;
+  float* xinv = nullptr;
+};
+
+Operand operand_of(void* op, int rows, int w) {
+  if (!op) return {};
+  XTG_CHECK(rows <= kMaxRows, "row kernels: %d rows for an operand of at most %d", rows, kMaxRows);
+  XTG_CHECK(w % 16 == 0, "row kernels: operand width %d (a multiple of 16)", w);
+  XTG_CHECK(aligned16(op), "row kernels: operand at %p is not 16-byte aligned", op);
+  return {static_cast<f16x8*>(op), reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(w))};
+}
+
+#define XTG_NORM_DISPATCH(KERNEL, ...)                                                                   \
+  do {                                                                                                   \
+    const int u_ = norm_chunks(w);                                                                       \
+    const dim3 g_{unsigned(rows)}, b_{unsigned(kNormThreads)};                                                     \
+    if (u_ == 1) hipLaunchKernelGGL(KERNEL<1>, g_, b_, 0, stream, __VA_ARGS__);                          \
+    else if (u_ == 2) hipLaunchKernelGGL(KERNEL<2>, g_, b_, 0, stream, __VA_ARGS__);                     \
+    else if (u_ == 4) hipLaunchKernelGGL(KERNEL<4>, g_, b_, 0, stream, __VA_ARGS__);                     \
+    else hipLaunchKernelGGL(KERNEL<8>, g_, b_, 0, stream, __VA_ARGS__);                                  \
+    HIP_CHECK(hipGetLastError());                                                                        \
+    return strf("%s<%d>", #KERNEL, u_);                                                                  \
+  } while (0)
+
+}  // namespace
 
 std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0,
                                 const float* inv_freq, const float* qscale, hipStream_t stream) {
@@ -149,29 +229,32 @@ std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_hea
   return "qk_rope_norm_kernel";
 }
 
-std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, hipStream_t stream) {
-  hipLaunchKernelGGL(slerp_norm_kernel, dim3(unsigned(rows)), dim3(kRowThreads), 0, stream, x, o, lr, w);
-  HIP_CHECK(hipGetLastError());
-  return "slerp_norm_kernel";
+std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op,
+                              hipStream_t stream) {
+  const Operand p = operand_of(op, rows, w);
+  const int vec = rows_vec(w, {x, o, lr});
+  XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, lr, w, vec, p.xop, p.xinv);
 }
 
-std::string launch_swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w,
-                               hipStream_t stream) {
-  hipLaunchKernelGGL(swiglu_norm_kernel, dim3(unsigned(rows)), dim3(kRowThreads), 0, stream, g, u, sg, su, w);
-  HIP_CHECK(hipGetLastError());
-  return "swiglu_norm_kernel";
+std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
+                               float* out, void* op, hipStream_t stream) {
+  const Operand p = operand_of(op, rows, w);
+  const int vec = rows_vec(w, {g, u, sg, su, out});
+  XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, sg, su, w, vec, out, p.xop, p.xinv);
 }
 
-std::string launch_gate_norm(float* a, const float* gate, const float* gs, int rows, int w, hipStream_t stream) {
-  hipLaunchKernelGGL(gate_norm_kernel, dim3(unsigned(rows)), dim3(kRowThreads), 0, stream, a, gate, gs, w);
-  HIP_CHECK(hipGetLastError());
-  return "gate_norm_kernel";
+std::string launch_gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op,
+                             hipStream_t stream) {
+  const Operand p = operand_of(op, rows, w);
+  const int vec = rows_vec(w, {a, gate, gs, out});
+  XTG_NORM_DISPATCH(gate_norm_kernel, a, gate, gs, w, vec, out, p.xop, p.xinv);
 }
 
-std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, hipStream_t stream) {
-  hipLaunchKernelGGL(add_norm_kernel, dim3(unsigned(rows)), dim3(kRowThreads), 0, stream, a, b, out, w);
-  HIP_CHECK(hipGetLastError());
-  return "add_norm_kernel";
+std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, void* op,
+                            hipStream_t stream) {
+  const Operand p = operand_of(op, rows, w);
+  const int vec = rows_vec(w, {a, b, out});
+  XTG_NORM_DISPATCH(add_norm_kernel, a, b, out, w, vec, p.xop, p.xinv);
 }
 
 }  // namespace xtg::hip

@@ -1,4 +1,6 @@
 // Launchers of the row kernels (rows.hip). All pointers are device memory; launchers return the kernel name.
+// op (optional): also write the rows as a GEMV activation operand (kernels.hpp layout, Backend::op_bytes(w) bytes:
+// the operand, then the rows' scales); rows <= kMaxRows and w % 16 == 0 then.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -9,10 +11,17 @@ namespace xtg::hip {
 
 std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0,
                                 const float* inv_freq, const float* qscale, hipStream_t stream);
-std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, hipStream_t stream);
-std::string launch_swiglu_norm(float* g, const float* u, const float* sg, const float* su, int rows, int w,
-                               hipStream_t stream);
-std::string launch_gate_norm(float* a, const float* gate, const float* gs, int rows, int w, hipStream_t stream);
-std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, hipStream_t stream);
+// x = justnorm(slerp) in place
+std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op,
+                              hipStream_t stream);
+// out (optional, may be g) = justnorm(silu(g sg) (u su))
+std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
+                               float* out, void* op, hipStream_t stream);
+// out (optional, may be a) = justnorm(a sigmoid(gate gs))
+std::string launch_gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op,
+                             hipStream_t stream);
+// out (may be a) = justnorm(a + b), b optional
+std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, void* op,
+                            hipStream_t stream);
 
 }  // namespace xtg::hip
