@@ -192,6 +192,8 @@ def main():
     ap.add_argument("--decode-contexts", default="4096,8192,32768")
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode-step measurement (for profiling it); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels are one GPU's share of a "
@@ -200,6 +202,16 @@ def main():
 
     pkg = load_package()
     import xtier_go_amd.workloads as wl
+
+    if args.decode_only:
+        hip = pkg.HipBackend(0)
+        contexts = [int(v) for v in args.decode_contexts.split(",") if v]
+        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2)
+        first = "ctx%d" % contexts[0]
+        print(json.dumps({"metric": "synthetic 4B decode tok/s", "value": decode[first]["tok_s"], "unit": "tok/s",
+                          "n_gpus": 1, "higher_is_better": True, "data": "synthetic", "decode": decode}))
+        hip.close()
+        return
 
     rng = np.random.default_rng(20261201)
     base = {name: [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes] for name, shapes in SHAPES}

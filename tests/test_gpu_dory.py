@@ -128,3 +128,62 @@ def test_4b_graph_replay_matches_eager(hip, model_4b):
     hip.graph_destroy(g)
     dx.free()
     dl.free()
+
+
+def sharpened(w, seed=9):
+    """q scaled up 40x and lr ~ U(0.3, 0.7): attention that depends on positions and masks (see
+    tests/test_oracle_dory.py)."""
+    rng = np.random.default_rng(seed)
+    for L in w.layers:
+        if "qscale" in L:
+            L["qscale"] *= np.float32(40)
+        L["lr"][:] = rng.uniform(0.3, 0.7, L["lr"].shape).astype(np.float32)
+    return w
+
+
+def device_steps(hip, w, x, pos0, chunk):
+    dev = hip.dory(w)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    dx = hip.array(shape=(8, H))
+    dl = hip.array(shape=(8, V))
+    out = []
+    try:
+        for r in range(0, x.shape[0], chunk):
+            m = min(chunk, x.shape[0] - r)
+            dx.upload(np.concatenate([x[r:r + m], np.zeros((8 - m, H), np.float32)]))
+            dev.forward(dx, m, pos0 + r, dl)
+            out.append(dl.numpy()[:m])
+    finally:
+        dx.free()
+        dl.free()
+        dev.destroy()
+    return np.concatenate(out)
+
+
+def test_sharp_chunks_and_steps(hip, orc, wl):
+    """A sharp-attention tiny model over 72 positions (the rings wrap): device chunks of 8 and device one-row
+    steps against the oracle's, and against each other (equal up to the BF16 rounding of cached keys)."""
+    w = sharpened(wl.DoryWeights(wl.DORY_TINY, seed=21, context=256))
+    x = unit_rows(np.random.default_rng(2), 72, w.cfg["hidden"])
+    ref = orc.Dory(w, wl)
+    want8 = np.concatenate([ref.forward(x[r:r + 8], r) for r in range(0, 72, 8)])
+    ref1 = orc.Dory(w, wl)
+    want1 = np.concatenate([ref1.forward(x[r:r + 1], r) for r in range(72)])
+    got8 = device_steps(hip, w, x, 0, 8)
+    got1 = device_steps(hip, w, x, 0, 1)
+    e8, e1, ec = rel_l2(got8, want8), rel_l2(got1, want1), rel_l2(got8, got1)
+    print("sharp tiny model: chunks %.2e, steps %.2e vs the oracle; chunks vs steps %.2e" % (e8, e1, ec))
+    assert e8 <= 1e-3 and e1 <= 1e-3
+    assert (got8.argmax(1) == want8.argmax(1)).all() and (got1.argmax(1) == want1.argmax(1)).all()
+    assert ec < 1e-2
+
+
+def test_window_one_chunks_equal_steps(hip, wl):
+    """Window 1 (every attention sees only its own row): device chunks and steps agree to FP32 rounding."""
+    w = sharpened(wl.DoryWeights(dict(wl.DORY_TINY, window=1), seed=23, context=64))
+    for i, k in enumerate(w.kinds):
+        if k == wl.FULL:
+            w.kinds[i] = wl.SLIDING
+            w.layers[i]["kind"] = wl.SLIDING
+    x = unit_rows(np.random.default_rng(3), 8, w.cfg["hidden"])
+    assert rel_l2(device_steps(hip, w, x, 0, 8), device_steps(hip, w, x, 0, 1)) < 1e-5
