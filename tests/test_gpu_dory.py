@@ -187,3 +187,17 @@ def test_window_one_chunks_equal_steps(hip, wl):
             w.layers[i]["kind"] = wl.SLIDING
     x = unit_rows(np.random.default_rng(3), 8, w.cfg["hidden"])
     assert rel_l2(device_steps(hip, w, x, 0, 8), device_steps(hip, w, x, 0, 1)) < 1e-5
+
+
+def test_ring_smaller_than_window_plus_chunk(hip, orc, wl):
+    """Window 60 in 64-slot rings with chunks of 8: storing before the scan would overwrite keys the chunk's
+    first rows still see, so the step stores after it (the reference's order); logits against the oracle."""
+    w = sharpened(wl.DoryWeights(dict(wl.DORY_TINY, window=60), seed=24, context=128))
+    x = unit_rows(np.random.default_rng(5), 96, w.cfg["hidden"])
+    ref = orc.Dory(w, wl)
+    want = np.concatenate([ref.forward(x[r:r + 8], r) for r in range(0, 96, 8)])
+    got = device_steps(hip, w, x, 0, 8)
+    e = rel_l2(got, want)
+    print("ring 64 / window 60 chunks of 8: logits rel-L2 %.2e" % e)
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()

@@ -343,29 +343,46 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
 // --------------------------------------------------------------------------------------------------- own keys
 
 // The online-softmax state of one q-col over own keys j0 .. j1 - 1 (kv.cpp:214-243 with this call's FP32 rows),
-// held by one wave: lane l < D / 2 holds dims l and l + D / 2 of the q vector (qa, qb; zero in the other lanes)
-// and of the output (a0, a1); key / value rows at kb + j * stride, vb + j * stride. Keys go in batches of 8 whose
-// loads are all issued first (indices clamped into the rows, so no load sits behind a branch); scores are in the
-// base-2 domain (scale2 = scale * log2 e).
+// computed by one wave. Scores: lane (key slot kk = lane / 8, part p = lane % 8) dots D / 8 dims of q with the same
+// dims of key jb + kk, the 8 lanes of a slot add up with three DPP steps, and each slot's score is read out as a
+// wave-uniform value. Outputs: lane l holds dims l mod (D / 2) and that + D / 2 (a0, a1). q at qp, key / value
+// rows at kb + j * stride, vb + j * stride; every load index is clamped into the rows, so none sits behind a
+// branch. Scores are in the base-2 domain (scale2 = scale * log2 e).
 template <int D>
-__device__ inline void own_state(float qa, float qb, const float* kb, const float* vb, size_t stride, int j0, int j1,
+__device__ inline void own_state(const float* qp, const float* kb, const float* vb, size_t stride, int j0, int j1,
                                  float scale2, float& M, float& L, float& a0, float& a1) {
-  const int l = (threadIdx.x & 63) & (D / 2 - 1);
+  constexpr int P = D / 8;
+  const int lane = threadIdx.x & 63, slot = lane >> 3, part = lane & 7, l = lane & (D / 2 - 1);
+  float q[P];
+#pragma unroll
+  for (int e = 0; e < P; e += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(qp + part * P + e);
+    q[e] = t.x, q[e + 1] = t.y, q[e + 2] = t.z, q[e + 3] = t.w;
+  }
   for (int jb = j0; jb < j1; jb += 8) {
-    float k0[8], k1[8], v0[8], v1[8];
+    const float* kr = kb + size_t(min(jb + slot, j1 - 1)) * stride + part * P;
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < P; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(kr + e);
+      dot += q[e] * t.x + q[e + 1] * t.y + q[e + 2] * t.z + q[e + 3] * t.w;
+    }
+    float v0[8], v1[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const size_t r = size_t(min(jb + u, j1 - 1)) * stride;
-      k0[u] = kb[r + l];
-      k1[u] = kb[r + l + D / 2];
       v0[u] = vb[r + l];
       v1[u] = vb[r + l + D / 2];
     }
-    float s[8], bm = -INFINITY;
+    dot += dpp<kDppXor1>(dot);
+    dot += dpp<kDppXor2>(dot);
+    dot += dpp<kDppHalfMirror>(dot);
+    const float sc = jb + slot < j1 ? dot * scale2 : -INFINITY;
+    float sj[8], bm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      s[u] = wave_sum(qa * k0[u] + qb * k1[u]) * scale2;
-      if (jb + u < j1) bm = fmaxf(bm, s[u]);
+      sj[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), 8 * u));
+      bm = fmaxf(bm, sj[u]);
     }
     const float mn = fmaxf(M, bm);   // finite: the batch holds at least one key
     const float corr = exp2_fast(M - mn);
@@ -374,7 +391,7 @@ __device__ inline void own_state(float qa, float qb, const float* kb, const floa
     a1 *= corr;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const float w = jb + u < j1 ? exp2_fast(s[u] - mn) : 0.f;
+      const float w = exp2_fast(sj[u] - mn);   // 0 for a slot past j1 (score -inf)
       L += w;
       a0 += w * v0[u];
       a1 += w * v1[u];
@@ -404,12 +421,10 @@ __global__ void __launch_bounds__(kWaves * 64) attn_own_kernel(const float* __re
   for (int c = wave; c < n_rows * group; c += kWaves) {
     const int r = c / group, hg = c % group, i = row0 + r;
     const float* qp = q + (size_t(r) * size_t(heads) + size_t(kvh * group + hg)) * D;
-    const int l = lane & (D / 2 - 1);
-    const float qa = lane < D / 2 ? qp[l] : 0.f, qb = lane < D / 2 ? qp[l + D / 2] : 0.f;
     const int j0 = window > 0 ? max(0, i - window + 1) : 0, j1 = min(i + 1, n_own);
     float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-    own_state<D>(qa, qb, k + size_t(kvh) * D, v + size_t(kvh) * D, size_t(kv_heads) * D, j0, j1, scale * kLog2e, M,
-                 L, a0, a1);
+    own_state<D>(qp, k + size_t(kvh) * D, v + size_t(kvh) * D, size_t(kv_heads) * D, j0, j1, scale * kLog2e, M, L,
+                 a0, a1);
     write_partial(acc, ml, (size_t(kvh) * size_t(splits1) + size_t(splits)) * size_t(qpad) + size_t(c), D, M, L, a0,
                   a1);
   }
@@ -418,12 +433,12 @@ __global__ void __launch_bounds__(kWaves * 64) attn_own_kernel(const float* __re
 // -------------------------------------------------------------------------------------------------- producer
 
 constexpr int kProdRows = 8, kProdGroup = 8;
-constexpr int kProdVecs = (kProdRows * (kProdGroup + 1) + kWaves - 1) / kWaves;   // vectors per wave, at most
 
 struct ProduceArgs {
   float* q;                // [m][heads][d], processed in place
-  float* k;                // [m][kv_heads][d], processed in place
+  const float* k;          // [m][kv_heads][d]
   const float* v;
+  float* kout;             // processed k rows (for a store after the scan), or NULL
   int m, heads, kv_heads, group, window, rpb, splits, splits1, qpad, store;
   long long pos0;
   float scale;
@@ -439,28 +454,36 @@ struct ProduceArgs {
   size_t blk_records;      // records per row block
 };
 
-// One work-group per KV head: RoPE + justnorm of its q heads and its k row for every row of the call, v copied,
-// the processed rows kept in LDS; then the own-key partial of every q-col.
-template <int D>
+// One work-group per (KV head, query row r). It takes RoPE + justnorm of row r's q heads of this KV head (times
+// qscale, written back in place) and of the k rows j0 .. r that row r attends to: each work-group recomputes
+// those few rows rather than wait for another's. Row r's k and v go to the cache (store set) and row r's
+// processed k to kout (if any); then each q-col of row r gets its own-key partial from one wave. VPW: the rows
+// a wave handles (at least ceil((group + r + 1 - j0) / 4)); they are processed without a branch, so their
+// reductions interleave.
+template <int D, int VPW>
 __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceArgs a) {
   constexpr int HALF = D / 2;
-  __shared__ float sq[kProdRows * kProdGroup * D], sk[kProdRows * D], sv[kProdRows * D];
+  constexpr int kT = kWaves * 64;
+  __shared__ float sq[kProdGroup * D], sk[kProdRows * D], sv[kProdRows * D];
   __shared__ float scos[kProdRows * HALF], ssin[kProdRows * HALF];
-  const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.x % a.kv_heads, r = blockIdx.x / a.kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool on = lane < HALF;
-  const int nq = a.m * a.group, nv = nq + a.m;
-
-  // every load first, each at an index clamped into its buffer (no load behind a branch): the wave's q / k pairs
-  // (lane l: dims l, l + d/2), their q scales, the rows' inverse frequencies and v
   const int l = lane & (HALF - 1);
-  float x1[kProdVecs], x2[kProdVecs], s1[kProdVecs], s2[kProdVecs];
+  const int j0 = a.window > 0 ? max(0, r - a.window + 1) : 0;   // the first own key row r sees
+  const int nk = r + 1 - j0;                                     // k rows j0 .. r (table rows 0 .. nk - 1)
+  const int nv = a.group + nk;                                   // row r's q heads, then those k rows
+  const long long slot_r = a.ring ? (a.pos0 + r) % a.slots : a.pos0 + r;
+
+  // every load first, each at an index clamped into its buffer (no load behind a branch)
+  float x1[VPW], x2[VPW], s1[VPW], s2[VPW];
 #pragma unroll
-  for (int it = 0; it < kProdVecs; ++it) {
+  for (int it = 0; it < VPW; ++it) {
     const int idx = min(wave + it * kWaves, nv - 1);
-    const bool is_q = idx < nq;
-    const int h = kvh * a.group + (is_q ? idx % a.group : 0);
-    const float* p = is_q ? a.q + (size_t(idx / a.group) * size_t(a.heads) + size_t(h)) * D
-                          : a.k + (size_t(idx - nq) * size_t(a.kv_heads) + size_t(kvh)) * D;
+    const bool is_q = idx < a.group;
+    const int h = kvh * a.group + (is_q ? idx : 0);
+    const float* p = is_q ? a.q + (size_t(r) * size_t(a.heads) + size_t(h)) * D
+                          : a.k + (size_t(j0 + idx - a.group) * size_t(a.kv_heads) + size_t(kvh)) * D;
     x1[it] = p[l];
     x2[it] = p[l + HALF];
     s1[it] = s2[it] = 1.f;
@@ -469,90 +492,82 @@ __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceAr
       s2[it] = a.qscale[size_t(h) * D + l + HALF];
     }
   }
-  constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
-  constexpr int kVals = (kProdRows * D + kWaves * 64 - 1) / (kWaves * 64);
+  constexpr int kAngles = (kProdRows * HALF + kT - 1) / kT;
+  constexpr int kVals = (kProdRows * D + kT - 1) / kT;
   float fr[kAngles], vv[kVals];
 #pragma unroll
-  for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[min(tid + u * kWaves * 64, a.m * HALF - 1) % HALF];
+  for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[min(tid + u * kT, nk * HALF - 1) % HALF];
 #pragma unroll
   for (int u = 0; u < kVals; ++u) {
-    const int e = min(tid + u * kWaves * 64, a.m * D - 1);
-    vv[u] = a.v[(size_t(e / D) * size_t(a.kv_heads) + size_t(kvh)) * D + size_t(e % D)];
+    const int e = min(tid + u * kT, nk * D - 1);
+    vv[u] = a.v[(size_t(j0 + e / D) * size_t(a.kv_heads) + size_t(kvh)) * D + size_t(e % D)];
   }
-  // the rows' rotation angles FP32(pos0 + r) * inv_freq[i] (engine/src/kernels.cpp:203-222), v into LDS and
-  // the cache
+  // the rows' rotation angles FP32(pos0 + row) * inv_freq[i] (engine/src/kernels.cpp:203-222); v rows into LDS,
+  // row r's into the cache
 #pragma unroll
   for (int u = 0; u < kAngles; ++u) {
-    const int e = tid + u * kWaves * 64;
-    if (e < a.m * HALF) {
-      const float ang = float(a.pos0 + e / HALF) * fr[u];
+    const int e = tid + u * kT;
+    if (e < nk * HALF) {
+      const float ang = float(a.pos0 + j0 + e / HALF) * fr[u];
       scos[e] = cosf(ang);
       ssin[e] = sinf(ang);
     }
   }
 #pragma unroll
   for (int u = 0; u < kVals; ++u) {
-    const int e = tid + u * kWaves * 64;
-    if (e < a.m * D) {
+    const int e = tid + u * kT;
+    if (e < nk * D) {
       sv[e] = vv[u];
-      if (a.store) {
-        const long long p = a.pos0 + e / D;
-        const int slot = int(a.ring ? p % a.slots : p);
-        a.cv[v_index(kvh, slot, e % D, a.slots_pad, D)] = f32_to_bf16_bits(vv[u]);
-      }
+      if (a.store && e / D == nk - 1)
+        a.cv[v_index(kvh, int(slot_r), e % D, a.slots_pad, D)] = f32_to_bf16_bits(vv[u]);
     }
   }
-  if (a.store && kvh == 0 && tid < a.m) {
-    const long long p = a.pos0 + tid;
-    a.slot_pos[a.ring ? p % a.slots : p] = int(p);
-  }
+  if (a.store && kvh == 0 && tid == 0) a.slot_pos[slot_r] = int(a.pos0 + r);
   __syncthreads();
 
 #pragma unroll
-  for (int it = 0; it < kProdVecs; ++it) {
+  for (int it = 0; it < VPW; ++it) {
     const int idx = wave + it * kWaves;
-    if (idx >= nv) break;   // uniform over the wave
-    const int r = idx < nq ? idx / a.group : idx - nq;
-    float o1 = 0.f, o2 = 0.f;
-    if (on) {
-      const float c = scos[r * HALF + lane], s = ssin[r * HALF + lane];
-      o1 = x1[it] * c - x2[it] * s;
-      o2 = x2[it] * c + x1[it] * s;
-    }
-    const float f = inv_norm_of(wave_sum(o1 * o1 + o2 * o2));
+    const bool live = idx < nv;
+    const int ic = min(idx, nv - 1);
+    const bool is_q = ic < a.group;
+    const int t = is_q ? nk - 1 : ic - a.group;   // table row: row r for q, row j0 + t for k
+    const float c = scos[t * HALF + l], s = ssin[t * HALF + l];
+    float o1 = x1[it] * c - x2[it] * s;
+    float o2 = x2[it] * c + x1[it] * s;
+    const float f = inv_norm_of(wave_sum(on ? o1 * o1 + o2 * o2 : 0.f));
     o1 *= f;
     o2 *= f;
-    if (on && idx < nq) {   // q: times qscale, back in place and into LDS
+    if (live && on && is_q) {   // q: times qscale, back in place and into LDS
       o1 *= s1[it];
       o2 *= s2[it];
-      float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + idx % a.group)) * D;
+      float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + ic)) * D;
       p[lane] = o1;
       p[lane + HALF] = o2;
-      sq[idx * D + lane] = o1;
-      sq[idx * D + lane + HALF] = o2;
-    } else if (on) {   // k: back in place (a store after the scan reads it there) and into LDS
-      float* p = a.k + (size_t(r) * size_t(a.kv_heads) + size_t(kvh)) * D;
-      p[lane] = o1;
-      p[lane + HALF] = o2;
-      sk[r * D + lane] = o1;
-      sk[r * D + lane + HALF] = o2;
-      if (a.store) {
-        const long long p = a.pos0 + r;
-        const int slot = int(a.ring ? p % a.slots : p);
-        a.ck[k_index(kvh, slot, lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
-        a.ck[k_index(kvh, slot, lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
+      sq[ic * D + lane] = o1;
+      sq[ic * D + lane + HALF] = o2;
+    } else if (live && on) {   // k row j0 + t into LDS; row r's to kout and the cache
+      sk[t * D + lane] = o1;
+      sk[t * D + lane + HALF] = o2;
+      if (t == nk - 1) {
+        if (a.kout) {
+          float* p = a.kout + (size_t(r) * size_t(a.kv_heads) + size_t(kvh)) * D;
+          p[lane] = o1;
+          p[lane + HALF] = o2;
+        }
+        if (a.store) {
+          a.ck[k_index(kvh, int(slot_r), lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
+          a.ck[k_index(kvh, int(slot_r), lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
+        }
       }
     }
   }
   __syncthreads();
 
-  // own keys: q-col c = r * group + hg of row r sees keys j <= r within the window
-  for (int c = wave; c < nq; c += kWaves) {
-    const int r = c / a.group, hg = c % a.group;
-    const float qa = on ? sq[c * D + l] : 0.f, qb = on ? sq[c * D + l + HALF] : 0.f;
-    const int j0 = a.window > 0 ? max(0, r - a.window + 1) : 0;
+  // own keys: q-col (r, hg) sees keys j0 .. r
+  for (int hg = wave; hg < a.group; hg += kWaves) {
     float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-    own_state<D>(qa, qb, sk, sv, D, j0, r + 1, a.scale * kLog2e, M, L, a0, a1);
+    own_state<D>(sq + hg * D, sk, sv, D, 0, nk, a.scale * kLog2e, M, L, a0, a1);
     const int blk = r / a.rpb, qc = (r % a.rpb) * a.group + hg;
     const size_t rec = size_t(blk) * a.blk_records + (size_t(kvh) * size_t(a.splits1) + size_t(a.splits)) * size_t(a.qpad) +
                        size_t(qc);
@@ -839,8 +854,8 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
   return strf("attn_merge_kernel<%d>", p.d);
 }
 
-std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float* k, const float* v, int m,
-                              int heads, long long pos0, int window, float scale, const float* inv_freq,
+std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
+                              int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
                               const float* qscale, bool store, float* part, hipStream_t stream) {
   XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
   XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
@@ -849,6 +864,7 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float
   a.q = q;
   a.k = k;
   a.v = v;
+  a.kout = kout;
   a.m = m;
   a.heads = heads;
   a.kv_heads = c.kv_heads;
@@ -872,12 +888,20 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float
   a.acc = part;
   a.ml = part + p.records() * size_t(p.d);
   a.blk_records = blk_records(p);
-  if (c.head_dim == 64)
-    hipLaunchKernelGGL(qk_produce_kernel<64>, dim3(unsigned(c.kv_heads)), dim3(kWaves * 64), 0, stream, a);
-  else
-    hipLaunchKernelGGL(qk_produce_kernel<128>, dim3(unsigned(c.kv_heads)), dim3(kWaves * 64), 0, stream, a);
+  const int keys = window > 0 ? std::min(m, window) : m;   // own key rows a query row sees, at most
+  const int vpw_need = (p.group + keys + kWaves - 1) / kWaves;
+  const dim3 grid{unsigned(c.kv_heads * m)}, block{unsigned(kWaves * 64)};
+  int vpw = 0;
+#define XTG_PROD(D, V)                                                                    \
+  if (c.head_dim == D && vpw_need <= V && !vpw) {                                         \
+    hipLaunchKernelGGL((qk_produce_kernel<D, V>), grid, block, 0, stream, a);             \
+    vpw = V;                                                                              \
+  }
+  XTG_PROD(64, 2) XTG_PROD(64, 4) XTG_PROD(128, 2) XTG_PROD(128, 4)
+#undef XTG_PROD
+  XTG_CHECK(vpw != 0, "producer: no kernel for head_dim %d and %d rows per wave", c.head_dim, vpw_need);
   HIP_CHECK(hipGetLastError());
-  return strf("qk_produce_kernel<%d>", c.head_dim);
+  return strf("qk_produce_kernel<%d, %d>", c.head_dim, vpw);
 }
 
 std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,

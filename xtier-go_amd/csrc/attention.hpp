@@ -56,11 +56,12 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
                               hipStream_t stream);
 
 // The decode step's producer (packs/dory/dory.cpp:482-490 and the cache store of :507): in one launch per
-// call (m <= 8 rows), RoPE + justnorm of q and k (q *= qscale; both written back in place), the own-key partials
-// from the FP32 rows, and -- when store is set -- k, v stored into the cache. Storing before the scan is exact
-// when no key the scan should see is overwritten: a linear cache, or a ring of at least window + m - 1 slots.
-std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, float* k, const float* v, int m,
-                              int heads, long long pos0, int window, float scale, const float* inv_freq,
+// call (m <= 8 rows), RoPE + justnorm of q and k (q *= qscale, q written back in place; k read only, the
+// processed rows also written to kout when it is not NULL), the own-key partials from the FP32 rows, and -- when
+// store is set -- k, v stored into the cache. Storing before the scan is exact when no key the scan should see is
+// overwritten: a linear cache, or a ring of at least window + m - 1 slots.
+std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
+                              int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
                               const float* qscale, bool store, float* part, hipStream_t stream);
 // The decode step's finish (dory.cpp:509-515): every row's merge, times sigmoid(g * gscale), justnorm over the
 // heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).

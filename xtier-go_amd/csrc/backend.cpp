@@ -29,7 +29,7 @@ Backend::~Backend() {
   for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.first);
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, hx_, hy_, part_})
+  for (void* p : {op_, hx_, hy_, part_, kproc_})
     if (p) (void)hipFree(p);
   for (DevKv* c : kvs_) {
     (void)hipFree(c->k);
@@ -269,7 +269,7 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
 }
 
 void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
-                        float* k, const float* v, const float* qscale, const float* g, const float* gscale,
+                        const float* k, const float* v, const float* qscale, const float* g, const float* gscale,
                         float* out, void* op) {
   XTG_CHECK(kvs_.count(c), "attention step: unknown cache");
   XTG_CHECK(m >= 1 && pos0 >= 0, "attention step: %d rows at %lld", m, pos0);
@@ -284,15 +284,21 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
   // storing before the scan hides nothing the scan should see: a linear cache's new slots are masked as
   // positions >= pos0, and a ring of window + m - 1 slots or more only drops positions outside every row's window
   const bool store_first = !c->ring || (window > 0 && c->slots >= (long long)window + m - 1);
+  float* kout = nullptr;   // the processed k rows, for a store after the scan
+  if (!store_first) {
+    ensure(kproc_, kproc_size_, size_t(m) * size_t(c->kv_heads) * size_t(c->head_dim) * sizeof(float));
+    kout = static_cast<float*>(kproc_);
+  }
   timed([&] {
-    return launch_qk_produce(*c, p, q, k, v, m, heads, pos0, window, scale, f, qscale, store_first, part, stream_);
+    return launch_qk_produce(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
+                             stream_);
   });
   if (p.splits > 0)
     for (int b = 0; b < p.blocks; ++b)
       timed([&] { return launch_attn_scan(*c, p, b, q, m, heads, pos0, window, scale, part, stream_); });
   if (!store_first)
     timed([&] {
-      launch_kv_store(*c, pos0, m, k, v, stream_);
+      launch_kv_store(*c, pos0, m, kout, v, stream_);
       return std::string("kv_store_kernel");
     });
   timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });

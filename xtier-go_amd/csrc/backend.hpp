@@ -53,11 +53,11 @@ class Backend {
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
   // The attention half of a decode-step sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
-  // k / v [m][kv_heads][d], g [m][heads * d]: RoPE + norms of q and k (both rewritten), the attention over the cache
+  // k / v [m][kv_heads][d], g [m][heads * d]: RoPE + norms of q (rewritten) and k, the attention over the cache
   // and this call's keys, the store of k / v into the cache, then out (optional) and op (optional, the
   // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)).
   void attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
-                 float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
+                 const float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
                  void* op);
   // the row kernels of the decode step (rows.hip); device memory. op (optional): also write the result rows as a
   // GEMV operand of op_bytes(w) bytes.
@@ -138,6 +138,8 @@ class Backend {
   size_t op_size_ = 0;
   void* part_ = nullptr;   // attention split partials
   size_t part_size_ = 0;
+  void* kproc_ = nullptr;  // processed k rows of a decode step whose store follows the scan
+  size_t kproc_size_ = 0;
   std::unordered_set<DevKv*> kvs_;
   std::vector<std::pair<std::pair<float, int>, float*>> inv_freq_;
   void* hx_ = nullptr;
