@@ -302,12 +302,12 @@ GemvFn gemv_fn(int r, int t, int threads) {
 bool shape_ok(int r, int t, int s) {
   if (s < 1 || s > 16) return false;
   if (r * t > 12) return false;
-  if (s > 8 && r * t > 4) return false;   // 1024-thread groups get 128 VGPRs per lane
+  if (s > 8 && t > 4) return false;   // 1024-thread groups get 128 VGPRs per lane: T > 4 spills there
   return gemv_fn(r, t, s * 64) != nullptr;
 }
 }  // namespace
 
-GemvShape gemv_shape(int kt, const int* nbs, int nw) {
+GemvShape gemv_shape(int kt, const int* nbs, int nw, int m) {
   if (const char* env = std::getenv("XTG_GEMV_SHAPE")) {   // "R,T": a fixed shape for experiments
     int r = 0, t = 0;
     if (std::sscanf(env, "%d,%d", &r, &t) == 2) {
@@ -315,29 +315,38 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw) {
       if (shape_ok(r, t, s)) return {r, t, s};
     }
   }
-  // Enough waves to cover the chip (256 CUs x 8), then as much work per wave as possible (more loads in
-  // flight per wave, more reuse of the activation operand across row-blocks).
+  // Measured on MI355X (rotated cold weights, launch-shape sweeps over the decode projections): many row-blocks
+  // want two k-tiles per wave with two row-blocks per wave (four at M >= 4, where the activation operand is
+  // wider and reused across more rows); few row-blocks want four k-tiles per wave and one row-block.
+  int nb = 0;
+  for (int i = 0; i < nw; ++i) nb += nbs[i];
+  const bool many = nb >= 512;
+  const int t = many && kt <= 32 ? 2 : 4;
+  const int r = many ? (m >= 4 ? 4 : 2) : 1;
+  const int s = (kt + t - 1) / t;
+  if (shape_ok(r, t, s)) return {r, t, s};
+  // otherwise: enough waves to cover the chip (256 CUs x 8), then as much work per wave as possible
   GemvShape best{1, 1, std::min(16, kt)};
   long best_waves = -1, best_rt = 0;
-  for (int r : {4, 2, 1})
-    for (int t : {8, 6, 4, 3, 2, 1}) {
-      const int s = (kt + t - 1) / t;
-      if (!shape_ok(r, t, s)) continue;
+  for (int rr : {4, 2, 1})
+    for (int tt : {8, 6, 4, 3, 2, 1}) {
+      const int ss = (kt + tt - 1) / tt;
+      if (!shape_ok(rr, tt, ss)) continue;
       long wgs = 0;
-      for (int i = 0; i < nw; ++i) wgs += (nbs[i] + r - 1) / r;
-      const long waves = wgs * s;
+      for (int i = 0; i < nw; ++i) wgs += (nbs[i] + rr - 1) / rr;
+      const long waves = wgs * ss;
       const bool full = waves >= 2048, best_full = best_waves >= 2048;
       bool take;
       if (full != best_full)
         take = full;
       else if (full)
-        take = r * t > best_rt || (r * t == best_rt && waves < best_waves);
+        take = rr * tt > best_rt || (rr * tt == best_rt && waves < best_waves);
       else
         take = waves > best_waves;
       if (take) {
-        best = {r, t, s};
+        best = {rr, tt, ss};
         best_waves = waves;
-        best_rt = r * t;
+        best_rt = rr * tt;
       }
     }
   return best;
@@ -353,7 +362,7 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
     XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
     nbs[i] = c.w[i]->nb;
   }
-  const GemvShape sh = gemv_shape(kt, nbs, c.nw);
+  const GemvShape sh = gemv_shape(kt, nbs, c.nw, c.m);
   int wgs = 0;
   for (int i = 0; i < c.nw; ++i) {
     a.tiles[i] = c.w[i]->tiles;

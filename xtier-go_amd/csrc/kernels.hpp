@@ -54,7 +54,7 @@ struct GemvCall {
 struct GemvShape {
   int r = 1, t = 1, s = 1;
 };
-GemvShape gemv_shape(int kt, const int* nbs, int nw);
+GemvShape gemv_shape(int kt, const int* nbs, int nw, int m);
 std::string launch_gemv(const GemvCall& c, hipStream_t stream);
 
 }  // namespace xtg::hip
