@@ -4,7 +4,7 @@
 Workload (one step): the three projection shapes of one synthetic 4B-shaped layer -- QKV (N=5120, K=3072),
 fused gate/up (2 x N=8192, K=3072, one launch) and down (N=3072, K=8192) -- each at M=1 (decode) and at M=8
 (the speculative-verify batch): 6 calls, each = activation-operand prep + the GEMV kernel. Weights follow the
-BASELINE distributions (uniform E2M1 codes, |N(0,1)|*0.05 E4M3 scales, tensor scale 1.0); activations are unit
+benchmark distributions (uniform E2M1 codes, |N(0,1)|*0.05 E4M3 scales, tensor scale 1.0); activations are unit
 BF16 rows. Consecutive calls read different copies of their weights, rotating over >= 1 GiB, so every launch
 streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed from HIP graphs (one per
 rotation phase), so host launch cost does not set the pace.

@@ -88,22 +88,24 @@ int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void
 /* ------------------------------------------------------------------------------------------- KV caches */
 
 /* Replaces xtg::KvCache(kv_heads, head_dim, slots, ring, dtype) (kv.h:24, kv.cpp:42-63): ring > 0 makes a ring of
- * `ring` slots (slot = position mod ring), else a linear cache of `slots` positions, in device memory. BF16 only
- * (dtype XTG_KV_BF16). Every slot starts empty. NULL on failure. */
+ * `ring` slots (slot = position mod ring), else a linear cache of `slots` positions, in device memory: BF16
+ * (XTG_KV_BF16) or E4M3 codes with one FP32 scale per (position, KV head) (XTG_KV_FP8). Every slot starts empty.
+ * NULL on failure. */
 xtg_hip_kv* xtg_hip_kv_create(xtg_hip* h, int kv_heads, int head_dim, int64_t slots, int ring, int dtype, char* err,
                               int err_len);
 void xtg_hip_kv_destroy(xtg_hip* h, xtg_hip_kv* kv);
 /* Replaces KvCache::store (kv.h:35, kv.cpp:75-112): rows of positions pos .. pos + n - 1 from device FP32 k, v
- * [n][kv_heads][head_dim], rounded to BF16 (nearest even); a ring keeps the last `ring` rows; queued. A linear
- * cache refuses positions beyond its capacity ("KV cache full"). */
+ * [n][kv_heads][head_dim], rounded to BF16 (nearest even), or for FP8 scaled by amax / 448 of each (row, head)
+ * and rounded as kv.cpp:19-40 does; a ring keeps the last `ring` rows; queued. A linear cache refuses positions
+ * beyond its capacity ("KV cache full"). */
 int xtg_hip_kv_store(xtg_hip* h, xtg_hip_kv* kv, int64_t pos, int n, const float* k, const float* v, char* err,
                      int err_len);
 /* Replaces KvCache::load (kv.h:37, kv.cpp:114-138): FP32 K and V rows of head `head` for positions p0 .. p1 - 1
  * into host k, v [p1 - p0][head_dim]; waits for queued work. */
 int xtg_hip_kv_load(xtg_hip* h, const xtg_hip_kv* kv, int head, int64_t p0, int64_t p1, float* k, float* v, char* err,
                     int err_len);
-/* Replaces KvCache::save / restore / release (kv.h:45-48): the whole cache (K, V and slot positions) as
- * xtg_hip_kv_bytes() host bytes and back; release empties every slot. */
+/* Replaces KvCache::save / restore / release (kv.h:45-48): the whole cache (K, V, FP8 scales and slot positions,
+ * in the device layout) as xtg_hip_kv_bytes() host bytes and back; release empties every slot. */
 int64_t xtg_hip_kv_bytes(xtg_hip* h, const xtg_hip_kv* kv);
 int xtg_hip_kv_save(xtg_hip* h, const xtg_hip_kv* kv, void* out, size_t bytes, char* err, int err_len);
 int xtg_hip_kv_restore(xtg_hip* h, xtg_hip_kv* kv, const void* in, size_t bytes, char* err, int err_len);
@@ -165,6 +167,7 @@ typedef struct xtg_dory_config {
   int window, ring_slots;          /* sliding window and the ring size of a sliding sublayer's cache */
   int64_t context;                 /* capacity of a full-attention cache */
   float theta_sliding, theta_full; /* RoPE theta per kind */
+  int kv_dtype;                    /* XTG_KV_BF16 or XTG_KV_FP8 (dory.cpp:141, 159-161) for every cache */
 } xtg_dory_config;
 /* One physical sublayer (dory.cpp:332-364) with the scale vectors already folded as the model constructor does
  * (qscale = (sqk * sqrt(d) / init_range)^2, gscale likewise, sg / su times sqrt(hidden), lr = |alpha * alpha_init /
@@ -182,7 +185,7 @@ typedef struct xtg_dory_layer {
 typedef struct xtg_hip_dory xtg_hip_dory;
 /* Replaces the DoryModel constructor's weight preparation (dory.cpp:365-371) and the GpuDorySession constructor
  * (dory.cpp:1043-1084): prepares every weight and the NVFP4 LM head [vocab][hidden], uploads the vectors and
- * logit_scale [vocab], creates the caches (BF16; sliding sublayers: rings of ring_slots). NULL on failure. The
+ * logit_scale [vocab], creates the caches (kv_dtype; sliding sublayers: rings of ring_slots). NULL on failure. The
  * host weights must stay alive and unchanged while the session exists (they key the prepared copies). */
 xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xtg_dory_layer* layers,
                                   const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len);

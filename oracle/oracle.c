@@ -695,7 +695,7 @@ xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, co
     for (int i = 0; i < inst; ++i)
       d->caches[(size_t)d->attn_of[l] * (size_t)c->loops + (size_t)i] =
           xo_kv_create(c->kv_heads, c->head_dim, c->context, layers[l].kind == XO_SLIDING ? c->ring_slots : 0,
-                       XO_KV_BF16);
+                       c->kv_dtype);
   }
   return d;
 }

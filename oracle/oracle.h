@@ -116,6 +116,7 @@ typedef struct xo_dory_config {
   int window, ring_slots;          /* sliding window and its ring size */
   int64_t context;                 /* linear cache capacity */
   float theta_sliding, theta_full;
+  int kv_dtype;                    /* XO_KV_BF16 | XO_KV_FP8 for every cache (dory.cpp:141, 159-161) */
 } xo_dory_config;
 typedef struct xo_dory xo_dory;
 /* Layers and vectors are borrowed (they must outlive the model); per_loop KV mode: a recurrent attention sublayer

@@ -33,7 +33,7 @@ class DoryConfig(ctypes.Structure):
     """xo_dory_config."""
     _fields_ = [(n, _I) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "n_in", "n_rec", "n_out",
                                   "loops", "window", "ring_slots")] + \
-               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F)]
+               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F), ("kv_dtype", _I)]
 
 
 class DoryLayer(ctypes.Structure):
@@ -265,6 +265,18 @@ class KvCache:
         v = np.empty_like(k)
         (ref().xr_kv_load if self.use_ref else oracle().xo_kv_load)(self.h, h, p0, p1, k.ctypes.data, v.ctypes.data)
         return k, v
+
+    def scales(self):
+        """An FP8 cache's K and V scales [slots][kv_heads] (copies)."""
+        n = self.slots * self.kv_heads
+        out = []
+        for f in (oracle().xo_kv_kscale, oracle().xo_kv_vscale):
+            p = f(self.h)
+            if not p:
+                raise ValueError("not an FP8 cache")
+            out.append(np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), (n,)).copy()
+                       .reshape(self.slots, self.kv_heads))
+        return out[0], out[1]
 
 
 def attention(q, k, v, cache, pos0, heads, kv_heads, head_dim, window=0, scale=None, pool_size=8, threads=8,

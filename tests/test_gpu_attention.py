@@ -1,14 +1,19 @@
 """GPU parity of the device KV cache (xtg_hip_kv_*) and decode attention (xtg_hip_attention) against the oracle's
 KvCache + attention (engine/src/kv.cpp:75-286) and ring mask (npu/xtg_npu.cpp:236-258), on the same seeded inputs.
 
-Bars: KV store / load bit-exact (BF16 round to nearest even); attention rel-L2 <= 1e-5 against the oracle and
-max |err| <= 2e-5 against an FP64 softmax of exactly what the cache holds (tests/kernels_test.cpp:103-183's bar);
-for the sharp cases (scores up to ~20) rel-L2 <= 5e-5 against the oracle, whose own FP32 error is of that order.
+Bars: KV store / load bit-exact (BF16 round to nearest even; FP8 codes and per-(position, head) scales as
+kv.cpp:19-40, 94-108 make them); attention rel-L2 <= 1e-5 against the oracle and max |err| <= 2e-5 against an FP64
+softmax of exactly what the cache holds (tests/kernels_test.cpp:103-183's bar); for the sharp cases (scores up to
+~20) rel-L2 <= 5e-5 against the oracle, whose own FP32 error is of that order.
 """
+import glob
+import os
+
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
 def rel_l2(y, ref):
@@ -37,7 +42,7 @@ def naive(q, Kc, Vc, pos0, heads, kvh, window, scale):
     return out
 
 
-def run_case(hip, orc, cached, n_q, window, heads, kvh, d, scale, rng, ring=None, qmul=1.0, unit=False):
+def run_case(hip, orc, cached, n_q, window, heads, kvh, d, scale, rng, ring=None, qmul=1.0, unit=False, fp8=False):
     total = cached + n_q
     if unit:
         K = rng.standard_normal((total, kvh, d)).astype(np.float32)
@@ -52,8 +57,8 @@ def run_case(hip, orc, cached, n_q, window, heads, kvh, d, scale, rng, ring=None
         q = rng.uniform(-1, 1, (n_q, heads, d)).astype(np.float32)
     q = (q * np.float32(qmul)).astype(np.float32)
     ring = ring if ring is not None else (window if window > 0 else 0)
-    oc = orc.KvCache(kvh, d, total + 8, ring=ring)
-    dc = hip.kv_cache(kvh, d, total + 8, ring=ring)
+    oc = orc.KvCache(kvh, d, total + 8, ring=ring, fp8=fp8)
+    dc = hip.kv_cache(kvh, d, total + 8, ring=ring, dtype=1 if fp8 else 0)
     for p in range(0, cached, 50):
         n = min(50, cached - p)
         oc.store(p, K[p:p + n], V[p:p + n])
@@ -65,22 +70,28 @@ def run_case(hip, orc, cached, n_q, window, heads, kvh, d, scale, rng, ring=None
     out = dout.numpy()
     for a in (dq, dk, dv, dout):
         a.free()
-    Kc, Vc = bf16_round(K), bf16_round(V)
-    Kc[cached:], Vc[cached:] = K[cached:], V[cached:]
-    sc = scale if scale is not None else float(np.float32(1) / np.sqrt(np.float32(d)))
-    exact = naive(q, Kc, Vc, cached, heads, kvh, window, sc) if cached * n_q <= 400000 else None
+    exact = None
+    if cached * n_q <= 400000:   # FP64 softmax over what the cache holds (the oracle's load) and the FP32 own rows
+        Kc, Vc = K.copy(), V.copy()
+        lo = max(0, cached - ring) if ring > 0 else 0
+        for h in range(kvh):
+            if cached > lo:
+                Kc[lo:cached, h], Vc[lo:cached, h] = oc.load(h, lo, cached)
+        sc = scale if scale is not None else float(np.float32(1) / np.sqrt(np.float32(d)))
+        exact = naive(q, Kc, Vc, cached, heads, kvh, window, sc)
     dc.destroy()
     return out, ref, exact
 
 
-# tests/kernels_test.cpp:139-141 (BF16 cache; the FP8 cases run with a BF16 cache here, FP8 being a later row)
-KT = [(300, 1, 0), (5000, 1, 0), (300, 1, 64), (100, 37, 0), (100, 37, 16), (0, 20, 0), (900, 3, 128)]
+# tests/kernels_test.cpp:139-141: (cached, n_q, window, FP8 cache)
+KT = [(300, 1, 0, 0), (5000, 1, 0, 0), (300, 1, 64, 0), (100, 37, 0, 0), (100, 37, 16, 1), (0, 20, 0, 1),
+      (900, 3, 128, 1)]
 
 
-@pytest.mark.parametrize("cached,n_q,window", KT)
-def test_reference_unit_cases(hip, orc, cached, n_q, window):
+@pytest.mark.parametrize("cached,n_q,window,fp8", KT)
+def test_reference_unit_cases(hip, orc, cached, n_q, window, fp8):
     rng = np.random.default_rng(42 + cached + n_q + window)
-    out, ref, exact = run_case(hip, orc, cached, n_q, window, 8, 2, 64, 0.7, rng)
+    out, ref, exact = run_case(hip, orc, cached, n_q, window, 8, 2, 64, 0.7, rng, fp8=bool(fp8))
     assert rel_l2(out, ref) <= 1e-5
     if exact is not None:
         assert np.max(np.abs(out - exact)) < 2e-5
@@ -95,6 +106,53 @@ def test_decode_global_cache(hip, orc, ctx, n_q):
     assert rel_l2(out, ref) <= 1e-5
 
 
+@pytest.mark.parametrize("ctx,n_q", [(4096, 1), (4096, 8), (32768, 1), (32768, 8)])
+def test_decode_global_cache_fp8(hip, orc, ctx, n_q):
+    """Config 2's shapes over an FP8 cache (the reference Dory's default KV dtype, dory.cpp:141)."""
+    rng = np.random.default_rng(ctx + n_q + 1)
+    out, ref, _ = run_case(hip, orc, ctx, n_q, 0, 32, 8, 128, None, rng, unit=True, fp8=True)
+    assert rel_l2(out, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("n_q", [1, 5, 16])
+def test_head_dim_128_group_8_fp8(hip, orc, n_q):
+    """Eight q heads per KV head (two q-blocks per MFMA pass at 4+ rows), FP8, a sharp softmax, 700 cached keys."""
+    rng = np.random.default_rng(70 + n_q)
+    out, ref, exact = run_case(hip, orc, 700, n_q, 0, 16, 2, 128, None, rng, unit=True, qmul=30.0, fp8=True)
+    assert rel_l2(out, ref) <= 5e-5
+    assert rel_l2(out, exact) <= max(3 * rel_l2(ref, exact), 1e-5)
+
+
+def test_golden_vectors(hip):
+    """The committed golden vectors (the seven unit cases and the 320-position configs, made by the oracle and
+    checked against the compiled reference) through the device cache and attention."""
+    files = sorted(glob.glob(os.path.join(GOLDEN, "attn_*.npz")))
+    assert files
+    for f in files:
+        d = np.load(f)
+        cached, window, fp8 = int(d["cached"]), int(d["window"]), int(d["fp8"])
+        heads, kvh, hd = int(d["heads"]), int(d["kv_heads"]), int(d["head_dim"])
+        q = d["q"]
+        n_q = q.shape[0]
+        if fp8:
+            K, V = d["K"], d["V"]
+        else:
+            K = np.concatenate([(d["Kc"].astype(np.uint32) << 16).view(np.float32), d["Kn"]])
+            V = np.concatenate([(d["Vc"].astype(np.uint32) << 16).view(np.float32), d["Vn"]])
+        dc = hip.kv_cache(kvh, hd, cached + n_q + 8, ring=window if window > 0 else 0, dtype=fp8)
+        for p in range(0, cached, 50):
+            n = min(50, cached - p)
+            dc.store_host(p, K[p:p + n], V[p:p + n])
+        dq, dk, dv = hip.array(q), hip.array(np.ascontiguousarray(K[cached:])), hip.array(np.ascontiguousarray(V[cached:]))
+        dout = hip.array(shape=q.shape)
+        hip.attention(dc, dq, dk, dv, dout, n_q, cached, heads, window=window, scale=float(d["scale"]))
+        out = dout.numpy()
+        for a in (dq, dk, dv, dout):
+            a.free()
+        dc.destroy()
+        assert rel_l2(out, d["out"]) <= 1e-5, f
+
+
 @pytest.mark.parametrize("qmul", [60.0, 250.0])
 def test_decode_sharp_softmax(hip, orc, qmul):
     """Peaked softmax (q scaled so that scores reach tens): the three-term q split keeps FP32-level scores."""
@@ -106,8 +164,8 @@ def test_decode_sharp_softmax(hip, orc, qmul):
     assert err_gpu <= max(3 * err_cpu, 1e-5), (err_gpu, err_cpu)
 
 
-@pytest.mark.parametrize("window", [1024, 1088])
-def test_ring_wrapped_config3(hip, orc, wl, window):
+@pytest.mark.parametrize("window,fp8", [(1024, False), (1088, False), (1024, True)])
+def test_ring_wrapped_config3(hip, orc, wl, window, fp8):
     """Config 3: a 1088-slot ring after 40000 positions (holding 38912..39999), 8 rows at 40000..40007, q and k
     produced by RoPE (theta 1e6) -> per-head norm -> q * qscale ~ U(0.5, 1.5); the mask is rebuilt from the stored
     slot positions. Compared with the oracle's position form and its slot form."""
@@ -116,8 +174,8 @@ def test_ring_wrapped_config3(hip, orc, wl, window):
     Kr = wl.unit_heads(rng, (ring, kvh), d)
     Vr = wl.unit_heads(rng, (ring, kvh), d)
     first = pos0 - ring
-    oc = orc.KvCache(kvh, d, 0, ring=ring)
-    dc = hip.kv_cache(kvh, d, 0, ring=ring)
+    oc = orc.KvCache(kvh, d, 0, ring=ring, fp8=fp8)
+    dc = hip.kv_cache(kvh, d, 0, ring=ring, dtype=1 if fp8 else 0)
     oc.store(first, Kr, Vr)
     dc.store_host(first, Kr, Vr)
     slot_pos = np.full(ring, -1, np.int64)
@@ -164,6 +222,87 @@ def test_kv_store_load_roundtrip(hip, orc):
             np.testing.assert_array_equal(gk, ok)
             np.testing.assert_array_equal(gv, ov)
         dc.destroy()
+
+
+def fp8_rows(rng, n, kvh, d):
+    """Random rows plus rows that hit the E4M3 rounding's edges: amax 448 (scale 1) with values at ties between
+    codes (normal and subnormal), below the smallest subnormal step, an all-zero row (scale 1), a row of one
+    nonzero, negative zero, and a NaN (its code 0x7f; the scale ignores it)."""
+    K = rng.standard_normal((n, kvh, d)).astype(np.float32)
+    ties = np.array([448.0, 1.0625, 1.1875, -1.0625, 3 * 2.0 ** -10, 5 * 2.0 ** -10, 2.0 ** -11, 2.0 ** -12,
+                     0.0, -0.0, 2.0 ** -6 - 2.0 ** -11, 15.5 * 2.0 ** -10, 240.0, 232.0, 0.5 + 2.0 ** -5,
+                     300.0], np.float32)
+    K[0, 0, :ties.size] = ties
+    K[0, 0, ties.size:] = 0.25
+    K[1, 0] = 0.0
+    K[2, 0] = 0.0
+    K[2, 0, 5] = -3e-5
+    K[3, 0, 7] = np.nan
+    return K
+
+
+def test_kv_fp8_store_load_bits(hip, orc):
+    """FP8 rows stored in chunks (linear and ring) and by one long call: the loaded values (code value x scale)
+    equal the oracle's bit for bit, and so do the per-(position, head) scales in the device snapshot."""
+    rng = np.random.default_rng(15)
+    kvh, d, n = 4, 128, 300
+    K = fp8_rows(rng, n, kvh, d)
+    V = fp8_rows(rng, n, kvh, d)[::-1].copy()
+    for ring, chunk in ((0, 37), (96, 37), (0, n)):
+        oc = orc.KvCache(kvh, d, 320, ring=ring, fp8=True)
+        dc = hip.kv_cache(kvh, d, 320, ring=ring, dtype=1)
+        for p in range(0, n, chunk):
+            oc.store(p, K[p:p + chunk], V[p:p + chunk])
+            dc.store_host(p, K[p:p + chunk], V[p:p + chunk])
+        lo = n - ring if ring else 0
+        for h in range(kvh):
+            ok, ov = oc.load(h, lo, n)
+            gk, gv = dc.load(h, lo, n)
+            np.testing.assert_array_equal(gk.view(np.uint32), ok.view(np.uint32))
+            np.testing.assert_array_equal(gv.view(np.uint32), ov.view(np.uint32))
+        # snapshot: K codes, V codes, K scales [head][slot], V scales, slot positions
+        snap = dc.save()
+        slots = ring if ring else 320
+        pad = (slots + 31) // 32 * 32
+        data = kvh * pad * d
+        ks = snap[2 * data:2 * data + 4 * kvh * pad].view(np.float32).reshape(kvh, pad)
+        vs = snap[2 * data + 4 * kvh * pad:2 * data + 8 * kvh * pad].view(np.float32).reshape(kvh, pad)
+        oks, ovs = oc.scales()
+        for p in range(lo, n):
+            s = p % slots if ring else p
+            np.testing.assert_array_equal(ks[:, s], oks[s])
+            np.testing.assert_array_equal(vs[:, s], ovs[s])
+        dc.destroy()
+
+
+def test_kv_fp8_save_restore(hip, orc):
+    rng = np.random.default_rng(16)
+    kvh, d = 2, 64
+    K = rng.standard_normal((64, kvh, d)).astype(np.float32)
+    V = rng.standard_normal((64, kvh, d)).astype(np.float32)
+    dc = hip.kv_cache(kvh, d, 0, ring=40, dtype=1)
+    oc = orc.KvCache(kvh, d, 0, ring=40, fp8=True)
+    dc.store_host(0, K[:40], V[:40])
+    oc.store(0, K[:40], V[:40])
+    snap = dc.save()
+    assert snap.nbytes == 2 * kvh * 64 * d + 2 * 4 * kvh * 64 + 4 * 64
+    dc.store_host(40, K[40:], V[40:])
+    dc.restore(snap)
+    for h in range(kvh):
+        gk, gv = dc.load(h, 0, 40)
+        ok, ov = oc.load(h, 0, 40)
+        np.testing.assert_array_equal(gk, ok)
+        np.testing.assert_array_equal(gv, ov)
+    dc.release()
+    q = rng.standard_normal((1, 4, d)).astype(np.float32)
+    dq, dk, dv = hip.array(q), hip.array(K[:1]), hip.array(V[:1])
+    dout = hip.array(shape=(1, 4, d))
+    hip.attention(dc, dq, dk, dv, dout, 1, 40, 4)   # released: only the call's own key is visible
+    out = dout.numpy()
+    np.testing.assert_allclose(out[0], np.repeat(V[:1, :, :], 2, axis=1)[0], rtol=0, atol=1e-6)
+    for a in (dq, dk, dv, dout):
+        a.free()
+    dc.destroy()
 
 
 def test_kv_ring_long_store_keeps_last(hip, orc):

@@ -1,8 +1,8 @@
 """GPU parity of the decode-step composition (xtg_hip_dory_*) against the oracle's (packs/dory/dory.cpp:467-578),
 on the same seeded random-init weights and inputs.
 
-Bars: logits rel-L2 <= 1e-3 and the same argmax per row (the north star's bounds), step after step; a graph
-replay of a step gives the eager step's logits exactly.
+Bars: logits rel-L2 <= 1e-3 and the same argmax per row (the parity bounds of the decode step), step after step; a
+graph replay of a step gives the eager step's logits exactly.
 """
 import numpy as np
 import pytest
@@ -199,5 +199,64 @@ def test_ring_smaller_than_window_plus_chunk(hip, orc, wl):
     got = device_steps(hip, w, x, 0, 8)
     e = rel_l2(got, want)
     print("ring 64 / window 60 chunks of 8: logits rel-L2 %.2e" % e)
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def oracle_steps(orc, wl, w, x, chunk):
+    ref = orc.Dory(w, wl)
+    return np.concatenate([ref.forward(x[r:r + chunk], r) for r in range(0, x.shape[0], chunk)])
+
+
+@pytest.mark.parametrize("window,chunk", [(48, 8), (48, 1), (60, 8)])
+def test_fp8_caches_chunks_and_steps(hip, orc, wl, window, chunk):
+    """FP8 KV caches (the reference Dory's default, dory.cpp:141) in a tiny model over 72 positions: chunks of 8
+    and one-row steps with window 48 (the producer quantises each row's own key into the cache before the scan)
+    and window 60 in 64-slot rings (the store follows the scan); logits against the oracle's FP8 caches.
+    Default scales: rel-L2 <= 1e-3. Sharpened (q x 40, lr ~ U(0.3, 0.7)) a key whose E4M3 rounding flips on a
+    1-ulp difference upstream moves the logits by ~1e-3, so there the bar is 3x the oracle's own change when its
+    inputs are perturbed by 1 ulp (about 1.4e-3, against 2.6e-4 with BF16 caches)."""
+    for sharp in (False, True):
+        w = wl.DoryWeights(dict(wl.DORY_TINY, window=window, kv_dtype=1), seed=25, context=128)
+        if sharp:
+            w = sharpened(w)
+        x = unit_rows(np.random.default_rng(8), 72, w.cfg["hidden"])
+        want = oracle_steps(orc, wl, w, x, chunk)
+        got = device_steps(hip, w, x, 0, chunk)
+        e = rel_l2(got, want)
+        bar = 1e-3
+        if sharp:
+            ulp = np.random.default_rng(1).choice([-1.0, 1.0], x.shape).astype(np.float32) * np.float32(2.0 ** -23)
+            xp = (x * (1 + ulp)).astype(np.float32)
+            bar = max(bar, 3 * rel_l2(oracle_steps(orc, wl, w, xp, chunk), want))
+        print("FP8 caches, window %d, chunks of %d, sharp %s: logits rel-L2 %.2e (bar %.2e)" % (window, chunk, sharp,
+                                                                                              e, bar))
+        assert e <= bar
+        assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def test_4b_decode_step_fp8(hip, orc, wl, model_4b):
+    """Config 4's model at a 4K context over FP8 caches: one verify step (m = 8) against the oracle's."""
+    import copy
+    w0, _, _, ctx = model_4b
+    w = copy.copy(w0)
+    w.cfg = dict(w0.cfg, kv_dtype=1)
+    ref = orc.Dory(w, wl)
+    dev = hip.dory(w)
+    try:
+        fill_context(w, ctx, ref, dev, hip, np.random.default_rng(6))
+        H, V = w.cfg["hidden"], w.cfg["vocab"]
+        x = unit_rows(np.random.default_rng(15), 8, H)
+        dx = hip.array(x)
+        dl = hip.array(shape=(8, V))
+        dev.forward(dx, 8, ctx, dl)
+        got = dl.numpy()
+        want = ref.forward(x, ctx, threads=16)
+        dx.free()
+        dl.free()
+    finally:
+        dev.destroy()
+    e = rel_l2(got, want)
+    print("4B step m=8, FP8 caches: logits rel-L2 %.2e" % e)
     assert e <= 1e-3
     assert (got.argmax(1) == want.argmax(1)).all()

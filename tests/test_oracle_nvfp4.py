@@ -60,7 +60,7 @@ def test_closed_form_catches_dropped_scale(orc, wl):
 
 @pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_matmul_config_shapes_vs_fp64(orc, wl, m):
-    """BASELINE distributions (uniform codes, |N(0,1)|*0.05 scales, unit BF16 rows) at K = N = 3072."""
+    """The benchmark distributions (uniform codes, |N(0,1)|*0.05 scales, unit BF16 rows) at K = N = 3072."""
     rng = np.random.default_rng(100 + m)
     codes, scales, g = wl.nvfp4_weight(rng, 3072, 3072)
     x = wl.bf16_to_f32(wl.unit_rows_bf16(rng, m, 3072))

@@ -13,6 +13,13 @@
 //      dim 16 dd + i of slots {4 g .. 4 g + 3, 16 + 4 g .. 16 + 4 g + 3}: the A operand (dims x keys) of the P.V
 //      product whose B operand (keys x queries) is exactly what each lane holds of the score tile's accumulator.
 //   slot_pos: int32 per slot, -1 = never written.
+// An FP8 cache (E4M3 codes, one FP32 scale per (slot, head): kv.cpp:94-108) keeps the same operand order with one
+// byte per element, two operands per 16-byte lane load:
+//   K: per head, per block of 16 slots, per pair of 32-wide chunks: 64 lanes x 16 bytes, bytes 0..7 of lane (g, i)
+//      the BF16 layout's entry for chunk 2 cp, bytes 8..15 for chunk 2 cp + 1.
+//   V: per head, per tile of 32 slots, per pair of 16-wide blocks: 64 lanes x 16 bytes likewise.
+//   kscale / vscale: FP32 [head][slot]. Codes become BF16 exactly (v_cvt_scalef32_pk_bf16_fp8 with scale 1); the
+//   key scale multiplies the scores, the value scale the softmax weights of the P.V product (not their sum).
 //
 // Work (flash decoding, partials laid out as AttnPlan says):
 //   attn_scan_kernel: a work-group of 4 waves per (KV head, split of the key tiles). Scores S^T = K Q^T with the q
@@ -30,6 +37,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "attention.hpp"
 #include "common.hpp"
@@ -60,8 +68,25 @@ __host__ __device__ inline size_t v_index(int h, int slot, int dim, int slots_pa
          size_t(e);
 }
 
+__host__ __device__ inline size_t k8_index(int h, int slot, int dim, int slots_pad, int d) {
+  const int b = slot >> 4, i = slot & 15, c = dim >> 5, g = (dim & 31) >> 3, e = dim & 7;
+  return ((((size_t(h) * size_t(slots_pad >> 4) + size_t(b)) * size_t(d >> 6) + size_t(c >> 1)) * 64 +
+           size_t(g * 16 + i)) * 16) + size_t((c & 1) * 8 + e);
+}
+
+__host__ __device__ inline size_t v8_index(int h, int slot, int dim, int slots_pad, int d) {
+  const int t = slot >> 5, kk = slot & 31;
+  const int half = kk >> 4, r = kk & 15;
+  const int g = r >> 2, e = half * 4 + (r & 3);
+  const int dd = dim >> 4, i = dim & 15;
+  return ((((size_t(h) * size_t(slots_pad >> 5) + size_t(t)) * size_t(d >> 5) + size_t(dd >> 1)) * 64 +
+           size_t(g * 16 + i)) * 16) + size_t((dd & 1) * 8 + e);
+}
+
 size_t kv_k_index(int h, int slot, int dim, int slots_pad, int d) { return k_index(h, slot, dim, slots_pad, d); }
 size_t kv_v_index(int h, int slot, int dim, int slots_pad, int d) { return v_index(h, slot, dim, slots_pad, d); }
+size_t kv_k8_index(int h, int slot, int dim, int slots_pad, int d) { return k8_index(h, slot, dim, slots_pad, d); }
+size_t kv_v8_index(int h, int slot, int dim, int slots_pad, int d) { return v8_index(h, slot, dim, slots_pad, d); }
 
 __device__ inline uint16_t f32_to_bf16_bits(float f) {
   // round to nearest even; a NaN stays a quiet NaN (engine/include/xtg/fp.h:18-24)
@@ -72,6 +97,49 @@ __device__ inline uint16_t f32_to_bf16_bits(float f) {
 }
 
 __device__ inline float bf16_bits_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// The cache's E4M3 rounding (engine/src/kv.cpp:19-40): below 2^-6 the value counts subnormal steps of 2^-9 (ties
+// to even); above, the FP32 mantissa is rounded to 3 bits (ties to even) and rebiased, capped at 0x7e (448); NaN
+// gives 0x7f with the sign.
+__device__ inline uint32_t e4m3_code(float x) {
+  const uint32_t bits = __float_as_uint(x);
+  const uint32_t sign = (bits >> 24) & 0x80u, a = bits & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  uint32_t code;
+  if (a < 0x3c800000u) {
+    const float t = __uint_as_float(a) * 512.f;   // exact: a power-of-two factor below the overflow range
+    const float lo = floorf(t);
+    const float frac = t - lo;                    // exact
+    code = uint32_t(lo);
+    code += (frac > 0.5f || (frac == 0.5f && (code & 1u))) ? 1u : 0u;
+  } else {
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    code = code > 0x7eu ? 0x7eu : code;
+  }
+  return sign | code;
+}
+
+// One row of D values held by a wave (lane l: dims l + 64 u) into an FP8 cache: scale amax / 448 (1 for an
+// all-zero row), codes of value / scale (kv.cpp:94-108). Every lane of the wave must be active.
+template <int D>
+__device__ inline void store_fp8_row(const float (&x)[D / 64], uint8_t* __restrict__ c8, float* __restrict__ scl,
+                                     bool is_v, int h, int slot, int slots_pad) {
+  const int lane = threadIdx.x & 63;
+  float am = 0.f;
+#pragma unroll
+  for (int u = 0; u < D / 64; ++u) am = fmaxf(am, fabsf(x[u]));
+  am = wave_max(am);
+  const float sc = am > 0.f ? am / 448.f : 1.f;
+  const float inv = 1.f / sc;
+#pragma unroll
+  for (int u = 0; u < D / 64; ++u) {
+    const int dim = lane + 64 * u;
+    const size_t at = is_v ? v8_index(h, slot, dim, slots_pad, D) : k8_index(h, slot, dim, slots_pad, D);
+    c8[at] = uint8_t(e4m3_code(x[u] * inv));
+  }
+  if (lane == 0) scl[size_t(h) * size_t(slots_pad) + size_t(slot)] = sc;
+}
 
 // ------------------------------------------------------------------------------------------------------ store
 
@@ -95,15 +163,56 @@ __global__ void __launch_bounds__(256) kv_store_kernel(const float* __restrict__
   if (h == 0 && dim == 0) slot_pos[slot] = int(p);
 }
 
-void launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const float* v, hipStream_t stream) {
+// FP8: one wave per (row kept, head, K or V), 4 waves per work-group; slot_pos by the first wave of each row.
+template <int D>
+__global__ void __launch_bounds__(256) kv_store_fp8_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                           uint8_t* __restrict__ ck, uint8_t* __restrict__ cv,
+                                                           float* __restrict__ ks, float* __restrict__ vs,
+                                                           int* __restrict__ slot_pos, long long pos, int first,
+                                                           int n, int kv_heads, long long slots, int ring,
+                                                           int slots_pad) {
+  const long long wv = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long long per_row = 2LL * kv_heads;
+  if (wv >= (long long)(n - first) * per_row) return;   // whole waves leave together
+  const int r = first + int(wv / per_row);
+  const int rem = int(wv % per_row), h = rem >> 1;
+  const bool is_v = rem & 1;
+  const long long p = pos + r;
+  const int slot = int(ring ? p % slots : p);
+  const float* src = (is_v ? v : k) + (size_t(r) * size_t(kv_heads) + size_t(h)) * D;
+  float x[D / 64];
+#pragma unroll
+  for (int u = 0; u < D / 64; ++u) x[u] = src[(threadIdx.x & 63) + 64 * u];
+  store_fp8_row<D>(x, is_v ? cv : ck, is_v ? vs : ks, is_v, h, slot, slots_pad);
+  if (rem == 0 && (threadIdx.x & 63) == 0) slot_pos[slot] = int(p);
+}
+
+std::string launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const float* v,
+                            hipStream_t stream) {
   int first = 0;
   if (c.ring && n > c.slots) first = int(n - c.slots);
+  if (n - first <= 0) return std::string();
+  if (c.fp8) {
+    const long long waves = (long long)(n - first) * 2 * c.kv_heads;
+    const dim3 grid{unsigned((waves + 3) / 4)}, block{256};
+    auto* ck = static_cast<uint8_t*>(c.k);
+    auto* cv = static_cast<uint8_t*>(c.v);
+    if (c.head_dim == 64)
+      hipLaunchKernelGGL(kv_store_fp8_kernel<64>, grid, block, 0, stream, k, v, ck, cv, c.kscale, c.vscale,
+                         c.slot_pos, pos, first, n, c.kv_heads, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
+    else
+      hipLaunchKernelGGL(kv_store_fp8_kernel<128>, grid, block, 0, stream, k, v, ck, cv, c.kscale, c.vscale,
+                         c.slot_pos, pos, first, n, c.kv_heads, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
+    HIP_CHECK(hipGetLastError());
+    return strf("kv_store_fp8_kernel<%d>", c.head_dim);
+  }
   const long long total = (long long)(n - first) * c.kv_heads * c.head_dim;
-  if (total <= 0) return;
   const unsigned blocks = unsigned((total + 255) / 256);
-  hipLaunchKernelGGL(kv_store_kernel, dim3(blocks), dim3(256), 0, stream, k, v, c.k, c.v, c.slot_pos, pos, first, n,
-                     c.kv_heads, c.head_dim, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
+  hipLaunchKernelGGL(kv_store_kernel, dim3(blocks), dim3(256), 0, stream, k, v, static_cast<uint16_t*>(c.k),
+                     static_cast<uint16_t*>(c.v), c.slot_pos, pos, first, n, c.kv_heads, c.head_dim,
+                     (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
   HIP_CHECK(hipGetLastError());
+  return "kv_store_kernel";
 }
 
 
@@ -114,6 +223,8 @@ struct ScanArgs {
   const uint4* ck;         // cache, operand layout
   const uint4* cv;
   const int* slot_pos;
+  const float* kscale;     // FP8 caches: [head][slot] scales
+  const float* vscale;
   float* acc;              // the block's partials: record (h, s, c) at (h * splits1 + s) * qpad + c
   float* ml;
   int n_rows, row0, heads, group, window, splits, splits1, qpad, slots_pad;
@@ -240,7 +351,124 @@ __device__ inline void scan_tile(const KvTile<D>& T, const bf16x8 (&qop)[QB][D /
   }
 }
 
+// The FP8 form of a tile: K as two 16-slot blocks of D / 64 lane loads (two operands each), V as D / 32 loads, the
+// positions and the key and value scales of the lane's 8 keys.
+template <int D>
+struct KvTile8 {
+  uint4 k[2][D / 64];
+  uint4 v[D / 32];
+  int4 p0, p1;
+  float4 ks0, ks1, vs0, vs1;
+};
+
+template <int D>
+__device__ inline void load_tile(KvTile8<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
+                                 const int* __restrict__ slot_pos, const float* __restrict__ ks,
+                                 const float* __restrict__ vs, int t, int lane) {
+  constexpr int NP = D / 64, NV = D / 32;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int c = 0; c < NP; ++c) T.k[b][c] = kb[(size_t(2 * t + b) * NP + size_t(c)) * 64 + size_t(lane)];
+#pragma unroll
+  for (int dp = 0; dp < NV; ++dp) T.v[dp] = vb[(size_t(t) * NV + size_t(dp)) * 64 + size_t(lane)];
+  const int at = t * kTile + 4 * (lane >> 4);
+  T.p0 = *reinterpret_cast<const int4*>(slot_pos + at);
+  T.p1 = *reinterpret_cast<const int4*>(slot_pos + at + 16);
+  T.ks0 = *reinterpret_cast<const float4*>(ks + at);
+  T.ks1 = *reinterpret_cast<const float4*>(ks + at + 16);
+  T.vs0 = *reinterpret_cast<const float4*>(vs + at);
+  T.vs1 = *reinterpret_cast<const float4*>(vs + at + 16);
+}
+
+// 8 E4M3 codes (two dwords, element 0 in the low byte) as 8 BF16 values, exactly.
+__device__ inline bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+  const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, false);
+  const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, true);
+  const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, false);
+  const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// scan_tile for an FP8 tile: each K and V operand is converted once and used for every q-block; the raw scores are
+// multiplied by their key's scale before the mask, and the softmax weights by their value's scale on the way into
+// the P.V product (the running sum takes them unscaled).
 template <int D, int QB>
+__device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D / 32][3], const int (&lo)[QB],
+                                 ScanState<D, QB>& st, int pos0) {
+  constexpr int NP = D / 64, NV = D / 32;
+  const int kpos[8] = {T.p0.x, T.p0.y, T.p0.z, T.p0.w, T.p1.x, T.p1.y, T.p1.z, T.p1.w};
+  const float ks[8] = {T.ks0.x, T.ks0.y, T.ks0.z, T.ks0.w, T.ks1.x, T.ks1.y, T.ks1.z, T.ks1.w};
+  const float vs[8] = {T.vs0.x, T.vs0.y, T.vs0.z, T.vs0.w, T.vs1.x, T.vs1.y, T.vs1.z, T.vs1.w};
+  f32x4 s[QB][2];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) s[qb][0] = s[qb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      const bf16x8 A0 = fp8x8_to_bf16(T.k[b][c].x, T.k[b][c].y);   // chunk 2 c
+      const bf16x8 A1 = fp8x8_to_bf16(T.k[b][c].z, T.k[b][c].w);   // chunk 2 c + 1
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int term = 0; term < 3; ++term) {
+          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, qop[qb][2 * c][term], s[qb][b], 0, 0, 0);
+          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, qop[qb][2 * c + 1][term], s[qb][b], 0, 0, 0);
+        }
+    }
+  bf16x8 phi[QB], plo[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    float sc[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sc[e] = kpos[e] >= lo[qb] && kpos[e] < pos0 ? s[qb][e >> 2][e & 3] * ks[e] : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = xor32_max(xor16_max(mx));
+    const float m_new = fmaxf(st.m[qb], mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = exp2_fast(st.m[qb] - m_ref);
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = exp2_fast(sc[e] - m_ref);
+      ps += p[e];
+    }
+    ps = xor32_sum(xor16_sum(ps));
+    st.l[qb] = st.l[qb] * corr + ps;
+    st.m[qb] = m_new;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pv = p[e] * vs[e];
+      const __bf16 h = to_bf16(pv);
+      phi[qb][e] = h;
+      plo[qb][e] = to_bf16(pv - of_bf16(h));
+    }
+    if (__ballot(corr != 1.f)) {
+#pragma unroll
+      for (int dd = 0; dd < D / 16; ++dd) st.acc[qb][dd] *= corr;
+    }
+  }
+#pragma unroll
+  for (int dp = 0; dp < NV; ++dp) {
+    const bf16x8 A0 = fp8x8_to_bf16(T.v[dp].x, T.v[dp].y);   // block 2 dp
+    const bf16x8 A1 = fp8x8_to_bf16(T.v[dp].z, T.v[dp].w);   // block 2 dp + 1
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      f32x4& x0 = st.acc[qb][2 * dp];
+      f32x4& x1 = st.acc[qb][2 * dp + 1];
+      x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, phi[qb], x0, 0, 0, 0);
+      x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, plo[qb], x0, 0, 0, 0);
+      x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, phi[qb], x1, 0, 0, 0);
+      x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, plo[qb], x1, 0, 0, 0);
+    }
+  }
+}
+
+template <int D, int QB, bool F8>
 __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a) {
   constexpr int NC = D / 32, ND = D / 16;
   extern __shared__ float lds[];
@@ -255,11 +483,22 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
   const int t_begin = a.tile_lo + int((long long)a.tiles * split / a.splits);
   const int t_end = a.tile_lo + int((long long)a.tiles * (split + 1) / a.splits);
   const int t_last = t_end - 1;
-  const uint4* kbase = a.ck + size_t(kvh) * size_t(a.slots_pad / kTile) * size_t(2 * NC) * 64;
-  const uint4* vbase = a.cv + size_t(kvh) * size_t(a.slots_pad / kTile) * size_t(ND) * 64;
+  // per head: slots_pad * D elements of K and of V (16 bytes = 8 BF16 or 16 FP8 per uint4)
+  const size_t head_u4 = size_t(a.slots_pad) * size_t(D) / (F8 ? 16 : 8);
+  const uint4* kbase = a.ck + size_t(kvh) * head_u4;
+  const uint4* vbase = a.cv + size_t(kvh) * head_u4;
+  const float* ksb = F8 ? a.kscale + size_t(kvh) * size_t(a.slots_pad) : nullptr;
+  const float* vsb = F8 ? a.vscale + size_t(kvh) * size_t(a.slots_pad) : nullptr;
+  using Tile = std::conditional_t<F8, KvTile8<D>, KvTile<D>>;
+  auto load = [&](Tile& T, int tt) {
+    if constexpr (F8)
+      load_tile<D>(T, kbase, vbase, a.slot_pos, ksb, vsb, tt, lane);
+    else
+      load_tile<D>(T, kbase, vbase, a.slot_pos, tt, lane);
+  };
   int t = t_begin + wave;
-  KvTile<D> A, B;
-  load_tile<D>(A, kbase, vbase, a.slot_pos, min(t, t_last), lane);
+  Tile A, B;
+  load(A, min(t, t_last));
 
   // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale * log2(e),
   // three terms. lo: the first stored position the column sees.
@@ -293,11 +532,11 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
     for (int dd = 0; dd < ND; ++dd) st.acc[qb][dd] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   while (t < t_end) {
-    load_tile<D>(B, kbase, vbase, a.slot_pos, min(t + kWaves, t_last), lane);
+    load(B, min(t + kWaves, t_last));
     scan_tile<D, QB>(A, qop, lo, st, a.pos0);
     t += kWaves;
     if (t >= t_end) break;
-    load_tile<D>(A, kbase, vbase, a.slot_pos, min(t + kWaves, t_last), lane);
+    load(A, min(t + kWaves, t_last));
     scan_tile<D, QB>(B, qop, lo, st, a.pos0);
     t += kWaves;
   }
@@ -444,8 +683,11 @@ struct ProduceArgs {
   float scale;
   const float* inv_freq;   // [d / 2]
   const float* qscale;     // [heads * d] or NULL
-  uint16_t* ck;
-  uint16_t* cv;
+  void* ck;                // the cache (BF16, or FP8 codes with the scales below)
+  void* cv;
+  float* kscale;
+  float* vscale;
+  int fp8;
   int* slot_pos;
   long long slots;
   int ring, slots_pad;
@@ -456,7 +698,8 @@ struct ProduceArgs {
 
 // One work-group per (KV head, query row r). It takes RoPE + justnorm of row r's q heads of this KV head (times
 // qscale, written back in place) and of the k rows j0 .. r that row r attends to: each work-group recomputes
-// those few rows rather than wait for another's. Row r's k and v go to the cache (store set) and row r's
+// those few rows rather than wait for another's. Row r's k and v go to the cache (store set: BF16 as they are
+// made, FP8 rows by waves 0 and 1 from LDS once complete, since their scale needs the whole row) and row r's
 // processed k to kout (if any); then each q-col of row r gets its own-key partial from one wave. VPW: the rows
 // a wave handles (at least ceil((group + r + 1 - j0) / 4)); they are processed without a branch, so their
 // reductions interleave.
@@ -518,8 +761,8 @@ __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceAr
     const int e = tid + u * kT;
     if (e < nk * D) {
       sv[e] = vv[u];
-      if (a.store && e / D == nk - 1)
-        a.cv[v_index(kvh, int(slot_r), e % D, a.slots_pad, D)] = f32_to_bf16_bits(vv[u]);
+      if (a.store && !a.fp8 && e / D == nk - 1)
+        static_cast<uint16_t*>(a.cv)[v_index(kvh, int(slot_r), e % D, a.slots_pad, D)] = f32_to_bf16_bits(vv[u]);
     }
   }
   if (a.store && kvh == 0 && tid == 0) a.slot_pos[slot_r] = int(a.pos0 + r);
@@ -555,14 +798,23 @@ __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceAr
           p[lane] = o1;
           p[lane + HALF] = o2;
         }
-        if (a.store) {
-          a.ck[k_index(kvh, int(slot_r), lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
-          a.ck[k_index(kvh, int(slot_r), lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
+        if (a.store && !a.fp8) {
+          uint16_t* ck = static_cast<uint16_t*>(a.ck);
+          ck[k_index(kvh, int(slot_r), lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
+          ck[k_index(kvh, int(slot_r), lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
         }
       }
     }
   }
   __syncthreads();
+  if (a.store && a.fp8 && wave < 2) {   // row r's k (wave 0) and v (wave 1), complete in LDS
+    const float* src = (wave == 0 ? sk : sv) + (nk - 1) * D;
+    float x[D / 64];
+#pragma unroll
+    for (int u = 0; u < D / 64; ++u) x[u] = src[lane + 64 * u];
+    store_fp8_row<D>(x, static_cast<uint8_t*>(wave == 0 ? a.ck : a.cv), wave == 0 ? a.kscale : a.vscale, wave == 1,
+                     kvh, int(slot_r), a.slots_pad);
+  }
 
   // own keys: q-col (r, hg) sees keys j0 .. r
   for (int hg = wave; hg < a.group; hg += kWaves) {
@@ -741,10 +993,11 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
 namespace {
 
 using ScanFn = void (*)(const ScanArgs);
-ScanFn scan_fn(int d, int qb) {
-#define XTG_CASE(D, Q) \
-  if (d == D && qb == Q) return attn_scan_kernel<D, Q>;
-  XTG_CASE(64, 1) XTG_CASE(64, 2) XTG_CASE(128, 1) XTG_CASE(128, 2)
+ScanFn scan_fn(int d, int qb, bool f8) {
+#define XTG_CASE(D, Q, F) \
+  if (d == D && qb == Q && f8 == F) return attn_scan_kernel<D, Q, F>;
+  XTG_CASE(64, 1, false) XTG_CASE(64, 2, false) XTG_CASE(128, 1, false) XTG_CASE(128, 2, false)
+  XTG_CASE(64, 1, true) XTG_CASE(64, 2, true) XTG_CASE(128, 1, true) XTG_CASE(128, 2, true)
 #undef XTG_CASE
   return nullptr;
 }
@@ -753,7 +1006,7 @@ ScanFn scan_fn(int d, int qb) {
 // has 160 KiB per CU): raise the kernel's limit once.
 void allow_lds(ScanFn fn, size_t lds) {
   if (lds <= 65536) return;
-  static thread_local ScanFn raised[4] = {};
+  static thread_local ScanFn raised[8] = {};
   for (ScanFn f : raised)
     if (f == fn) return;
   HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -800,6 +1053,8 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const flo
   a.ck = reinterpret_cast<const uint4*>(c.k);
   a.cv = reinterpret_cast<const uint4*>(c.v);
   a.slot_pos = c.slot_pos;
+  a.kscale = c.kscale;
+  a.vscale = c.vscale;
   a.acc = part_acc(p, part, b);
   a.ml = part_ml(p, part, b);
   a.n_rows = nr;
@@ -816,14 +1071,14 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const flo
   a.pos0 = int(pos0);
   a.scale2 = scale * kLog2e;
   const int qb = (nr * p.group + 15) / 16;
-  ScanFn fn = scan_fn(c.head_dim, qb);
+  ScanFn fn = scan_fn(c.head_dim, qb, c.fp8);
   XTG_CHECK(fn != nullptr, "attention: no kernel for head_dim %d and %d column blocks", c.head_dim, qb);
   const int nd = c.head_dim / 16;
   const size_t lds = (size_t(kWaves) * qb * 2 * 16 + size_t(kWaves) * qb * nd * 64 * 4) * sizeof(float);
   allow_lds(fn, lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits)), dim3(kWaves * 64), lds, stream, a);
   HIP_CHECK(hipGetLastError());
-  return strf("attn_scan_kernel<%d, %d>", c.head_dim, qb);
+  return strf("attn_scan_kernel<%d, %d, %s>", c.head_dim, qb, c.fp8 ? "true" : "false");
 }
 
 std::string launch_attn_own(const AttnPlan& p, int b, const float* q, const float* k, const float* v, int n_q,
@@ -881,6 +1136,9 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const
   a.qscale = qscale;
   a.ck = c.k;
   a.cv = c.v;
+  a.kscale = c.kscale;
+  a.vscale = c.vscale;
+  a.fp8 = c.fp8 ? 1 : 0;
   a.slot_pos = c.slot_pos;
   a.slots = c.slots;
   a.ring = c.ring ? 1 : 0;

@@ -16,18 +16,27 @@ struct DevKv {
   long long slots = 0;
   int slots_pad = 0;
   bool ring = false;
-  uint16_t* k = nullptr;    // kv_heads * slots_pad * head_dim BF16
-  uint16_t* v = nullptr;
-  int* slot_pos = nullptr;  // slots_pad, -1 = empty
+  bool fp8 = false;            // E4M3 codes + an FP32 scale per (slot, head) (kv.cpp:94-108), else BF16
+  void* k = nullptr;           // kv_heads * slots_pad * head_dim elements (2 bytes BF16, 1 byte FP8)
+  void* v = nullptr;
+  float* kscale = nullptr;     // FP8: [kv_heads][slots_pad]
+  float* vscale = nullptr;
+  int* slot_pos = nullptr;     // slots_pad, -1 = empty
+  size_t elems() const { return size_t(kv_heads) * size_t(slots_pad) * size_t(head_dim); }
+  size_t data_bytes() const { return elems() * (fp8 ? 1 : 2); }
+  size_t scale_bytes() const { return fp8 ? size_t(kv_heads) * size_t(slots_pad) * sizeof(float) : 0; }
 };
 
-// Element offsets of (head, slot, dim) in the K and V layouts (for host-side load / save).
+// Element offsets of (head, slot, dim) in the K and V layouts (for host-side load / save), BF16 and FP8.
 size_t kv_k_index(int h, int slot, int dim, int slots_pad, int d);
 size_t kv_v_index(int h, int slot, int dim, int slots_pad, int d);
+size_t kv_k8_index(int h, int slot, int dim, int slots_pad, int d);
+size_t kv_v8_index(int h, int slot, int dim, int slots_pad, int d);
 
 // The rows of positions pos .. pos + n - 1 from FP32 device k, v [n][kv_heads][head_dim]; a ring keeps the last
 // `slots` rows.
-void launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const float* v, hipStream_t stream);
+std::string launch_kv_store(const DevKv& c, long long pos, int n, const float* k, const float* v,
+                            hipStream_t stream);
 
 // How one attention call (n_q query rows at pos0) is cut up. Query rows go in blocks of rpb rows (at most 32
 // (row, head) columns per KV head); each block's key tiles go to `splits` work-groups per KV head, plus one more

@@ -32,9 +32,9 @@ Backend::~Backend() {
   for (void* p : {op_, hx_, hy_, part_, kproc_})
     if (p) (void)hipFree(p);
   for (DevKv* c : kvs_) {
-    (void)hipFree(c->k);
-    (void)hipFree(c->v);
-    (void)hipFree(c->slot_pos);
+    for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
+                    static_cast<void*>(c->slot_pos)})
+      if (p) (void)hipFree(p);
     delete c;
   }
   for (auto& f : inv_freq_) (void)hipFree(f.second);
@@ -139,7 +139,7 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
 
 DevKv* Backend::kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype) {
   XTG_CHECK(!capturing_, "kv_create: not during a graph capture");
-  XTG_CHECK(dtype == XTG_KV_BF16, "kv_create: only BF16 caches are implemented on the device");
+  XTG_CHECK(dtype == XTG_KV_BF16 || dtype == XTG_KV_FP8, "kv_create: unknown KV dtype %d", dtype);
   XTG_CHECK(head_dim == 64 || head_dim == 128, "kv_create: head_dim %d (64 or 128)", head_dim);
   XTG_CHECK(kv_heads > 0, "kv_create: %d KV heads", kv_heads);
   const long long n = ring > 0 ? ring : slots;   // kv.cpp:42-44: ring > 0 gives a ring of `ring` slots
@@ -150,17 +150,37 @@ DevKv* Backend::kv_create(int kv_heads, int head_dim, long long slots, int ring,
   c->slots = n;
   c->slots_pad = int((n + 31) / 32 * 32);
   c->ring = ring > 0;
-  const size_t elems = size_t(kv_heads) * size_t(c->slots_pad) * size_t(head_dim);
-  HIP_CHECK(hipMalloc(&c->k, elems * 2));
-  HIP_CHECK(hipMalloc(&c->v, elems * 2));
-  HIP_CHECK(hipMalloc(&c->slot_pos, size_t(c->slots_pad) * sizeof(int)));
-  HIP_CHECK(hipMemsetAsync(c->k, 0, elems * 2, stream_));
-  HIP_CHECK(hipMemsetAsync(c->v, 0, elems * 2, stream_));
-  HIP_CHECK(hipMemsetAsync(c->slot_pos, 0xff, size_t(c->slots_pad) * sizeof(int), stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
+  c->fp8 = dtype == XTG_KV_FP8;
+  try {
+    HIP_CHECK(hipMalloc(&c->k, c->data_bytes()));
+    HIP_CHECK(hipMalloc(&c->v, c->data_bytes()));
+    HIP_CHECK(hipMalloc(&c->slot_pos, size_t(c->slots_pad) * sizeof(int)));
+    if (c->fp8) {
+      HIP_CHECK(hipMalloc(&c->kscale, c->scale_bytes()));
+      HIP_CHECK(hipMalloc(&c->vscale, c->scale_bytes()));
+    }
+  } catch (...) {
+    for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
+                    static_cast<void*>(c->slot_pos)})
+      if (p) (void)hipFree(p);
+    throw;
+  }
   DevKv* p = c.release();
   kvs_.insert(p);
+  clear_kv(p);
   return p;
+}
+
+// Every slot empty: zero codes and scales, slot positions -1.
+void Backend::clear_kv(DevKv* c) {
+  HIP_CHECK(hipMemsetAsync(c->k, 0, c->data_bytes(), stream_));
+  HIP_CHECK(hipMemsetAsync(c->v, 0, c->data_bytes(), stream_));
+  if (c->fp8) {
+    HIP_CHECK(hipMemsetAsync(c->kscale, 0, c->scale_bytes(), stream_));
+    HIP_CHECK(hipMemsetAsync(c->vscale, 0, c->scale_bytes(), stream_));
+  }
+  HIP_CHECK(hipMemsetAsync(c->slot_pos, 0xff, size_t(c->slots_pad) * sizeof(int), stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 void Backend::kv_destroy(DevKv* c) {
@@ -168,9 +188,9 @@ void Backend::kv_destroy(DevKv* c) {
   if (it == kvs_.end()) return;
   XTG_CHECK(!capturing_, "kv_destroy: not during a graph capture");
   HIP_CHECK(hipStreamSynchronize(stream_));
-  HIP_CHECK(hipFree(c->k));
-  HIP_CHECK(hipFree(c->v));
-  HIP_CHECK(hipFree(c->slot_pos));
+  for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
+                  static_cast<void*>(c->slot_pos)})
+    if (p) HIP_CHECK(hipFree(p));
   kvs_.erase(it);
   delete c;
 }
@@ -183,11 +203,25 @@ void Backend::kv_store(DevKv* c, long long pos, int n, const float* k, const flo
   XTG_CHECK(pos + n < (1LL << 31), "kv_store: position %lld beyond the 32-bit slot positions", pos + n);
   if (n == 0) return;
   XTG_CHECK(k && v, "kv_store: NULL rows");
-  timed([&] {
-    launch_kv_store(*c, pos, n, k, v, stream_);
-    return std::string("kv_store_kernel");
-  });
+  timed([&] { return launch_kv_store(*c, pos, n, k, v, stream_); });
 }
+
+namespace {
+
+// The value of an E4M3 code (engine/src/fp.cpp:12-28: bias 7, subnormal step 2^-9, 0x7f / 0xff NaN).
+float e4m3_value(uint8_t b) {
+  const int e = (b >> 3) & 15, m = b & 7;
+  float mag;
+  if ((b & 0x7f) == 0x7f)
+    mag = NAN;
+  else if (e == 0)
+    mag = std::ldexp(float(m), -9);
+  else
+    mag = std::ldexp(1.f + float(m) / 8.f, e - 7);
+  return (b & 0x80) ? -mag : mag;
+}
+
+}  // namespace
 
 void Backend::kv_load(const DevKv* c, int h, long long p0, long long p1, float* k, float* v) {
   XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "kv_load: unknown cache");
@@ -195,58 +229,82 @@ void Backend::kv_load(const DevKv* c, int h, long long p0, long long p1, float* 
   XTG_CHECK(h >= 0 && h < c->kv_heads && p0 >= 0 && p0 <= p1, "kv_load: head %d, positions %lld..%lld", h, p0, p1);
   XTG_CHECK(c->ring || p1 <= c->slots, "kv_load: position %lld beyond the cache", p1);
   const int d = c->head_dim;
-  const size_t elems = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(d);
-  std::vector<uint16_t> hk(elems), hv(elems);
-  HIP_CHECK(hipMemcpyAsync(hk.data(), c->k, elems * 2, hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipMemcpyAsync(hv.data(), c->v, elems * 2, hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
+  std::vector<uint8_t> snap(kv_bytes(c));
+  snapshot(c, snap.data());
+  const uint8_t* hk = snap.data();
+  const uint8_t* hv = hk + c->data_bytes();
+  const float* ks = reinterpret_cast<const float*>(hv + c->data_bytes());
+  const float* vs = ks + size_t(c->kv_heads) * size_t(c->slots_pad);
   for (long long p = p0; p < p1; ++p) {
     const int slot = int(c->ring ? p % c->slots : p);
-    for (int j = 0; j < d; ++j) {
-      const uint32_t kb = uint32_t(hk[kv_k_index(h, slot, j, c->slots_pad, d)]) << 16;
-      const uint32_t vb = uint32_t(hv[kv_v_index(h, slot, j, c->slots_pad, d)]) << 16;
-      std::memcpy(k + size_t(p - p0) * size_t(d) + size_t(j), &kb, 4);
-      std::memcpy(v + size_t(p - p0) * size_t(d) + size_t(j), &vb, 4);
+    float* ok = k + size_t(p - p0) * size_t(d);
+    float* ov = v + size_t(p - p0) * size_t(d);
+    if (c->fp8) {
+      const size_t si = size_t(h) * size_t(c->slots_pad) + size_t(slot);
+      for (int j = 0; j < d; ++j) {   // kv.cpp:128-136: code value times the row's scale
+        ok[j] = e4m3_value(hk[kv_k8_index(h, slot, j, c->slots_pad, d)]) * ks[si];
+        ov[j] = e4m3_value(hv[kv_v8_index(h, slot, j, c->slots_pad, d)]) * vs[si];
+      }
+    } else {
+      const uint16_t* bk = reinterpret_cast<const uint16_t*>(hk);
+      const uint16_t* bv = reinterpret_cast<const uint16_t*>(hv);
+      for (int j = 0; j < d; ++j) {
+        const uint32_t kb = uint32_t(bk[kv_k_index(h, slot, j, c->slots_pad, d)]) << 16;
+        const uint32_t vb = uint32_t(bv[kv_v_index(h, slot, j, c->slots_pad, d)]) << 16;
+        std::memcpy(ok + j, &kb, 4);
+        std::memcpy(ov + j, &vb, 4);
+      }
     }
   }
 }
 
+// Snapshot layout: K data, V data, K scales, V scales (FP8 only), slot positions, each in its device layout.
 size_t Backend::kv_bytes(const DevKv* c) const {
-  return size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 4 + size_t(c->slots_pad) * sizeof(int);
+  return 2 * c->data_bytes() + 2 * c->scale_bytes() + size_t(c->slots_pad) * sizeof(int);
+}
+
+void Backend::snapshot(const DevKv* c, void* out) {
+  char* o = static_cast<char*>(out);
+  const size_t db = c->data_bytes(), sb = c->scale_bytes();
+  HIP_CHECK(hipMemcpyAsync(o, c->k, db, hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipMemcpyAsync(o + db, c->v, db, hipMemcpyDeviceToHost, stream_));
+  if (sb) {
+    HIP_CHECK(hipMemcpyAsync(o + 2 * db, c->kscale, sb, hipMemcpyDeviceToHost, stream_));
+    HIP_CHECK(hipMemcpyAsync(o + 2 * db + sb, c->vscale, sb, hipMemcpyDeviceToHost, stream_));
+  }
+  HIP_CHECK(hipMemcpyAsync(o + 2 * db + 2 * sb, c->slot_pos, size_t(c->slots_pad) * sizeof(int),
+                           hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 void Backend::kv_save(const DevKv* c, void* out, size_t bytes) {
   XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "kv_save: unknown cache");
   XTG_CHECK(!capturing_, "kv_save: not during a graph capture");
   XTG_CHECK(bytes == kv_bytes(c), "kv_save: %zu bytes for a cache of %zu", bytes, kv_bytes(c));
-  const size_t half = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 2;
-  char* o = static_cast<char*>(out);
-  HIP_CHECK(hipMemcpyAsync(o, c->k, half, hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipMemcpyAsync(o + half, c->v, half, hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipMemcpyAsync(o + 2 * half, c->slot_pos, size_t(c->slots_pad) * sizeof(int), hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
+  snapshot(c, out);
 }
 
 void Backend::kv_restore(DevKv* c, const void* in, size_t bytes) {
   XTG_CHECK(kvs_.count(c), "kv_restore: unknown cache");
   XTG_CHECK(!capturing_, "kv_restore: not during a graph capture");
   XTG_CHECK(bytes == kv_bytes(c), "KV snapshot of %zu bytes for a cache of %zu", bytes, kv_bytes(c));
-  const size_t half = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim) * 2;
   const char* s = static_cast<const char*>(in);
-  HIP_CHECK(hipMemcpyAsync(c->k, s, half, hipMemcpyHostToDevice, stream_));
-  HIP_CHECK(hipMemcpyAsync(c->v, s + half, half, hipMemcpyHostToDevice, stream_));
-  HIP_CHECK(hipMemcpyAsync(c->slot_pos, s + 2 * half, size_t(c->slots_pad) * sizeof(int), hipMemcpyHostToDevice, stream_));
+  const size_t db = c->data_bytes(), sb = c->scale_bytes();
+  HIP_CHECK(hipMemcpyAsync(c->k, s, db, hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(c->v, s + db, db, hipMemcpyHostToDevice, stream_));
+  if (sb) {
+    HIP_CHECK(hipMemcpyAsync(c->kscale, s + 2 * db, sb, hipMemcpyHostToDevice, stream_));
+    HIP_CHECK(hipMemcpyAsync(c->vscale, s + 2 * db + sb, sb, hipMemcpyHostToDevice, stream_));
+  }
+  HIP_CHECK(hipMemcpyAsync(c->slot_pos, s + 2 * db + 2 * sb, size_t(c->slots_pad) * sizeof(int),
+                           hipMemcpyHostToDevice, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 void Backend::kv_release(DevKv* c) {
   XTG_CHECK(kvs_.count(c), "kv_release: unknown cache");
   XTG_CHECK(!capturing_, "kv_release: not during a graph capture");
-  const size_t elems = size_t(c->kv_heads) * size_t(c->slots_pad) * size_t(c->head_dim);
-  HIP_CHECK(hipMemsetAsync(c->k, 0, elems * 2, stream_));
-  HIP_CHECK(hipMemsetAsync(c->v, 0, elems * 2, stream_));
-  HIP_CHECK(hipMemsetAsync(c->slot_pos, 0xff, size_t(c->slots_pad) * sizeof(int), stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
+  clear_kv(c);
 }
 
 void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
@@ -296,11 +354,7 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
   if (p.splits > 0)
     for (int b = 0; b < p.blocks; ++b)
       timed([&] { return launch_attn_scan(*c, p, b, q, m, heads, pos0, window, scale, part, stream_); });
-  if (!store_first)
-    timed([&] {
-      launch_kv_store(*c, pos0, m, kout, v, stream_);
-      return std::string("kv_store_kernel");
-    });
+  if (!store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
   timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
 

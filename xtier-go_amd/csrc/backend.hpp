@@ -113,6 +113,8 @@ class Backend {
 
  private:
   void ensure(void*& buf, size_t& size, size_t need);
+  void clear_kv(DevKv* c);
+  void snapshot(const DevKv* c, void* out);   // kv_bytes(c) host bytes
   hipEvent_t event();
   struct Pending {
     std::string name;

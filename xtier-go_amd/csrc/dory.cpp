@@ -66,7 +66,7 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
       const int inst = L.recurrent ? c.loops : 1;
       for (int i = 0; i < c.loops; ++i)
         caches_.push_back(i < inst ? b_.kv_create(c.kv_heads, c.head_dim, c.context,
-                                                   L.w.kind == XTG_DORY_SLIDING ? c.ring_slots : 0, XTG_KV_BF16)
+                                                   L.w.kind == XTG_DORY_SLIDING ? c.ring_slots : 0, c.kv_dtype)
                                    : nullptr);
       b_.inv_freq(L.w.kind == XTG_DORY_SLIDING ? c.theta_sliding : c.theta_full, c.head_dim);
     }

@@ -143,8 +143,9 @@ def dory_kinds(cfg):
 
 class DoryWeights:
     """Random-init weights of a Dory-shaped model with the scale vectors already folded (as the reference's model
-    constructor leaves them): NVFP4 projections with the BASELINE distributions; qscale, gscale ~ U(0.5, 1.5);
-    sg, su ~ U(5, 15) (so silu sees arguments of order one); lr ~ U(0.02, 0.1); logit_scale ~ U(0.5, 1.5)."""
+    constructor leaves them): NVFP4 projections with the benchmark distributions (uniform codes, |N(0,1)|*0.05
+    scales); qscale, gscale ~ U(0.5, 1.5); sg, su ~ U(5, 15) (so silu sees arguments of order one);
+    lr ~ U(0.02, 0.1); logit_scale ~ U(0.5, 1.5)."""
 
     def __init__(self, cfg, seed=0, context=4096, workers=8):
         import concurrent.futures
@@ -210,7 +211,7 @@ def dory_structs(w, nvfp4_type, layer_type, config_type):
     c = w.cfg
     cfg = config_type(c["hidden"], c["ffn"], c["heads"], c["kv_heads"], c["head_dim"], c["vocab"], c["n_in"],
                       c["n_rec"], c["n_out"], c["loops"], c["window"], c["ring_slots"], c["context"],
-                      c["theta_sliding"], c["theta_full"])
+                      c["theta_sliding"], c["theta_full"], c.get("kv_dtype", 0))
     return cfg, arr, nv(w.head)
 
 
