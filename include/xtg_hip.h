@@ -38,6 +38,13 @@ typedef struct xtg_nvfp4 {
   int n_out, k;
 } xtg_nvfp4;
 
+/* A BF16 weight [n_out][k], row-major (a BF16 checkpoint's LM head): field for field xtg::Bf16Weight
+ * (engine/include/xtg/kernels.h:22-25). data is a host pointer; it keys the prepared device copy. */
+typedef struct xtg_bf16 {
+  const uint16_t* data;   /* [n_out][k] BF16 bits */
+  int n_out, k;
+} xtg_bf16;
+
 enum { XTG_X_F32 = 0, XTG_X_BF16 = 1 };   /* activation element type of the device matmul */
 enum { XTG_KV_BF16 = 0, XTG_KV_FP8 = 1 }; /* xtg::KvDtype (engine/include/xtg/kv.h:18) */
 
@@ -84,6 +91,22 @@ size_t xtg_hip_x_operand_bytes(int k);
 int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* op, char* err, int err_len);
 int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* op, int m, float* y, size_t y_offset,
                             char* err, int err_len);
+
+/* ---------------------------------------------------------------------------------------------- BF16 path */
+
+/* Replaces OpenClBackend::prepare(const Bf16Weight&) (opencl.h:33, opencl.cpp:516-521): copy the weight to the
+ * device in the GEMV tile layout. Idempotent, keyed by w->data. n_out > 0 and k % 4 == 0 (as opencl.cpp:519). */
+int xtg_hip_prepare_bf16(xtg_hip* h, const xtg_bf16* w, char* err, int err_len);
+/* Drops the device copy prepared for `data` (0 also when there is none). */
+int xtg_hip_release_bf16(xtg_hip* h, const uint16_t* data, char* err, int err_len);
+/* Replaces xtg::matmul_bf16(ThreadPool&, w, x, m, y) (kernels.h:31, kernels.cpp:140-155) and the host
+ * OpenClBackend::matmul(const Bf16Weight&, x, m, y) (opencl.h:35, opencl.cpp:602-628): y[m][n_out] =
+ * x[m][k] * W^T with FP32 products and sums; x, y host memory; synchronous; m >= 1 (8 rows per pass). */
+int xtg_hip_matmul_bf16(xtg_hip* h, const xtg_bf16* w, const float* x, int m, float* y, char* err, int err_len);
+/* Replaces OpenClBackend::matmul(const Bf16Weight&, Mem x, m, Mem y) (opencl.h:56, opencl.cpp:755-780): device
+ * x ([m][k], FP32 or BF16 per x_dtype) into device y [m][n_out] from y_offset floats. Queued; 1 <= m <= 8. */
+int xtg_hip_matmul_bf16_dev(xtg_hip* h, const xtg_bf16* w, const void* x, int x_dtype, int m, float* y,
+                            size_t y_offset, char* err, int err_len);
 
 /* ------------------------------------------------------------------------------------------- KV caches */
 

@@ -178,6 +178,24 @@ int xo_matmul_nvfp4(const xo_nvfp4* ws, int n_w, const float* x, int m, float* c
   return 0;
 }
 
+int xo_matmul_bf16(const uint16_t* w, int n_out, int k, const float* x, int m, float* y, int threads) {
+  /* engine/src/kernels.cpp:140-155: each weight row converted to FP32, then dot_f32 with every input row */
+  if (n_out <= 0 || k <= 0 || m <= 0) return -1;
+  if (threads < 1) threads = 1;
+#pragma omp parallel num_threads(threads)
+  {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)k);
+#pragma omp for schedule(static)
+    for (int n = 0; n < n_out; ++n) {
+      const uint16_t* r = w + (size_t)n * (size_t)k;
+      for (int j = 0; j < k; ++j) wrow[j] = xo_bf16_to_f32(r[j]);
+      for (int i = 0; i < m; ++i) y[(size_t)i * (size_t)n_out + (size_t)n] = dot_f32(wrow, x + (size_t)i * (size_t)k, k);
+    }
+    free(wrow);
+  }
+  return 0;
+}
+
 /* --------------------------------------------------------------------------------------------- row kernels */
 
 void xo_bf16_row(const uint16_t* table, int64_t row, int width, float* out) {

@@ -41,6 +41,8 @@ void xo_nvfp4_row(const xo_nvfp4* w, int n, float* out);          /* kernels.cpp
 /* kernels.cpp:84-138: m <= 2 decode branch (dot_nvfp4 :48-60), m > 2 prefill branch (nvfp4_row + dot_f32).
  * ys[i] holds m * ws[i].n_out floats. Returns 0, or -1 when the widths differ / k % 16 != 0 (kernels.cpp:86-88). */
 int xo_matmul_nvfp4(const xo_nvfp4* ws, int n_w, const float* x, int m, float* const* ys, int threads);
+int xo_matmul_bf16(const uint16_t* w, int n_out, int k, const float* x, int m, float* y,
+                   int threads);   /* kernels.cpp:140-155 */
 
 /* --- row kernels: engine/src/kernels.cpp:157-234 --- */
 void xo_bf16_row(const uint16_t* table, int64_t row, int width, float* out);               /* :157-160 */

@@ -60,6 +60,7 @@ _ORACLE_SIGS = [
     ("xo_e2m1", _F, [_I]),
     ("xo_nvfp4_row", None, [ctypes.POINTER(Nvfp4), _I, _P]),
     ("xo_matmul_nvfp4", _I, [ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P), _I]),
+    ("xo_matmul_bf16", _I, [_P, _I, _I, _P, _I, _P, _I]),
     ("xo_bf16_row", None, [_P, _I64, _I, _P]),
     ("xo_justnorm", None, [_P, _I, _I]),
     ("xo_slerp_residual", None, [_P, _P, _P, _I, _I]),
@@ -93,6 +94,7 @@ _REF_SIGS = [
     ("xr_bf16_to_f32", _F, [ctypes.c_uint16]),
     ("xr_nvfp4_row", None, [ctypes.POINTER(Nvfp4), _I, _P]),
     ("xr_matmul_nvfp4", _I, [ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P), _I]),
+    ("xr_matmul_bf16", _I, [_P, _I, _I, _P, _I, _P, _I]),
     ("xr_justnorm", None, [_P, _I, _I]),
     ("xr_slerp_residual", None, [_P, _P, _P, _I, _I]),
     ("xr_rope", None, [_P, _I, _I, _I, _I64, _F]),
@@ -155,6 +157,19 @@ def matmul_nvfp4(ws, x, threads=8, use_ref=False):
     if rc != 0:
         raise ValueError("matmul_nvfp4 rejected its arguments")
     return ys
+
+
+def matmul_bf16(w, x, threads=8, use_ref=False):
+    """w: uint16 BF16 bits [n_out][k]; x float32 [m][k]. Returns float32 [m][n_out]."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    x = _f32(x)
+    m, (n, k) = x.shape[0], w.shape
+    assert x.shape[1] == k
+    y = np.empty((m, n), dtype=np.float32)
+    f = ref().xr_matmul_bf16 if use_ref else oracle().xo_matmul_bf16
+    if f(w.ctypes.data, n, k, x.ctypes.data, m, y.ctypes.data, threads) != 0:
+        raise ValueError("matmul_bf16 rejected its arguments")
+    return y
 
 
 def nvfp4_row(codes, scales, glob, n, use_ref=False):

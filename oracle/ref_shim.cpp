@@ -59,6 +59,16 @@ int xr_matmul_nvfp4(const xr_nvfp4* ws, int n_w, const float* x, int m, float* c
   }
 }
 
+int xr_matmul_bf16(const uint16_t* w, int n_out, int k, const float* x, int m, float* y, int threads) {
+  try {
+    xtg::Bf16Weight b{w, n_out, k};
+    xtg::matmul_bf16(pool_of(threads), b, x, m, y);
+    return 0;
+  } catch (...) {
+    return -1;
+  }
+}
+
 void xr_justnorm(float* x, int rows, int width) { xtg::justnorm(x, rows, width); }
 void xr_slerp_residual(float* a, const float* b, const float* lr, int rows, int width) {
   xtg::slerp_residual(a, b, lr, rows, width);

@@ -97,9 +97,31 @@ def write_rows():
     del r
 
 
+def write_bf16():
+    """matmul_bf16 (kernels.cpp:140-155): random BF16 weights (N(0,1) rounded to nearest even) and FP32 rows, at
+    k = 320 (not a multiple of the 128-wide tiles) and k = 260 (k % 8 == 4, the smallest granule the reference's
+    GPU path takes), m = 1, 3, 8."""
+    rng = np.random.default_rng(20261204)
+    for k in (320, 260):
+        w = wl.f32_to_bf16(rng.standard_normal((96, k)).astype(np.float32))
+        arrays = {"w": w}
+        for m in (1, 3, 8):
+            x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+            arrays["x%d" % m] = x
+            arrays["y%d" % m] = orc.matmul_bf16(w, x, threads=4, use_ref=True)
+        np.savez_compressed(os.path.join(HERE, "bf16_k%d.npz" % k), **arrays)
+
+
 def main():
     if not orc.ref_available():
         sys.exit("oracle/_ref/libxtgref.so is missing: run `make -C oracle ref` where the reference tree exists")
+    only = set(sys.argv[1:])   # e.g. "bf16": write that group only
+    if only:
+        if "bf16" in only:
+            write_bf16()
+        print("golden vectors written to", HERE)
+        return
+    write_bf16()
     for name, ws, x in nvfp4_cases():
         ys = orc.matmul_nvfp4(ws, x, use_ref=True, threads=4)
         arrays = {"x": x}

@@ -27,6 +27,11 @@ class Nvfp4(ctypes.Structure):
     _fields_ = [("codes", _P), ("scales", _P), ("glob", ctypes.c_float), ("n_out", _I), ("k", _I)]
 
 
+class Bf16(ctypes.Structure):
+    """xtg_bf16 (same fields as xtg::Bf16Weight, engine/include/xtg/kernels.h:22-25)."""
+    _fields_ = [("data", _P), ("n_out", _I), ("k", _I)]
+
+
 class AttnArgs(ctypes.Structure):
     """xtg_attn_args (the fields of xtg::AttnArgs, engine/include/xtg/kv.h:67-78)."""
     _fields_ = [("n_q", _I), ("pos0", ctypes.c_int64), ("heads", _I), ("kv_heads", _I), ("head_dim", _I),
@@ -60,6 +65,10 @@ SIGNATURES = [
     ("xtg_hip_release_nvfp4", _I, [_P, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P)] + _ERR),
     ("xtg_hip_matmul_nvfp4_dev", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _I, _P, _SZ] + _ERR),
+    ("xtg_hip_prepare_bf16", _I, [_P, ctypes.POINTER(Bf16)] + _ERR),
+    ("xtg_hip_release_bf16", _I, [_P, _P] + _ERR),
+    ("xtg_hip_matmul_bf16", _I, [_P, ctypes.POINTER(Bf16), _P, _I, _P] + _ERR),
+    ("xtg_hip_matmul_bf16_dev", _I, [_P, ctypes.POINTER(Bf16), _P, _I, _I, _P, _SZ] + _ERR),
     ("xtg_hip_kv_create", _P, [_P, _I, _I, _I64, _I, _I] + _ERR),
     ("xtg_hip_kv_destroy", None, [_P, _P]),
     ("xtg_hip_kv_store", _I, [_P, _P, _I64, _I, _P, _P] + _ERR),
@@ -240,6 +249,39 @@ class HipBackend:
         """Queued: the projections of a prepared operand into y (as matmul_dev)."""
         err = _errbuf()
         _check(lib().xtg_hip_matmul_nvfp4_op(self.h, self._hold(ws), len(ws), _ptr(op), m, _ptr(y), y_offset, err,
+                                             len(err)), err)
+
+    # ---- BF16 weights (xtg::Bf16Weight): w is a C-contiguous uint16 array [n_out][k] of BF16 bits
+    def _bf16(self, w):
+        assert w.dtype == np.uint16 and w.ndim == 2 and w.flags.c_contiguous
+        self._weights.setdefault(w.ctypes.data, w)
+        return Bf16(w.ctypes.data, w.shape[0], w.shape[1])
+
+    def prepare_bf16(self, w):
+        err = _errbuf()
+        st = self._bf16(w)
+        _check(lib().xtg_hip_prepare_bf16(self.h, ctypes.byref(st), err, len(err)), err)
+
+    def release_bf16(self, w):
+        err = _errbuf()
+        _check(lib().xtg_hip_release_bf16(self.h, w.ctypes.data, err, len(err)), err)
+        self._weights.pop(w.ctypes.data, None)
+
+    def matmul_bf16(self, w, x):
+        """Host-synchronous matmul_bf16: x float32 [m][k] -> float32 [m][n_out]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty((x.shape[0], w.shape[0]), dtype=np.float32)
+        err = _errbuf()
+        st = self._bf16(w)
+        _check(lib().xtg_hip_matmul_bf16(self.h, ctypes.byref(st), x.ctypes.data, x.shape[0], y.ctypes.data, err,
+                                         len(err)), err)
+        return y
+
+    def matmul_bf16_dev(self, w, x, x_dtype, m, y, y_offset=0):
+        """Queued device matmul_bf16: x, y are device addresses."""
+        err = _errbuf()
+        st = self._bf16(w)
+        _check(lib().xtg_hip_matmul_bf16_dev(self.h, ctypes.byref(st), _ptr(x), x_dtype, m, _ptr(y), y_offset, err,
                                              len(err)), err)
 
     def alloc(self, nbytes):

@@ -28,8 +28,9 @@ Backend::~Backend() {
   if (stream_) (void)hipStreamSynchronize(stream_);
   for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.first);
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
+  for (auto& kv : bf16_weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, hx_, hy_, part_, kproc_})
+  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_})
     if (p) (void)hipFree(p);
   for (DevKv* c : kvs_) {
     for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
@@ -133,6 +134,76 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
   c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
   c.col_scale[0] = col_scale;
   timed([&] { return launch_gemv(c, stream_); });
+}
+
+// ------------------------------------------------------------------------------------------------ BF16 path
+
+const PackedBf16& Backend::prepare(const xtg_bf16& w) {
+  XTG_CHECK(w.data, "prepare_bf16: NULL data");
+  auto it = bf16_weights_.find(w.data);
+  if (it != bf16_weights_.end()) {
+    XTG_CHECK(it->second.n == w.n_out && it->second.k == w.k,
+              "prepare_bf16: weight %p seen before as %dx%d, now %dx%d", static_cast<const void*>(w.data),
+              it->second.n, it->second.k, w.n_out, w.k);
+    return it->second;
+  }
+  XTG_CHECK(w.n_out > 0 && w.k > 0 && w.k % 4 == 0, "prepare_bf16: invalid BF16 shape %dx%d (k %% 4 == 0)", w.n_out,
+            w.k);
+  XTG_CHECK(!capturing_, "prepare_bf16: weights must be prepared before a graph capture");
+  std::vector<uint16_t> host;
+  pack_bf16_tiles(w.data, w.n_out, w.k, host);
+  PackedBf16 p;
+  p.n = w.n_out;
+  p.k = w.k;
+  p.nb = (w.n_out + kTileRows - 1) / kTileRows;
+  p.kt = (w.k + kTileK - 1) / kTileK;
+  p.bytes = host.size() * sizeof(uint16_t);
+  HIP_CHECK(hipMalloc(&p.tiles, p.bytes));
+  const hipError_t e = hipMemcpy(p.tiles, host.data(), p.bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(p.tiles);
+    HIP_CHECK(e);
+  }
+  weight_bytes_ += p.bytes;
+  return bf16_weights_.emplace(w.data, p).first->second;
+}
+
+void Backend::release_bf16(const uint16_t* data) {
+  XTG_CHECK(!capturing_, "release_bf16: not during a graph capture");
+  auto it = bf16_weights_.find(data);
+  if (it == bf16_weights_.end()) return;
+  HIP_CHECK(hipStreamSynchronize(stream_));   // queued launches may still read it
+  HIP_CHECK(hipFree(it->second.tiles));
+  weight_bytes_ -= it->second.bytes;
+  bf16_weights_.erase(it);
+}
+
+void Backend::matmul_bf16_dev(const xtg_bf16& w, const void* x, int x_dtype, int m, float* y, size_t y_off,
+                              const float* col_scale) {
+  XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul_bf16: %d rows (1..%d per device call)", m, kMaxRows);
+  XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul_bf16: unknown activation type %d", x_dtype);
+  XTG_CHECK(x && y, "matmul_bf16: NULL input or output");
+  const PackedBf16& p = prepare(w);
+  ensure(opb_, opb_size_, xop_bf16_bytes(w.k));
+  timed([&] { return launch_prep_x_bf16(x, x_dtype, m, w.k, opb_, stream_); });
+  timed([&] { return launch_gemv_bf16(p, opb_, m, y + y_off, col_scale, stream_); });
+}
+
+void Backend::matmul_bf16(const xtg_bf16& w, const float* x, int m, float* y) {
+  XTG_CHECK(m >= 1 && x && y, "matmul_bf16: %d rows", m);
+  XTG_CHECK(!capturing_, "matmul_bf16: the host-synchronous call cannot be captured (use the device call)");
+  prepare(w);
+  ensure(hx_, hx_size_, size_t(kMaxRows) * size_t(w.k) * sizeof(float));
+  ensure(hy_, hy_size_, size_t(kMaxRows) * size_t(w.n_out) * sizeof(float));
+  for (int r0 = 0; r0 < m; r0 += kMaxRows) {
+    const int rows = std::min(kMaxRows, m - r0);
+    HIP_CHECK(hipMemcpyAsync(hx_, x + size_t(r0) * size_t(w.k), size_t(rows) * size_t(w.k) * sizeof(float),
+                             hipMemcpyHostToDevice, stream_));
+    matmul_bf16_dev(w, hx_, kXF32, rows, static_cast<float*>(hy_), 0);
+    HIP_CHECK(hipMemcpyAsync(y + size_t(r0) * size_t(w.n_out), hy_, size_t(rows) * size_t(w.n_out) * sizeof(float),
+                             hipMemcpyDeviceToHost, stream_));
+    HIP_CHECK(hipStreamSynchronize(stream_));
+  }
 }
 
 // ------------------------------------------------------------------------------------------------- KV caches

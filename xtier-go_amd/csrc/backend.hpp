@@ -40,6 +40,14 @@ class Backend {
   void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
                  const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]
 
+  // opencl.h:33, 35, 56: the BF16 weight path (keyed by w.data)
+  const PackedBf16& prepare(const xtg_bf16& w);
+  void release_bf16(const uint16_t* data);
+  void matmul_bf16(const xtg_bf16& w, const float* x, int m, float* y);   // host x, y; any m
+  // device x [m][k] (x_dtype) into device y + y_off; col_scale (device, optional): y[.][n] *= col_scale[n]
+  void matmul_bf16_dev(const xtg_bf16& w, const void* x, int x_dtype, int m, float* y, size_t y_off,
+                       const float* col_scale = nullptr);
+
   // KV caches (xtg::KvCache, kv.h:21-62): device storage, host-side load / save for tests and snapshots
   DevKv* kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype);
   void kv_destroy(DevKv* c);
@@ -133,6 +141,9 @@ class Backend {
   int device_ = 0;
   hipStream_t stream_ = nullptr;
   std::unordered_map<const uint8_t*, PackedNvfp4> weights_;
+  std::unordered_map<const uint16_t*, PackedBf16> bf16_weights_;
+  void* opb_ = nullptr;    // the BF16 GEMV's activation operand
+  size_t opb_size_ = 0;
   std::unordered_set<void*> allocs_;
   size_t weight_bytes_ = 0;
   // scratch (grown on demand, owned): activation operand, its row scales, host-call staging

@@ -104,6 +104,35 @@ int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const voi
   });
 }
 
+int xtg_hip_prepare_bf16(xtg_hip* h, const xtg_bf16* w, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && w, "prepare_bf16: NULL argument");
+    h->b->prepare(*w);
+  });
+}
+
+int xtg_hip_release_bf16(xtg_hip* h, const uint16_t* data, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "release_bf16: NULL handle");
+    h->b->release_bf16(data);
+  });
+}
+
+int xtg_hip_matmul_bf16(xtg_hip* h, const xtg_bf16* w, const float* x, int m, float* y, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && w && x && y, "matmul_bf16: NULL argument");
+    h->b->matmul_bf16(*w, x, m, y);
+  });
+}
+
+int xtg_hip_matmul_bf16_dev(xtg_hip* h, const xtg_bf16* w, const void* x, int x_dtype, int m, float* y,
+                            size_t y_offset, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && w, "matmul_bf16: NULL argument");
+    h->b->matmul_bf16_dev(*w, x, x_dtype, m, y, y_offset);
+  });
+}
+
 xtg_hip_kv* xtg_hip_kv_create(xtg_hip* h, int kv_heads, int head_dim, int64_t slots, int ring, int dtype, char* err,
                               int err_len) {
   xtg::hip::DevKv* c = nullptr;

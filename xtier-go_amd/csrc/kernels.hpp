@@ -57,4 +57,28 @@ struct GemvShape {
 GemvShape gemv_shape(int kt, const int* nbs, int nw, int m);
 std::string launch_gemv(const GemvCall& c, hipStream_t stream);
 
+// ---- BF16 GEMV / skinny GEMM (gemv_bf16.hip) ----
+//
+// Device weight layout: tiles of 16 rows x 128 inputs, 4096 bytes each, row-block major ([rb][kt]): step s
+// (inputs 32 s .. 32 s + 31 of the tile) at 1024 s, lane l's 8 BF16 at 1024 s + 16 l = row rb*16 + (l & 15),
+// inputs kt*128 + 32 s + 8 (l >> 4) .. +8. Rows past n_out and inputs past k are zeros.
+constexpr int kBf16TileBytes = 4096;
+
+struct PackedBf16 {
+  uint16_t* tiles = nullptr;   // device
+  size_t bytes = 0;
+  int n = 0, k = 0, nb = 0, kt = 0;
+};
+
+void pack_bf16_tiles(const uint16_t* w, int n, int k, std::vector<uint16_t>& out);
+// The activations as MFMA B operands: [kt][4 steps][2 column blocks][64 entries][8 BF16]; column 3 r + t of block
+// cb is term t of row 5 cb + r (the three BF16 terms sum to the FP32 row), entry 4 column + g holds inputs
+// 32 step + 8 g .. +8 of the k-tile.
+inline size_t xop_bf16_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 8192; }
+std::string launch_prep_x_bf16(const void* x, int x_dtype, int m, int k, void* xop, hipStream_t stream);
+GemvShape gemv_bf16_shape(int kt, int nb, int m);
+// y [m][n] (+ optional per-column factors col_scale[n]) from the operand of m <= 8 rows.
+std::string launch_gemv_bf16(const PackedBf16& w, const void* xop, int m, float* y, const float* col_scale,
+                             hipStream_t stream);
+
 }  // namespace xtg::hip
