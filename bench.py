@@ -80,6 +80,44 @@ def cpu_baseline(base, xs, seconds):
                       "same weights and inputs, one weight copy), %.1f s on %d threads" % (done, el, threads)}
 
 
+def bf16_head_bench(pkg, wl, hip, reps):
+    """matmul_bf16 on the BF16 checkpoint's LM head shape (131072 x 2560, 671 MB): two copies (1.34 GB) read in
+    turn so each launch streams from HBM; every launch bracketed by events on the backend's stream. Returns
+    per-row-count kernel times and GB/s (algorithmic bytes: weights + FP32 x + FP32 y)."""
+    n, k = 131072, 2560
+    rng = np.random.default_rng(31)
+    base = wl.f32_to_bf16(rng.standard_normal((n, k), dtype=np.float32))
+    ws = [base, base.copy()]
+    for w in ws:
+        hip.prepare_bf16(w)
+    x = rng.standard_normal((8, k)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    dx, dy = hip.array(x), hip.array(shape=(8, n))
+    out = {"shape": [n, k]}
+    for m in (1, 8):
+        for w in ws:   # warm (and size the operand)
+            hip.matmul_bf16_dev(w, dx, pkg.X_F32, m, dy)
+        hip.finish()
+        hip.profile(True)
+        for _ in range(reps):
+            for w in ws:
+                hip.matmul_bf16_dev(w, dx, pkg.X_F32, m, dy)
+        rep = hip.profile_report()
+        hip.profile(False)
+        name = [kk for kk in rep if kk.startswith("gemv_bf16_kernel")][0]
+        us = rep[name]["ms"] * 1e3 / rep[name]["calls"]
+        b = n * k * 2 + 4 * m * k + 4 * m * n
+        out["m%d" % m] = {"kernel": name, "us_per_launch": round(us, 2), "bytes": b, "gbs": round(b / us / 1e3, 1),
+                          "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log("BF16 head %dx%d M=%d: %s %.1f us, %.0f GB/s (%.1f%% of HBM peak)"
+            % (n, k, m, name, us, b / us / 1e3, b / us / 1e3 / HBM_PEAK_GBS * 100))
+    for w in ws:
+        hip.release_bf16(w)
+    dx.free()
+    dy.free()
+    return out
+
+
 def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
     """Config 4: the synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
     row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
@@ -150,6 +188,40 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
     kernels = {k: {"calls": v["calls"], "us": round(v["ms"] * 1e3, 1)} for k, v in
                sorted(rep.items(), key=lambda kv: -kv[1]["ms"])}
     results["kernels_ctx%d_m1_eager" % ctx_max] = kernels
+    # the same model over FP8 caches (the reference Dory's default KV dtype): M=1 at every context
+    import copy
+    w8 = copy.copy(w)
+    w8.cfg = dict(w.cfg, kv_dtype=1)
+    dev8 = hip.dory(w8)
+    fp8 = {}
+    for a, kind in zip(attn, kinds):
+        if kind == wl.FULL:
+            dev8.cache(a).store(0, ctx_max, dK, dV)
+    for ctx in contexts:
+        for a, kind in zip(attn, kinds):
+            if kind == wl.SLIDING:
+                dev8.cache(a).store(ctx - ring, ring, dK.ptr + (ctx - ring) * row, dV.ptr + (ctx - ring) * row)
+        hip.finish()
+        dev8.forward(dx, 1, ctx, dl)
+        hip.finish()
+        hip.graph_begin()
+        dev8.forward(dx, 1, ctx, dl)
+        g = hip.graph_end("dory_step_fp8_ctx%d" % ctx)
+        for _ in range(3):
+            hip.graph_launch(g)
+        hip.finish()
+        t = time.perf_counter()
+        for _ in range(reps):
+            hip.graph_launch(g)
+        hip.finish()
+        ms = (time.perf_counter() - t) / reps * 1e3
+        hip.graph_destroy(g)
+        kv8 = kv_step[ctx] // 2 + kv_step[ctx] // (2 * d) * 4   # 1-byte codes + a 4-byte scale per (row, head)
+        fp8["ctx%d" % ctx] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1), "kv_bytes": kv8,
+                              "hbm_gbs": round((w.weight_bytes() + kv8) / (ms / 1e3) / 1e9, 1)}
+        log("decode ctx %5d, FP8 caches: M=1 %.3f ms/token (%.0f tok/s)" % (ctx, ms, 1e3 / ms))
+    dev8.destroy()
+    results["fp8_kv_m1"] = fp8
     cpu = None
     if cpu_seconds > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -311,6 +383,8 @@ def main():
         cpu = cpu_baseline(base, xs, args.cpu_seconds)
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
+    bf16_head = bf16_head_bench(pkg, wl, hip, 10)
+
     decode = None
     if not args.no_decode:
         for name in list(base):   # the projection bench's weights are no longer needed
@@ -346,6 +420,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
+        "bf16_lm_head": bf16_head,
         "decode": decode,
     }
     hip.close()

@@ -214,7 +214,7 @@ using Bf16Fn = void (*)(const Bf16Args);
 Bf16Fn bf16_fn(int r, int t, int cb) {
 #define XTG_CASE(R, T) \
   if (r == R && t == T) return cb == 1 ? gemv_bf16_kernel<R, T, 1> : gemv_bf16_kernel<R, T, 2>;
-  XTG_CASE(1, 1) XTG_CASE(1, 2) XTG_CASE(1, 4) XTG_CASE(2, 2)
+  XTG_CASE(1, 1) XTG_CASE(1, 2) XTG_CASE(1, 4) XTG_CASE(2, 1) XTG_CASE(2, 2) XTG_CASE(4, 1) XTG_CASE(4, 2)
 #undef XTG_CASE
   if (r == 2 && t == 4 && cb == 1) return gemv_bf16_kernel<2, 4, 1>;   // with two column blocks it spills
   return nullptr;
@@ -222,10 +222,11 @@ Bf16Fn bf16_fn(int r, int t, int cb) {
 
 }  // namespace
 
-// Work-groups of S <= 8 waves (512 threads: up to 256 VGPRs per lane). Registers per lane: weights 16 R T,
-// activation terms 16 T CB, accumulators 4 R CB; R = 2 with T = 4 fits only with one column block. Many row-blocks
-// take four k-tiles per wave (16 KiB of weights in flight per wave, or 32 KiB at R = 2); few take two, for more
-// waves.
+// Work-groups of S <= 8 waves (512 threads: up to 256 VGPRs per lane); a wave takes rounds of T k-tiles until k is
+// covered. Measured on MI355X (131072 x 2560 and 32768 x 3072, rotated cold weights): one or two rows want one
+// row-block and two k-tiles per wave (88% of HBM peak on the 671 MB head); from three rows on, two row-blocks
+// and one k-tile per wave (86% at 5 rows, 83% at 6, 78% at 8), which halves the activation terms each weight
+// byte brings in from L2. Few row-blocks keep one row-block per wave, for more work-groups.
 GemvShape gemv_bf16_shape(int kt, int nb, int m) {
   const int cb = m > kRowsPerBlock ? 2 : 1;
   if (const char* env = std::getenv("XTG_GEMV_BF16_SHAPE")) {   // "R,T": a fixed shape for experiments
@@ -233,10 +234,8 @@ GemvShape gemv_bf16_shape(int kt, int nb, int m) {
     if (std::sscanf(env, "%d,%d", &r, &t) == 2 && bf16_fn(r, t, cb))
       return {r, t, std::max(1, std::min(8, (kt + t - 1) / t))};
   }
-  const bool many = nb >= 512;
-  int t = 1;
-  while (t * 2 <= (many ? 4 : 2) && t * 2 <= kt) t *= 2;
-  const int r = many && cb == 1 && nb >= 2048 ? 2 : 1;
+  const bool wide = nb >= 512 && m >= 3;
+  const int r = wide ? 2 : 1, t = wide || kt < 2 ? 1 : 2;
   return {r, t, std::max(1, std::min(8, (kt + t - 1) / t))};
 }
 
