@@ -12,7 +12,9 @@ rotation phase), so host launch cost does not set the pace.
 value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
 roofline: the GEMV kernel alone. For each (shape, rows) a graph of one GEMV launch per weight copy on a prepared
 operand is replayed between two HIP events on the backend's stream; achieved = algorithmic bytes of those
-launches / their time, against the 8 TB/s HBM peak.
+launches / their time, against the 8 TB/s HBM peak. traffic: HBM bytes per launch (mean over the 6 calls) from
+rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known size
+(profiles/gemv_layer_projections_traffic_pmc.md).
 cpu_baseline: the reference engine's own CPU matmul_nvfp4 (oracle/_ref, compiled from the reference sources)
 on the same shapes and inputs on this host's cores, or the oracle restatement when that library is absent.
 """
@@ -80,6 +82,58 @@ def cpu_baseline(base, xs, seconds):
                       "same weights and inputs, one weight copy), %.1f s on %d threads" % (done, el, threads)}
 
 
+COPY_BYTES = 256 << 20
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_layer_projections_traffic_pmc.md")
+
+
+def measured_traffic():
+    """Per-call HBM bytes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over --pmc-pass (the JSON
+    block of profiles/gemv_layer_projections_traffic_pmc.md, counters calibrated on a copy of known size), or
+    None when that summary is absent."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+        block = text[text.index("```json") + 7:]
+        return json.loads(block[:block.index("```")])["per_call"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def pmc_pass(pkg, wl):
+    """Counter pass: the copy first (known bytes read and written once), then the GEMV calls, each followed by a
+    finish so dispatches stay apart. Kernel dispatch order: copy, then per call prep_x_kernel + gemv_kernel."""
+    hip = pkg.HipBackend(0)
+    src, dst = hip.alloc(COPY_BYTES), hip.alloc(COPY_BYTES)
+    hip.copy(src, dst, COPY_BYTES)
+    hip.finish()
+    rng = np.random.default_rng(20261201)
+    base = {name: [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes] for name, shapes in SHAPES}
+    set_bytes = sum(w.codes.nbytes + w.scales.nbytes for ws in base.values() for w in ws)
+    copies = max(2, -(-(1 << 30) // set_bytes) + 1)
+    sets = []
+    for _ in range(copies):
+        s = {name: [pkg.Weight(w.codes.copy(), w.scales.copy(), w.glob) for w in ws] for name, ws in base.items()}
+        for ws in s.values():
+            for w in ws:
+                hip.prepare(w)
+        sets.append(s)
+    dy = hip.array(shape=(8 * 16384 + 64,))
+    i = 0
+    for m in ROWS:
+        for name, shapes in SHAPES:
+            xb = wl.unit_rows_bf16(rng, m, shapes[0][1])
+            dx = hip.array(xb)
+            for _ in range(4):
+                hip.matmul_dev(sets[i % copies][name], dx, pkg.X_BF16, m, dy)
+                hip.finish()
+                i += 1
+            dx.free()
+    hip.release(src)
+    hip.release(dst)
+    hip.close()
+
+
 def bf16_head_bench(pkg, wl, hip, reps):
     """matmul_bf16 on the BF16 checkpoint's LM head shape (131072 x 2560, 671 MB): two copies (1.34 GB) read in
     turn so each launch streams from HBM; every launch bracketed by events on the backend's stream. Returns
@@ -118,7 +172,7 @@ def bf16_head_bench(pkg, wl, hip, reps):
     return out
 
 
-def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
+def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     """Config 4: the synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
     row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
     synthetic context of unit-norm K / V rows; a replay re-decodes position ctx, so every replay is the same step."""
@@ -189,15 +243,15 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
                sorted(rep.items(), key=lambda kv: -kv[1]["ms"])}
     results["kernels_ctx%d_m1_eager" % ctx_max] = kernels
     # the same model over FP8 caches (the reference Dory's default KV dtype): M=1 at every context
+    fp8 = {} if kv != "bf16" else None
     import copy
     w8 = copy.copy(w)
     w8.cfg = dict(w.cfg, kv_dtype=1)
-    dev8 = hip.dory(w8)
-    fp8 = {}
-    for a, kind in zip(attn, kinds):
+    dev8 = hip.dory(w8) if fp8 is not None else None
+    for a, kind in zip(attn, kinds) if dev8 else []:
         if kind == wl.FULL:
             dev8.cache(a).store(0, ctx_max, dK, dV)
-    for ctx in contexts:
+    for ctx in contexts if dev8 else []:
         for a, kind in zip(attn, kinds):
             if kind == wl.SLIDING:
                 dev8.cache(a).store(ctx - ring, ring, dK.ptr + (ctx - ring) * row, dV.ptr + (ctx - ring) * row)
@@ -220,7 +274,8 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds):
         fp8["ctx%d" % ctx] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1), "kv_bytes": kv8,
                               "hbm_gbs": round((w.weight_bytes() + kv8) / (ms / 1e3) / 1e9, 1)}
         log("decode ctx %5d, FP8 caches: M=1 %.3f ms/token (%.0f tok/s)" % (ctx, ms, 1e3 / ms))
-    dev8.destroy()
+    if dev8:
+        dev8.destroy()
     results["fp8_kv_m1"] = fp8
     cpu = None
     if cpu_seconds > 0:
@@ -264,6 +319,12 @@ def main():
     ap.add_argument("--decode-contexts", default="4096,8192,32768")
     ap.add_argument("--decode-reps", type=int, default=50)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="the workload for a rocprofv3 --pmc pass: a 256 MiB device copy (the counters' calibration), "
+                         "then each of the step's 6 calls 4 times on rotated weights; prints nothing else")
+    ap.add_argument("--decode-kv", default="both", choices=["bf16", "both"],
+                    help="KV dtypes of the decode measurement: the BF16 caches of the benchmark configuration only, "
+                         "or also the FP8 caches of the reference Dory's default (M=1; the default)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step measurement (for profiling it); prints its own JSON line")
     args = ap.parse_args()
@@ -275,10 +336,15 @@ def main():
     pkg = load_package()
     import xtier_go_amd.workloads as wl
 
+    if args.pmc_pass:
+        pmc_pass(pkg, wl)
+        return
+
     if args.decode_only:
         hip = pkg.HipBackend(0)
         contexts = [int(v) for v in args.decode_contexts.split(",") if v]
-        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2)
+        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2,
+                              args.decode_kv)
         first = "ctx%d" % contexts[0]
         print(json.dumps({"metric": "synthetic 4B decode tok/s", "value": decode[first]["tok_s"], "unit": "tok/s",
                           "n_gpus": 1, "higher_is_better": True, "data": "synthetic", "decode": decode}))
@@ -368,6 +434,11 @@ def main():
         tot_bytes += b * launches
         tot_s += t["ms"] / 1e3
     achieved = tot_bytes / tot_s / 1e9
+    traffic = measured_traffic()
+    if traffic:
+        for key, v in per_call.items():
+            if key in traffic:
+                v["traffic"] = traffic[key]["traffic_bytes"]
     by_m = {}
     for m in ROWS:
         keys = ["%s_m%d" % (name, m) for name, _ in SHAPES]
@@ -393,7 +464,8 @@ def main():
                     hip.release_weight(w)
         sets.clear()
         contexts = [int(v) for v in args.decode_contexts.split(",") if v]
-        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2)
+        decode = decode_bench(pkg, wl, hip, contexts, args.decode_reps, 0 if args.no_cpu else args.cpu_seconds / 2,
+                              args.decode_kv)
 
     out = {
         "metric": METRIC,
@@ -418,7 +490,11 @@ def main():
             "per_call": per_call,
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     # HBM bytes per launch, averaged over the 6 calls as achieved is (algorithmic: the mean of
+                     # per_call bytes); per-call values in config.per_call
+                     "traffic": (int(sum(v["traffic"] for v in per_call.values()) / len(per_call))
+                                 if all("traffic" in v for v in per_call.values()) else None)},
         "cpu_baseline": cpu,
         "bf16_lm_head": bf16_head,
         "decode": decode,

@@ -320,6 +320,9 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m) {
   // wider and reused across more rows); few row-blocks want four k-tiles per wave and one row-block.
   int nb = 0;
   for (int i = 0; i < nw; ++i) nb += nbs[i];
+  // a very tall weight (an LM head) streams best with the most bytes in flight per wave that still fits 512-thread
+  // groups: four row-blocks x three k-tiles (64% of HBM peak on 131072 x 3072 at M=1, against 59% for 2 x 2)
+  if (nb >= 4096 && kt <= 24 && shape_ok(4, 3, (kt + 2) / 3)) return {4, 3, (kt + 2) / 3};
   const bool many = nb >= 512;
   const int t = many && kt <= 32 ? 2 : 4;
   const int r = many ? (m >= 4 ? 4 : 2) : 1;
