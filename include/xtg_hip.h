@@ -207,12 +207,17 @@ typedef struct xtg_dory_layer {
 } xtg_dory_layer;
 typedef struct xtg_hip_dory xtg_hip_dory;
 /* Replaces the DoryModel constructor's weight preparation (dory.cpp:365-371) and the GpuDorySession constructor
- * (dory.cpp:1043-1084): prepares every weight and the NVFP4 LM head [vocab][hidden], uploads the vectors and
- * logit_scale [vocab], creates the caches (kv_dtype; sliding sublayers: rings of ring_slots). NULL on failure. The
- * host weights must stay alive and unchanged while the session exists (they key the prepared copies). */
+ * (dory.cpp:1043-1084): prepares every weight and the NVFP4 LM head [vocab][hidden] (head may be NULL when a BF16
+ * head follows through xtg_hip_dory_head_bf16), uploads the vectors and logit_scale [vocab], creates the caches
+ * (kv_dtype; sliding sublayers: rings of ring_slots). NULL on failure. The host weights must stay alive and
+ * unchanged while the session exists (they key the prepared copies). */
 xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xtg_dory_layer* layers,
                                   const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len);
 void xtg_hip_dory_destroy(xtg_hip_dory* d);
+/* A BF16 LM head [vocab][hidden] in place of the NVFP4 one: a BF16 checkpoint's lm_head.weight (dory.cpp:325),
+ * the head the resident GPU session runs (dory.cpp:1203, opencl.h:56). The logits become (x * W^T) * logit_scale
+ * with FP32 products and sums (kernels.cpp:140-155). Prepared on the call; not during a graph capture. */
+int xtg_hip_dory_head_bf16(xtg_hip_dory* d, const xtg_bf16* head, char* err, int err_len);
 /* Replaces GpuDorySession::run_chunk + the head of forward (dory.cpp:1150-1214; CPU dory.cpp:520-578) for one
  * chunk of m <= 8 rows: from the hidden rows x [m][hidden] (device, the embedding rows) at positions pos0 ..
  * pos0 + m - 1 to logits [m][vocab] (device, times logit_scale); each attention sublayer's cache gains the chunk's

@@ -687,6 +687,7 @@ struct xo_dory {
   xo_dory_config c;
   const xo_dory_layer* layers;
   const xo_nvfp4* head;
+  const uint16_t* head_bf16; /* [vocab][hidden] BF16, or NULL */
   const float* logit_scale;
   int n_layers, n_attn;
   int* attn_of;    /* per sublayer: its attention index, or -1 */
@@ -725,6 +726,8 @@ void xo_dory_free(xo_dory* d) {
   free(d->attn_of);
   free(d);
 }
+
+void xo_dory_head_bf16(xo_dory* d, const uint16_t* w) { d->head_bf16 = w; }
 
 xo_kv* xo_dory_cache(xo_dory* d, int attn, int inst) {
   if (attn < 0 || attn >= d->n_attn || inst < 0 || inst >= d->c.loops) return NULL;
@@ -810,8 +813,12 @@ int xo_dory_forward(xo_dory* d, const float* x, int m, int64_t pos0, float* logi
   }
   memcpy(xs, state, sizeof(float) * n);
   for (l = c->n_in + c->n_rec; l < d->n_layers; ++l) xo_sublayer(d, l, xs, m, pos0, 0, 1, &s, threads);
-  float* yl[1] = {logits};
-  xo_matmul_nvfp4(d->head, 1, xs, m, yl, threads);
+  if (d->head_bf16) { /* the BF16 checkpoint's head (dory.cpp:325, 401-402: matmul_bf16) */
+    xo_matmul_bf16(d->head_bf16, c->vocab, H, xs, m, logits, threads);
+  } else {
+    float* yl[1] = {logits};
+    xo_matmul_nvfp4(d->head, 1, xs, m, yl, threads);
+  }
   for (int r = 0; r < m; ++r) {
     float* lg = logits + (size_t)r * (size_t)c->vocab;
     for (int j = 0; j < c->vocab; ++j) lg[j] *= d->logit_scale[j];

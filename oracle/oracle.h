@@ -128,6 +128,8 @@ xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, co
 void xo_dory_free(xo_dory* d);
 /* The cache of attention sublayer `attn` (counted over attention sublayers), loop instance `inst`. */
 xo_kv* xo_dory_cache(xo_dory* d, int attn, int inst);
+/* A BF16 LM head [vocab][hidden] (borrowed) in place of the NVFP4 one: dory.cpp:325, 401-402 */
+void xo_dory_head_bf16(xo_dory* d, const uint16_t* w);
 /* dory.cpp:520-544 run_chunk from the hidden rows x [m][hidden] (the embedding rows) at positions pos0 .., then the
  * head for every row times logit_scale (dory.cpp:566-576): logits [m][vocab]; the caches gain the chunk's keys. */
 int xo_dory_forward(xo_dory* d, const float* x, int m, int64_t pos0, float* logits, int threads);

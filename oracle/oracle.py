@@ -84,6 +84,7 @@ _ORACLE_SIGS = [
     ("xo_dory_create", _P, [ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4), _P]),
     ("xo_dory_free", None, [_P]),
     ("xo_dory_cache", _P, [_P, _I, _I]),
+    ("xo_dory_head_bf16", None, [_P, _P]),
     ("xo_dory_forward", _I, [_P, _P, _I, _I64, _P, _I]),
 ]
 
@@ -340,6 +341,11 @@ class Dory:
         out = np.empty((m, self.w.cfg["vocab"]), dtype=np.float32)
         oracle().xo_dory_forward(self.h, x.ctypes.data, m, pos0, out.ctypes.data, threads)
         return out
+
+    def set_head_bf16(self, w):
+        """A BF16 LM head (uint16 BF16 bits [vocab][hidden], kept referenced) in place of the NVFP4 one."""
+        self._head_bf16 = np.ascontiguousarray(w, dtype=np.uint16)
+        oracle().xo_dory_head_bf16(self.h, self._head_bf16.ctypes.data)
 
     def cache(self, attn, inst=0):
         """The KvCache of attention sublayer `attn`, loop `inst` (owned by the model)."""

@@ -260,3 +260,35 @@ def test_4b_decode_step_fp8(hip, orc, wl, model_4b):
     print("4B step m=8, FP8 caches: logits rel-L2 %.2e" % e)
     assert e <= 1e-3
     assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def test_bf16_head_and_fp8_caches(hip, orc, wl):
+    """The BF16 checkpoint's configuration (dory.cpp:141, 325, 1203): a BF16 LM head over FP8 caches, the tiny
+    model over 24 positions in chunks of 8 and single rows; logits against the oracle with the same head."""
+    w = wl.DoryWeights(dict(wl.DORY_TINY, kv_dtype=1), seed=27, context=64)
+    head = wl.f32_to_bf16(np.random.default_rng(28).standard_normal((w.cfg["vocab"], w.cfg["hidden"]),
+                                                                     dtype=np.float32))
+    x = unit_rows(np.random.default_rng(29), 24, w.cfg["hidden"])
+    ref = orc.Dory(w, wl)
+    ref.set_head_bf16(head)
+    want = np.concatenate([ref.forward(x[r:r + 8], r) for r in range(0, 16, 8)] +
+                          [ref.forward(x[r:r + 1], r) for r in range(16, 24)])
+    dev = hip.dory(w)
+    dev.set_head_bf16(head)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    dx, dl = hip.array(shape=(8, H)), hip.array(shape=(8, V))
+    got = []
+    try:
+        for r, m in [(0, 8), (8, 8)] + [(p, 1) for p in range(16, 24)]:
+            dx.upload(np.concatenate([x[r:r + m], np.zeros((8 - m, H), np.float32)]))
+            dev.forward(dx, m, r, dl)
+            got.append(dl.numpy()[:m])
+    finally:
+        dx.free()
+        dl.free()
+        dev.destroy()
+    got = np.concatenate(got)
+    e = rel_l2(got, want)
+    print("BF16 head, FP8 caches: logits rel-L2 %.2e" % e)
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()

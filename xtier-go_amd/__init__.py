@@ -86,6 +86,7 @@ SIGNATURES = [
     ("xtg_hip_dory_create", _P, [_P, ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4),
                                  _P] + _ERR),
     ("xtg_hip_dory_destroy", None, [_P]),
+    ("xtg_hip_dory_head_bf16", _I, [_P, ctypes.POINTER(Bf16)] + _ERR),
     ("xtg_hip_dory_forward", _I, [_P, _P, _I, _I64, _P] + _ERR),
     ("xtg_hip_dory_cache", _P, [_P, _I, _I]),
     ("xtg_hip_x_operand_bytes", _SZ, [_I]),
@@ -409,6 +410,14 @@ class DorySession:
     def forward(self, x, m, pos0, logits):
         err = _errbuf()
         _check(lib().xtg_hip_dory_forward(self.h, _ptr(x), m, pos0, _ptr(logits), err, len(err)), err)
+
+    def set_head_bf16(self, w):
+        """A BF16 LM head (uint16 BF16 bits [vocab][hidden], kept referenced) in place of the NVFP4 one."""
+        assert w.dtype == np.uint16 and w.flags.c_contiguous
+        self._head_bf16 = w
+        st = Bf16(w.ctypes.data, w.shape[0], w.shape[1])
+        err = _errbuf()
+        _check(lib().xtg_hip_dory_head_bf16(self.h, ctypes.byref(st), err, len(err)), err)
 
     def cache(self, attn, inst=0):
         h = lib().xtg_hip_dory_cache(self.h, attn, inst)

@@ -42,6 +42,7 @@ class Backend {
 
   // opencl.h:33, 35, 56: the BF16 weight path (keyed by w.data)
   const PackedBf16& prepare(const xtg_bf16& w);
+  bool has_bf16(const uint16_t* data) const { return bf16_weights_.count(data) != 0; }
   void release_bf16(const uint16_t* data);
   void matmul_bf16(const xtg_bf16& w, const float* x, int m, float* y);   // host x, y; any m
   // device x [m][k] (x_dtype) into device y + y_off; col_scale (device, optional): y[.][n] *= col_scale[n]

@@ -249,11 +249,20 @@ xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xt
                                   const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len) {
   xtg_hip_dory* d = nullptr;
   int rc = guarded(err, err_len, [&] {
-    XTG_CHECK(h && c && layers && head && logit_scale, "dory_create: NULL argument");
-    auto s = std::make_unique<xtg::hip::DorySession>(*h->b, *c, layers, *head, logit_scale);
+    XTG_CHECK(h && c && layers && logit_scale, "dory_create: NULL argument");
+    const xtg_nvfp4 none{nullptr, nullptr, 1.f, 0, 0};
+    auto s = std::make_unique<xtg::hip::DorySession>(*h->b, *c, layers, head ? *head : none, logit_scale);
     d = new xtg_hip_dory{h, std::move(s)};
   });
   return rc == 0 ? d : nullptr;
+}
+
+int xtg_hip_dory_head_bf16(xtg_hip_dory* d, const xtg_bf16* head, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(d && head, "dory_head_bf16: NULL argument");
+    XTG_CHECK(!d->h->b->capturing(), "dory_head_bf16: not during a graph capture");
+    d->s->set_head_bf16(*head);
+  });
 }
 
 void xtg_hip_dory_destroy(xtg_hip_dory* d) {

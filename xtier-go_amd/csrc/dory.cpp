@@ -71,9 +71,11 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
       b_.inv_freq(L.w.kind == XTG_DORY_SLIDING ? c.theta_sliding : c.theta_full, c.head_dim);
     }
   }
-  prepare(head_);
-  XTG_CHECK(head_.k == H && head_.n_out == c.vocab, "dory: LM head %dx%d for hidden %d, vocab %d", head_.n_out,
-            head_.k, H, c.vocab);
+  if (head_.codes) {   // else a BF16 head comes with set_head_bf16
+    prepare(head_);
+    XTG_CHECK(head_.k == H && head_.n_out == c.vocab, "dory: LM head %dx%d for hidden %d, vocab %d", head_.n_out,
+              head_.k, H, c.vocab);
+  }
   logit_scale_ = upload(logit_scale, size_t(c.vocab));
   auto scratch = [&](size_t floats) {
     float* p = static_cast<float*>(b_.alloc(floats * sizeof(float)));
@@ -100,11 +102,13 @@ void DorySession::release_all() {
       if (c) b_.kv_destroy(c);
     for (void* p : owned_) b_.release(p);
     for (const uint8_t* codes : prepared_) b_.release_weight(codes);
+    for (const uint16_t* data : prepared_bf16_) b_.release_bf16(data);
   } catch (...) {
   }
   caches_.clear();
   owned_.clear();
   prepared_.clear();
+  prepared_bf16_.clear();
 }
 
 DorySession::~DorySession() { release_all(); }
@@ -114,6 +118,15 @@ DevKv* DorySession::cache(int attn, int inst) {
   DevKv* c = caches_[size_t(attn) * size_t(c_.loops) + size_t(inst)];
   XTG_CHECK(c, "dory: attention sublayer %d has no loop instance %d", attn, inst);
   return c;
+}
+
+void DorySession::set_head_bf16(const xtg_bf16& head) {
+  XTG_CHECK(head.data && head.n_out == c_.vocab && head.k == c_.hidden,
+            "dory: BF16 LM head %dx%d for hidden %d, vocab %d", head.n_out, head.k, c_.hidden, c_.vocab);
+  const bool fresh = !b_.has_bf16(head.data);
+  b_.prepare(head);
+  if (fresh) prepared_bf16_.push_back(head.data);
+  head_bf16_ = head;
 }
 
 void DorySession::sublayer(Layer& L, int m, long long pos0, int inst) {
@@ -162,7 +175,12 @@ void DorySession::forward(const float* x, int m, long long pos0, float* logits) 
   }
   b_.copy(state_, 0, x_, 0, bytes);
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0);
-  b_.matmul_op(&head_, 1, op_h_, m, logits, 0, logit_scale_);
+  if (head_bf16_.data) {   // from the FP32 rows: the BF16 GEMV makes its own three-term operand
+    b_.matmul_bf16_dev(head_bf16_, x_, XTG_X_F32, m, logits, 0, logit_scale_);
+  } else {
+    XTG_CHECK(head_.codes, "dory: no LM head (pass an NVFP4 head to create or set a BF16 one)");
+    b_.matmul_op(&head_, 1, op_h_, m, logits, 0, logit_scale_);
+  }
 }
 
 }  // namespace xtg::hip

@@ -22,6 +22,9 @@ class DorySession {
   // run_chunk from the hidden rows x [m][hidden] (device; the embedding rows) at positions pos0 .. pos0 + m - 1,
   // then the LM head times logit_scale into logits [m][vocab] (device). m <= 8. The caches gain the chunk's keys.
   void forward(const float* x, int m, long long pos0, float* logits);
+  // A BF16 LM head [vocab][hidden] in place of the NVFP4 one (a BF16 checkpoint's lm_head.weight, dory.cpp:325;
+  // the resident GPU session's head matmul, dory.cpp:1203). Not during a graph capture.
+  void set_head_bf16(const xtg_bf16& head);
   DevKv* cache(int attn, int inst);
   Backend& backend() { return b_; }
   int n_attn() const { return n_attn_; }
@@ -46,7 +49,8 @@ class DorySession {
   Backend& b_;
   xtg_dory_config c_;
   std::vector<Layer> layers_;
-  xtg_nvfp4 head_;
+  xtg_nvfp4 head_;            // codes NULL: no NVFP4 head (a BF16 head must be set)
+  xtg_bf16 head_bf16_{};      // data non-NULL: the head in use
   float* logit_scale_ = nullptr;
   int n_attn_ = 0;
   std::vector<DevKv*> caches_;   // [attn][loops]
@@ -54,6 +58,7 @@ class DorySession {
   // weights this session prepared (their device copies go with it: the host arrays that key them may be freed
   // and their addresses reused once the session is gone)
   std::vector<const uint8_t*> prepared_;
+  std::vector<const uint16_t*> prepared_bf16_;
   // scratch for up to 8 rows
   float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
         *o_ = nullptr;
