@@ -141,5 +141,5 @@ def test_errors_are_reported(hip, pkg):
     b = kt_weight(rng, 8, 128)
     with pytest.raises(pkg.XtgError, match="widths differ"):
         hip.matmul([pkg.Weight(*a), pkg.Weight(*b)], np.zeros((1, 256), np.float32))
-    with pytest.raises(pkg.XtgError, match="rows"):
-        hip.matmul_dev([pkg.Weight(*a)], 0, pkg.X_F32, 9, 0)
+    with pytest.raises(pkg.XtgError, match="rows"):   # one device call takes at most 4096 rows
+        hip.matmul_dev([pkg.Weight(*a)], 0, pkg.X_F32, 5000, 0)

@@ -99,24 +99,24 @@ void Backend::release_weight(const uint8_t* codes) {
 void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off) {
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
   const int k = ws[0].k;
-  ensure(op_, op_size_, op_bytes(k));
+  XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
+  ensure(op_, op_size_, size_t((m + kMaxRows - 1) / kMaxRows) * op_bytes(k));
   prep_x(x, x_dtype, m, k, op_);
   matmul_op(ws, nw, op_, m, y, y_off);
 }
 
 void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op) {
-  XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul: %d rows (1..%d per device call)", m, kMaxRows);
+  XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
   XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul: unknown activation type %d", x_dtype);
   XTG_CHECK(x && op, "prep_x: NULL input or operand");
-  float* xinv = reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(k));
-  timed([&] { return launch_prep_x(x, x_dtype, m, k, op, xinv, stream_); });
+  timed([&] { return launch_prep_x(x, x_dtype, m, k, op, stream_); });
 }
 
 void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
                         const float* col_scale) {
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
   XTG_CHECK(!col_scale || nw == 1, "matmul: a column scale applies to a single weight");
-  XTG_CHECK(m >= 1 && m <= kMaxRows, "matmul: %d rows (1..%d per device call)", m, kMaxRows);
+  XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
   XTG_CHECK(op && y, "matmul: NULL operand or output");
   const int k = ws[0].k;
   GemvCall c;
@@ -133,7 +133,11 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
   c.xop = op;
   c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
   c.col_scale[0] = col_scale;
-  timed([&] { return launch_gemv(c, stream_); });
+  // up to 8 rows: the bandwidth-bound GEMV; more (a prefill chunk): the matrix-core GEMM over 8-row groups
+  if (m <= kMaxRows)
+    timed([&] { return launch_gemv(c, stream_); });
+  else
+    timed([&] { return launch_gemm(c, stream_); });
 }
 
 // ------------------------------------------------------------------------------------------------ BF16 path
@@ -557,10 +561,11 @@ void Backend::matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* 
   // more than four weights: groups of four, each group one fused launch
   size_t out_per_row = 0;
   for (int i = 0; i < nw; ++i) out_per_row += size_t(ws[i].n_out);
-  ensure(hx_, hx_size_, size_t(kMaxRows) * size_t(k) * sizeof(float));
-  ensure(hy_, hy_size_, size_t(kMaxRows) * out_per_row * sizeof(float));
-  for (int r0 = 0; r0 < m; r0 += kMaxRows) {
-    const int rows = std::min(kMaxRows, m - r0);
+  const int pass = std::min(m, kHostPassRows);
+  ensure(hx_, hx_size_, size_t(pass) * size_t(k) * sizeof(float));
+  ensure(hy_, hy_size_, size_t(pass) * out_per_row * sizeof(float));
+  for (int r0 = 0; r0 < m; r0 += pass) {
+    const int rows = std::min(pass, m - r0);
     HIP_CHECK(hipMemcpyAsync(hx_, x + size_t(r0) * size_t(k), size_t(rows) * size_t(k) * sizeof(float),
                              hipMemcpyHostToDevice, stream_));
     size_t off = 0;

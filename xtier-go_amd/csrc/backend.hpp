@@ -19,6 +19,9 @@
 
 namespace xtg::hip {
 
+// Rows of one device matmul call (prefill chunks), and of one pass of the host-synchronous call.
+constexpr int kMaxDeviceRows = 4096, kHostPassRows = 512;
+
 class Backend {
  public:
   explicit Backend(int device);
@@ -30,12 +33,12 @@ class Backend {
   const PackedNvfp4& prepare(const xtg_nvfp4& w);
   bool has_weight(const uint8_t* codes) const { return weights_.count(codes) != 0; }
   void release_weight(const uint8_t* codes);
-  // opencl.h:34 host matmul: upload, compute, read back (8 rows per pass)
+  // opencl.h:34 host matmul: upload, compute, read back (up to kHostPassRows rows per pass)
   void matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* const* ys);
   // opencl.h:54-55 device matmul into consecutive [m][n_i] blocks from y_off
   void matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off);
   // the two halves of matmul_dev: the activation operand ([xop][8 row scales], op_bytes(k)) and the GEMV on it
-  static size_t op_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
+  static size_t op_bytes(int k) { return op_group_bytes(k); }   // per 8 rows
   void prep_x(const void* x, int x_dtype, int m, int k, void* op);
   void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
                  const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]

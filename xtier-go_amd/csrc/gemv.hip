@@ -25,11 +25,11 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "nvfp4.hpp"
 #include "rowops.hpp"
 
 namespace xtg::hip {
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -86,28 +86,32 @@ __device__ inline void load_chunk(const void* x, int x_dtype, int j, int k, int 
   }
 }
 
-// One work-group per activation row j < m: the row's largest magnitude picks the power of two 2^e that brings it
-// to [2^14, 2^15); the scaled row is split into f16 high and low parts in MFMA B-operand order (columns j and
-// 8 + j). Rows up to 8192 wide make one read of x (chunks held in registers); wider rows read x twice. Columns of
-// rows >= m are not written: the GEMV never loads them.
+// One work-group per activation row: the row's largest magnitude picks the power of two 2^e that brings it to
+// [2^14, 2^15); the scaled row is split into f16 high and low parts in MFMA B-operand order (columns 2 jj and
+// 2 jj + 1 of its group of 8 rows: row j is row jj = j % 8 of group j / 8, whose operand starts at
+// op + (j / 8) * op_group_bytes(k)). Rows up to 8192 wide make one read of x (chunks held in registers); wider
+// rows read x twice. Columns of rows >= m are not written: the GEMV and the GEMM never use them.
 constexpr int kPrepThreads = 256, kPrepChunks = 4;
 __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __restrict__ x, int x_dtype, int k, int kt,
-                                                              f16x8* __restrict__ xop, float* __restrict__ xinv) {
+                                                              char* __restrict__ op, size_t stride) {
   __shared__ float red[kPrepThreads / 64];
-  const int j = blockIdx.x, tid = threadIdx.x;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  f16x8* __restrict__ xop = reinterpret_cast<f16x8*>(op + size_t(row / kMaxRows) * stride);
+  float* __restrict__ xinv = reinterpret_cast<float*>(op + size_t(row / kMaxRows) * stride + size_t(kt) * 4096);
+  const int j = row % kMaxRows;
   const int chunks = kt * 16;
   float v[kPrepChunks][8];
   float mx = 0.f;
 #pragma unroll
   for (int u = 0; u < kPrepChunks; ++u) {
     const int c = tid + u * kPrepThreads;
-    load_chunk(x, x_dtype, j, k, c < chunks ? c : chunks, v[u]);
+    load_chunk(x, x_dtype, row, k, c < chunks ? c : chunks, v[u]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
   }
   for (int c = tid + kPrepChunks * kPrepThreads; c < chunks; c += kPrepThreads) {
     float w[8];
-    load_chunk(x, x_dtype, j, k, c, w);
+    load_chunk(x, x_dtype, row, k, c, w);
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(w[i]));
   }
@@ -128,18 +132,18 @@ __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __rest
   }
   for (int c = tid + kPrepChunks * kPrepThreads; c < chunks; c += kPrepThreads) {
     float w[8];
-    load_chunk(x, x_dtype, j, k, c, w);
+    load_chunk(x, x_dtype, row, k, c, w);
     store_chunk(xop, j, c, w, up);
   }
 }
 
-std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream) {
-  XTG_CHECK(m >= 1 && m <= kMaxRows, "prep_x: %d rows (1..%d)", m, kMaxRows);
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream) {
+  XTG_CHECK(m >= 1, "prep_x: %d rows", m);
   XTG_CHECK(k > 0 && k % 16 == 0, "prep_x: width %d (a multiple of 16)", k);
   XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, "prep_x: activations at %p are not 16-byte aligned", x);
   const int kt = (k + kTileK - 1) / kTileK;
   hipLaunchKernelGGL(prep_x_kernel, dim3(unsigned(m)), dim3(kPrepThreads), 0, stream, x, x_dtype, k, kt,
-                     static_cast<f16x8*>(xop), xinv);
+                     static_cast<char*>(op), op_group_bytes(k));
   HIP_CHECK(hipGetLastError());
   return "prep_x_kernel";
 }
@@ -161,31 +165,6 @@ struct GemvArgs {
   const float* xinv;
   float* y;
 };
-
-__device__ inline f16x8 dequant8(uint32_t word, f16x2 s) {
-  const f16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 0) * s;
-  const f16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 1) * s;
-  const f16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 2) * s;
-  const f16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 3) * s;
-  f16x8 a;
-  a[0] = p0[0];
-  a[1] = p0[1];
-  a[2] = p1[0];
-  a[3] = p1[1];
-  a[4] = p2[0];
-  a[5] = p2[1];
-  a[6] = p3[0];
-  a[7] = p3[1];
-  return a;
-}
-
-__device__ inline f16x2 scale_pair(uint32_t sbits, int which) {
-  const _Float16 s = (_Float16)(which ? __builtin_amdgcn_cvt_f32_fp8(sbits, 1) : __builtin_amdgcn_cvt_f32_fp8(sbits, 0));
-  f16x2 r;
-  r[0] = s;
-  r[1] = s;
-  return r;
-}
 
 // Output of one accumulator fragment: for activation row j, rows 4 g .. 4 g + 3 of the row-block (high and low
 // columns already added).

@@ -35,10 +35,13 @@ void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k,
 // first 128 m bytes of every step (one cache line per step at m = 1).
 inline size_t xop_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 4096; }
 constexpr int kMaxRows = 8;
+// One group's operand: xop_bytes(k), then its 8 row factors xinv. m rows take ceil(m / 8) consecutive groups.
+inline size_t op_group_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
 
 enum XDtype { kXF32 = 0, kXBF16 = 1 };
 // Launchers return the kernel's name (as rocprof prints it, without the namespace) for the profiler.
-std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* xop, float* xinv, hipStream_t stream);
+// The operand of m >= 1 rows into op (ceil(m / 8) groups of op_group_bytes(k)).
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream);
 
 struct GemvCall {
   const PackedNvfp4* w[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -56,6 +59,11 @@ struct GemvShape {
 };
 GemvShape gemv_shape(int kt, const int* nbs, int nw, int m);
 std::string launch_gemv(const GemvCall& c, hipStream_t stream);
+
+// ---- NVFP4 GEMM for prefill chunks of m > 8 rows (gemm.hip) ----
+// The same weights and call description (c.xop: group 0 of ceil(m / 8) operand groups of op_group_bytes(k);
+// c.xinv unused), any m >= 1; y[i] blocks as in the GEMV.
+std::string launch_gemm(const GemvCall& c, hipStream_t stream);
 
 // ---- BF16 GEMV / skinny GEMM (gemv_bf16.hip) ----
 //
