@@ -63,7 +63,7 @@ def test_fused_weights(hip, pkg, orc, wl):
         assert rel_l2(y, r) <= 1e-5
 
 
-@pytest.mark.parametrize("shape", ["4,8", "2,8", "1,8", "4,4", "2,4", "1,4"])
+@pytest.mark.parametrize("shape", ["4,4", "2,4", "1,4"])
 def test_every_launch_shape(hip, pkg, orc, wl, shape):
     rng = np.random.default_rng(7)
     w = wl.nvfp4_weight(rng, 1200, 1024)

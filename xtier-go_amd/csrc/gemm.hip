@@ -9,11 +9,12 @@
 //    activations in 8-row groups of the GEMV's operand (each row as f16 high and low parts, columns 2 r and
 //    2 r + 1), so v_mfma_f32_16x16x32_f16 keeps ~22 bits of every activation and accumulates in FP32.
 //  - A work-group of 4 waves owns 4 RB row-blocks (64 RB output rows) and GB activation groups (8 GB rows).
-//    Each k-tile (128 inputs) the work-group copies the groups' operand tile (4 KiB each) into LDS with direct
-//    global-to-LDS loads, double-buffered, in lane order (no bank conflicts on the 16-byte reads, no staging
-//    registers); each wave dequantises its RB weight tiles once and runs them against all GB groups: 4 RB GB
-//    matrix ops per k-tile per wave. The next k-tile's loads are issued before the current one's math, one
-//    barrier per k-tile.
+//    Each k-tile (128 inputs) the work-group stages the groups' operand tile (4 KiB each) in LDS, double-buffered,
+//    in lane order (contiguous 16-byte writes and reads); each wave dequantises its RB weight tiles once and runs
+//    them against all GB groups: 4 RB GB matrix ops per k-tile per wave. The next k-tile's loads go out into
+//    registers before the current one's math and are written to LDS after it, one barrier per k-tile. (Direct
+//    global-to-LDS loads would save those registers, but the compiler then waits for them before every LDS read
+//    of the current buffer, serialising the pipeline.)
 //  - Tiles are dealt so that work-group i, which runs on XCD i mod 8, gets a contiguous run of tiles: the
 //    work-groups of one XCD share weight tiles (consecutive m-tiles of one n-tile) in that XCD's L2.
 #include <algorithm>
@@ -46,9 +47,40 @@ struct GemmArgs {
   float* y;
 };
 
-// 16 bytes per lane from global memory straight into LDS: lane L writes lds_block + 16 L (wave-uniform block).
-__device__ inline void copy_to_lds16(const uint4* src, uint4* lds_block) {
-  __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
+template <int GB>
+struct XTile {
+  uint4 v[GB];
+};
+template <int RB>
+struct WTile {
+  u32x4 c[RB];
+  uint32_t s[RB];
+};
+
+// A k-tile's activation operand for groups g0 .. g0 + GB - 1: lane L of wave w fetches, for every group, entry
+// 4 (L & 15) + (L >> 4) of step w (a permutation within one run of 1 KiB), which it later stores at lane slot L:
+// the lane that reads it back as its B operand. Every load is unconditional (a branch around a load makes its
+// other path wait for it): a group past the last one reloads the last group, whose results for it are never stored.
+template <int GB>
+__device__ inline XTile<GB> load_x(const char* op, size_t stride, int groups, int g0, int kt, int wave, int lane) {
+  XTile<GB> r;
+  const size_t at = (size_t(kt) * 4 + size_t(wave)) * 64 + size_t(4 * (lane & 15) + (lane >> 4));
+#pragma unroll
+  for (int i = 0; i < GB; ++i) r.v[i] = reinterpret_cast<const uint4*>(op + size_t(min(g0 + i, groups - 1)) * stride)[at];
+  return r;
+}
+
+// Row-blocks rb0 .. rb0 + RB - 1 of k-tile kt (a row-block past the last reloads the last one).
+template <int RB>
+__device__ inline WTile<RB> load_w(const uint8_t* tiles, int nb, int kt_count, int rb0, int kt, int lane) {
+  WTile<RB> w;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint8_t* tile = tiles + (size_t(min(rb0 + r, nb - 1)) * size_t(kt_count) + size_t(kt)) * kTileBytes;
+    w.c[r] = *reinterpret_cast<const u32x4*>(tile + 16 * lane);
+    w.s[r] = uint32_t(*reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane));
+  }
+  return w;
 }
 
 // RB row-blocks per wave, GB activation groups per work-group tile, OCC work-groups per CU the registers are
@@ -74,62 +106,31 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
   const int nb = a.nb[wi], KT = a.kt;
   const uint8_t* __restrict__ tiles = a.tiles[wi];
 
-  // a k-tile's activation operand into LDS buffer buf, straight from global memory (global_load_lds_dwordx4:
-  // lane L of a wave writes 16 bytes at the block's base + 16 L). Wave w moves step w of every group; lane L
-  // fetches the entry 4 (L & 15) + (L >> 4) that lane L reads back as its B operand. Absent groups (past the
-  // last row) are skipped: their stale columns produce outputs that are never stored.
-  auto xload = [&](int kt, int buf) {
-    const int e = 4 * (lane & 15) + (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < kTileGroups; ++i)
-      if (g0 + i < a.groups) {
-        const uint4* src = reinterpret_cast<const uint4*>(a.op + size_t(g0 + i) * a.op_stride) +
-                           (size_t(kt) * 4 + size_t(wave)) * 64 + size_t(e);
-        copy_to_lds16(src, &xs[buf][i][wave][0]);
-      }
-  };
-  auto wload = [&](int kt, u32x4 (&cw)[RB], uint32_t (&sw)[RB]) {
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      if (rb0 + r < nb) {
-        const uint8_t* tile = tiles + (size_t(rb0 + r) * size_t(KT) + size_t(kt)) * kTileBytes;
-        cw[r] = *reinterpret_cast<const u32x4*>(tile + 16 * lane);
-        sw[r] = uint32_t(*reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane));
-      } else {
-        cw[r] = u32x4{0u, 0u, 0u, 0u};
-        sw[r] = 0u;
-      }
-    }
-  };
-
   f32x4 acc[RB][kTileGroups];
 #pragma unroll
   for (int r = 0; r < RB; ++r)
 #pragma unroll
     for (int g = 0; g < kTileGroups; ++g) acc[r][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 cw[RB];
-  uint32_t sw[RB];
-  xload(0, 0);
-  wload(0, cw, sw);
+  WTile<RB> w = load_w<RB>(tiles, nb, KT, rb0, 0, lane);
+  {
+    const XTile<GB> x0 = load_x<GB>(a.op, a.op_stride, a.groups, g0, 0, wave, lane);
+#pragma unroll
+    for (int i = 0; i < GB; ++i) xs[0][i][wave][lane] = x0.v[i];
+  }
   for (int kt = 0; kt < KT; ++kt) {
-    // this wave's loads of k-tile kt have landed (its LDS copies included); after the barrier every wave's have,
-    // and every wave is done reading the other buffer
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    __syncthreads();   // buffer kt & 1 is complete, and every wave is done reading the other one
     const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    u32x4 cwn[RB];
-    uint32_t swn[RB];
-    if (more) {
-      xload(kt + 1, cur ^ 1);
-      wload(kt + 1, cwn, swn);
-    }
+    const int nxt = min(kt + 1, KT - 1);   // the last k-tile reloads itself: no branch around the loads
+    // the next k-tile's loads, in flight during this one's math
+    const XTile<GB> xn = load_x<GB>(a.op, a.op_stride, a.groups, g0, nxt, wave, lane);
+    const WTile<RB> wn = load_w<RB>(tiles, nb, KT, rb0, nxt, lane);
+    __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the math (the scheduler would sink them to their use)
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       f16x8 A[RB];
 #pragma unroll
-      for (int r = 0; r < RB; ++r) A[r] = dequant8(cw[r][s], scale_pair(sw[r], s >> 1));
+      for (int r = 0; r < RB; ++r) A[r] = dequant8(w.c[r][s], scale_pair(w.s[r], s >> 1));
 #pragma unroll
       for (int g = 0; g < kTileGroups; ++g) {
         const f16x8 B = __builtin_bit_cast(f16x8, xs[cur][g][s][lane]);
@@ -137,13 +138,9 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
         for (int r = 0; r < RB; ++r) acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], B, acc[r][g], 0, 0, 0);
       }
     }
-    if (more) {
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        cw[r] = cwn[r];
-        sw[r] = swn[r];
-      }
-    }
+    for (int i = 0; i < GB; ++i) xs[cur ^ 1][i][wave][lane] = xn.v[i];
+    w = wn;
   }
 
   // lane (grp, col) holds rows 4 grp .. 4 grp + 3 of its row-block for operand column col; columns 2 j and
@@ -179,33 +176,40 @@ using GemmFn = void (*)(const GemmArgs);
 static GemmFn gemm_fn(int rb, int gb) {
 #define XTG_GEMM(R, G, O) \
   if (rb == R && gb == G) return gemm_kernel<R, G, O>;
-  XTG_GEMM(4, 8, 1) XTG_GEMM(2, 8, 2) XTG_GEMM(1, 8, 2) XTG_GEMM(4, 4, 2) XTG_GEMM(2, 4, 2) XTG_GEMM(1, 4, 2)
+  XTG_GEMM(4, 4, 2) XTG_GEMM(2, 4, 2) XTG_GEMM(1, 4, 2)
 #undef XTG_GEMM
   return nullptr;
 }
 
+static std::string run_gemm(const GemvCall& c, int rb, int gb, hipStream_t stream);
+
 std::string launch_gemm(const GemvCall& c, hipStream_t stream) {
   XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemm: %d weights (1..4)", c.nw);
   XTG_CHECK(c.m >= 1, "gemm: %d rows", c.m);
-  const int kt = c.w[0]->kt;
   const int groups = (c.m + kMaxRows - 1) / kMaxRows;
-  // launch shape (XTG_GEMM_SHAPE=RB,GB fixes it, for experiments): four row-blocks per wave and eight groups per
-  // tile when that still gives a work-group per CU, else smaller tiles
-  int rb = 4, gb = 8;
+  // launch shape (XTG_GEMM_SHAPE=RB,GB fixes it, for experiments)
   auto tiles_for = [&](int r, int g) {
     const int mt = (groups + g - 1) / g;
     long t = 0;
     for (int i = 0; i < c.nw; ++i) t += long((c.w[i]->nb + kGemmWaves * r - 1) / (kGemmWaves * r)) * mt;
     return t;
   };
-  if (tiles_for(4, 8) < 256) {
-    rb = 2;
-    if (tiles_for(2, 8) < 256) gb = 4;
-  }
+  // measured on MI355X over the 4B-shaped projections at 64 .. 2048 rows: four groups per tile throughout; two
+  // row-blocks per wave (34 % of the dense f16 peak on gate/up at 512 rows), four only with thousands of tiles
+  // (2048-row chunks of the wide projections), one when two would leave most CUs idle
+  const int gb = 4;
+  const int rb = tiles_for(4, 4) >= 2048 ? 4 : tiles_for(2, 4) >= 128 ? 2 : 1;
   if (const char* env = std::getenv("XTG_GEMM_SHAPE")) {
     int r = 0, g = 0;
-    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && (r == 1 || r == 2 || r == 4) && (g == 4 || g == 8)) rb = r, gb = g;
+    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && (r == 1 || r == 2 || r == 4) && g == 4)
+      return run_gemm(c, r, g, stream);
   }
+  return run_gemm(c, rb, gb, stream);
+}
+
+static std::string run_gemm(const GemvCall& c, int rb, int gb, hipStream_t stream) {
+  const int kt = c.w[0]->kt;
+  const int groups = (c.m + kMaxRows - 1) / kMaxRows;
   const int mtiles = (groups + gb - 1) / gb;
   GemmArgs a{};
   int end = 0;
