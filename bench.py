@@ -134,6 +134,94 @@ def pmc_pass(pkg, wl):
     hip.close()
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 matrix-core peak
+
+
+def prefill_gemm_bench(pkg, wl, hip, rows, reps):
+    """The NVFP4 GEMM on a prefill chunk: one 4B-shaped layer's projections (q/k/v/g 10240x3072, fused gate/up
+    2x8192x3072, o 3072x4096, down 3072x8192) at `rows` rows of FP32 activations, operand prepared once, each
+    launch bracketed by events. Compute-bound: reported against the dense f16 matrix-core peak with the
+    algorithmic 2 m n k flops (the kernel issues twice that: each activation is a high and a low f16 part)."""
+    rng = np.random.default_rng(41)
+    calls = [("qkvg10240", [(10240, 3072)]), ("gateup2x8192", [(8192, 3072), (8192, 3072)]),
+             ("o3072x4096", [(3072, 4096)]), ("down3072x8192", [(3072, 8192)])]
+    out = {"rows": rows, "per_call": {}}
+    tot_flops, tot_us = 0.0, 0.0
+    for name, shapes in calls:
+        ws = [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes]
+        k = shapes[0][1]
+        for w in ws:
+            hip.prepare(w)
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        dx = hip.array(x)
+        dy = hip.array(shape=(rows * sum(n for n, _ in shapes),))
+        op = hip.array(shape=((rows + 7) // 8 * hip.x_operand_bytes(k),), dtype=np.uint8)
+        hip.prep_x(dx, pkg.X_F32, rows, k, op)
+        for _ in range(3):
+            hip.matmul_op(ws, op, rows, dy)
+        hip.finish()
+        hip.profile(True)
+        for _ in range(reps):
+            hip.matmul_op(ws, op, rows, dy)
+        rep = hip.profile_report()
+        hip.profile(False)
+        kname = [kk for kk in rep if kk.startswith("gemm_kernel")][0]
+        us = rep[kname]["ms"] * 1e3 / rep[kname]["calls"]
+        flops = 2.0 * rows * k * sum(n for n, _ in shapes)
+        out["per_call"][name] = {"kernel": kname, "us_per_launch": round(us, 2),
+                                 "tflops": round(flops / us / 1e6, 1),
+                                 "frac": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+        tot_flops += flops
+        tot_us += us
+        log("prefill GEMM %s at %d rows: %s %.1f us, %.1f TFLOP/s (%.1f%% of the dense f16 peak; matrix-core "
+            "issue %.1f%%)" % (name, rows, kname, us, flops / us / 1e6, flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS * 100,
+                               2 * flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS * 100))
+        for a in (dx, dy, op):
+            a.free()
+        for w in ws:
+            hip.release_weight(w)
+    achieved = tot_flops / tot_us / 1e6
+    out["roofline"] = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                       "issue_frac": round(2 * achieved / MFMA_F16_PEAK_TFLOPS, 4)}
+    return out
+
+
+def prefill_attention_bench(pkg, wl, hip, rows, ctx, reps):
+    """The attention ABI call on a prefill chunk of `rows` rows after `ctx` cached positions, on the 4B model's
+    heads (32 query heads over 8 KV heads of 128, a BF16 global cache): the own-key, scan and merge launches,
+    each bracketed by events. Reported as the algorithmic 4 d flops per (query head, visible key) pair."""
+    rng = np.random.default_rng(43)
+    heads, kvh, d = 32, 8, 128
+    dc = hip.kv_cache(kvh, d, ctx + rows, ring=0)
+    for p in range(0, ctx, 512):
+        n = min(512, ctx - p)
+        dc.store_host(p, wl.unit_heads(rng, (n, kvh), d), wl.unit_heads(rng, (n, kvh), d))
+    dq = hip.array(wl.unit_heads(rng, (rows, heads), d))
+    dk = hip.array(wl.unit_heads(rng, (rows, kvh), d))
+    dv = hip.array(wl.unit_heads(rng, (rows, kvh), d))
+    dout = hip.array(shape=(rows, heads, d))
+    for _ in range(3):
+        hip.attention(dc, dq, dk, dv, dout, rows, ctx, heads)
+    hip.finish()
+    hip.profile(True)
+    for _ in range(reps):
+        hip.attention(dc, dq, dk, dv, dout, rows, ctx, heads)
+    rep = hip.profile_report()
+    hip.profile(False)
+    for a in (dq, dk, dv, dout):
+        a.free()
+    dc.destroy()
+    us = sum(v["ms"] for v in rep.values()) * 1e3 / reps
+    pairs = rows * heads * (ctx + (rows + 1) / 2.0)
+    tflops = 4.0 * d * pairs / us / 1e6
+    kern = {k: round(v["ms"] * 1e3 / v["calls"], 2) for k, v in rep.items()}
+    log("prefill attention %d rows after %d cached: %.1f us per call (%s), %.1f TFLOP/s algorithmic"
+        % (rows, ctx, us, ", ".join("%s %.1f us" % kv for kv in kern.items()), tflops))
+    return {"rows": rows, "cached": ctx, "us_per_call": round(us, 2), "tflops": round(tflops, 1),
+            "kernels_us": kern}
+
+
 def bf16_head_bench(pkg, wl, hip, reps):
     """matmul_bf16 on the BF16 checkpoint's LM head shape (131072 x 2560, 671 MB): two copies (1.34 GB) read in
     turn so each launch streams from HBM; every launch bracketed by events on the backend's stream. Returns
@@ -455,6 +543,8 @@ def main():
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
     bf16_head = bf16_head_bench(pkg, wl, hip, 10)
+    prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
+    prefill["attention_ctx4096"] = prefill_attention_bench(pkg, wl, hip, 512, 4096, 10)
 
     decode = None
     if not args.no_decode:
@@ -497,6 +587,7 @@ def main():
                                  if all("traffic" in v for v in per_call.values()) else None)},
         "cpu_baseline": cpu,
         "bf16_lm_head": bf16_head,
+        "prefill_gemm": prefill,
         "decode": decode,
     }
     hip.close()

@@ -97,6 +97,16 @@ def test_reference_unit_cases(hip, orc, cached, n_q, window, fp8):
         assert np.max(np.abs(out - exact)) < 2e-5
 
 
+@pytest.mark.parametrize("cached,n_q,window,fp8", [(1500, 300, 0, 0), (1500, 300, 256, 1), (0, 129, 0, 0),
+                                                   (2000, 512, 1024, 0)])
+def test_prefill_rows(hip, orc, cached, n_q, window, fp8):
+    """Prefill-sized calls (many row blocks, the last one partial, in one own-key and one scan launch) on the
+    4B model's heads: 32 query heads over 8 KV heads of 128."""
+    rng = np.random.default_rng(cached + n_q + window + fp8)
+    out, ref, _ = run_case(hip, orc, cached, n_q, window, 32, 8, 128, None, rng, unit=True, fp8=bool(fp8))
+    assert rel_l2(out, ref) <= 1e-5
+
+
 @pytest.mark.parametrize("ctx", [4096, 8192, 32768])
 @pytest.mark.parametrize("n_q", [1, 8])
 def test_decode_global_cache(hip, orc, ctx, n_q):

@@ -219,15 +219,17 @@ std::string launch_kv_store(const DevKv& c, long long pos, int n, const float* k
 // ------------------------------------------------------------------------------------------------------- scan
 
 struct ScanArgs {
-  const float* q;          // the block's rows [n_rows][heads][d]
+  const float* q;          // every row of the call [n_q][heads][d]
   const uint4* ck;         // cache, operand layout
   const uint4* cv;
   const int* slot_pos;
   const float* kscale;     // FP8 caches: [head][slot] scales
   const float* vscale;
-  float* acc;              // the block's partials: record (h, s, c) at (h * splits1 + s) * qpad + c
-  float* ml;
-  int n_rows, row0, heads, group, window, splits, splits1, qpad, slots_pad;
+  float* acc;              // the call's partials: block b's record (h, s, c) at b * blk_records + (h * splits1 + s) *
+  float* ml;               // qpad + c
+  size_t blk_records;
+  int b0, rpb, n_q;        // work-group column y takes block b0 + y: rows (b0 + y) * rpb .. (at most rpb, below n_q)
+  int heads, group, window, splits, splits1, qpad, slots_pad;
   int tile_lo, tiles;      // the key tiles to scan: tile_lo .. tile_lo + tiles - 1
   int pos0;                // positions are below 2^31 (the slot-position array is int32)
   float scale2;            // scale * log2(e)
@@ -475,7 +477,11 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int kvh = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
-  const int qcols = a.n_rows * a.group;
+  const int blk = a.b0 + int(blockIdx.y), row0 = blk * a.rpb;
+  const int qcols = min(a.rpb, a.n_q - row0) * a.group;
+  const float* __restrict__ qrows = a.q + size_t(row0) * size_t(a.heads) * D;
+  float* __restrict__ acc_out = a.acc + size_t(blk) * a.blk_records * D;
+  float* __restrict__ ml_out = a.ml + size_t(blk) * a.blk_records * 2;
 
   // this split's tiles (at least one: splits <= tiles), dealt to the waves round-robin; the first tile's loads go
   // out before the q operands are built, and every later tile's while the previous one is worked on (an index
@@ -509,9 +515,9 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
     const int qc = qb * 16 + j;
     const bool live = qc < qcols;
     const int qrow = live ? qc / a.group : 0;
-    const int qpos = a.pos0 + a.row0 + qrow;
+    const int qpos = a.pos0 + row0 + qrow;
     lo[qb] = !live ? INT_MAX : (a.window > 0 ? max(0, qpos - a.window + 1) : 0);
-    const float* qp = a.q + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (live ? qc % a.group : 0))) * D;
+    const float* qp = qrows + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (live ? qc % a.group : 0))) * D;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
@@ -569,12 +575,12 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
     }
     if (qc >= qcols) continue;
     const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(split)) * size_t(a.qpad) + size_t(qc);
-    if (g == 0) *reinterpret_cast<float2*>(a.ml + rec * 2) = make_float2(M, L);
+    if (g == 0) *reinterpret_cast<float2*>(ml_out + rec * 2) = make_float2(M, L);
     for (int dd = 0; dd < ND; ++dd) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < kWaves; ++w)
         s += f[w] * *reinterpret_cast<const f32x4*>(accs + ((size_t(w * QB + qb) * ND + dd) * 64 + lane) * 4);
-      *reinterpret_cast<f32x4*>(a.acc + rec * D + 16 * dd + 4 * g) = s;
+      *reinterpret_cast<f32x4*>(acc_out + rec * D + 16 * dd + 4 * g) = s;
     }
   }
 }
@@ -648,18 +654,21 @@ __device__ inline void write_partial(float* acc, float* ml, size_t rec, int d, f
   }
 }
 
-// One work-group per KV head for one block of query rows: wave w takes q-cols w, w + 4, ...
+// One work-group per (KV head, block of query rows b0 + blockIdx.y): wave w takes the block's q-cols w, w + 4, ...
 template <int D>
 __global__ void __launch_bounds__(kWaves * 64) attn_own_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                               const float* __restrict__ v, int n_rows, int row0,
+                                                               const float* __restrict__ v, int rpb, int b0,
                                                                int n_own, int heads, int kv_heads, int group,
-                                                               int window, float scale, float* __restrict__ acc,
-                                                               float* __restrict__ ml, int splits, int splits1,
-                                                               int qpad) {
+                                                               int window, float scale, float* __restrict__ acc_all,
+                                                               float* __restrict__ ml_all, size_t blk_records,
+                                                               int splits, int splits1, int qpad) {
   const int kvh = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int blk = b0 + int(blockIdx.y), row0 = blk * rpb, n_rows = min(rpb, n_own - row0);
+  float* acc = acc_all + size_t(blk) * blk_records * D;
+  float* ml = ml_all + size_t(blk) * blk_records * 2;
   for (int c = wave; c < n_rows * group; c += kWaves) {
     const int r = c / group, hg = c % group, i = row0 + r;
-    const float* qp = q + (size_t(r) * size_t(heads) + size_t(kvh * group + hg)) * D;
+    const float* qp = q + (size_t(i) * size_t(heads) + size_t(kvh * group + hg)) * D;
     const int j0 = window > 0 ? max(0, i - window + 1) : 0, j1 = min(i + 1, n_own);
     float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
     own_state<D>(qp, k + size_t(kvh) * D, v + size_t(kvh) * D, size_t(kv_heads) * D, j0, j1, scale * kLog2e, M, L,
@@ -975,10 +984,11 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
     p.tile_lo = int(lo / kTile);
     p.tiles = hi > lo ? int((hi + kTile - 1) / kTile - lo / kTile) : 0;
   }
-  // about 256 work-groups over the KV heads (one per CU), at least two tiles per wave, at most one split per tile
+  // about 256 work-groups over the KV heads and row blocks (one per CU), at least two tiles per wave, at most one
+  // split per tile
   // (XTG_ATTN_SPLITS=n fixes the count, for experiments)
   if (p.tiles > 0) {
-    const int want = std::max(1, 256 / c.kv_heads);
+    const int want = std::max(1, 256 / (c.kv_heads * p.blocks));   // about 256 work-groups over all blocks
     p.splits = std::max(1, std::min(want, (p.tiles + 2 * kWaves - 1) / (2 * kWaves)));
     if (const char* env = std::getenv("XTG_ATTN_SPLITS")) p.splits = std::max(1, std::atoi(env));
     p.splits = std::min(p.splits, p.tiles);
@@ -1019,10 +1029,6 @@ void allow_lds(ScanFn fn, size_t lds) {
 }
 
 size_t blk_records(const AttnPlan& p) { return size_t(p.kv_heads) * size_t(p.splits + 1) * size_t(p.qpad); }
-float* part_acc(const AttnPlan& p, float* part, int b) { return part + size_t(b) * blk_records(p) * size_t(p.d); }
-float* part_ml(const AttnPlan& p, float* part, int b) {
-  return part + p.records() * size_t(p.d) + size_t(b) * blk_records(p) * 2;
-}
 
 MergeArgs merge_args(const AttnPlan& p, int heads, const float* part) {
   MergeArgs a;
@@ -1044,21 +1050,24 @@ int block_rows(const AttnPlan& p, int n_q, int b) {
 
 }  // namespace
 
-std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const float* q, int n_q, int heads,
-                             long long pos0, int window, float scale, float* part, hipStream_t stream) {
+std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblocks, const float* q, int n_q,
+                             int heads, long long pos0, int window, float scale, float* part, hipStream_t stream) {
   XTG_CHECK(p.splits >= 1 && p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
-  const int nr = block_rows(p, n_q, b);
+  XTG_CHECK(nblocks >= 1 && b0 + nblocks <= p.blocks, "attention: blocks %d .. %d of %d", b0, b0 + nblocks, p.blocks);
+  const int nr = block_rows(p, n_q, b0);   // the widest block of the launch
   ScanArgs a{};
-  a.q = q + size_t(b) * size_t(p.rpb) * size_t(heads) * size_t(p.d);
+  a.q = q;
   a.ck = reinterpret_cast<const uint4*>(c.k);
   a.cv = reinterpret_cast<const uint4*>(c.v);
   a.slot_pos = c.slot_pos;
   a.kscale = c.kscale;
   a.vscale = c.vscale;
-  a.acc = part_acc(p, part, b);
-  a.ml = part_ml(p, part, b);
-  a.n_rows = nr;
-  a.row0 = b * p.rpb;
+  a.acc = part;
+  a.ml = part + p.records() * size_t(p.d);
+  a.blk_records = blk_records(p);
+  a.b0 = b0;
+  a.rpb = p.rpb;
+  a.n_q = n_q;
   a.heads = heads;
   a.group = p.group;
   a.window = window;
@@ -1076,24 +1085,23 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const flo
   const int nd = c.head_dim / 16;
   const size_t lds = (size_t(kWaves) * qb * 2 * 16 + size_t(kWaves) * qb * nd * 64 * 4) * sizeof(float);
   allow_lds(fn, lds);
-  hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits)), dim3(kWaves * 64), lds, stream, a);
+  hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits), unsigned(nblocks)), dim3(kWaves * 64), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   return strf("attn_scan_kernel<%d, %d, %s>", c.head_dim, qb, c.fp8 ? "true" : "false");
 }
 
-std::string launch_attn_own(const AttnPlan& p, int b, const float* q, const float* k, const float* v, int n_q,
-                            int heads, int window, float scale, float* part, hipStream_t stream) {
-  const int nr = block_rows(p, n_q, b);
-  const float* qb = q + size_t(b) * size_t(p.rpb) * size_t(heads) * size_t(p.d);
-  float* acc = part_acc(p, part, b);
-  float* ml = part_ml(p, part, b);
-  const dim3 grid{unsigned(p.kv_heads)}, block{unsigned(kWaves * 64)};
+std::string launch_attn_own(const AttnPlan& p, int b0, int nblocks, const float* q, const float* k, const float* v,
+                            int n_q, int heads, int window, float scale, float* part, hipStream_t stream) {
+  XTG_CHECK(nblocks >= 1 && b0 + nblocks <= p.blocks, "attention: blocks %d .. %d of %d", b0, b0 + nblocks, p.blocks);
+  float* acc = part;
+  float* ml = part + p.records() * size_t(p.d);
+  const dim3 grid{unsigned(p.kv_heads), unsigned(nblocks)}, block{unsigned(kWaves * 64)};
   if (p.d == 64)
-    hipLaunchKernelGGL(attn_own_kernel<64>, grid, block, 0, stream, qb, k, v, nr, b * p.rpb, n_q, heads, p.kv_heads,
-                       p.group, window, scale, acc, ml, p.splits, p.splits + 1, p.qpad);
+    hipLaunchKernelGGL(attn_own_kernel<64>, grid, block, 0, stream, q, k, v, p.rpb, b0, n_q, heads, p.kv_heads,
+                       p.group, window, scale, acc, ml, blk_records(p), p.splits, p.splits + 1, p.qpad);
   else
-    hipLaunchKernelGGL(attn_own_kernel<128>, grid, block, 0, stream, qb, k, v, nr, b * p.rpb, n_q, heads, p.kv_heads,
-                       p.group, window, scale, acc, ml, p.splits, p.splits + 1, p.qpad);
+    hipLaunchKernelGGL(attn_own_kernel<128>, grid, block, 0, stream, q, k, v, p.rpb, b0, n_q, heads, p.kv_heads,
+                       p.group, window, scale, acc, ml, blk_records(p), p.splits, p.splits + 1, p.qpad);
   HIP_CHECK(hipGetLastError());
   return strf("attn_own_kernel<%d>", p.d);
 }

@@ -55,12 +55,13 @@ struct AttnPlan {
 };
 AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window);
 
-// Per block b (rows b * rpb .. of the call; device q / k / v as xtg::AttnArgs, engine/include/xtg/kv.h:67-78):
-// the own-key partials and the split partials. Then the merge of every row into out [n_q][heads][d].
-std::string launch_attn_own(const AttnPlan& p, int b, const float* q, const float* k, const float* v, int n_q,
-                            int heads, int window, float scale, float* part, hipStream_t stream);
-std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b, const float* q, int n_q, int heads,
-                             long long pos0, int window, float scale, float* part, hipStream_t stream);
+// For blocks b0 .. b0 + nblocks - 1 (block b: rows b * rpb .. of the call; device q / k / v as xtg::AttnArgs,
+// engine/include/xtg/kv.h:67-78), one launch each: the own-key partials and the split partials. Then the merge of
+// every row into out [n_q][heads][d].
+std::string launch_attn_own(const AttnPlan& p, int b0, int nblocks, const float* q, const float* k, const float* v,
+                            int n_q, int heads, int window, float scale, float* part, hipStream_t stream);
+std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblocks, const float* q, int n_q,
+                             int heads, long long pos0, int window, float scale, float* part, hipStream_t stream);
 std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
                               hipStream_t stream);
 

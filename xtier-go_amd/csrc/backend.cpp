@@ -393,11 +393,10 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
   const AttnPlan p = attn_plan(*c, n_q, heads, pos0, window);
   ensure(part_, part_size_, p.part_floats() * sizeof(float));
   float* part = static_cast<float*>(part_);
-  for (int b = 0; b < p.blocks; ++b) {
-    timed([&] { return launch_attn_own(p, b, q, k, v, n_q, heads, window, scale, part, stream_); });
-    if (p.splits > 0)
-      timed([&] { return launch_attn_scan(*c, p, b, q, n_q, heads, pos0, window, scale, part, stream_); });
-  }
+  // every row block in one launch each (the last block may be partial: its q-cols past the rows are masked)
+  timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_); });
+  if (p.splits > 0)
+    timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_); });
   timed([&] { return launch_attn_merge(p, n_q, heads, part, out, stream_); });
 }
 
@@ -427,8 +426,7 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
                              stream_);
   });
   if (p.splits > 0)
-    for (int b = 0; b < p.blocks; ++b)
-      timed([&] { return launch_attn_scan(*c, p, b, q, m, heads, pos0, window, scale, part, stream_); });
+    timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
   if (!store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
   timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
