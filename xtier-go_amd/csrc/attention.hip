@@ -28,8 +28,9 @@
 //     and the query rows are stacked as MFMA columns (q-col = row * group + head), so every K and V byte is read
 //     once per KV head. Each wave streams its tiles with the next tile's loads in flight; the waves' states are
 //     merged in LDS into one partial per q-col.
-//   Own keys (FP32, not rounded to the cache's BF16): one wave per q-col on the vector ALUs, in attn_own_kernel or
-//     inside the decode step's producer (qk_produce_kernel), as one more partial.
+//   Own keys (FP32, not rounded to the cache's BF16), one more partial: for the attention call, FP32 MFMA over
+//     tiles of 16 q-cols x 16 keys (attn_own_mfma_kernel); inside the decode step's producer (qk_produce_kernel),
+//     one wave per q-col on the vector ALUs.
 //   attn_merge_kernel / attn_gate_kernel: one work-group per query row merges its partials (kv.cpp:262-285);
 //     the gate variant applies the decode step's sigmoid gate and norm and writes the o-projection's operand.
 #include <algorithm>
@@ -654,28 +655,123 @@ __device__ inline void write_partial(float* acc, float* ml, size_t rec, int d, f
   }
 }
 
-// One work-group per (KV head, block of query rows b0 + blockIdx.y): wave w takes the block's q-cols w, w + 4, ...
+// Own keys on the matrix cores (FP32 MFMA 16x16x4), for calls of many rows: one wave per tile of 16 q-cols of a
+// row block, over every own key any of its columns sees, 16 keys a step.
+//   S^T (16 keys x 16 q-cols) = K Q^T: at step s lane group g (lane / 16) feeds dim (D / 4) g + s of key / q-col
+//   lane % 16, so each lane's K and Q values are D / 4 contiguous floats; lane (g, j) gets S^T[key 4 g + r][col j].
+//   O^T (D x 16 q-cols) += V^T P^T: step r sums keys 4 g + r over the lane groups, so P^T comes straight from the
+//   scores' registers; lane (g, j) holds O^T[16 t + 4 g + r][col j] in accumulator t.
+// The online softmax runs per column over the lane groups (max and sum through two xor shuffles); the partial
+// record (M, L, O) goes to the own-key slot (split index `splits`) of the column's block.
+struct OwnArgs {
+  const float* q;          // [n_own][heads][D]
+  const float* k;          // [n_own][kv_heads][D]
+  const float* v;
+  float* acc;              // partials as ScanArgs
+  float* ml;
+  size_t blk_records;
+  int b0, nblocks, rpb, n_own, heads, kv_heads, group, window, splits, splits1, qpad, tiles;   // tiles per block
+  float scale2;
+};
+
 template <int D>
-__global__ void __launch_bounds__(kWaves * 64) attn_own_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                               const float* __restrict__ v, int rpb, int b0,
-                                                               int n_own, int heads, int kv_heads, int group,
-                                                               int window, float scale, float* __restrict__ acc_all,
-                                                               float* __restrict__ ml_all, size_t blk_records,
-                                                               int splits, int splits1, int qpad) {
-  const int kvh = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int blk = b0 + int(blockIdx.y), row0 = blk * rpb, n_rows = min(rpb, n_own - row0);
-  float* acc = acc_all + size_t(blk) * blk_records * D;
-  float* ml = ml_all + size_t(blk) * blk_records * 2;
-  for (int c = wave; c < n_rows * group; c += kWaves) {
-    const int r = c / group, hg = c % group, i = row0 + r;
-    const float* qp = q + (size_t(i) * size_t(heads) + size_t(kvh * group + hg)) * D;
-    const int j0 = window > 0 ? max(0, i - window + 1) : 0, j1 = min(i + 1, n_own);
-    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-    own_state<D>(qp, k + size_t(kvh) * D, v + size_t(kvh) * D, size_t(kv_heads) * D, j0, j1, scale * kLog2e, M, L,
-                 a0, a1);
-    write_partial(acc, ml, (size_t(kvh) * size_t(splits1) + size_t(splits)) * size_t(qpad) + size_t(c), D, M, L, a0,
-                  a1);
+__global__ void __launch_bounds__(256) attn_own_mfma_kernel(const OwnArgs a) {
+  constexpr int S = D / 4, T = D / 16;
+  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  const int w = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+  const int per_blk = a.kv_heads * a.tiles;
+  if (w >= per_blk * a.nblocks) return;   // no barriers below: a spare wave just leaves
+  // the last (longest) blocks first
+  const int blk = a.b0 + a.nblocks - 1 - w / per_blk, kvh = (w % per_blk) / a.tiles, tile = w % a.tiles;
+  const int row0 = blk * a.rpb, n_rows = min(a.rpb, a.n_own - row0), cols = n_rows * a.group;
+  const int qc = tile * 16 + j;
+  if (tile * 16 >= cols) return;           // a padding tile of the block
+  const bool live = qc < cols;
+  const int r = live ? qc / a.group : 0, i = row0 + r;
+  const int lo = a.window > 0 ? max(0, i - a.window + 1) : 0;
+  // the tile's key range: its rows run from the first column's to the last live column's
+  const int i_first = row0 + (tile * 16) / a.group, i_last = row0 + (min(tile * 16 + 15, cols - 1)) / a.group;
+  const int kmin = a.window > 0 ? max(0, i_first - a.window + 1) : 0, kmax = i_last + 1;
+
+  float qv[S];
+  {
+    const float* qp = a.q + (size_t(i) * size_t(a.heads) + size_t(kvh * a.group + (live ? qc % a.group : 0))) * D + S * g;
+#pragma unroll
+    for (int e = 0; e < S; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(qp + e);
+      qv[e] = t.x, qv[e + 1] = t.y, qv[e + 2] = t.z, qv[e + 3] = t.w;
+    }
   }
+  const size_t stride = size_t(a.kv_heads) * D;
+  const float* kbase = a.k + size_t(kvh) * D + S * g;
+  const float* vbase = a.v + size_t(kvh) * D + j;
+  float kn[S], vn[4][T];
+  auto load = [&](int kb) {   // key rows past the call's end load its last row (their scores are masked)
+    const float* kr = kbase + size_t(min(kb + j, a.n_own - 1)) * stride;
+#pragma unroll
+    for (int e = 0; e < S; e += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(kr + e);
+      kn[e] = t.x, kn[e + 1] = t.y, kn[e + 2] = t.z, kn[e + 3] = t.w;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const float* vr = vbase + size_t(min(kb + 4 * g + rr, a.n_own - 1)) * stride;
+#pragma unroll
+      for (int t = 0; t < T; ++t) vn[rr][t] = vr[16 * t];
+    }
+  };
+  f32x4 o[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float M = -INFINITY, L = 0.f;
+  load(kmin);
+  for (int kb = kmin; kb < kmax; kb += 16) {
+    float kc[S], vc[4][T];
+#pragma unroll
+    for (int e = 0; e < S; ++e) kc[e] = kn[e];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int t = 0; t < T; ++t) vc[rr][t] = vn[rr][t];
+    load(min(kb + 16, kmax - 1));
+    f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < S; ++e) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[e], qv[e], st, 0, 0, 0);
+    float sc[4], mt = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int key = kb + 4 * g + rr;
+      sc[rr] = key >= lo && key <= i ? st[rr] * a.scale2 : -INFINITY;
+      mt = fmaxf(mt, sc[rr]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mn = fmaxf(M, mt);
+    const float base = mn == -INFINITY ? 0.f : mn;   // no key of the column yet: nothing to rescale
+    const float corr = exp2_fast(M - base);
+    M = mn;
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      p[rr] = exp2_fast(sc[rr] - base);
+      ps += p[rr];
+    }
+    L = L * corr + ps;
+#pragma unroll
+    for (int t = 0; t < T; ++t) o[t] *= corr;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int t = 0; t < T; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vc[rr][t], p[rr], o[t], 0, 0, 0);
+  }
+  L += __shfl_xor(L, 16);
+  L += __shfl_xor(L, 32);
+  if (!live) return;
+  const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(a.splits)) * size_t(a.qpad) + size_t(qc);
+  float* acc = a.acc + size_t(blk) * a.blk_records * D + rec * D;
+  if (g == 0) *reinterpret_cast<float2*>(a.ml + (size_t(blk) * a.blk_records + rec) * 2) = make_float2(M, L);
+#pragma unroll
+  for (int t = 0; t < T; ++t) *reinterpret_cast<f32x4*>(acc + 16 * t + 4 * g) = o[t];
 }
 
 // -------------------------------------------------------------------------------------------------- producer
@@ -1093,17 +1189,35 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblo
 std::string launch_attn_own(const AttnPlan& p, int b0, int nblocks, const float* q, const float* k, const float* v,
                             int n_q, int heads, int window, float scale, float* part, hipStream_t stream) {
   XTG_CHECK(nblocks >= 1 && b0 + nblocks <= p.blocks, "attention: blocks %d .. %d of %d", b0, b0 + nblocks, p.blocks);
-  float* acc = part;
-  float* ml = part + p.records() * size_t(p.d);
-  const dim3 grid{unsigned(p.kv_heads), unsigned(nblocks)}, block{unsigned(kWaves * 64)};
+  XTG_CHECK(p.qpad % 16 == 0, "attention: %d padded q-cols", p.qpad);
+  OwnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.acc = part;
+  a.ml = part + p.records() * size_t(p.d);
+  a.blk_records = blk_records(p);
+  a.b0 = b0;
+  a.nblocks = nblocks;
+  a.rpb = p.rpb;
+  a.n_own = n_q;
+  a.heads = heads;
+  a.kv_heads = p.kv_heads;
+  a.group = p.group;
+  a.window = window;
+  a.splits = p.splits;
+  a.splits1 = p.splits + 1;
+  a.qpad = p.qpad;
+  a.tiles = p.qpad / 16;
+  a.scale2 = scale * kLog2e;
+  const long long waves = (long long)p.kv_heads * a.tiles * nblocks;
+  const dim3 grid{unsigned((waves + 3) / 4)}, block{256};
   if (p.d == 64)
-    hipLaunchKernelGGL(attn_own_kernel<64>, grid, block, 0, stream, q, k, v, p.rpb, b0, n_q, heads, p.kv_heads,
-                       p.group, window, scale, acc, ml, blk_records(p), p.splits, p.splits + 1, p.qpad);
+    hipLaunchKernelGGL(attn_own_mfma_kernel<64>, grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL(attn_own_kernel<128>, grid, block, 0, stream, q, k, v, p.rpb, b0, n_q, heads, p.kv_heads,
-                       p.group, window, scale, acc, ml, blk_records(p), p.splits, p.splits + 1, p.qpad);
+    hipLaunchKernelGGL(attn_own_mfma_kernel<128>, grid, block, 0, stream, a);
   HIP_CHECK(hipGetLastError());
-  return strf("attn_own_kernel<%d>", p.d);
+  return strf("attn_own_mfma_kernel<%d>", p.d);
 }
 
 std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
