@@ -219,10 +219,20 @@ void xtg_hip_dory_destroy(xtg_hip_dory* d);
  * with FP32 products and sums (kernels.cpp:140-155). Prepared on the call; not during a graph capture. */
 int xtg_hip_dory_head_bf16(xtg_hip_dory* d, const xtg_bf16* head, char* err, int err_len);
 /* Replaces GpuDorySession::run_chunk + the head of forward (dory.cpp:1150-1214; CPU dory.cpp:520-578) for one
- * chunk of m <= 8 rows: from the hidden rows x [m][hidden] (device, the embedding rows) at positions pos0 ..
+ * chunk of m <= 512 rows: from the hidden rows x [m][hidden] (device, the embedding rows) at positions pos0 ..
  * pos0 + m - 1 to logits [m][vocab] (device, times logit_scale); each attention sublayer's cache gains the chunk's
- * keys. Queued: capturable into a graph (xtg_hip_graph_*) once the call has run. */
+ * keys. Up to 8 rows (a decode or verify step) run the fused decode kernels; more run the prefill kernels (the
+ * matrix-core GEMM, many-row attention). Queued: capturable into a graph (xtg_hip_graph_*) once the call has run
+ * with the same m. */
 int xtg_hip_dory_forward(xtg_hip_dory* d, const float* x, int m, int64_t pos0, float* logits, char* err, int err_len);
+/* Which rows get logits (xtg::Logits, engine/include/xtg/model.h:28). */
+enum { XTG_LOGITS_NONE = 0, XTG_LOGITS_LAST = 1, XTG_LOGITS_ALL = 2 };
+/* Replaces DorySession::forward's chunk loop (dory.cpp:554-578): n rows of x [n][hidden] (device) at positions
+ * pos0 .. pos0 + n - 1 in chunks of up to 512 rows (the prefill chunk), with logits (device, times logit_scale)
+ * for every row ([n][vocab], XTG_LOGITS_ALL), the last row ([vocab], XTG_LOGITS_LAST) or none (logits may be
+ * NULL). Queued. */
+int xtg_hip_dory_prefill(xtg_hip_dory* d, const float* x, int n, int64_t pos0, int want, float* logits, char* err,
+                         int err_len);
 /* The cache of attention sublayer `attn` (counted over attention sublayers) for loop `inst`, e.g. to fill a
  * context with xtg_hip_kv_store. NULL when there is none. */
 xtg_hip_kv* xtg_hip_dory_cache(xtg_hip_dory* d, int attn, int inst);

@@ -292,3 +292,88 @@ def test_bf16_head_and_fp8_caches(hip, orc, wl):
     print("BF16 head, FP8 caches: logits rel-L2 %.2e" % e)
     assert e <= 1e-3
     assert (got.argmax(1) == want.argmax(1)).all()
+
+
+@pytest.mark.parametrize("kv_dtype,sharp", [(0, False), (0, True), (1, False)])
+def test_tiny_prefill_chunks_then_steps(hip, pkg, orc, wl, kv_dtype, sharp):
+    """The prefill path (chunks of more than 8 rows: GEMM projections, the many-row attention with its own-key
+    tiles, the store after the scan) on the tiny model: prefill() over 700 rows in chunks of 512 + 188 with
+    logits for every row, then four one-row steps, against the oracle's chunks of the same sizes. The 64-slot
+    rings take whole chunks (a ring keeps a chunk's last 64 rows)."""
+    w = wl.DoryWeights(dict(wl.DORY_TINY, kv_dtype=kv_dtype), seed=31 + kv_dtype, context=800)
+    if sharp:
+        w = sharpened(w, seed=32)
+    H, V, n = w.cfg["hidden"], w.cfg["vocab"], 700
+    x = unit_rows(np.random.default_rng(33), n + 4, H)
+    ref = orc.Dory(w, wl)
+    want = np.concatenate([ref.forward(x[0:512], 0, threads=16), ref.forward(x[512:n], 512, threads=16)] +
+                          [ref.forward(x[p:p + 1], p) for p in range(n, n + 4)])
+    dev = hip.dory(w)
+    dx, dl = hip.array(x[:n]), hip.array(shape=(n, V))
+    dx1, dl1 = hip.array(shape=(1, H)), hip.array(shape=(1, V))
+    got = []
+    try:
+        dev.prefill(dx, n, 0, pkg.LOGITS_ALL, dl)
+        got.append(dl.numpy())
+        for p in range(n, n + 4):
+            dx1.upload(x[p:p + 1])
+            dev.forward(dx1, 1, p, dl1)
+            got.append(dl1.numpy())
+    finally:
+        for a in (dx, dl, dx1, dl1):
+            a.free()
+        dev.destroy()
+    got = np.concatenate(got)
+    e = rel_l2(got, want)
+    print("tiny prefill 512 + 188 rows then steps (KV dtype %d, sharp %s): logits rel-L2 %.2e" % (kv_dtype, sharp, e))
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+def test_tiny_prefill_logits_last_and_none(hip, pkg, orc, wl):
+    """prefill() with logits for the last row only (one row of the second chunk: its own operand), and with none
+    followed by a step, against the oracle."""
+    w = wl.DoryWeights(wl.DORY_TINY, seed=35, context=1400)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(36), 1201, H)
+    ref = orc.Dory(w, wl)
+    want_last = None
+    for r in range(0, 600, 512):
+        want_last = ref.forward(x[r:min(600, r + 512)], r, threads=16)[-1]
+    for r in range(600, 1200, 512):
+        ref.forward(x[r:min(1200, r + 512)], r, threads=16)
+    want_step = ref.forward(x[1200:1201], 1200)[0]
+    dev = hip.dory(w)
+    dx, dl = hip.array(x), hip.array(shape=(1, V))
+    try:
+        dev.prefill(dx, 600, 0, pkg.LOGITS_LAST, dl)
+        got_last = dl.numpy()[0]
+        dev.prefill(dx.ptr + 600 * H * 4, 600, 600, pkg.LOGITS_NONE)   # rows 600 .. 1199 of x
+        dev.forward(dx.ptr + 1200 * H * 4, 1, 1200, dl)
+        got_step = dl.numpy()[0]
+    finally:
+        dx.free()
+        dl.free()
+        dev.destroy()
+    for got, want in ((got_last, want_last), (got_step, want_step)):
+        assert rel_l2(got, want) <= 1e-3
+        assert got.argmax() == want.argmax()
+
+
+def test_4b_prefill_chunk(hip, orc, model_4b):
+    """Config 4's model at a 4K context: one 40-row chunk (five operand groups on the GEMM, five attention row
+    blocks) against the oracle's."""
+    w, ref, dev, ctx = model_4b
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(41), 40, H)
+    dx = hip.array(x)
+    dl = hip.array(shape=(40, V))
+    dev.forward(dx, 40, ctx, dl)
+    got = dl.numpy()
+    want = ref.forward(x, ctx, threads=16)
+    dx.free()
+    dl.free()
+    e = rel_l2(got, want)
+    print("4B chunk of 40 rows: logits rel-L2 %.2e" % e)
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libxtg_hip.so")
 
 X_F32, X_BF16 = 0, 1
 KV_BF16, KV_FP8 = 0, 1
+LOGITS_NONE, LOGITS_LAST, LOGITS_ALL = 0, 1, 2   # xtg::Logits order (engine/include/xtg/model.h:28)
 
 # Every function the header declares, with its ctypes signature: (name, restype, argtypes).
 _P = ctypes.c_void_p
@@ -88,6 +89,7 @@ SIGNATURES = [
     ("xtg_hip_dory_destroy", None, [_P]),
     ("xtg_hip_dory_head_bf16", _I, [_P, ctypes.POINTER(Bf16)] + _ERR),
     ("xtg_hip_dory_forward", _I, [_P, _P, _I, _I64, _P] + _ERR),
+    ("xtg_hip_dory_prefill", _I, [_P, _P, _I, _I64, _I, _P] + _ERR),
     ("xtg_hip_dory_cache", _P, [_P, _I, _I]),
     ("xtg_hip_x_operand_bytes", _SZ, [_I]),
     ("xtg_hip_prep_x", _I, [_P, _P, _I, _I, _I, _P] + _ERR),
@@ -388,7 +390,8 @@ class HipBackend:
 
 
 class DorySession:
-    """xtg_hip_dory: forward(x, m, pos0, logits) on device buffers; cache(attn, inst) for filling contexts."""
+    """xtg_hip_dory: forward(x, m, pos0, logits) and prefill(x, n, pos0, want, logits) on device buffers;
+    cache(attn, inst) for filling contexts."""
 
     def __init__(self, backend, weights):
         import xtier_go_amd.workloads as wl
@@ -408,8 +411,15 @@ class DorySession:
             self.h = None
 
     def forward(self, x, m, pos0, logits):
+        """One chunk of m <= 512 rows; logits for every row."""
         err = _errbuf()
         _check(lib().xtg_hip_dory_forward(self.h, _ptr(x), m, pos0, _ptr(logits), err, len(err)), err)
+
+    def prefill(self, x, n, pos0, want, logits=None):
+        """n rows in chunks of up to 512; logits for all rows, the last or none (LOGITS_*)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_dory_prefill(self.h, _ptr(x), n, pos0, want, _ptr(logits) if logits is not None else None,
+                                          err, len(err)), err)
 
     def set_head_bf16(self, w):
         """A BF16 LM head (uint16 BF16 bits [vocab][hidden], kept referenced) in place of the NVFP4 one."""

@@ -776,7 +776,6 @@ __global__ void __launch_bounds__(256) attn_own_mfma_kernel(const OwnArgs a) {
 
 // -------------------------------------------------------------------------------------------------- producer
 
-constexpr int kProdRows = 8, kProdGroup = 8;
 
 struct ProduceArgs {
   float* q;                // [m][heads][d], processed in place
@@ -1020,7 +1019,7 @@ template <int D, int U>
 __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArgs a, const float* __restrict__ g,
                                                                    const float* __restrict__ gs, int vec,
                                                                    float* __restrict__ out, f16x8* __restrict__ xop,
-                                                                   float* __restrict__ xinv) {
+                                                                   float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[2 * kMergeThreads / 64];
   const int row = blockIdx.x, Q = a.heads * D;
   float gv[U][8], sv[U][8], t[U][8];
@@ -1050,7 +1049,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[u][e] *= f;
   if (out) store_row<kMergeThreads, U>(out + size_t(row) * Q, Q, vec, t);
-  if (xop) emit_operand<kMergeThreads, U>(t, Q, row, xop, xinv, red);
+  if (xop) emit_operand<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, red);
 }
 
 // ------------------------------------------------------------------------------------------------------- plan
@@ -1291,7 +1290,7 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
   f16x8* xop = nullptr;
   float* xinv = nullptr;
   if (op) {
-    XTG_CHECK(m <= kMaxRows, "attention gate: %d rows for an operand", m);
+    XTG_CHECK(m <= kMaxOperandRows, "attention gate: %d rows for an operand", m);
     xop = static_cast<f16x8*>(op);
     xinv = reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(Q));
   }
@@ -1302,7 +1301,8 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
   int u = 0;
 #define XTG_GATE(D, U)                                                                                      \
   if (p.d == D && chunks <= U * kMergeThreads && !u) {                                                      \
-    hipLaunchKernelGGL((attn_gate_kernel<D, U>), grid, block, 0, stream, a, g, gs, vec, out, xop, xinv);    \
+    hipLaunchKernelGGL((attn_gate_kernel<D, U>), grid, block, 0, stream, a, g, gs, vec, out, xop, xinv,    \
+                       op_group_bytes(Q));                                                               \
     u = U;                                                                                                  \
   }
   XTG_GATE(64, 1) XTG_GATE(64, 2) XTG_GATE(64, 4) XTG_GATE(128, 1) XTG_GATE(128, 2) XTG_GATE(128, 4)

@@ -65,6 +65,8 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblo
 std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
                               hipStream_t stream);
 
+constexpr int kProdRows = 8, kProdGroup = 8;   // the producer's rows per call and q heads per KV head
+
 // The decode step's producer (packs/dory/dory.cpp:482-490 and the cache store of :507): in one launch per
 // call (m <= 8 rows), RoPE + justnorm of q and k (q *= qscale, q written back in place; k read only, the
 // processed rows also written to kout when it is not NULL), the own-key partials from the FP32 rows, and -- when

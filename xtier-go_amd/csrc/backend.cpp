@@ -401,7 +401,7 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
 }
 
 void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
-                        const float* k, const float* v, const float* qscale, const float* g, const float* gscale,
+                        float* k, const float* v, const float* qscale, const float* g, const float* gscale,
                         float* out, void* op) {
   XTG_CHECK(kvs_.count(c), "attention step: unknown cache");
   XTG_CHECK(m >= 1 && pos0 >= 0, "attention step: %d rows at %lld", m, pos0);
@@ -413,6 +413,19 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
   ensure(part_, part_size_, p.part_floats() * sizeof(float));
   float* part = static_cast<float*>(part_);
   const float* f = inv_freq(theta, c->head_dim);
+  if (m > kProdRows) {
+    // a prefill chunk (the reference's order, dory.cpp:481-515): RoPE + norms in place, the attention over the
+    // read-only cache and the chunk's own keys (matrix-core own-key tiles), the store of the chunk's k / v, then
+    // the merge with the gate and norm
+    timed([&] { return launch_qk_rope_norm(q, k, m, heads, c->kv_heads, c->head_dim, pos0, f,
+                                           qscale, stream_); });
+    timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, m, heads, window, scale, part, stream_); });
+    if (p.splits > 0)
+      timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
+    timed([&] { return launch_kv_store(*c, pos0, m, k, v, stream_); });
+    timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
+    return;
+  }
   // storing before the scan hides nothing the scan should see: a linear cache's new slots are masked as
   // positions >= pos0, and a ring of window + m - 1 slots or more only drops positions outside every row's window
   const bool store_first = !c->ring || (window > 0 && c->slots >= (long long)window + m - 1);

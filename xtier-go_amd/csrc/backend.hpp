@@ -64,15 +64,16 @@ class Backend {
   // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
-  // The attention half of a decode-step sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
+  // The attention half of a Dory sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
   // k / v [m][kv_heads][d], g [m][heads * d]: RoPE + norms of q (rewritten) and k, the attention over the cache
   // and this call's keys, the store of k / v into the cache, then out (optional) and op (optional, the
-  // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)).
+  // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)). Up to 8 rows (a decode or verify step)
+  // in one fused producer; more (a prefill chunk): k is rewritten too, and the steps run as separate launches.
   void attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
-                 const float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
+                 float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
                  void* op);
   // the row kernels of the decode step (rows.hip); device memory. op (optional): also write the result rows as a
-  // GEMV operand of op_bytes(w) bytes.
+  // GEMV / GEMM operand of ceil(rows / 8) groups of op_bytes(w) bytes.
   void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
                     const float* qscale);
   void slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op = nullptr);

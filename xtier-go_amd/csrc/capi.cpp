@@ -279,6 +279,14 @@ int xtg_hip_dory_forward(xtg_hip_dory* d, const float* x, int m, int64_t pos0, f
   });
 }
 
+int xtg_hip_dory_prefill(xtg_hip_dory* d, const float* x, int n, int64_t pos0, int want, float* logits, char* err,
+                         int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(d && x, "dory_prefill: NULL argument");
+    d->s->prefill(x, n, pos0, want, logits);
+  });
+}
+
 xtg_hip_kv* xtg_hip_dory_cache(xtg_hip_dory* d, int attn, int inst) {
   xtg::hip::DevKv* c = nullptr;
   if (!d || guarded(nullptr, 0, [&] { c = d->s->cache(attn, inst); }) != 0) return nullptr;

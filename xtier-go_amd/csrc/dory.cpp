@@ -1,5 +1,6 @@
 #include "dory.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -7,7 +8,7 @@
 namespace xtg::hip {
 
 namespace {
-constexpr int kMaxStepRows = 8;
+constexpr int kChunkRows = 512;   // rows of one run_chunk: the reference's prefill chunk (dory.cpp:145-148)
 }
 
 float* DorySession::upload(const float* v, size_t n) {
@@ -82,16 +83,16 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
     owned_.push_back(p);
     return p;
   };
-  const size_t R = kMaxStepRows;
+  const size_t R = kChunkRows;
   x_ = scratch(R * H);
   input_ = scratch(R * H);
   state_ = scratch(R * H);
   proj_ = scratch(R * size_t(2 * Q + 2 * KV));
   gu_ = scratch(R * 2 * size_t(F));
   o_ = scratch(R * H);
-  for (auto* op : {&op_h_, &op_q_, &op_f_}) {
-    const int k = op == &op_h_ ? H : op == &op_q_ ? Q : F;
-    *op = b_.alloc(Backend::op_bytes(k));
+  for (auto* op : {&op_h_, &op_q_, &op_f_, &op_last_}) {
+    const int k = op == &op_q_ ? Q : op == &op_f_ ? F : H;
+    *op = b_.alloc(Backend::op_bytes(k) * (op == &op_last_ ? 1 : size_t(kChunkRows / 8)));
     owned_.push_back(*op);
   }
 }
@@ -154,9 +155,9 @@ void DorySession::sublayer(Layer& L, int m, long long pos0, int inst) {
   b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
 }
 
-void DorySession::forward(const float* x, int m, long long pos0, float* logits) {
-  // packs/dory/dory.cpp:520-544 from the embedding rows, then the head (:566-576)
-  XTG_CHECK(m >= 1 && m <= kMaxStepRows, "dory: %d rows per step (1..%d)", m, kMaxStepRows);
+void DorySession::run_chunk(const float* x, int m, long long pos0) {
+  // packs/dory/dory.cpp:520-544 from the embedding rows; x's operand is in op_h_ on exit
+  XTG_CHECK(m >= 1 && m <= kChunkRows, "dory: %d rows per chunk (1..%d)", m, kChunkRows);
   XTG_CHECK(pos0 >= 0 && pos0 + m <= c_.context, "context full: %lld + %d > %lld tokens", pos0, m,
             (long long)c_.context);
   const int H = c_.hidden;
@@ -175,11 +176,48 @@ void DorySession::forward(const float* x, int m, long long pos0, float* logits) 
   }
   b_.copy(state_, 0, x_, 0, bytes);
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0);
-  if (head_bf16_.data) {   // from the FP32 rows: the BF16 GEMV makes its own three-term operand
-    b_.matmul_bf16_dev(head_bf16_, x_, XTG_X_F32, m, logits, 0, logit_scale_);
-  } else {
-    XTG_CHECK(head_.codes, "dory: no LM head (pass an NVFP4 head to create or set a BF16 one)");
-    b_.matmul_op(&head_, 1, op_h_, m, logits, 0, logit_scale_);
+}
+
+void DorySession::head(int r0, int rows, float* logits) {
+  // the head times logit_scale (dory.cpp:566-575) for chunk rows r0 .. r0 + rows - 1 into logits [rows][vocab]
+  const int H = c_.hidden;
+  const float* x = x_ + size_t(r0) * H;
+  if (head_bf16_.data) {   // from the FP32 rows: the BF16 GEMV makes its own three-term operand, 8 rows a call
+    for (int r = 0; r < rows; r += 8)
+      b_.matmul_bf16_dev(head_bf16_, x + size_t(r) * H, XTG_X_F32, std::min(8, rows - r), logits,
+                         size_t(r) * size_t(c_.vocab), logit_scale_);
+    return;
+  }
+  XTG_CHECK(head_.codes, "dory: no LM head (pass an NVFP4 head to create or set a BF16 one)");
+  const void* op = op_h_;   // the chunk's operand when the rows are all of it, else the rows' own
+  if (r0 != 0) {
+    XTG_CHECK(rows == 1, "dory: head rows %d .. %d of a chunk", r0, r0 + rows - 1);
+    b_.prep_x(x, XTG_X_F32, 1, H, op_last_);
+    op = op_last_;
+  }
+  b_.matmul_op(&head_, 1, op, rows, logits, 0, logit_scale_);
+}
+
+void DorySession::forward(const float* x, int m, long long pos0, float* logits) {
+  // one chunk, then the head over all its rows (dory.cpp:566-576 with Logits::All)
+  run_chunk(x, m, pos0);
+  head(0, m, logits);
+}
+
+void DorySession::prefill(const float* x, int n, long long pos0, int want, float* logits) {
+  // DorySession::forward (dory.cpp:554-578): chunks of up to 512 rows; logits for every row (ALL, [n][vocab]),
+  // the last row (LAST, [vocab]) or none
+  XTG_CHECK(n >= 1, "dory: %d rows", n);
+  XTG_CHECK(want == XTG_LOGITS_NONE || want == XTG_LOGITS_LAST || want == XTG_LOGITS_ALL, "dory: logits mode %d",
+            want);
+  XTG_CHECK(want == XTG_LOGITS_NONE || logits, "dory: NULL logits");
+  XTG_CHECK(pos0 >= 0 && pos0 + n <= c_.context, "context full: %lld + %d > %lld tokens", pos0, n,
+            (long long)c_.context);
+  for (int off = 0; off < n; off += kChunkRows) {
+    const int m = std::min(kChunkRows, n - off);
+    run_chunk(x + size_t(off) * size_t(c_.hidden), m, pos0 + off);
+    if (want == XTG_LOGITS_ALL) head(0, m, logits + size_t(off) * size_t(c_.vocab));
+    else if (want == XTG_LOGITS_LAST && off + m == n) head(m - 1, 1, logits);
   }
 }
 

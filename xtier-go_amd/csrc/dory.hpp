@@ -20,8 +20,11 @@ class DorySession {
   DorySession& operator=(const DorySession&) = delete;
 
   // run_chunk from the hidden rows x [m][hidden] (device; the embedding rows) at positions pos0 .. pos0 + m - 1,
-  // then the LM head times logit_scale into logits [m][vocab] (device). m <= 8. The caches gain the chunk's keys.
+  // then the LM head times logit_scale into logits [m][vocab] (device). m <= 512. The caches gain the chunk's keys.
   void forward(const float* x, int m, long long pos0, float* logits);
+  // DorySession::forward (dory.cpp:554-578) over n rows in chunks of up to 512, with logits for all rows
+  // ([n][vocab]), the last ([vocab]) or none (want: XTG_LOGITS_*).
+  void prefill(const float* x, int n, long long pos0, int want, float* logits);
   // A BF16 LM head [vocab][hidden] in place of the NVFP4 one (a BF16 checkpoint's lm_head.weight, dory.cpp:325;
   // the resident GPU session's head matmul, dory.cpp:1203). Not during a graph capture.
   void set_head_bf16(const xtg_bf16& head);
@@ -41,6 +44,8 @@ class DorySession {
     float* lr = nullptr;
   };
   void sublayer(Layer& L, int m, long long pos0, int inst);
+  void run_chunk(const float* x, int m, long long pos0);
+  void head(int r0, int rows, float* logits);
   float* upload(const float* v, size_t n);
   void build(const xtg_dory_layer* layers, const float* logit_scale);
   void prepare(const xtg_nvfp4& w);
@@ -59,7 +64,7 @@ class DorySession {
   // and their addresses reused once the session is gone)
   std::vector<const uint8_t*> prepared_;
   std::vector<const uint16_t*> prepared_bf16_;
-  // scratch for up to 8 rows
+  // scratch for up to 512 rows (one chunk)
   float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
         *o_ = nullptr;
   // GEMV operands, each written by the kernel that produces its rows: x's (K = hidden; by the slerp / loop norms
@@ -67,6 +72,7 @@ class DorySession {
   void* op_h_ = nullptr;
   void* op_q_ = nullptr;
   void* op_f_ = nullptr;
+  void* op_last_ = nullptr;   // one row's operand (K = hidden), for the head of a chunk's last row
 };
 
 }  // namespace xtg::hip

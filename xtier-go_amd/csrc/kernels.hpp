@@ -35,6 +35,7 @@ void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k,
 // first 128 m bytes of every step (one cache line per step at m = 1).
 inline size_t xop_bytes(int k) { return size_t((k + kTileK - 1) / kTileK) * 4096; }
 constexpr int kMaxRows = 8;
+constexpr int kMaxOperandRows = 4096;   // rows of one grouped operand (the GEMM's limit)
 // One group's operand: xop_bytes(k), then its 8 row factors xinv. m rows take ceil(m / 8) consecutive groups.
 inline size_t op_group_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(float); }
 

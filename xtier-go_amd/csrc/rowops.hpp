@@ -172,10 +172,16 @@ __device__ inline int operand_exponent(float mx) {
   return e < -120 ? -120 : (e > 120 ? 120 : e);
 }
 
-// Row j of the operand from a row tile (values past w are zero): the work-group's max, then every chunk of the
-// row's kt = ceil(w / 128) k-tiles (zero chunks past w included). red: 2 * NT / 64 floats.
+// Row `row` of an operand of consecutive 8-row groups `stride` bytes apart (xop / xinv: group 0's operand and row
+// factors), from a row tile (values past w are zero): the work-group's max, then every chunk of the row's
+// kt = ceil(w / 128) k-tiles (zero chunks past w included). red: 2 * NT / 64 floats.
 template <int NT, int U>
-__device__ inline void emit_operand(const float (&v)[U][8], int w, int j, f16x8* xop, float* xinv, float* red) {
+__device__ inline void emit_operand(const float (&v)[U][8], int w, int row, f16x8* xop, float* xinv, size_t stride,
+                                    float* red) {
+  const size_t off = size_t(row / kMaxRows) * stride;
+  xop = reinterpret_cast<f16x8*>(reinterpret_cast<char*>(xop) + off);
+  xinv = reinterpret_cast<float*>(reinterpret_cast<char*>(xinv) + off);
+  const int j = row % kMaxRows;
   float mx = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u)

@@ -59,20 +59,21 @@ __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q,
 // The normalised row t * f: written to out (if any) and as operand row j (if any).
 template <int U>
 __device__ inline void finish_row(float (&t)[U][8], float sumsq, int w, bool vec, float* out, f16x8* xop, float* xinv,
-                                  float* red) {
+                                  size_t ostride, float* red) {
   const float f = inv_norm_of(block_sum<kNormThreads>(sumsq, red));
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[u][e] *= f;
   if (out) store_row<kNormThreads, U>(out, w, vec, t);
-  if (xop) emit_operand<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, red);
+  if (xop) emit_operand<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, ostride, red);
 }
 
 template <int U>
 __global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
                                                                    const float* __restrict__ lr, int w, int vec,
-                                                                   f16x8* __restrict__ xop, float* __restrict__ xinv) {
+                                                                   f16x8* __restrict__ xop, float* __restrict__ xinv,
+                                                                   size_t ostride) {
   __shared__ float red[kNormRed];
   float* xr = x + size_t(blockIdx.x) * w;
   float a[U][8], b[U][8], l[U][8];
@@ -98,7 +99,7 @@ __global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restr
       a[u][e] = ya + l[u][e] * (yb - ya);
       s += a[u][e] * a[u][e];
     }
-  finish_row<U>(a, s, w, vec, xr, xop, xinv, red);
+  finish_row<U>(a, s, w, vec, xr, xop, xinv, ostride, red);
 }
 
 template <int U>
@@ -107,7 +108,7 @@ __global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* 
                                                                     const float* __restrict__ sg,
                                                                     const float* __restrict__ su, int w, int vec,
                                                                     float* out, f16x8* __restrict__ xop,
-                                                                    float* __restrict__ xinv) {
+                                                                    float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float a[U][8], b[U][8], s1[U][8], s2[U][8];
   load_row<kNormThreads, U>(g + size_t(blockIdx.x) * w, w, vec, a);
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* 
       a[u][e] = z / (1.f + expf(-z)) * (b[u][e] * s2[u][e]);
       s += a[u][e] * a[u][e];
     }
-  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, red);
+  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, ostride, red);
 }
 
 template <int U>
@@ -131,7 +132,7 @@ __global__ void __launch_bounds__(kNormThreads) gate_norm_kernel(const float* a_
                                                                   const float* __restrict__ gate,
                                                                   const float* __restrict__ gs, int w, int vec,
                                                                   float* out, f16x8* __restrict__ xop,
-                                                                  float* __restrict__ xinv) {
+                                                                  float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float a[U][8], g[U][8], sc[U][8];
   load_row<kNormThreads, U>(a_ + size_t(blockIdx.x) * w, w, vec, a);
@@ -145,14 +146,14 @@ __global__ void __launch_bounds__(kNormThreads) gate_norm_kernel(const float* a_
       a[u][e] = a[u][e] * (1.f / (1.f + expf(-g[u][e] * sc[u][e])));
       s += a[u][e] * a[u][e];
     }
-  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, red);
+  finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, ostride, red);
 }
 
 template <int U>
 __global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_, const float* __restrict__ b_,
                                                                  float* out,
                                                                  int w, int vec, f16x8* __restrict__ xop,
-                                                                 float* __restrict__ xinv) {
+                                                                 float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float a[U][8], b[U][8];
   load_row<kNormThreads, U>(a_ + size_t(blockIdx.x) * w, w, vec, a);
@@ -168,7 +169,7 @@ __global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_,
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += a[u][e] * a[u][e];
-  finish_row<U>(a, s, w, vec, out + size_t(blockIdx.x) * w, xop, xinv, red);
+  finish_row<U>(a, s, w, vec, out + size_t(blockIdx.x) * w, xop, xinv, ostride, red);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -196,14 +197,15 @@ bool rows_vec(int w, std::initializer_list<const void*> ptrs) {
 struct Operand {
   f16x8* xop = nullptr;
   float* xinv = nullptr;
+  size_t stride = 0;   // bytes from one 8-row group to the next
 };
 
 Operand operand_of(void* op, int rows, int w) {
   if (!op) return {};
-  XTG_CHECK(rows <= kMaxRows, "row kernels: %d rows for an operand of at most %d", rows, kMaxRows);
+  XTG_CHECK(rows <= kMaxOperandRows, "row kernels: %d rows for an operand of at most %d", rows, kMaxOperandRows);
   XTG_CHECK(w % 16 == 0, "row kernels: operand width %d (a multiple of 16)", w);
   XTG_CHECK(aligned16(op), "row kernels: operand at %p is not 16-byte aligned", op);
-  return {static_cast<f16x8*>(op), reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(w))};
+  return {static_cast<f16x8*>(op), reinterpret_cast<float*>(static_cast<char*>(op) + xop_bytes(w)), op_group_bytes(w)};
 }
 
 #define XTG_NORM_DISPATCH(KERNEL, ...)                                                                   \
@@ -233,28 +235,28 @@ std::string launch_slerp_norm(float* x, const float* o, const float* lr, int row
                               hipStream_t stream) {
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {x, o, lr});
-  XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, lr, w, vec, p.xop, p.xinv);
+  XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, lr, w, vec, p.xop, p.xinv, p.stride);
 }
 
 std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
                                float* out, void* op, hipStream_t stream) {
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {g, u, sg, su, out});
-  XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, sg, su, w, vec, out, p.xop, p.xinv);
+  XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, sg, su, w, vec, out, p.xop, p.xinv, p.stride);
 }
 
 std::string launch_gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op,
                              hipStream_t stream) {
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {a, gate, gs, out});
-  XTG_NORM_DISPATCH(gate_norm_kernel, a, gate, gs, w, vec, out, p.xop, p.xinv);
+  XTG_NORM_DISPATCH(gate_norm_kernel, a, gate, gs, w, vec, out, p.xop, p.xinv, p.stride);
 }
 
 std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, void* op,
                             hipStream_t stream) {
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {a, b, out});
-  XTG_NORM_DISPATCH(add_norm_kernel, a, b, out, w, vec, p.xop, p.xinv);
+  XTG_NORM_DISPATCH(add_norm_kernel, a, b, out, w, vec, p.xop, p.xinv, p.stride);
 }
 
 }  // namespace xtg::hip

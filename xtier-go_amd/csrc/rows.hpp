@@ -1,6 +1,6 @@
 // Launchers of the row kernels (rows.hip). All pointers are device memory; launchers return the kernel name.
-// op (optional): also write the rows as a GEMV activation operand (kernels.hpp layout, Backend::op_bytes(w) bytes:
-// the operand, then the rows' scales); rows <= kMaxRows and w % 16 == 0 then.
+// op (optional): also write the rows as a GEMV / GEMM activation operand (kernels.hpp layout: ceil(rows / 8) groups of
+// Backend::op_bytes(w) bytes, each the operand of 8 rows, then their scales); w % 16 == 0 then.
 #pragma once
 
 #include <hip/hip_runtime.h>
