@@ -260,6 +260,44 @@ def bf16_head_bench(pkg, wl, hip, reps):
     return out
 
 
+def prefill_run(pkg, hip, dev, w, rng, prompts):
+    """Prompt processing on the 4B-shaped model (BF16 caches): xtg_hip_dory_prefill over n unit-norm rows from
+    position 0 in chunks of 512 with logits for the last row only (the reference's Logits::Last), queued eagerly;
+    wall time from the call to the end of its work. Plus a per-kernel split (events around every launch) of the
+    first prompt."""
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    out = {}
+    nmax = max(prompts)
+    x = rng.standard_normal((nmax, H)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    dx, dl = hip.array(x), hip.array(shape=(1, V))
+    dev.prefill(dx, 512, 0, pkg.LOGITS_LAST, dl)   # scratch sized, kernels loaded
+    hip.finish()
+    for n in prompts:
+        times = []
+        for _ in range(2):
+            t = time.perf_counter()
+            dev.prefill(dx, n, 0, pkg.LOGITS_LAST, dl)
+            hip.finish()
+            times.append(time.perf_counter() - t)
+        s = min(times)
+        out["prompt%d" % n] = {"s": round(s, 4), "tok_s": round(n / s, 1)}
+        log("prefill %5d tokens (chunks of 512, last-row logits): %.1f ms, %.0f tok/s" % (n, s * 1e3, n / s))
+    n = min(prompts)
+    hip.profile(True)
+    dev.prefill(dx, n, 0, pkg.LOGITS_LAST, dl)
+    rep = hip.profile_report()
+    hip.profile(False)
+    tot = sum(v["ms"] for v in rep.values())
+    out["kernels_prompt%d" % n] = {k: {"calls": v["calls"], "ms": round(v["ms"], 2)} for k, v in
+                                   sorted(rep.items(), key=lambda kv: -kv[1]["ms"])}
+    log("prefill %d tokens, kernel time %.1f ms: %s" % (n, tot, ", ".join(
+        "%s %.1f" % (k, v["ms"]) for k, v in sorted(rep.items(), key=lambda kv: -kv[1]["ms"])[:6])))
+    dx.free()
+    dl.free()
+    return out
+
+
 def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     """Config 4: the synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
     row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
@@ -365,6 +403,7 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     if dev8:
         dev8.destroy()
     results["fp8_kv_m1"] = fp8
+    results["prefill"] = prefill_run(pkg, hip, dev, w, rng, [n for n in (4096, 32768) if n <= ctx_max])
     cpu = None
     if cpu_seconds > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
