@@ -73,20 +73,21 @@ int xtg_hip_release_nvfp4(xtg_hip* h, const uint8_t* codes, char* err, int err_l
 /* Replaces xtg::matmul_nvfp4(ThreadPool&, ws, x, m, ys) (kernels.h:27-30, kernels.cpp:84-138) and the host
  * OpenClBackend::matmul (opencl.h:34, opencl.cpp:523-601): y_i[m][n_out_i] = x[m][k] * W_i^T for n_w weights
  * sharing k; x and every ys[i] are host memory; synchronous. Prepares weights not seen before. m >= 1 (rows are
- * processed 8 at a time). */
+ * processed in passes of up to 512: the GEMV for 1-8 rows, the matrix-core GEMM above). */
 int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* x, int m, float* const* ys,
                          char* err, int err_len);
 /* Replaces OpenClBackend::matmul(ws, Mem x, m, Mem y, y_offset) (opencl.h:54-55, opencl.cpp:694-754): the n_w
  * projections of the device input x ([m][k], FP32 or BF16 per x_dtype) into consecutive [m][n_out_i] blocks of
- * the device output y starting at y_offset floats. Queued; 1 <= m <= 8, n_w <= 4 per call (the fused q/k/v/g
- * and gate/up of the Dory sublayers). */
+ * the device output y starting at y_offset floats. Queued; 1 <= m <= 4096 (1-8 rows: the GEMV; more: the GEMM),
+ * n_w <= 4 per call (the fused q/k/v/g and gate/up of the Dory sublayers). */
 int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
                              size_t y_offset, char* err, int err_len);
 
 /* The device matmul in its two steps, for callers that reuse one activation operand or produce it themselves
  * (no counterpart in the reference, whose kernels read FP32 x directly): xtg_hip_x_operand_bytes(k) bytes of
- * device memory hold the matrix-core form of up to 8 rows of x; xtg_hip_prep_x fills it (queued) and
- * xtg_hip_matmul_nvfp4_op runs the projections on it with the same output convention as the call above. */
+ * device memory hold the matrix-core form of 8 rows of x, and m rows take ceil(m / 8) such groups back to back;
+ * xtg_hip_prep_x fills it (queued) and xtg_hip_matmul_nvfp4_op runs the projections on it with the same output
+ * convention as the call above (1 <= m <= 4096). */
 size_t xtg_hip_x_operand_bytes(int k);
 int xtg_hip_prep_x(xtg_hip* h, const void* x, int x_dtype, int m, int k, void* op, char* err, int err_len);
 int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* op, int m, float* y, size_t y_offset,
