@@ -134,6 +134,9 @@ int64_t xtg_hip_kv_bytes(xtg_hip* h, const xtg_hip_kv* kv);
 int xtg_hip_kv_save(xtg_hip* h, const xtg_hip_kv* kv, void* out, size_t bytes, char* err, int err_len);
 int xtg_hip_kv_restore(xtg_hip* h, xtg_hip_kv* kv, const void* in, size_t bytes, char* err, int err_len);
 int xtg_hip_kv_release(xtg_hip* h, xtg_hip_kv* kv, char* err, int err_len);
+/* GpuDorySession::snapshot / restore's per-ring device copies (dory.cpp:1231-1273): the whole state of src (data,
+ * FP8 scales, slot positions) into dst, a cache of the same shape, ring size and dtype; device to device, queued. */
+int xtg_hip_kv_copy(xtg_hip* h, const xtg_hip_kv* src, xtg_hip_kv* dst, char* err, int err_len);
 
 /* ------------------------------------------------------------------------------------------- attention */
 
@@ -180,6 +183,10 @@ int xtg_hip_gate_norm(xtg_hip* h, float* att, const float* gate, const float* gs
  * justnorm(a) when b is NULL; out may be a; queued. */
 int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int rows, int width, char* err,
                      int err_len);
+/* xtg::argmax (engine/include/xtg/sampler.h:29, engine/src/sampler.cpp:8-13), greedy decoding's token, per row of
+ * device logits [rows][n] into device out [rows] (int32): the first index of the largest value; NaNs never win, and
+ * a NaN in element 0 gives 0, as the reference's scan does. Queued. */
+int xtg_hip_argmax(xtg_hip* h, const float* logits, int rows, int n, int32_t* out, char* err, int err_len);
 
 /* ----------------------------------------------------------------------------------- Dory decode step */
 
@@ -234,6 +241,12 @@ enum { XTG_LOGITS_NONE = 0, XTG_LOGITS_LAST = 1, XTG_LOGITS_ALL = 2 };
  * NULL). Queued. */
 int xtg_hip_dory_prefill(xtg_hip_dory* d, const float* x, int n, int64_t pos0, int want, float* logits, char* err,
                          int err_len);
+/* Replaces DorySession / GpuDorySession::snapshot and restore (dory.cpp:591-614, 1231-1273): device copies of
+ * every sliding sublayer's ring into snapshot slot `slot` (0..63; its storage is made on first use), and back.
+ * Global caches are not copied: keys written past the restored position are masked by position. The caller keeps
+ * the position (the reference's n_). Queued. */
+int xtg_hip_dory_snapshot(xtg_hip_dory* d, int slot, char* err, int err_len);
+int xtg_hip_dory_restore(xtg_hip_dory* d, int slot, char* err, int err_len);
 /* The cache of attention sublayer `attn` (counted over attention sublayers) for loop `inst`, e.g. to fill a
  * context with xtg_hip_kv_store. NULL when there is none. */
 xtg_hip_kv* xtg_hip_dory_cache(xtg_hip_dory* d, int attn, int inst);

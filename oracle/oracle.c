@@ -302,6 +302,15 @@ void xo_gate_norm(float* att, const float* gate, const float* gs, int rows, int 
   xo_justnorm(att, rows, width);
 }
 
+int xo_argmax(const float* x, int n) {
+  /* engine/src/sampler.cpp:8-13: the first index whose value no later value exceeds; a NaN never compares
+     greater (and a NaN at 0 is never displaced) */
+  int best = 0;
+  for (int i = 1; i < n; ++i)
+    if (x[i] > x[best]) best = i;
+  return best;
+}
+
 void xo_add_norm(const float* a, const float* b, float* out, int rows, int width) {
   /* packs/dory/dory.cpp:532-541: loop entry x = justnorm(state + input); loop exit state = justnorm(x) */
   const size_t n = (size_t)rows * (size_t)width;

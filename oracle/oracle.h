@@ -59,6 +59,7 @@ void xo_rope_table(float* cs, int m, int head_dim, int64_t pos0, float theta);
 void xo_gate_norm(float* att, const float* gate, const float* gs, int rows, int width);
 /* :532-541: out = justnorm(a + b) (b non-NULL) or justnorm(a); out may alias a */
 void xo_add_norm(const float* a, const float* b, float* out, int rows, int width);
+int xo_argmax(const float* x, int n);                                                      /* sampler.cpp:8-13 */
 
 /* --- Q/K producer: packs/dory/dory.cpp:481-490 (RoPE q and k, justnorm per head, q *= qscale) --- */
 void xo_qk_produce(float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0, float theta,

@@ -70,6 +70,7 @@ _ORACLE_SIGS = [
     ("xo_qk_produce", None, [_P, _P, _I, _I, _I, _I, _I64, _F, _P]),
     ("xo_gate_norm", None, [_P, _P, _P, _I, _I]),
     ("xo_add_norm", None, [_P, _P, _P, _I, _I]),
+    ("xo_argmax", _I, [_P, _I]),
     ("xo_kv_create", _P, [_I, _I, _I64, _I, _I]),
     ("xo_kv_free", None, [_P]),
     ("xo_kv_slots", _I64, [_P]),
@@ -97,6 +98,7 @@ _REF_SIGS = [
     ("xr_matmul_nvfp4", _I, [ctypes.POINTER(Nvfp4), _I, _P, _I, ctypes.POINTER(_P), _I]),
     ("xr_matmul_bf16", _I, [_P, _I, _I, _P, _I, _P, _I]),
     ("xr_justnorm", None, [_P, _I, _I]),
+    ("xr_argmax", _I, [_P, _I]),
     ("xr_slerp_residual", None, [_P, _P, _P, _I, _I]),
     ("xr_rope", None, [_P, _I, _I, _I, _I64, _F]),
     ("xr_swiglu_scaled", None, [_P, _P, _P, _P, _I, _I]),
@@ -225,6 +227,13 @@ def gate_norm(att, gate, gs):
     rows = att.shape[0] if att.ndim > 1 else 1
     oracle().xo_gate_norm(att.ctypes.data, _f32(gate).ctypes.data, _f32(gs).ctypes.data, rows, att.shape[-1])
     return att
+
+
+def argmax(x, use_ref=False):
+    """xtg::argmax (sampler.cpp:8-13) of each row of x float32 [rows][n] -> int32 [rows]."""
+    x = np.atleast_2d(_f32(x))
+    fn = ref().xr_argmax if use_ref else oracle().xo_argmax
+    return np.array([fn(x[r].ctypes.data, x.shape[1]) for r in range(x.shape[0])], np.int32)
 
 
 def add_norm(a, b=None):

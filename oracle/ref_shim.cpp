@@ -1,7 +1,7 @@
 // extern "C" entry points into the reference engine's own CPU kernels, compiled from the reference sources by
 // oracle/Makefile into oracle/_ref/libxtgref.so. TEST INFRASTRUCTURE ONLY: used to pin the oracle restatement
 // and, when present, as the CPU baseline. Calls go straight to xtg::matmul_nvfp4 / attention / KvCache / rope /
-// justnorm / slerp_residual / swiglu_scaled / f32_to_e4m3 (engine/include/xtg/{fp,kernels,kv}.h).
+// justnorm / slerp_residual / swiglu_scaled / f32_to_e4m3 / argmax (engine/include/xtg/{fp,kernels,kv,sampler}.h).
 #include <cstdint>
 #include <map>
 #include <memory>
@@ -11,6 +11,7 @@
 #include "xtg/fp.h"
 #include "xtg/kernels.h"
 #include "xtg/kv.h"
+#include "xtg/sampler.h"
 #include "xtg/threadpool.h"
 
 namespace {
@@ -70,6 +71,7 @@ int xr_matmul_bf16(const uint16_t* w, int n_out, int k, const float* x, int m, f
 }
 
 void xr_justnorm(float* x, int rows, int width) { xtg::justnorm(x, rows, width); }
+int xr_argmax(const float* x, int n) { return xtg::argmax(x, n); }
 void xr_slerp_residual(float* a, const float* b, const float* lr, int rows, int width) {
   xtg::slerp_residual(a, b, lr, rows, width);
 }

@@ -361,3 +361,32 @@ def test_errors(hip, pkg):
             dc.destroy()
     with pytest.raises(pkg.XtgError, match="head_dim"):
         hip.kv_cache(2, 96, 32)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_kv_copy_device_snapshot(hip, pkg, dtype):
+    """A device copy (the resident session's ring snapshots) holds exactly the source's state: its host blob equals
+    the source's, later stores into the source leave it unchanged, and copying it back restores the source.
+    Caches of another shape are refused."""
+    rng = np.random.default_rng(17 + dtype)
+    kvh, d = 2, 128
+    K = rng.standard_normal((150, kvh, d)).astype(np.float32)
+    V = rng.standard_normal((150, kvh, d)).astype(np.float32)
+    src = hip.kv_cache(kvh, d, 0, ring=96, dtype=dtype)
+    snap = hip.kv_cache(kvh, d, 0, ring=96, dtype=dtype)
+    other = hip.kv_cache(kvh, d, 0, ring=64, dtype=dtype)
+    try:
+        src.store_host(0, K[:100], V[:100])
+        before = src.save()
+        src.copy_to(snap)
+        np.testing.assert_array_equal(snap.save(), before)
+        src.store_host(100, K[100:], V[100:])
+        assert not np.array_equal(src.save(), before)
+        np.testing.assert_array_equal(snap.save(), before)
+        snap.copy_to(src)
+        np.testing.assert_array_equal(src.save(), before)
+        with pytest.raises(pkg.XtgError):
+            src.copy_to(other)
+    finally:
+        for c in (src, snap, other):
+            c.destroy()

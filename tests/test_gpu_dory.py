@@ -377,3 +377,33 @@ def test_4b_prefill_chunk(hip, orc, model_4b):
     print("4B chunk of 40 rows: logits rel-L2 %.2e" % e)
     assert e <= 1e-3
     assert (got.argmax(1) == want.argmax(1)).all()
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_snapshot_restore_rings(hip, wl, kv_dtype):
+    """Snapshot slot 0 after a 200-row prompt, run a step, run 100 more rows (the 64-slot rings lose the keys the
+    step needs), restore slot 0 and run the step again: the logits equal the first run's exactly. Without the
+    restore they differ."""
+    w = wl.DoryWeights(dict(wl.DORY_TINY, kv_dtype=kv_dtype), seed=45, context=400)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(46), 308, H)
+    dev = hip.dory(w)
+    dx, dl = hip.array(x), hip.array(shape=(8, V))
+    step = dx.ptr + 200 * H * 4   # rows 200 .. 207
+    try:
+        dev.prefill(dx, 200, 0, 0)
+        dev.snapshot(0)
+        dev.forward(step, 8, 200, dl)
+        first = dl.numpy()
+        dev.prefill(dx.ptr + 208 * H * 4, 100, 208, 0)
+        dev.forward(step, 8, 200, dl)
+        stale = dl.numpy()
+        dev.restore(0)
+        dev.forward(step, 8, 200, dl)
+        again = dl.numpy()
+    finally:
+        dx.free()
+        dl.free()
+        dev.destroy()
+    np.testing.assert_array_equal(again, first)
+    assert rel_l2(stale, first) > 1e-4

@@ -80,3 +80,27 @@ def test_gate_and_add_norm(hip, orc, rows):
     assert rel_l2(dx.numpy(), orc.add_norm(a)) <= 1e-6
     for arr in (da, dgt, dgs, dx, dy, dz):
         arr.free()
+
+
+@pytest.mark.parametrize("rows,n", [(1, 131072), (8, 131072), (3, 1001), (2, 1), (4, 4096)])
+def test_argmax(hip, orc, rows, n):
+    """Greedy decoding's token per row (xtg::argmax, sampler.cpp:8-13), equal to the oracle's: rounded values (many
+    ties, first index wins), a planted pair of equal maxima, NaN at element 0 (answer 0), NaNs elsewhere (passed
+    over), a row of -inf (answer 0)."""
+    rng = np.random.default_rng(rows * 7 + n)
+    x = np.round(rng.standard_normal((rows, n)) * 4).astype(np.float32)
+    if n > 10:
+        x[0, n // 3] = x[0, n - 2] = x[0].max() + 1
+    if rows > 1:
+        x[1, 0] = np.nan
+    if rows > 2:
+        x[2, ::5] = np.nan
+    if rows > 3:
+        x[3] = -np.inf
+    dx = hip.array(x)
+    dout = hip.array(shape=(rows,), dtype=np.int32)
+    hip.argmax(dx, rows, n, dout)
+    got = dout.numpy()
+    dx.free()
+    dout.free()
+    np.testing.assert_array_equal(got, orc.argmax(x))

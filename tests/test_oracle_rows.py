@@ -102,3 +102,31 @@ def test_rows_vs_reference_bitwise(orc):
     np.testing.assert_array_equal(orc.slerp_residual(x, b, lr), orc.slerp_residual(x, b, lr, use_ref=True))
     qk = rng.standard_normal((8, 40, 128)).astype(np.float32)
     np.testing.assert_array_equal(orc.rope(qk, 40, 128, 39999, 1e6), orc.rope(qk, 40, 128, 39999, 1e6, use_ref=True))
+
+
+def argmax_cases():
+    """Rows with known answers: ties go to the first index, NaNs never win, a NaN at 0 is never displaced, -inf
+    everywhere gives 0."""
+    nan, inf = np.float32("nan"), np.float32("inf")
+    return [([1, 3, 3, 2], 1), ([5, 1, 5], 0), ([nan, 5, 6], 0), ([1, nan, 0.5], 0), ([-1, nan, 7, 7, nan], 2),
+            ([-inf, -inf], 0), ([-inf, nan, -1], 2), ([0.0, -0.0], 0), ([-0.0, 0.0], 0), ([2], 0),
+            ([-3, -2, -2.5, -2], 1)]
+
+
+def test_argmax_known_answers(orc):
+    for row, want in argmax_cases():
+        assert int(orc.argmax(np.array(row, np.float32))[0]) == want, row
+
+
+@pytest.mark.skipif(not __import__("oracle").ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_argmax_vs_reference(orc):
+    """The reference's own xtg::argmax on the known-answer rows and on 131072-wide rows with planted ties and NaNs."""
+    for row, _ in argmax_cases():
+        x = np.array(row, np.float32)
+        assert orc.argmax(x, use_ref=True)[0] == orc.argmax(x)[0]
+    rng = np.random.default_rng(7)
+    x = np.round(rng.standard_normal((6, 131072)) * 4).astype(np.float32)   # many equal values
+    x[1, 0] = np.nan
+    x[2, ::3] = np.nan
+    x[3, 5000] = x[3, 90000] = x[3].max() + 1
+    np.testing.assert_array_equal(orc.argmax(x, use_ref=True), orc.argmax(x))

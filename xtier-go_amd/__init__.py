@@ -77,6 +77,7 @@ SIGNATURES = [
     ("xtg_hip_kv_bytes", _I64, [_P, _P]),
     ("xtg_hip_kv_save", _I, [_P, _P, _P, _SZ] + _ERR),
     ("xtg_hip_kv_restore", _I, [_P, _P, _P, _SZ] + _ERR),
+    ("xtg_hip_kv_copy", _I, [_P, _P, _P] + _ERR),
     ("xtg_hip_kv_release", _I, [_P, _P] + _ERR),
     ("xtg_hip_attention", _I, [_P, ctypes.POINTER(AttnArgs)] + _ERR),
     ("xtg_hip_qk_rope_norm", _I, [_P, _P, _P, _I, _I, _I, _I, _I64, _F, _P] + _ERR),
@@ -84,6 +85,7 @@ SIGNATURES = [
     ("xtg_hip_swiglu_norm", _I, [_P, _P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_gate_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_add_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
+    ("xtg_hip_argmax", _I, [_P, _P, _I, _I, _P] + _ERR),
     ("xtg_hip_dory_create", _P, [_P, ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4),
                                  _P] + _ERR),
     ("xtg_hip_dory_destroy", None, [_P]),
@@ -91,6 +93,8 @@ SIGNATURES = [
     ("xtg_hip_dory_forward", _I, [_P, _P, _I, _I64, _P] + _ERR),
     ("xtg_hip_dory_prefill", _I, [_P, _P, _I, _I64, _I, _P] + _ERR),
     ("xtg_hip_dory_cache", _P, [_P, _I, _I]),
+    ("xtg_hip_dory_snapshot", _I, [_P, _I] + _ERR),
+    ("xtg_hip_dory_restore", _I, [_P, _I] + _ERR),
     ("xtg_hip_x_operand_bytes", _SZ, [_I]),
     ("xtg_hip_prep_x", _I, [_P, _P, _I, _I, _I, _P] + _ERR),
     ("xtg_hip_matmul_nvfp4_op", _I, [_P, ctypes.POINTER(Nvfp4), _I, _P, _I, _P, _SZ] + _ERR),
@@ -388,6 +392,11 @@ class HipBackend:
         err = _errbuf()
         _check(lib().xtg_hip_add_norm(self.h, _ptr(a), _ptr(b), _ptr(out), rows, width, err, len(err)), err)
 
+    def argmax(self, logits, rows, n, out):
+        """out[r] (device int32) = the first index of the largest of logits[r][:n] (device)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_argmax(self.h, _ptr(logits), rows, n, _ptr(out), err, len(err)), err)
+
 
 class DorySession:
     """xtg_hip_dory: forward(x, m, pos0, logits) and prefill(x, n, pos0, want, logits) on device buffers;
@@ -428,6 +437,14 @@ class DorySession:
         st = Bf16(w.ctypes.data, w.shape[0], w.shape[1])
         err = _errbuf()
         _check(lib().xtg_hip_dory_head_bf16(self.h, ctypes.byref(st), err, len(err)), err)
+
+    def snapshot(self, slot):
+        err = _errbuf()
+        _check(lib().xtg_hip_dory_snapshot(self.h, slot, err, len(err)), err)
+
+    def restore(self, slot):
+        err = _errbuf()
+        _check(lib().xtg_hip_dory_restore(self.h, slot, err, len(err)), err)
 
     def cache(self, attn, inst=0):
         h = lib().xtg_hip_dory_cache(self.h, attn, inst)
@@ -497,6 +514,11 @@ class KvCache:
     def release(self):
         err = _errbuf()
         _check(lib().xtg_hip_kv_release(self.b.h, self.h, err, len(err)), err)
+
+    def copy_to(self, dst):
+        """Device copy of this cache's whole state into dst (same shape, ring and dtype)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_kv_copy(self.b.h, self.h, dst.h, err, len(err)), err)
 
 
 class DeviceArray:

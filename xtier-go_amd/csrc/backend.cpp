@@ -382,6 +382,22 @@ void Backend::kv_release(DevKv* c) {
   clear_kv(c);
 }
 
+void Backend::kv_copy(const DevKv* src, DevKv* dst) {
+  XTG_CHECK(kvs_.count(const_cast<DevKv*>(src)) && kvs_.count(dst), "kv_copy: unknown cache");
+  XTG_CHECK(src->kv_heads == dst->kv_heads && src->head_dim == dst->head_dim && src->slots == dst->slots &&
+                src->ring == dst->ring && src->fp8 == dst->fp8,
+            "kv_copy: caches of different shapes or dtypes");
+  if (src == dst) return;
+  HIP_CHECK(hipMemcpyAsync(dst->k, src->k, src->data_bytes(), hipMemcpyDeviceToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(dst->v, src->v, src->data_bytes(), hipMemcpyDeviceToDevice, stream_));
+  if (src->fp8) {
+    HIP_CHECK(hipMemcpyAsync(dst->kscale, src->kscale, src->scale_bytes(), hipMemcpyDeviceToDevice, stream_));
+    HIP_CHECK(hipMemcpyAsync(dst->vscale, src->vscale, src->scale_bytes(), hipMemcpyDeviceToDevice, stream_));
+  }
+  HIP_CHECK(hipMemcpyAsync(dst->slot_pos, src->slot_pos, size_t(src->slots_pad) * sizeof(int),
+                           hipMemcpyDeviceToDevice, stream_));
+}
+
 void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                         const float* k, const float* v, float* out) {
   XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "attention: unknown cache");
@@ -485,6 +501,11 @@ void Backend::gate_norm(const float* a, const float* gate, const float* gs, int 
 void Backend::add_norm(const float* a, const float* b, float* out, int rows, int w, void* op) {
   XTG_CHECK(a && out && rows >= 1 && w >= 1, "add_norm: bad arguments");
   timed([&] { return launch_add_norm(a, b, out, rows, w, op, stream_); });
+}
+
+void Backend::argmax(const float* x, int rows, int n, int* out) {
+  XTG_CHECK(x && out && rows >= 1 && n >= 1, "argmax: bad arguments");
+  timed([&] { return launch_argmax(x, rows, n, out, stream_); });
 }
 
 hipEvent_t Backend::event() {

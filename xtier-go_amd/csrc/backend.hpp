@@ -61,6 +61,8 @@ class Backend {
   void kv_save(const DevKv* c, void* out, size_t bytes);
   void kv_restore(DevKv* c, const void* in, size_t bytes);
   void kv_release(DevKv* c);
+  // device copy of src's whole state (data, scales, slot positions) into dst of the same shape and dtype; queued
+  void kv_copy(const DevKv* src, DevKv* dst);
   // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
@@ -81,6 +83,8 @@ class Backend {
                    void* op = nullptr);
   void gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op = nullptr);
   void add_norm(const float* a, const float* b, float* out, int rows, int w, void* op = nullptr);
+  // greedy decoding's token (xtg::argmax, sampler.cpp:8-13) of each of `rows` rows of n logits; device out int32
+  void argmax(const float* x, int rows, int n, int* out);
   // 1 / theta^(2i/d) in FP32 computed on the host as engine/src/kernels.cpp:191-201 does, kept on the device
   const float* inv_freq(float theta, int d);
 

@@ -189,6 +189,13 @@ int xtg_hip_kv_release(xtg_hip* h, xtg_hip_kv* kv, char* err, int err_len) {
   });
 }
 
+int xtg_hip_kv_copy(xtg_hip* h, const xtg_hip_kv* src, xtg_hip_kv* dst, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && src && dst, "kv_copy: NULL argument");
+    h->b->kv_copy(reinterpret_cast<const xtg::hip::DevKv*>(src), reinterpret_cast<xtg::hip::DevKv*>(dst));
+  });
+}
+
 int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h && a && a->cache, "attention: NULL argument");
@@ -240,6 +247,13 @@ int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int
   });
 }
 
+int xtg_hip_argmax(xtg_hip* h, const float* logits, int rows, int n, int32_t* out, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "argmax: NULL handle");
+    h->b->argmax(logits, rows, n, out);
+  });
+}
+
 struct xtg_hip_dory {
   xtg_hip* h;
   std::unique_ptr<xtg::hip::DorySession> s;
@@ -284,6 +298,20 @@ int xtg_hip_dory_prefill(xtg_hip_dory* d, const float* x, int n, int64_t pos0, i
   return guarded(err, err_len, [&] {
     XTG_CHECK(d && x, "dory_prefill: NULL argument");
     d->s->prefill(x, n, pos0, want, logits);
+  });
+}
+
+int xtg_hip_dory_snapshot(xtg_hip_dory* d, int slot, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(d, "dory_snapshot: NULL handle");
+    d->s->snapshot(slot);
+  });
+}
+
+int xtg_hip_dory_restore(xtg_hip_dory* d, int slot, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(d, "dory_restore: NULL handle");
+    d->s->restore(slot);
   });
 }
 

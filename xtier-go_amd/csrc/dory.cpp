@@ -9,6 +9,7 @@ namespace xtg::hip {
 
 namespace {
 constexpr int kChunkRows = 512;   // rows of one run_chunk: the reference's prefill chunk (dory.cpp:145-148)
+constexpr int kMaxSnapshots = 64;
 }
 
 float* DorySession::upload(const float* v, size_t n) {
@@ -99,6 +100,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
 
 void DorySession::release_all() {
   try {
+    for (auto& snap : snaps_)
+      for (DevKv* c : snap) b_.kv_destroy(c);
     for (DevKv* c : caches_)
       if (c) b_.kv_destroy(c);
     for (void* p : owned_) b_.release(p);
@@ -107,6 +110,7 @@ void DorySession::release_all() {
   } catch (...) {
   }
   caches_.clear();
+  snaps_.clear();
   owned_.clear();
   prepared_.clear();
   prepared_bf16_.clear();
@@ -119,6 +123,28 @@ DevKv* DorySession::cache(int attn, int inst) {
   DevKv* c = caches_[size_t(attn) * size_t(c_.loops) + size_t(inst)];
   XTG_CHECK(c, "dory: attention sublayer %d has no loop instance %d", attn, inst);
   return c;
+}
+
+void DorySession::snapshot(int slot) {
+  XTG_CHECK(slot >= 0 && slot < kMaxSnapshots, "dory: snapshot slot %d (0..%d)", slot, kMaxSnapshots - 1);
+  if (size_t(slot) >= snaps_.size()) snaps_.resize(size_t(slot) + 1);
+  std::vector<DevKv*>& snap = snaps_[size_t(slot)];
+  size_t i = 0;
+  for (DevKv* c : caches_) {
+    if (!c || !c->ring) continue;
+    if (i == snap.size())   // first use of the slot: a ring like this one
+      snap.push_back(b_.kv_create(c->kv_heads, c->head_dim, c->slots, int(c->slots), c->fp8 ? XTG_KV_FP8 : XTG_KV_BF16));
+    b_.kv_copy(c, snap[i++]);
+  }
+}
+
+void DorySession::restore(int slot) {
+  XTG_CHECK(slot >= 0 && size_t(slot) < snaps_.size() && !snaps_[size_t(slot)].empty(),
+            "dory: snapshot slot %d holds nothing", slot);
+  const std::vector<DevKv*>& snap = snaps_[size_t(slot)];
+  size_t i = 0;
+  for (DevKv* c : caches_)
+    if (c && c->ring) b_.kv_copy(snap[i++], c);
 }
 
 void DorySession::set_head_bf16(const xtg_bf16& head) {

@@ -29,6 +29,11 @@ class DorySession {
   // the resident GPU session's head matmul, dory.cpp:1203). Not during a graph capture.
   void set_head_bf16(const xtg_bf16& head);
   DevKv* cache(int attn, int inst);
+  // DorySession / GpuDorySession::snapshot and restore (dory.cpp:591-614, 1231-1273): device copies of every ring
+  // cache into snapshot slot `slot` (storage made on its first use) and back. Global caches need no copy: what a
+  // later call wrote past the restored position is masked by position. The caller keeps the position.
+  void snapshot(int slot);
+  void restore(int slot);
   Backend& backend() { return b_; }
   int n_attn() const { return n_attn_; }
 
@@ -59,6 +64,7 @@ class DorySession {
   float* logit_scale_ = nullptr;
   int n_attn_ = 0;
   std::vector<DevKv*> caches_;   // [attn][loops]
+  std::vector<std::vector<DevKv*>> snaps_;   // [slot][ring caches in caches_ order]
   std::vector<void*> owned_;     // device vectors and scratch
   // weights this session prepared (their device copies go with it: the host arrays that key them may be freed
   // and their addresses reused once the session is gone)

@@ -13,6 +13,7 @@
 // The norms run one work-group of 512 threads per row with the whole row in registers (one read of each input,
 // the sums as block reductions), and can also write the row as the next projection's GEMV operand (the f16
 // high / low split prep_x_kernel makes), so no separate operand pass runs between a norm and its projection.
+#include <climits>
 #include <cmath>
 
 #include "common.hpp"
@@ -172,6 +173,56 @@ __global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_,
   finish_row<U>(a, s, w, vec, out + size_t(blockIdx.x) * w, xop, xinv, ostride, red);
 }
 
+// xtg::argmax (engine/src/sampler.cpp:8-13) of each row of n logits: the first index of the largest value. A NaN
+// never compares greater, so NaNs are passed over, except that a NaN in element 0 is never displaced (answer 0).
+// One work-group of 1024 threads per row; (value, index) pairs reduce with "greater, or equal at a smaller index".
+constexpr int kArgmaxThreads = 1024;
+
+__device__ inline void argmax_take(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const float* __restrict__ x, int n, int vec,
+                                                                 int* __restrict__ out) {
+  __shared__ float sv[kArgmaxThreads / 64];
+  __shared__ int si[kArgmaxThreads / 64];
+  const float* r = x + size_t(blockIdx.x) * size_t(n);
+  float bv = -INFINITY;
+  int bi = INT_MAX;   // no element yet (an element equal to -inf still takes the place)
+  int i0 = 0;
+  if (vec) {
+    const int n4 = n / 4;
+    for (int c = threadIdx.x; c < n4; c += kArgmaxThreads) {
+      const float4 t = reinterpret_cast<const float4*>(r)[c];
+      argmax_take(bv, bi, t.x, 4 * c);
+      argmax_take(bv, bi, t.y, 4 * c + 1);
+      argmax_take(bv, bi, t.z, 4 * c + 2);
+      argmax_take(bv, bi, t.w, 4 * c + 3);
+    }
+    i0 = 4 * n4;
+  }
+  for (int i = i0 + int(threadIdx.x); i < n; i += kArgmaxThreads) argmax_take(bv, bi, r[i], i);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v = __shfl_xor(bv, off);
+    const int i = __shfl_xor(bi, off);
+    argmax_take(bv, bi, v, i);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_take(bv, bi, sv[w], si[w]);
+    out[blockIdx.x] = (r[0] != r[0] || bi == INT_MAX) ? 0 : bi;
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 
 namespace {
@@ -257,6 +308,13 @@ std::string launch_add_norm(const float* a, const float* b, float* out, int rows
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {a, b, out});
   XTG_NORM_DISPATCH(add_norm_kernel, a, b, out, w, vec, p.xop, p.xinv, p.stride);
+}
+
+std::string launch_argmax(const float* x, int rows, int n, int* out, hipStream_t stream) {
+  const int vec = rows_vec(n, {x});
+  hipLaunchKernelGGL(argmax_kernel, dim3(unsigned(rows)), dim3(kArgmaxThreads), 0, stream, x, n, vec, out);
+  HIP_CHECK(hipGetLastError());
+  return "argmax_kernel";
 }
 
 }  // namespace xtg::hip

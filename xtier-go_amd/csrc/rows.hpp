@@ -23,5 +23,7 @@ std::string launch_gate_norm(const float* a, const float* gate, const float* gs,
 // out (may be a) = justnorm(a + b), b optional
 std::string launch_add_norm(const float* a, const float* b, float* out, int rows, int w, void* op,
                             hipStream_t stream);
+// out[r] = the first index of the largest of x[r][0 .. n) (xtg::argmax, sampler.cpp:8-13), int32 per row
+std::string launch_argmax(const float* x, int rows, int n, int* out, hipStream_t stream);
 
 }  // namespace xtg::hip
