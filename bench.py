@@ -3,16 +3,17 @@
 
 Workload (one step): the three projection shapes of one synthetic 4B-shaped layer -- QKV (N=5120, K=3072),
 fused gate/up (2 x N=8192, K=3072, one launch) and down (N=3072, K=8192) -- each at M=1 (decode) and at M=8
-(the speculative-verify batch): 6 calls, each = activation-operand prep + the GEMV kernel. Weights follow the
+(the speculative-verify batch): 6 calls of xtg_hip_matmul_nvfp4_dev on BF16 rows, each one GEMV launch that
+builds its matrix-core operand from the rows itself. Weights follow the
 benchmark distributions (uniform E2M1 codes, |N(0,1)|*0.05 E4M3 scales, tensor scale 1.0); activations are unit
 BF16 rows. Consecutive calls read different copies of their weights, rotating over >= 1 GiB, so every launch
 streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed from HIP graphs (one per
 rotation phase), so host launch cost does not set the pace.
 
 value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
-roofline: the GEMV kernel alone. For each (shape, rows) a graph of one GEMV launch per weight copy on a prepared
-operand is replayed between two HIP events on the backend's stream; achieved = algorithmic bytes of those
-launches / their time, against the 8 TB/s HBM peak. traffic: HBM bytes per launch (mean over the 6 calls) from
+roofline: the GEMV kernel alone (the whole call). For each (shape, rows) a graph of one call per weight copy is
+replayed between two HIP events on the backend's stream; achieved = algorithmic bytes of those launches / their
+time, against the 8 TB/s HBM peak. traffic: HBM bytes per launch (mean over the 6 calls) from
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known size
 (profiles/gemv_layer_projections_traffic_pmc.md).
 cpu_baseline: the reference engine's own CPU matmul_nvfp4 (oracle/_ref, compiled from the reference sources)
@@ -102,7 +103,7 @@ def measured_traffic():
 
 def pmc_pass(pkg, wl):
     """Counter pass: the copy first (known bytes read and written once), then the GEMV calls, each followed by a
-    finish so dispatches stay apart. Kernel dispatch order: copy, then per call prep_x_kernel + gemv_kernel."""
+    finish so dispatches stay apart. Kernel dispatch order: copy, then one gemv_kernel per call."""
     hip = pkg.HipBackend(0)
     src, dst = hip.alloc(COPY_BYTES), hip.alloc(COPY_BYTES)
     hip.copy(src, dst, COPY_BYTES)
@@ -496,15 +497,13 @@ def main():
         sets.append(s)
     log("prepared %d weight copies (%.2f GB on the device)" % (copies, hip.info()["weight_bytes"] / 1e9))
 
-    xs, dx, ops = {}, {}, {}
+    xs, dx = {}, {}
     for name, shapes in SHAPES:
         k = shapes[0][1]
         xb = wl.unit_rows_bf16(rng, 8, k)
         for m in ROWS:
             xs[(name, m)] = wl.bf16_to_f32(xb[:m])
             dx[(name, m)] = hip.array(xb[:m])
-            ops[(name, m)] = hip.array(shape=(hip.x_operand_bytes(k),), dtype=np.uint8)
-            hip.prep_x(dx[(name, m)], pkg.X_BF16, m, k, ops[(name, m)])
     dy = hip.array(shape=(8 * 16384 + 64,))
     calls = [(name, m) for m in ROWS for name, _ in SHAPES]
     step_bytes = sum(call_bytes(dict(SHAPES)[name], m) for name, m in calls)
@@ -533,13 +532,13 @@ def main():
     log("timed %d steps: %.4f ms/step, %.1f GB/s whole-step (%.1f%% of HBM peak)"
         % (args.steps, ms_per_step, value, value / HBM_PEAK_GBS * 100))
 
-    # roofline: GEMV-only graphs (one launch per weight copy on a prepared operand), timed by events
+    # roofline: per-call graphs (one GEMV launch per weight copy, the step's own kernel), timed by events
     per_call = {}
     gemv_graphs = {}
     for name, m in calls:
         hip.graph_begin()
         for c in range(copies):
-            hip.matmul_op(sets[c][name], ops[(name, m)], m, dy)
+            hip.matmul_dev(sets[c][name], dx[(name, m)], pkg.X_BF16, m, dy)
         gemv_graphs[(name, m)] = hip.graph_end("gemv_%s_m%d" % (name, m))
     for g in gemv_graphs.values():   # warm
         hip.graph_launch(g)

@@ -78,8 +78,9 @@ int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* 
                          char* err, int err_len);
 /* Replaces OpenClBackend::matmul(ws, Mem x, m, Mem y, y_offset) (opencl.h:54-55, opencl.cpp:694-754): the n_w
  * projections of the device input x ([m][k], FP32 or BF16 per x_dtype) into consecutive [m][n_out_i] blocks of
- * the device output y starting at y_offset floats. Queued; 1 <= m <= 4096 (1-8 rows: the GEMV; more: the GEMM),
- * n_w <= 4 per call (the fused q/k/v/g and gate/up of the Dory sublayers). */
+ * the device output y starting at y_offset floats. Queued; 1 <= m <= 4096 (1-8 rows: the GEMV, which reads the rows
+ * as they are; more: the GEMM on a prepared operand), n_w <= 4 per call (the fused q/k/v/g and gate/up of the Dory
+ * sublayers). x must be 16-byte aligned. */
 int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
                              size_t y_offset, char* err, int err_len);
 

@@ -124,6 +124,42 @@ def test_fused_gate_up_device_f32(hip, pkg, orc, wl):
     assert rel_l2(y[16 + m * 8192:].reshape(m, 8192), ru) <= 1e-5
 
 
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+@pytest.mark.parametrize("n,k", [(5120, 3072), (3072, 8192), (40, 272)])
+def test_raw_rows_and_prepared_operand(hip, pkg, orc, wl, xdt, n, k):
+    """The device entry reads FP32 / BF16 rows as they are where the launch shape allows (the GEMV builds each
+    k-tile's operand with its own power of two) and otherwise prepares the operand first; both against the oracle,
+    and so is the explicit two-step path (prep_x + matmul_op). Rows whose magnitude changes by 1e9 along k; rows
+    that do not start on a 16-byte boundary are refused."""
+    rng = np.random.default_rng(n + k)
+    w = wl.nvfp4_weight(rng, n, k)
+    for m in (1, 3, 8):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[0, :128] *= 1e6
+        x[-1, k // 2:] *= 1e-3
+        if xdt == "bf16":
+            payload, dt = wl.f32_to_bf16(x).ravel(), pkg.X_BF16
+            x = wl.bf16_to_f32(payload.reshape(m, k))
+        else:
+            payload, dt = x.ravel(), pkg.X_F32
+        e = payload.dtype.itemsize
+        pad = np.zeros(16 // e, payload.dtype)
+        (r,) = orc.matmul_nvfp4([w], x)
+        buf = hip.array(shape=(payload.size + pad.size,), dtype=payload.dtype)
+        dy = hip.array(shape=(m, n))
+        op = hip.array(shape=((m + 7) // 8 * hip.x_operand_bytes(k),), dtype=np.uint8)
+        buf.upload(np.concatenate([payload, pad]))
+        hip.matmul_dev([pkg.Weight(*w)], buf.ptr, dt, m, dy)
+        assert rel_l2(dy.numpy(), r) <= 1e-5, (m, "aligned")
+        hip.prep_x(buf.ptr, dt, m, k, op)
+        hip.matmul_op([pkg.Weight(*w)], op, m, dy)
+        assert rel_l2(dy.numpy(), r) <= 1e-5, (m, "two-step")
+        with pytest.raises(pkg.XtgError):   # rows must start on a 16-byte boundary
+            hip.matmul_dev([pkg.Weight(*w)], buf.ptr + e, dt, m, dy)
+        for arr in (buf, dy, op):
+            arr.free()
+
+
 def test_fused_qkvg_four_weights(hip, pkg, orc, wl):
     """q / k / v / g of the attention sublayer (4096 + 1024 + 1024 + 4096 rows) in one launch."""
     rng = np.random.default_rng(78)
@@ -143,3 +179,32 @@ def test_errors_are_reported(hip, pkg):
         hip.matmul([pkg.Weight(*a), pkg.Weight(*b)], np.zeros((1, 256), np.float32))
     with pytest.raises(pkg.XtgError, match="rows"):   # one device call takes at most 4096 rows
         hip.matmul_dev([pkg.Weight(*a)], 0, pkg.X_F32, 5000, 0)
+
+
+def test_raw_bf16_tiny_and_nonfinite_rows(hip, pkg, orc, wl):
+    """BF16 rows read raw: a row of BF16 subnormals and tiny normals (the tile exponent is capped), a row spanning
+    2^-60 .. 2^60 within one tile, a zero row, and a row holding a NaN (its outputs are NaN; the other rows are
+    untouched)."""
+    rng = np.random.default_rng(12)
+    n, k = 48, 384
+    w = kt_weight(rng, n, k)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    x[0] *= np.float32(2.0 ** -128)
+    x[1, ::2] *= np.float32(2.0 ** 60)
+    x[1, 1::2] *= np.float32(2.0 ** -60)
+    x[2] = 0.0
+    x[4, 200] = np.nan
+    xb = wl.f32_to_bf16(x)
+    x = wl.bf16_to_f32(xb)
+    dx, dy = hip.array(xb), hip.array(shape=(5, n))
+    hip.matmul_dev([pkg.Weight(*w)], dx, pkg.X_BF16, 5, dy)
+    y = dy.numpy()
+    dx.free()
+    dy.free()
+    (r,) = orc.matmul_nvfp4([w], np.where(np.isnan(x), 0, x).astype(np.float32))
+    for i in range(4):
+        if i == 2:
+            assert (y[i] == 0).all()
+        else:
+            assert rel_l2(y[i], r[i]) <= 1e-5, i
+    assert np.isnan(y[4]).all()

@@ -100,6 +100,29 @@ void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
   const int k = ws[0].k;
   XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
+  XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, "matmul: rows at %p are not 16-byte aligned", x);
+  if (m <= kMaxRows) {   // the GEMV takes the rows as they are when its shape allows
+    XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul: unknown activation type %d", x_dtype);
+    XTG_CHECK(x && y, "matmul: NULL input or output");
+    GemvCall c;
+    c.nw = nw;
+    size_t off = y_off;
+    for (int i = 0; i < nw; ++i) {
+      XTG_CHECK(ws[i].k == k, "matmul: input widths differ (%d, %d)", ws[i].k, k);
+      c.w[i] = &prepare(ws[i]);
+      c.y_off[i] = off;
+      off += size_t(m) * size_t(ws[i].n_out);
+    }
+    c.y = y;
+    c.m = m;
+    c.x = x;
+    c.x_dtype = x_dtype;
+    c.k = k;
+    if (gemv_takes_raw(c)) {
+      timed([&] { return launch_gemv(c, stream_); });
+      return;
+    }
+  }
   ensure(op_, op_size_, size_t((m + kMaxRows - 1) / kMaxRows) * op_bytes(k));
   prep_x(x, x_dtype, m, k, op_);
   matmul_op(ws, nw, op_, m, y, y_off);
@@ -109,6 +132,8 @@ void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op) {
   XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
   XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul: unknown activation type %d", x_dtype);
   XTG_CHECK(x && op, "prep_x: NULL input or operand");
+  XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(op) % 16 == 0,
+            "prep_x: rows and operand must be 16-byte aligned");
   timed([&] { return launch_prep_x(x, x_dtype, m, k, op, stream_); });
 }
 

@@ -162,7 +162,9 @@ struct GemvArgs {
   int kt;
   int m;
   const uint4* xop;
-  const float* xinv;
+  const float* xinv;   // the operand's row factors (NULL: the rows were taken raw)
+  const void* x;       // raw rows [m][k] (FP32 or BF16) when the kernel builds its own operand
+  int k;
   float* y;
 };
 
@@ -172,7 +174,7 @@ __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int 
   if (j >= a.m) return;
   const int n = a.n[wi];
   const int n0 = rb * kTileRows + 4 * g;
-  const float f = a.global[wi] * a.xinv[j];
+  const float f = a.xinv ? a.global[wi] * a.xinv[j] : a.global[wi];
   float* yp = a.y + a.y_off[wi] + (long long)j * n;
   const float* cs = a.col_scale[wi];
 #pragma unroll
@@ -180,7 +182,55 @@ __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int 
     if (n0 + e < n) yp[n0 + e] = cs ? (v[e] * f) * cs[n0 + e] : v[e] * f;
 }
 
-template <int R, int T, int MAXT>
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// The operand's entries of one k-tile built in the lane that consumes them, from raw BF16 rows: lane (c, g) holds
+// row c / 2's inputs 32 g .. 32 g + 31 of the tile (w4: 16 BF16 pairs), scaled by the power of two 2^e that brings
+// the tile's largest magnitude in that row to [2^14, 2^15) (prep_x_kernel's rule, per 128 inputs instead of per
+// row; the four lane groups holding the row's tile agree on it through two xor shuffles). Returns 2^-e, the factor
+// the tile's products take. Built in 16-bit integer steps on the bit pairs (2.5 VALU operations per input).
+// BF16 carries 8 significant bits, so f16(x * 2^e) is exact wherever it is a normal f16 and the low part is zero:
+// the odd (low-part) columns get +-0. An input whose scaled value falls below f16's normal range (at
+// least 2^28 times smaller than the tile's largest) is flushed, an error below 2^-28 of that largest magnitude;
+// e is capped at 112 so the exponent shift stays a subtraction (tiles whose largest magnitude is under 2^-98 keep
+// at least 6 of f16's 11 bits above their largest value, still more than BF16's 8). With the abs bits
+// a = [E:8][M:7], the f16 of x * 2^e is [E - 112 + e : 5][M : 7][000]: a saturating subtraction of (112 - e) << 7
+// (0 when the result would be below the normal range), a shift by 3 and the sign put back. A row whose tile holds
+// an infinity or NaN gets NaN operands (NaN outputs, as the prepared operand gives).
+__device__ inline float bf16_operand(const uint4 (&w4)[4], bool hi, uint4 (&xb)[4]) {
+  uint32_t w[16];
+  u16x2 m2 = {0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[4 * i] = w4[i].x, w[4 * i + 1] = w4[i].y, w[4 * i + 2] = w4[i].z, w[4 * i + 3] = w4[i].w;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
+  uint32_t mx = m2.x > m2.y ? m2.x : m2.y;
+  mx = max(mx, uint32_t(__shfl_xor(int(mx), 16)));
+  mx = max(mx, uint32_t(__shfl_xor(int(mx), 32)));
+  const int e = mx == 0 || mx >= 0x7f80u ? 0 : min(141 - int(mx >> 7), 112);
+  const unsigned short c = hi ? (unsigned short)((112 - e) << 7) : (unsigned short)0x7f80u;   // low columns: all 0
+  const u16x2 c2 = {c, c};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu), c2);
+    const u16x2 f = d << (unsigned short)3;
+    w[i] = (w[i] & 0x80008000u) | __builtin_bit_cast(uint32_t, f);
+  }
+  if (__any(mx >= 0x7f80u)) {   // an infinity or NaN in a lane's tile: that row's products become NaN
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = mx >= 0x7f80u ? 0x7e007e00u : w[i];
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) xb[t] = make_uint4(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3]);
+  return ldexpf(1.f, -e);
+}
+
+// XR: false = a prepared operand (xop / xinv); true = raw BF16 rows (the kernel builds the operand per k-tile in
+// registers, so no separate prep pass runs). FP32 rows keep the prepared operand: their high / low split costs
+// more per wave than the separate prep launch saves.
+template <int R, int T, int MAXT, bool XR>
 __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   extern __shared__ f32x4 red[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
@@ -199,16 +249,52 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   uint4 xb[T][4];
   uint4 cw[T][R];
   uint32_t sw[T][R];
+  // raw rows: the lane's 32 inputs of each k-tile (8 BF16 per load; k is a multiple of 16, so a load is wholly
+  // inside the row or wholly past its end)
+  uint4 xr[XR ? T : 1][4];
+  if constexpr (XR) {
+    // the raw rows first, so they are turned into the operand while the weights are in flight; buffer loads
+    // return zeros past the rows (absent rows, k-tiles past k), so no load sits behind a branch
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(a.x), (short)0, a.m * a.k * 2, 0x00020000);
+    const uint32_t xrow = uint32_t(col >> 1) * uint32_t(a.k) * 2u;
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+      const int kt = kt0 + u;
+      const int k0 = kt * kTileK + 32 * grp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ki = k0 + i * 8;
+        const bool in = kt < KT && live_col && ki < a.k;
+        const uint32_t off = in ? xrow + uint32_t(ki) * 2u : 0x80000000u;
+        xr[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, int(off), 0, 0));
+      }
+    }
+  }
 #pragma unroll
   for (int u = 0; u < T; ++u) {
     const int kt = kt0 + u;
     const bool ok = kt < KT;
+    if constexpr (!XR) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      xb[u][t] = ok && live_col ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(entry)] : make_uint4(0, 0, 0, 0);
+      for (int t = 0; t < 4; ++t)
+        xb[u][t] = ok && live_col ? a.xop[(size_t(kt) * 4 + size_t(t)) * 64 + size_t(entry)] : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bool ok2 = ok && rb0 + r < nb;
+      if constexpr (XR) {
+        // branch-free, so the conversion can wait for the rows alone: an absent tile loads a tile of the same
+        // weight (clamped) and is used as it is: past the last row-block its results are not stored, past k its
+        // products meet zero inputs
+        (void)ok2;
+        const uint8_t* tile =
+            tiles + (size_t(min(rb0 + r, nb - 1)) * size_t(KT) + size_t(min(kt, KT - 1))) * kTileBytes;
+        const u32x4 c4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + 16 * lane));
+        cw[u][r] = make_uint4(c4[0], c4[1], c4[2], c4[3]);
+        sw[u][r] = uint32_t(__builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane)));
+        continue;
+      }
       const uint8_t* tile = tiles + (size_t(rb0 + r) * size_t(KT) + size_t(kt)) * kTileBytes;
       if (ok2) {
         const u32x4 c4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + 16 * lane));
@@ -220,6 +306,13 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
       }
     }
   }
+  float xs[T];   // raw rows: each k-tile's factor 2^-e for the lane's column
+  if constexpr (XR) __builtin_amdgcn_sched_barrier(0);   // every load issued before the conversion waits on x
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    xs[u] = 1.f;
+    if constexpr (XR) xs[u] = bf16_operand(xr[u], (col & 1) == 0, xb[u]);
+  }
   f32x4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -229,12 +322,17 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     for (int r = 0; r < R; ++r) {
       const f16x2 s0 = scale_pair(sw[u][r], 0), s1 = scale_pair(sw[u][r], 1);
       const uint32_t words[4] = {cw[u][r].x, cw[u][r].y, cw[u][r].z, cw[u][r].w};
+      f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const f16x8 A = dequant8(words[t], t < 2 ? s0 : s1);
         const f16x8 B = __builtin_bit_cast(f16x8, xb[u][t]);
-        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[r], 0, 0, 0);
+        if constexpr (!XR)
+          acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[r], 0, 0, 0);
+        else
+          part = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, part, 0, 0, 0);
       }
+      if constexpr (XR) acc[r] += part * xs[u];   // a power of two: exact
     }
   }
   if (S == 1) {
@@ -262,15 +360,25 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
 namespace {
 using GemvFn = void (*)(const GemvArgs);
 
+// Raw BF16 rows hold 32 inputs (16 VGPRs) per k-tile until the tile's operand is built. Kernels that would exceed
+// a 1024-thread group's 128 VGPRs (spill) or take more than 4 k-tiles per wave are not made: those calls take the
+// prepared operand.
 template <int R, int T>
-GemvFn pick_fn(int threads) {
-  if (threads <= 512) return gemv_kernel<R, T, 512>;
-  return gemv_kernel<R, T, 1024>;
+GemvFn pick_fn(int threads, bool xr) {
+  if (xr) {
+    if constexpr (T <= 4) {
+      if (threads <= 512) return gemv_kernel<R, T, 512, true>;
+      if constexpr (T <= 2 || R == 1) return gemv_kernel<R, T, 1024, true>;
+    }
+    return nullptr;
+  }
+  if (threads <= 512) return gemv_kernel<R, T, 512, false>;
+  return gemv_kernel<R, T, 1024, false>;
 }
 
-GemvFn gemv_fn(int r, int t, int threads) {
+GemvFn gemv_fn(int r, int t, int threads, bool xr = false) {
 #define XTG_CASE(R, T) \
-  if (r == R && t == T) return pick_fn<R, T>(threads);
+  if (r == R && t == T) return pick_fn<R, T>(threads, xr);
   XTG_CASE(1, 1) XTG_CASE(1, 2) XTG_CASE(1, 3) XTG_CASE(1, 4) XTG_CASE(1, 6) XTG_CASE(1, 8)
   XTG_CASE(2, 1) XTG_CASE(2, 2) XTG_CASE(2, 3) XTG_CASE(2, 4) XTG_CASE(2, 6)
   XTG_CASE(4, 1) XTG_CASE(4, 2) XTG_CASE(4, 3)
@@ -278,21 +386,31 @@ GemvFn gemv_fn(int r, int t, int threads) {
   return nullptr;
 }
 
-bool shape_ok(int r, int t, int s) {
+bool shape_ok(int r, int t, int s, bool raw = false) {
   if (s < 1 || s > 16) return false;
   if (r * t > 12) return false;
   if (s > 8 && t > 4) return false;   // 1024-thread groups get 128 VGPRs per lane: T > 4 spills there
-  return gemv_fn(r, t, s * 64) != nullptr;
+  return gemv_fn(r, t, s * 64, raw) != nullptr;
 }
 }  // namespace
 
-GemvShape gemv_shape(int kt, const int* nbs, int nw, int m) {
+GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw) {
   if (const char* env = std::getenv("XTG_GEMV_SHAPE")) {   // "R,T": a fixed shape for experiments
     int r = 0, t = 0;
     if (std::sscanf(env, "%d,%d", &r, &t) == 2) {
       const int s = (kt + t - 1) / t;
-      if (shape_ok(r, t, s)) return {r, t, s};
+      if (shape_ok(r, t, s, raw)) return {r, t, s};
     }
+  }
+  if (raw) {
+    // raw BF16 rows (measured the same way): each wave converts its k-tiles of x once for all its row-blocks, so
+    // more row-blocks per wave pay: four with many row-blocks, two with few, and four k-tiles per wave only where
+    // K needs them (16 waves at most per work-group)
+    int nb = 0;
+    for (int i = 0; i < nw; ++i) nb += nbs[i];
+    const int r = nb >= 512 ? 4 : 2, t = (kt + 1) / 2 <= 16 ? 2 : 4;
+    if (shape_ok(r, t, (kt + t - 1) / t, true)) return {r, t, (kt + t - 1) / t};
+    if (shape_ok(1, 4, (kt + 3) / 4, true)) return {1, 4, (kt + 3) / 4};
   }
   // Measured on MI355X (rotated cold weights, launch-shape sweeps over the decode projections): many row-blocks
   // want two k-tiles per wave with two row-blocks per wave (four at M >= 4, where the activation operand is
@@ -334,17 +452,31 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m) {
   return best;
 }
 
+namespace {
+bool raw_kind(const GemvCall& c) { return c.x && c.x_dtype == kXBF16; }
+
+GemvShape call_shape(const GemvCall& c) {
+  int nbs[4];
+  for (int i = 0; i < c.nw; ++i) nbs[i] = c.w[i]->nb;
+  return gemv_shape(c.w[0]->kt, nbs, c.nw, c.m, raw_kind(c));
+}
+}  // namespace
+
+bool gemv_takes_raw(const GemvCall& c) {
+  if (!raw_kind(c) || c.m < 1 || c.m > kMaxRows || reinterpret_cast<uintptr_t>(c.x) % 16 != 0) return false;
+  const GemvShape sh = call_shape(c);
+  return gemv_fn(sh.r, sh.t, sh.s * 64, raw_kind(c)) != nullptr;
+}
+
 std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
   XTG_CHECK(c.m >= 1 && c.m <= kMaxRows, "gemv: %d rows (1..%d)", c.m, kMaxRows);
+  XTG_CHECK(raw_kind(c) || c.xop, "gemv: no activations");
   GemvArgs a{};
   const int kt = c.w[0]->kt;
-  int nbs[4];
-  for (int i = 0; i < c.nw; ++i) {
-    XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
-    nbs[i] = c.w[i]->nb;
-  }
-  const GemvShape sh = gemv_shape(kt, nbs, c.nw, c.m);
+  for (int i = 0; i < c.nw; ++i) XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
+  const GemvShape sh = call_shape(c);
+  const bool xr = raw_kind(c);
   int wgs = 0;
   for (int i = 0; i < c.nw; ++i) {
     a.tiles[i] = c.w[i]->tiles;
@@ -360,16 +492,19 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.nw = c.nw;
   a.kt = kt;
   a.m = c.m;
-  a.xop = static_cast<const uint4*>(c.xop);
-  a.xinv = c.xinv;
+  a.xop = xr ? nullptr : static_cast<const uint4*>(c.xop);
+  a.xinv = xr ? nullptr : c.xinv;
+  a.x = c.x;
+  a.k = c.k;
   a.y = c.y;
   const int threads = sh.s * 64;
-  GemvFn fn = gemv_fn(sh.r, sh.t, threads);
-  XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d", sh.r, sh.t);
+  GemvFn fn = gemv_fn(sh.r, sh.t, threads, xr);
+  XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d%s", sh.r, sh.t, xr ? " on raw rows" : "");
   const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * 64 * sizeof(f32x4) : 0;
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
-  return strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, threads <= 512 ? 512 : 1024);
+  return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, threads <= 512 ? 512 : 1024)
+            : strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, threads <= 512 ? 512 : 1024);
 }
 
 }  // namespace xtg::hip

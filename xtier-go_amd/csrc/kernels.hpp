@@ -53,13 +53,18 @@ struct GemvCall {
   int m = 0;
   const void* xop = nullptr;
   const float* xinv = nullptr;
+  const void* x = nullptr;   // raw rows [m][k] (x_dtype) in place of a prepared operand: the GEMV builds its own
+  int x_dtype = 0;
+  int k = 0;
 };
 // The launch shape: R row-blocks and T k-tiles per wave, S waves per work-group along k.
 struct GemvShape {
   int r = 1, t = 1, s = 1;
 };
-GemvShape gemv_shape(int kt, const int* nbs, int nw, int m);
+GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw = false);   // raw: BF16 rows read as they are
 std::string launch_gemv(const GemvCall& c, hipStream_t stream);
+// whether launch_gemv takes c's raw rows for its shape (otherwise prepare the operand first)
+bool gemv_takes_raw(const GemvCall& c);
 
 // ---- NVFP4 GEMM for prefill chunks of m > 8 rows (gemm.hip) ----
 // The same weights and call description (c.xop: group 0 of ceil(m / 8) operand groups of op_group_bytes(k);
