@@ -70,6 +70,11 @@ int xtg_hip_prepare_nvfp4(xtg_hip* h, const xtg_nvfp4* w, char* err, int err_len
  * reference frees its device weights only with the backend (opencl.cpp:349-353); callers that recycle host
  * buffers need this to keep the codes-pointer key unambiguous. 0 also when nothing was prepared for it. */
 int xtg_hip_release_nvfp4(xtg_hip* h, const uint8_t* codes, char* err, int err_len);
+/* The device tile layout prepare() made for the weight keyed by `codes` (16 rows x 128 inputs per 1152-byte tile:
+ * 1024 bytes of codes, lane l's 16 at 16 l, then lane l's two scales at 1024 + 2 l), copied to host memory; bytes
+ * must be ceil(n/16) * ceil(k/128) * 1152. No counterpart in the reference (whose OpenCL repack is internal): for
+ * checking the device repack of a checkpoint's arrays. */
+int xtg_hip_nvfp4_tiles(xtg_hip* h, const uint8_t* codes, void* out, size_t bytes, char* err, int err_len);
 /* Replaces xtg::matmul_nvfp4(ThreadPool&, ws, x, m, ys) (kernels.h:27-30, kernels.cpp:84-138) and the host
  * OpenClBackend::matmul (opencl.h:34, opencl.cpp:523-601): y_i[m][n_out_i] = x[m][k] * W_i^T for n_w weights
  * sharing k; x and every ys[i] are host memory; synchronous. Prepares weights not seen before. m >= 1 (rows are

@@ -334,6 +334,8 @@ class Dory:
         cfg, layers, head = wl.dory_structs(weights, Nvfp4, DoryLayer, DoryConfig)
         self._keep = (cfg, layers, head)
         self.h = oracle().xo_dory_create(ctypes.byref(cfg), layers, ctypes.byref(head), weights.logit_scale.ctypes.data)
+        if getattr(weights, "head_bf16", None) is not None:   # a checkpoint's BF16 LM head
+            self.set_head_bf16(weights.head_bf16)
 
     def __del__(self):
         try:

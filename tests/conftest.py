@@ -53,3 +53,20 @@ def hip(pkg):
     b = pkg.HipBackend(0)
     yield b
     b.close()
+
+
+@pytest.fixture(scope="session")
+def ck():
+    """The checkpoint reader (xtier-go_amd/checkpoint.py)."""
+    load_package()
+    import xtier_go_amd.checkpoint as c
+    return c
+
+
+@pytest.fixture(scope="session")
+def ckpt_dir(tmp_path_factory):
+    """A small Dory checkpoint in ModelOpt's NVFP4 layout, written by the safetensors library in a process of its own
+    (tests/make_checkpoint.py)."""
+    d = str(tmp_path_factory.mktemp("dory_ckpt"))
+    subprocess.run([sys.executable, os.path.join(ROOT, "tests", "make_checkpoint.py"), d, "3"], check=True)
+    return d

@@ -208,3 +208,32 @@ def test_raw_bf16_tiny_and_nonfinite_rows(hip, pkg, orc, wl):
         else:
             assert rel_l2(y[i], r[i]) <= 1e-5, i
     assert np.isnan(y[4]).all()
+
+
+def tiles_np(codes, scales):
+    """The documented tile layout: tile (rb, kt) holds lane l = 16 g + r's 16 code bytes (row rb * 16 + r, inputs
+    kt * 128 + 32 g .. + 32) at 16 l and its two scale bytes at 1024 + 2 l; zeros past n and k."""
+    n, k = codes.shape[0], codes.shape[1] * 2
+    nb, kt = -(-n // 16), -(-k // 128)
+    cp = np.zeros((nb * 16, kt * 64), np.uint8)
+    cp[:n, :k // 2] = codes
+    sp = np.zeros((nb * 16, kt * 8), np.uint8)
+    sp[:n, :k // 16] = scales
+    c = cp.reshape(nb, 16, kt, 4, 16).transpose(0, 2, 3, 1, 4).reshape(nb, kt, 1024)
+    s = sp.reshape(nb, 16, kt, 4, 2).transpose(0, 2, 3, 1, 4).reshape(nb, kt, 128)
+    return np.concatenate([c, s], axis=2).ravel()
+
+
+@pytest.mark.parametrize("n,k", [(17, 48), (40, 272), (3072, 3072), (24576, 8192)])
+def test_device_repack_matches_layout(hip, pkg, n, k):
+    """prepare() copies the checkpoint's row-major arrays to the device and repacks them there (row-blocks at a
+    time through a 64 MiB staging buffer: the last shape takes two chunks); the tiles equal the documented
+    layout byte for byte."""
+    rng = np.random.default_rng(n + k)
+    codes = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    scales = rng.integers(0, 127, size=(n, k // 16), dtype=np.uint8)
+    w = pkg.Weight(codes, scales, 0.5)
+    hip.prepare(w)
+    got = hip.nvfp4_tiles(w)
+    hip.release_weight(w)
+    np.testing.assert_array_equal(got, tiles_np(codes, scales))

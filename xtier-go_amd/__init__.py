@@ -78,6 +78,7 @@ SIGNATURES = [
     ("xtg_hip_kv_save", _I, [_P, _P, _P, _SZ] + _ERR),
     ("xtg_hip_kv_restore", _I, [_P, _P, _P, _SZ] + _ERR),
     ("xtg_hip_kv_copy", _I, [_P, _P, _P] + _ERR),
+    ("xtg_hip_nvfp4_tiles", _I, [_P, _P, _P, _SZ] + _ERR),
     ("xtg_hip_kv_release", _I, [_P, _P] + _ERR),
     ("xtg_hip_attention", _I, [_P, ctypes.POINTER(AttnArgs)] + _ERR),
     ("xtg_hip_qk_rope_norm", _I, [_P, _P, _P, _I, _I, _I, _I, _I64, _F, _P] + _ERR),
@@ -219,6 +220,14 @@ class HipBackend:
         err = _errbuf()
         arr = self._hold([w])
         _check(lib().xtg_hip_prepare_nvfp4(self.h, arr, err, len(err)), err)
+
+    def nvfp4_tiles(self, w):
+        """The device tile layout prepared for w (uint8, ceil(n/16) * ceil(k/128) * 1152 bytes)."""
+        n, k = w.codes.shape[0], w.codes.shape[1] * 2
+        out = np.empty(((n + 15) // 16) * ((k + 127) // 128) * 1152, np.uint8)
+        err = _errbuf()
+        _check(lib().xtg_hip_nvfp4_tiles(self.h, w.codes.ctypes.data, out.ctypes.data, out.nbytes, err, len(err)), err)
+        return out
 
     def release_weight(self, w):
         """Drop the device copy of w (and let its host arrays go)."""
@@ -413,6 +422,8 @@ class DorySession:
                                            weights.logit_scale.ctypes.data, err, len(err))
         if not self.h:
             raise XtgError(err.value.decode(errors="replace"))
+        if getattr(weights, "head_bf16", None) is not None:   # a checkpoint's BF16 LM head
+            self.set_head_bf16(weights.head_bf16)
 
     def destroy(self):
         if self.h:

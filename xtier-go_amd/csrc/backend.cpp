@@ -30,7 +30,7 @@ Backend::~Backend() {
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (auto& kv : bf16_weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_})
+  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_})
     if (p) (void)hipFree(p);
   for (DevKv* c : kvs_) {
     for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
@@ -71,19 +71,42 @@ const PackedNvfp4& Backend::prepare(const xtg_nvfp4& w) {
   }
   XTG_CHECK(w.n_out > 0 && w.k > 0 && w.k % 16 == 0, "prepare: invalid NVFP4 shape %dx%d (k %% 16 == 0)", w.n_out, w.k);
   XTG_CHECK(!capturing_, "prepare: weights must be prepared before a graph capture");
-  std::vector<uint8_t> host;
-  pack_nvfp4_tiles(w.codes, w.scales, w.n_out, w.k, host);
   PackedNvfp4 p;
   p.n = w.n_out;
   p.k = w.k;
   p.nb = (w.n_out + kTileRows - 1) / kTileRows;
   p.kt = (w.k + kTileK - 1) / kTileK;
   p.global = w.global;
-  p.bytes = host.size();
+  p.bytes = size_t(p.nb) * size_t(p.kt) * kTileBytes;
+  // the checkpoint's arrays as they are to a staging buffer (at most kStageBytes: row-blocks at a time), then the
+  // tile layout of those row-blocks on the device
   HIP_CHECK(hipMalloc(&p.tiles, p.bytes));
-  HIP_CHECK(hipMemcpy(p.tiles, host.data(), p.bytes, hipMemcpyHostToDevice));
+  const size_t row_c = size_t(w.k / 2), row_s = size_t(w.k / 16);
+  const int chunk = int(std::max<size_t>(1, kStageBytes / ((row_c + row_s) * kTileRows)) * kTileRows);
+  ensure(stage_, stage_size_, size_t(std::min(chunk, p.nb * kTileRows)) * (row_c + row_s) + 256);
+  uint8_t* st = static_cast<uint8_t*>(stage_);
+  for (int r0 = 0; r0 < w.n_out; r0 += chunk) {
+    const int rows = std::min(chunk, w.n_out - r0);
+    const size_t cb = size_t(rows) * row_c, s_off = (cb + 255) / 256 * 256;
+    HIP_CHECK(hipMemcpyAsync(st, w.codes + size_t(r0) * row_c, cb, hipMemcpyHostToDevice, stream_));
+    HIP_CHECK(hipMemcpyAsync(st + s_off, w.scales + size_t(r0) * row_s, size_t(rows) * row_s, hipMemcpyHostToDevice,
+                             stream_));
+    timed([&] {
+      return launch_pack_nvfp4(st, st + s_off, rows, w.k, p.tiles + size_t(r0 / kTileRows) * p.kt * kTileBytes,
+                               stream_);
+    });
+    HIP_CHECK(hipStreamSynchronize(stream_));   // the staging buffer takes the next chunk
+  }
   weight_bytes_ += p.bytes;
   return weights_.emplace(w.codes, p).first->second;
+}
+
+void Backend::read_tiles(const uint8_t* codes, void* out, size_t bytes) {
+  auto it = weights_.find(codes);
+  XTG_CHECK(it != weights_.end(), "nvfp4_tiles: no weight prepared for %p", static_cast<const void*>(codes));
+  XTG_CHECK(bytes == it->second.bytes, "nvfp4_tiles: %zu bytes for tiles of %zu", bytes, it->second.bytes);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipMemcpy(out, it->second.tiles, bytes, hipMemcpyDeviceToHost));
 }
 
 void Backend::release_weight(const uint8_t* codes) {

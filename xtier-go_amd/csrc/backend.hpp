@@ -33,6 +33,8 @@ class Backend {
   const PackedNvfp4& prepare(const xtg_nvfp4& w);
   bool has_weight(const uint8_t* codes) const { return weights_.count(codes) != 0; }
   void release_weight(const uint8_t* codes);
+  // the prepared tiles of the weight keyed by codes, to host memory (bytes = their size)
+  void read_tiles(const uint8_t* codes, void* out, size_t bytes);
   // opencl.h:34 host matmul: upload, compute, read back (up to kHostPassRows rows per pass)
   void matmul(const xtg_nvfp4* ws, int nw, const float* x, int m, float* const* ys);
   // opencl.h:54-55 device matmul into consecutive [m][n_i] blocks from y_off
@@ -166,6 +168,9 @@ class Backend {
   std::vector<std::pair<std::pair<float, int>, float*>> inv_freq_;
   void* hx_ = nullptr;
   size_t hx_size_ = 0;
+  void* stage_ = nullptr;   // a weight's checkpoint arrays on their way to the tile layout
+  size_t stage_size_ = 0;
+  static constexpr size_t kStageBytes = size_t(64) << 20;
   void* hy_ = nullptr;
   size_t hy_size_ = 0;
 };

@@ -189,6 +189,13 @@ int xtg_hip_kv_release(xtg_hip* h, xtg_hip_kv* kv, char* err, int err_len) {
   });
 }
 
+int xtg_hip_nvfp4_tiles(xtg_hip* h, const uint8_t* codes, void* out, size_t bytes, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && codes && out, "nvfp4_tiles: NULL argument");
+    h->b->read_tiles(codes, out, bytes);
+  });
+}
+
 int xtg_hip_kv_copy(xtg_hip* h, const xtg_hip_kv* src, xtg_hip_kv* dst, char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h && src && dst, "kv_copy: NULL argument");

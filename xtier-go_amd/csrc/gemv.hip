@@ -33,22 +33,41 @@ namespace xtg::hip {
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out) {
-  const int nb = (n + kTileRows - 1) / kTileRows, kt = (k + kTileK - 1) / kTileK;
-  out.assign(size_t(nb) * size_t(kt) * kTileBytes, 0);
-  const size_t row_c = size_t(k) / 2, row_s = size_t(k) / 16;
-  for (int rb = 0; rb < nb; ++rb)
-    for (int t = 0; t < kt; ++t) {
-      uint8_t* tile = out.data() + (size_t(rb) * size_t(kt) + size_t(t)) * kTileBytes;
-      for (int l = 0; l < 64; ++l) {
-        const int row = rb * kTileRows + (l & 15);
-        const int k0 = t * kTileK + 32 * (l >> 4);   // the lane's first input
-        if (row >= n || k0 >= k) continue;
-        const int nk = std::min(32, k - k0);         // 16 or 32: k is a multiple of 16
-        std::memcpy(tile + 16 * l, codes + size_t(row) * row_c + size_t(k0 / 2), size_t(nk / 2));
-        std::memcpy(tile + 1024 + 2 * l, scales + size_t(row) * row_s + size_t(k0 / 16), size_t(nk / 16));
-      }
+// The tile layout from the checkpoint's row-major layout (ModelOpt NVFP4: codes [n][k/2], E4M3 scales [n][k/16]),
+// on the device: one wave per tile, lane l takes row rb * 16 + (l & 15), inputs kt * 128 + 32 (l >> 4) .. + 32 (16
+// or 32 of them: k is a multiple of 16), zeros for rows past n and inputs past k.
+__global__ void __launch_bounds__(256) pack_nvfp4_kernel(const uint8_t* __restrict__ codes,
+                                                          const uint8_t* __restrict__ scales, int n, int k, int nb,
+                                                          int kt, uint8_t* __restrict__ tiles) {
+  const long long tile = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (long long)nb * kt) return;
+  const int l = threadIdx.x & 63, rb = int(tile / kt), t = int(tile % kt);
+  const int row = rb * kTileRows + (l & 15), k0 = t * kTileK + 32 * (l >> 4);
+  uint2 c0 = make_uint2(0, 0), c1 = make_uint2(0, 0);
+  uint32_t s = 0;
+  if (row < n && k0 < k) {
+    const uint8_t* cr = codes + size_t(row) * size_t(k / 2) + size_t(k0 / 2);   // 8-byte aligned: k / 2 % 8 == 0
+    const uint8_t* sr = scales + size_t(row) * size_t(k / 16) + size_t(k0 / 16);
+    c0 = *reinterpret_cast<const uint2*>(cr);
+    s = sr[0];
+    if (k0 + 16 < k) {
+      c1 = *reinterpret_cast<const uint2*>(cr + 8);
+      s |= uint32_t(sr[1]) << 8;
     }
+  }
+  uint8_t* dst = tiles + size_t(tile) * kTileBytes;
+  *reinterpret_cast<uint4*>(dst + 16 * l) = make_uint4(c0.x, c0.y, c1.x, c1.y);
+  *reinterpret_cast<uint16_t*>(dst + 1024 + 2 * l) = uint16_t(s);
+}
+
+std::string launch_pack_nvfp4(const uint8_t* codes, const uint8_t* scales, int n, int k, uint8_t* tiles,
+                              hipStream_t stream) {
+  const int nb = (n + kTileRows - 1) / kTileRows, kt = (k + kTileK - 1) / kTileK;
+  const long long waves = (long long)nb * kt;
+  hipLaunchKernelGGL(pack_nvfp4_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, stream, codes, scales, n, k,
+                     nb, kt, tiles);
+  HIP_CHECK(hipGetLastError());
+  return "pack_nvfp4_kernel";
 }
 
 // ---------------------------------------------------------------------------------------- activation operand

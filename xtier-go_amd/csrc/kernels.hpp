@@ -26,8 +26,10 @@ struct PackedNvfp4 {
   float global = 1.f;
 };
 
-// Host repack of [n][k/2] codes and [n][k/16] scales into the tile layout above.
-void pack_nvfp4_tiles(const uint8_t* codes, const uint8_t* scales, int n, int k, std::vector<uint8_t>& out);
+// Device repack of [n][k/2] codes and [n][k/16] scales (device copies of the checkpoint's arrays, 8-byte aligned)
+// into the tile layout above.
+std::string launch_pack_nvfp4(const uint8_t* codes, const uint8_t* scales, int n, int k, uint8_t* tiles,
+                              hipStream_t stream);
 
 // The MFMA operand form of the activations: [kt][4 steps][64 entries][8 f16] (4096 bytes per k-tile). Operand
 // column 2 r is the high f16 part of row r scaled by 2^s_r, column 2 r + 1 the low part; xinv[r] = 2^-s_r. Entry

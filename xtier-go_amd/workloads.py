@@ -212,7 +212,7 @@ def dory_structs(w, nvfp4_type, layer_type, config_type):
     cfg = config_type(c["hidden"], c["ffn"], c["heads"], c["kv_heads"], c["head_dim"], c["vocab"], c["n_in"],
                       c["n_rec"], c["n_out"], c["loops"], c["window"], c["ring_slots"], c["context"],
                       c["theta_sliding"], c["theta_full"], c.get("kv_dtype", 0))
-    return cfg, arr, nv(w.head)
+    return cfg, arr, nv(w.head) if w.head is not None else zero
 
 
 # The projection shapes of one synthetic 4B-shaped layer (d_model 3072, 32 q / 8 KV heads of 128, FFN 8192).
