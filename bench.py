@@ -310,7 +310,9 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
                                                                                 time.perf_counter() - t0))
     t0 = time.perf_counter()
     dev = hip.dory(w)
-    log("decode: weights prepared on the device in %.1f s" % (time.perf_counter() - t0))
+    prep_s = time.perf_counter() - t0
+    log("decode: weights prepared on the device in %.2f s (%.1f GB/s from host memory: copies of the checkpoint "
+        "layout, repacked on the device)" % (prep_s, w.weight_bytes() / prep_s / 1e9))
     c = w.cfg
     kvh, d, ring, H, V = c["kv_heads"], c["head_dim"], c["ring_slots"], c["hidden"], c["vocab"]
     rng = np.random.default_rng(12)
@@ -404,6 +406,7 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     if dev8:
         dev8.destroy()
     results["fp8_kv_m1"] = fp8
+    results["prepare"] = {"bytes": w.weight_bytes(), "s": round(prep_s, 3), "gbs": round(w.weight_bytes() / prep_s / 1e9, 2)}
     results["prefill"] = prefill_run(pkg, hip, dev, w, rng, [n for n in (4096, 32768) if n <= ctx_max])
     cpu = None
     if cpu_seconds > 0:
