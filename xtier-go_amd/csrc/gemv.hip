@@ -431,44 +431,26 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw) {
     if (shape_ok(r, t, (kt + t - 1) / t, true)) return {r, t, (kt + t - 1) / t};
     if (shape_ok(1, 4, (kt + 3) / 4, true)) return {1, 4, (kt + 3) / 4};
   }
-  // Measured on MI355X (rotated cold weights, launch-shape sweeps over the decode projections): many row-blocks
-  // want two k-tiles per wave with two row-blocks per wave (four at M >= 4, where the activation operand is
-  // wider and reused across more rows); few row-blocks want four k-tiles per wave and one row-block.
-  int nb = 0;
-  for (int i = 0; i < nw; ++i) nb += nbs[i];
-  // a very tall weight (an LM head) streams best with the most bytes in flight per wave that still fits 512-thread
-  // groups: four row-blocks x three k-tiles (64% of HBM peak on 131072 x 3072 at M=1, against 59% for 2 x 2)
-  if (nb >= 4096 && kt <= 24 && shape_ok(4, 3, (kt + 2) / 3)) return {4, 3, (kt + 2) / 3};
-  const bool many = nb >= 512;
-  const int t = many && kt <= 32 ? 2 : 4;
-  const int r = many ? (m >= 4 ? 4 : 2) : 1;
+  // The k-split -- T k-tiles per wave, S = ceil(kt / T) waves added in a fixed order -- fixes every output's
+  // summation order, so it depends on k alone: a weight's outputs are bit-identical alone and fused with others
+  // (the reference's device test, tests/opencl_test.cpp:24-31). Two k-tiles per wave up to 32, four up to 64,
+  // then six or eight (those spill in 1024-thread groups: slower, still exact). The row-blocks per wave only
+  // choose which rows a wave computes: measured on MI355X (rotated cold weights, launch-shape sweeps over the
+  // decode projections), many row-blocks want two per wave (four at M >= 4, where the activation operand is
+  // wider and reused across more rows), few want one.
+  int nb = 0, nb_min = nbs[0];
+  for (int i = 0; i < nw; ++i) nb += nbs[i], nb_min = std::min(nb_min, nbs[i]);
+  // very tall weights only (LM heads), each of them: the most bytes in flight per wave that still fits 512-thread
+  // groups, four row-blocks x three k-tiles (64% of HBM peak on 131072 x 3072 at M=1, against 59% for 2 x 2)
+  if (nb_min >= 4096 && kt <= 24 && shape_ok(4, 3, (kt + 2) / 3)) return {4, 3, (kt + 2) / 3};
+  int t = 0;
+  for (int tt : {2, 4, 6, 8})
+    if (!t && (kt + tt - 1) / tt <= 16 && gemv_fn(1, tt, 1024) != nullptr) t = tt;
+  XTG_CHECK(t != 0, "gemv: %d k-tiles (K up to 16384)", kt);
   const int s = (kt + t - 1) / t;
-  if (shape_ok(r, t, s)) return {r, t, s};
-  // otherwise: enough waves to cover the chip (256 CUs x 8), then as much work per wave as possible
-  GemvShape best{1, 1, std::min(16, kt)};
-  long best_waves = -1, best_rt = 0;
-  for (int rr : {4, 2, 1})
-    for (int tt : {8, 6, 4, 3, 2, 1}) {
-      const int ss = (kt + tt - 1) / tt;
-      if (!shape_ok(rr, tt, ss)) continue;
-      long wgs = 0;
-      for (int i = 0; i < nw; ++i) wgs += (nbs[i] + rr - 1) / rr;
-      const long waves = wgs * ss;
-      const bool full = waves >= 2048, best_full = best_waves >= 2048;
-      bool take;
-      if (full != best_full)
-        take = full;
-      else if (full)
-        take = rr * tt > best_rt || (rr * tt == best_rt && waves < best_waves);
-      else
-        take = waves > best_waves;
-      if (take) {
-        best = {rr, tt, ss};
-        best_waves = waves;
-        best_rt = rr * tt;
-      }
-    }
-  return best;
+  int r = nb >= 512 ? (m >= 4 ? 4 : 2) : 1;
+  while (r > 1 && !shape_ok(r, t, s)) r /= 2;
+  return {r, t, s};
 }
 
 namespace {
@@ -516,6 +498,7 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.x = c.x;
   a.k = c.k;
   a.y = c.y;
+  XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
   const int threads = sh.s * 64;
   GemvFn fn = gemv_fn(sh.r, sh.t, threads, xr);
   XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d%s", sh.r, sh.t, xr ? " on raw rows" : "");
