@@ -234,6 +234,8 @@ struct ScanArgs {
   int tile_lo, tiles;      // the key tiles to scan: tile_lo .. tile_lo + tiles - 1
   int pos0;                // positions are below 2^31 (the slot-position array is int32)
   float scale2;            // scale * log2(e)
+  const float* inv_freq;   // raw q rows only (the decode step's fused launch): the RoPE table [d / 2]
+  const float* qscale;     //   and the per-dim q scale [heads * d] (NULL: none)
 };
 
 // FP32 -> BF16 on the vector ALU (v_cvt_pk_bf16_f32, round to nearest even) and back (exact).
@@ -471,13 +473,23 @@ __device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D 
   }
 }
 
-template <int D, int QB, bool F8>
-__global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a) {
+// LDS of a scan work-group: the wave merge, then (raw q rows) the rows' RoPE cosines and sines.
+template <int D, int QB>
+constexpr int scan_merge_floats() { return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16) * 64 * 4; }
+template <int D, int QB, bool RAWQ>
+constexpr int scan_lds_floats() { return scan_merge_floats<D, QB>() + (RAWQ ? 2 * kProdRows * (D / 2) : 0); }
+
+// One scan work-group (KV head, split) of a row block. RAWQ: q arrives as the projection wrote it, and the work-group
+// applies the producer's RoPE, justnorm and qscale itself (packs/dory/dory.cpp:482-490) before the scale: the q-col's
+// four lane groups hold dims i and i + d/2 of each RoPE pair in the same lane, so the rotation is in-lane and the
+// norm one sum over the lane groups; the rows' angles FP32(pos) * inv_freq[i] go through a cosine / sine table in
+// LDS (at most kProdRows rows), one entry per thread.
+template <int D, int QB, bool F8, bool RAWQ>
+__device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   constexpr int NC = D / 32, ND = D / 16;
-  extern __shared__ float lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
-  const int kvh = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+  const int kvh = bx / a.splits, split = bx % a.splits;
   const int blk = a.b0 + int(blockIdx.y), row0 = blk * a.rpb;
   const int qcols = min(a.rpb, a.n_q - row0) * a.group;
   const float* __restrict__ qrows = a.q + size_t(row0) * size_t(a.heads) * D;
@@ -511,6 +523,9 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
   // three terms. lo: the first stored position the column sees.
   bf16x8 qop[QB][NC][3];
   int lo[QB];
+  float xq[QB][NC][8];
+  int qh[QB];
+  bool qlive[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qc = qb * 16 + j;
@@ -518,17 +533,69 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
     const int qrow = live ? qc / a.group : 0;
     const int qpos = a.pos0 + row0 + qrow;
     lo[qb] = !live ? INT_MAX : (a.window > 0 ? max(0, qpos - a.window + 1) : 0);
-    const float* qp = qrows + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (live ? qc % a.group : 0))) * D;
+    qh[qb] = kvh * a.group + (live ? qc % a.group : 0);
+    qlive[qb] = live;
+    const float* qp = qrows + (size_t(qrow) * size_t(a.heads) + size_t(qh[qb])) * D;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
       const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
-      float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+      const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = live ? x[e] * a.scale2 : 0.f;
-      split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
+      for (int e = 0; e < 8; ++e) xq[qb][c][e] = x[e];
     }
   }
+  if constexpr (RAWQ) {
+    constexpr int HALF = D / 2;
+    float* scos = lds + scan_merge_floats<D, QB>();
+    float* ssin = scos + kProdRows * HALF;
+    const int nrows = min(a.rpb, a.n_q - row0);
+    for (int e = int(threadIdx.x); e < nrows * HALF; e += kWaves * 64) {
+      const float ang = float(a.pos0 + row0 + e / HALF) * a.inv_freq[e % HALF];
+      scos[e] = cosf(ang);
+      ssin[e] = sinf(ang);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qrow = qlive[qb] ? (qb * 16 + j) / a.group : 0;
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC / 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 32 * c + 8 * g + e;
+          const float cs = scos[qrow * HALF + i], sn = ssin[qrow * HALF + i];
+          const float x1 = xq[qb][c][e], x2 = xq[qb][c + NC / 2][e];
+          const float o1 = x1 * cs - x2 * sn, o2 = x2 * cs + x1 * sn;
+          xq[qb][c][e] = o1;
+          xq[qb][c + NC / 2][e] = o2;
+          ss += o1 * o1 + o2 * o2;
+        }
+      const float f = inv_norm_of(xor32_sum(xor16_sum(ss)));
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float sc[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        if (a.qscale) {
+          const float* sp = a.qscale + size_t(qh[qb]) * D + 32 * c + 8 * g;
+          const float4 u = *reinterpret_cast<const float4*>(sp);
+          const float4 w = *reinterpret_cast<const float4*>(sp + 4);
+          sc[0] = u.x, sc[1] = u.y, sc[2] = u.z, sc[3] = u.w, sc[4] = w.x, sc[5] = w.y, sc[6] = w.z, sc[7] = w.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xq[qb][c][e] = (xq[qb][c][e] * f) * sc[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? xq[qb][c][e] * a.scale2 : 0.f;
+      split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
+    }
 
   ScanState<D, QB> st;
 #pragma unroll
@@ -584,6 +651,12 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
       *reinterpret_cast<f32x4*>(acc_out + rec * D + 16 * dd + 4 * g) = s;
     }
   }
+}
+
+template <int D, int QB, bool F8>
+__global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a) {
+  extern __shared__ float lds[];
+  scan_split<D, QB, F8, false>(a, int(blockIdx.x), lds);
 }
 
 // --------------------------------------------------------------------------------------------------- own keys
@@ -798,7 +871,12 @@ struct ProduceArgs {
   float* acc;              // partials of the whole call
   float* ml;
   size_t blk_records;      // records per row block
+  int write_q;             // write the processed q rows back in place
 };
+
+// LDS of one producer work-group: row r's processed q heads, the k and v rows it attends to, their RoPE table.
+template <int D>
+constexpr int prod_lds_floats() { return (kProdGroup + 2 * kProdRows) * D + 2 * kProdRows * (D / 2); }
 
 // One work-group per (KV head, query row r). It takes RoPE + justnorm of row r's q heads of this KV head (times
 // qscale, written back in place) and of the k rows j0 .. r that row r attends to: each work-group recomputes
@@ -808,12 +886,14 @@ struct ProduceArgs {
 // a wave handles (at least ceil((group + r + 1 - j0) / 4)); they are processed without a branch, so their
 // reductions interleave.
 template <int D, int VPW>
-__global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceArgs a) {
+__device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* lds) {
   constexpr int HALF = D / 2;
   constexpr int kT = kWaves * 64;
-  __shared__ float sq[kProdGroup * D], sk[kProdRows * D], sv[kProdRows * D];
-  __shared__ float scos[kProdRows * HALF], ssin[kProdRows * HALF];
-  const int kvh = blockIdx.x % a.kv_heads, r = blockIdx.x / a.kv_heads;
+  float* sq = lds;
+  float* sk = sq + kProdGroup * D;
+  float* sv = sk + kProdRows * D;
+  float* scos = sv + kProdRows * D;
+  float* ssin = scos + kProdRows * HALF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool on = lane < HALF;
   const int l = lane & (HALF - 1);
@@ -885,12 +965,14 @@ __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceAr
     const float f = inv_norm_of(wave_sum(on ? o1 * o1 + o2 * o2 : 0.f));
     o1 *= f;
     o2 *= f;
-    if (live && on && is_q) {   // q: times qscale, back in place and into LDS
+    if (live && on && is_q) {   // q: times qscale, into LDS (and back in place)
       o1 *= s1[it];
       o2 *= s2[it];
-      float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + ic)) * D;
-      p[lane] = o1;
-      p[lane + HALF] = o2;
+      if (a.write_q) {
+        float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + ic)) * D;
+        p[lane] = o1;
+        p[lane + HALF] = o2;
+      }
       sq[ic * D + lane] = o1;
       sq[ic * D + lane + HALF] = o2;
     } else if (live && on) {   // k row j0 + t into LDS; row r's to kout and the cache
@@ -929,6 +1011,30 @@ __global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceAr
                        size_t(qc);
     write_partial(a.acc, a.ml, rec, D, M, L, a0, a1);
   }
+}
+
+template <int D, int VPW>
+__global__ void __launch_bounds__(kWaves * 64) qk_produce_kernel(const ProduceArgs a) {
+  __shared__ float lds[prod_lds_floats<D>()];
+  produce_row<D, VPW>(a, int(blockIdx.x) % a.kv_heads, int(blockIdx.x) / a.kv_heads, lds);
+}
+
+// The decode step's producer and scan in one launch (one row block): work-groups 0 .. kv_heads * splits - 1 scan
+// (from the raw q rows, each processing them itself), the last kv_heads * m produce (store, own-key partials;
+// q is not written back, since the scan work-groups read it raw). They run concurrently: the scan reads only
+// stored positions below pos0 and the store writes only slots that no row sees under their old position nor
+// under the new one (the store-first condition), and every slot holds finite values (a new cache is zeroed), so a
+// scan that reads a slot while it is rewritten gives it weight 0 either way.
+template <int D, int QB, bool F8, int VPW>
+__global__ void __launch_bounds__(kWaves * 64) attn_step_kernel(const ScanArgs a, const ProduceArgs pa) {
+  extern __shared__ float lds[];
+  const int scan_wgs = int(gridDim.x) - pa.kv_heads * pa.m;
+  if (int(blockIdx.x) >= scan_wgs) {
+    const int pr = int(blockIdx.x) - scan_wgs;
+    produce_row<D, VPW>(pa, pr % pa.kv_heads, pr / pa.kv_heads, lds);
+    return;
+  }
+  scan_split<D, QB, F8, true>(a, int(blockIdx.x), lds);
 }
 
 // ------------------------------------------------------------------------------------------------------ merge
@@ -1109,14 +1215,13 @@ ScanFn scan_fn(int d, int qb, bool f8) {
 
 // The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks (gfx950
 // has 160 KiB per CU): raise the kernel's limit once.
-void allow_lds(ScanFn fn, size_t lds) {
+void allow_lds(const void* fn, size_t lds) {
   if (lds <= 65536) return;
-  static thread_local ScanFn raised[8] = {};
-  for (ScanFn f : raised)
+  static thread_local const void* raised[32] = {};
+  for (const void* f : raised)
     if (f == fn) return;
-  HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                int(lds)));
-  for (ScanFn& f : raised)
+  HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  for (const void*& f : raised)
     if (!f) {
       f = fn;
       return;
@@ -1143,13 +1248,8 @@ int block_rows(const AttnPlan& p, int n_q, int b) {
   return std::min(p.rpb, n_q - b * p.rpb);
 }
 
-}  // namespace
-
-std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblocks, const float* q, int n_q,
-                             int heads, long long pos0, int window, float scale, float* part, hipStream_t stream) {
-  XTG_CHECK(p.splits >= 1 && p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
-  XTG_CHECK(nblocks >= 1 && b0 + nblocks <= p.blocks, "attention: blocks %d .. %d of %d", b0, b0 + nblocks, p.blocks);
-  const int nr = block_rows(p, n_q, b0);   // the widest block of the launch
+ScanArgs scan_args(const DevKv& c, const AttnPlan& p, int b0, const float* q, int n_q, int heads, long long pos0,
+                   int window, float scale, float* part) {
   ScanArgs a{};
   a.q = q;
   a.ck = reinterpret_cast<const uint4*>(c.k);
@@ -1174,12 +1274,72 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblo
   a.tiles = p.tiles;
   a.pos0 = int(pos0);
   a.scale2 = scale * kLog2e;
+  return a;
+}
+
+ProduceArgs produce_args(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
+                         int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
+                         const float* qscale, bool store, float* part) {
+  XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
+  XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
+  XTG_CHECK(!store || !c.ring || c.slots >= m, "producer: %d rows into a %lld-slot ring", m, c.slots);
+  ProduceArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.kout = kout;
+  a.m = m;
+  a.heads = heads;
+  a.kv_heads = c.kv_heads;
+  a.group = p.group;
+  a.window = window;
+  a.rpb = p.rpb;
+  a.splits = p.splits;
+  a.splits1 = p.splits + 1;
+  a.qpad = p.qpad;
+  a.store = store ? 1 : 0;
+  a.pos0 = pos0;
+  a.scale = scale;
+  a.inv_freq = inv_freq;
+  a.qscale = qscale;
+  a.ck = c.k;
+  a.cv = c.v;
+  a.kscale = c.kscale;
+  a.vscale = c.vscale;
+  a.fp8 = c.fp8 ? 1 : 0;
+  a.slot_pos = c.slot_pos;
+  a.slots = c.slots;
+  a.ring = c.ring ? 1 : 0;
+  a.slots_pad = c.slots_pad;
+  a.acc = part;
+  a.ml = part + p.records() * size_t(p.d);
+  a.blk_records = blk_records(p);
+  a.write_q = 1;
+  return a;
+}
+
+// The producer's rows per wave: row r's q heads and the own k rows it sees (at most min(m, window)), over 4 waves.
+int produce_vpw(const AttnPlan& p, int m, int window) {
+  const int keys = window > 0 ? std::min(m, window) : m;
+  const int need = (p.group + keys + kWaves - 1) / kWaves;
+  XTG_CHECK(need <= 4, "producer: %d rows per wave", need);
+  return need <= 2 ? 2 : 4;
+}
+
+}  // namespace
+
+std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblocks, const float* q, int n_q,
+                             int heads, long long pos0, int window, float scale, float* part, hipStream_t stream) {
+  XTG_CHECK(p.splits >= 1 && p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
+  XTG_CHECK(nblocks >= 1 && b0 + nblocks <= p.blocks, "attention: blocks %d .. %d of %d", b0, b0 + nblocks, p.blocks);
+  const int nr = block_rows(p, n_q, b0);   // the widest block of the launch
+  const ScanArgs a = scan_args(c, p, b0, q, n_q, heads, pos0, window, scale, part);
   const int qb = (nr * p.group + 15) / 16;
   ScanFn fn = scan_fn(c.head_dim, qb, c.fp8);
   XTG_CHECK(fn != nullptr, "attention: no kernel for head_dim %d and %d column blocks", c.head_dim, qb);
   const int nd = c.head_dim / 16;
   const size_t lds = (size_t(kWaves) * qb * 2 * 16 + size_t(kWaves) * qb * nd * 64 * 4) * sizeof(float);
-  allow_lds(fn, lds);
+  allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits), unsigned(nblocks)), dim3(kWaves * 64), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   return strf("attn_scan_kernel<%d, %d, %s>", c.head_dim, qb, c.fp8 ? "true" : "false");
@@ -1233,54 +1393,60 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
 std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
                               int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
                               const float* qscale, bool store, float* part, hipStream_t stream) {
-  XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
-  XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
-  XTG_CHECK(!store || !c.ring || c.slots >= m, "producer: %d rows into a %lld-slot ring", m, c.slots);
-  ProduceArgs a{};
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.kout = kout;
-  a.m = m;
-  a.heads = heads;
-  a.kv_heads = c.kv_heads;
-  a.group = p.group;
-  a.window = window;
-  a.rpb = p.rpb;
-  a.splits = p.splits;
-  a.splits1 = p.splits + 1;
-  a.qpad = p.qpad;
-  a.store = store ? 1 : 0;
-  a.pos0 = pos0;
-  a.scale = scale;
-  a.inv_freq = inv_freq;
-  a.qscale = qscale;
-  a.ck = c.k;
-  a.cv = c.v;
-  a.kscale = c.kscale;
-  a.vscale = c.vscale;
-  a.fp8 = c.fp8 ? 1 : 0;
-  a.slot_pos = c.slot_pos;
-  a.slots = c.slots;
-  a.ring = c.ring ? 1 : 0;
-  a.slots_pad = c.slots_pad;
-  a.acc = part;
-  a.ml = part + p.records() * size_t(p.d);
-  a.blk_records = blk_records(p);
-  const int keys = window > 0 ? std::min(m, window) : m;   // own key rows a query row sees, at most
-  const int vpw_need = (p.group + keys + kWaves - 1) / kWaves;
+  const ProduceArgs a =
+      produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, inv_freq, qscale, store, part);
+  const int vpw = produce_vpw(p, m, window);
   const dim3 grid{unsigned(c.kv_heads * m)}, block{unsigned(kWaves * 64)};
-  int vpw = 0;
-#define XTG_PROD(D, V)                                                                    \
-  if (c.head_dim == D && vpw_need <= V && !vpw) {                                         \
-    hipLaunchKernelGGL((qk_produce_kernel<D, V>), grid, block, 0, stream, a);             \
-    vpw = V;                                                                              \
-  }
+#define XTG_PROD(D, V) \
+  if (c.head_dim == D && vpw == V) hipLaunchKernelGGL((qk_produce_kernel<D, V>), grid, block, 0, stream, a);
   XTG_PROD(64, 2) XTG_PROD(64, 4) XTG_PROD(128, 2) XTG_PROD(128, 4)
 #undef XTG_PROD
-  XTG_CHECK(vpw != 0, "producer: no kernel for head_dim %d and %d rows per wave", c.head_dim, vpw_need);
+  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "producer: head_dim %d", c.head_dim);
   HIP_CHECK(hipGetLastError());
   return strf("qk_produce_kernel<%d, %d>", c.head_dim, vpw);
+}
+
+bool attn_step_fuses(const AttnPlan& p, int m) {
+  return p.blocks == 1 && p.splits >= 1 && m <= kProdRows && (m * p.group + 15) / 16 <= 2;
+}
+
+std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
+                             float* kout, int m, int heads, long long pos0, int window, float scale,
+                             const float* inv_freq, const float* qscale, bool store, float* part,
+                             hipStream_t stream) {
+  XTG_CHECK(attn_step_fuses(p, m), "attention step: %d rows in %d blocks, %d splits: no fused launch", m, p.blocks,
+            p.splits);
+  XTG_CHECK(p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
+  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "attention step: head_dim %d", c.head_dim);
+  XTG_CHECK(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(qscale) % 16 == 0,
+            "attention step: q and qscale must be 16-byte aligned");
+  ScanArgs a = scan_args(c, p, 0, q, m, heads, pos0, window, scale, part);
+  a.inv_freq = inv_freq;
+  a.qscale = qscale;
+  ProduceArgs pa = produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, inv_freq, qscale, store, part);
+  pa.write_q = 0;   // the scan work-groups read q raw while the producers run
+  const int vpw = produce_vpw(p, m, window);
+  const int qb = (m * p.group + 15) / 16;
+  const dim3 grid{unsigned(c.kv_heads * p.splits + c.kv_heads * m)}, block{unsigned(kWaves * 64)};
+  bool done = false;
+#define XTG_STEP(D, Q, F, V)                                                                                   \
+  if (!done && c.head_dim == D && qb == Q && c.fp8 == F && vpw == V) {                                         \
+    auto fn = attn_step_kernel<D, Q, F, V>;                                                                    \
+    const size_t lds = size_t(std::max(scan_lds_floats<D, Q, true>(), prod_lds_floats<D>())) * sizeof(float);   \
+    allow_lds(reinterpret_cast<const void*>(fn), lds);                                                         \
+    hipLaunchKernelGGL(fn, grid, block, lds, stream, a, pa);                                                   \
+    done = true;                                                                                               \
+  }
+#define XTG_STEP_D(D) \
+  XTG_STEP(D, 1, false, 2) XTG_STEP(D, 1, false, 4) XTG_STEP(D, 2, false, 2) XTG_STEP(D, 2, false, 4) \
+  XTG_STEP(D, 1, true, 2) XTG_STEP(D, 1, true, 4) XTG_STEP(D, 2, true, 2) XTG_STEP(D, 2, true, 4)
+  XTG_STEP_D(64) XTG_STEP_D(128)
+#undef XTG_STEP_D
+#undef XTG_STEP
+  XTG_CHECK(done, "attention step: no kernel for head_dim %d, %d column blocks, %d rows per wave", c.head_dim, qb,
+            vpw);
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_step_kernel<%d, %d, %s, %d>", c.head_dim, qb, c.fp8 ? "true" : "false", vpw);
 }
 
 std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,

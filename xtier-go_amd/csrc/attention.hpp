@@ -75,6 +75,15 @@ constexpr int kProdRows = 8, kProdGroup = 8;   // the producer's rows per call a
 std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
                               int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
                               const float* qscale, bool store, float* part, hipStream_t stream);
+// The producer and the scan in one launch (same arguments and results as launch_qk_produce followed by
+// launch_attn_scan, except that q is not written back): for a call of one row block with cached keys to scan
+// (attn_step_fuses). The store may run concurrently with the scan only under the store-first condition above;
+// otherwise pass store = false and kout, and store after.
+bool attn_step_fuses(const AttnPlan& p, int m);
+std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
+                             float* kout, int m, int heads, long long pos0, int window, float scale,
+                             const float* inv_freq, const float* qscale, bool store, float* part,
+                             hipStream_t stream);
 // The decode step's finish (dory.cpp:509-515): every row's merge, times sigmoid(g * gscale), justnorm over the
 // heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).
 std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,

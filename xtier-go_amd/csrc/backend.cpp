@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 
@@ -498,12 +499,19 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
     ensure(kproc_, kproc_size_, size_t(m) * size_t(c->kv_heads) * size_t(c->head_dim) * sizeof(float));
     kout = static_cast<float*>(kproc_);
   }
-  timed([&] {
-    return launch_qk_produce(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
-                             stream_);
-  });
-  if (p.splits > 0)
-    timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
+  if (attn_step_fuses(p, m) && !std::getenv("XTG_ATTN_UNFUSED")) {
+    timed([&] {
+      return launch_attn_step(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
+                              stream_);
+    });
+  } else {
+    timed([&] {
+      return launch_qk_produce(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
+                               stream_);
+    });
+    if (p.splits > 0)
+      timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
+  }
   if (!store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
   timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
