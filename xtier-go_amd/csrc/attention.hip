@@ -477,13 +477,16 @@ __device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D 
 template <int D, int QB>
 constexpr int scan_merge_floats() { return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16) * 64 * 4; }
 template <int D, int QB, bool RAWQ>
-constexpr int scan_lds_floats() { return scan_merge_floats<D, QB>() + (RAWQ ? 2 * kProdRows * (D / 2) : 0); }
+constexpr int scan_lds_floats() {
+  return scan_merge_floats<D, QB>() + (RAWQ ? QB * 16 * D + 2 * kProdRows * (D / 2) : 0);
+}
 
 // One scan work-group (KV head, split) of a row block. RAWQ: q arrives as the projection wrote it, and the work-group
-// applies the producer's RoPE, justnorm and qscale itself (packs/dory/dory.cpp:482-490) before the scale: the q-col's
-// four lane groups hold dims i and i + d/2 of each RoPE pair in the same lane, so the rotation is in-lane and the
-// norm one sum over the lane groups; the rows' angles FP32(pos) * inv_freq[i] go through a cosine / sine table in
-// LDS (at most kProdRows rows), one entry per thread.
+// applies the producer's RoPE, justnorm and qscale itself (packs/dory/dory.cpp:482-490) before the scale, once per
+// q-col: the rows' angles FP32(pos) * inv_freq[i] go into a cosine / sine table in LDS (at most kProdRows rows, one
+// entry per thread); then 16 / QB threads per q-col take d / 2 * QB / 16 consecutive RoPE pairs (i, i + d/2) each,
+// rotate them, add their squares over those lanes, scale, and leave the processed q-col in LDS, from which every
+// lane takes its operand dims.
 template <int D, int QB, bool F8, bool RAWQ>
 __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   constexpr int NC = D / 32, ND = D / 16;
@@ -523,79 +526,112 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   // three terms. lo: the first stored position the column sees.
   bf16x8 qop[QB][NC][3];
   int lo[QB];
-  float xq[QB][NC][8];
-  int qh[QB];
   bool qlive[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qc = qb * 16 + j;
-    const bool live = qc < qcols;
-    const int qrow = live ? qc / a.group : 0;
-    const int qpos = a.pos0 + row0 + qrow;
-    lo[qb] = !live ? INT_MAX : (a.window > 0 ? max(0, qpos - a.window + 1) : 0);
-    qh[qb] = kvh * a.group + (live ? qc % a.group : 0);
-    qlive[qb] = live;
-    const float* qp = qrows + (size_t(qrow) * size_t(a.heads) + size_t(qh[qb])) * D;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
-      const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
-      const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xq[qb][c][e] = x[e];
-    }
+    qlive[qb] = qc < qcols;
+    const int qpos = a.pos0 + row0 + (qlive[qb] ? qc / a.group : 0);
+    lo[qb] = !qlive[qb] ? INT_MAX : (a.window > 0 ? max(0, qpos - a.window + 1) : 0);
   }
   if constexpr (RAWQ) {
     constexpr int HALF = D / 2;
-    float* scos = lds + scan_merge_floats<D, QB>();
+    constexpr int TPV = 16 / QB;          // threads per q-col
+    constexpr int PP = HALF / TPV;        // RoPE pairs per thread
+    constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
+    static_assert(PP % 2 == 0 && TPV * QB * 16 == kWaves * 64, "q-col split");
+    float* sq = lds + scan_merge_floats<D, QB>();   // processed q-cols [QB * 16][D]
+    float* scos = sq + QB * 16 * D;
     float* ssin = scos + kProdRows * HALF;
     const int nrows = min(a.rpb, a.n_q - row0);
-    for (int e = int(threadIdx.x); e < nrows * HALF; e += kWaves * 64) {
-      const float ang = float(a.pos0 + row0 + e / HALF) * a.inv_freq[e % HALF];
-      scos[e] = cosf(ang);
-      ssin[e] = sinf(ang);
+    const int v = int(threadIdx.x) / TPV, p0 = (int(threadIdx.x) % TPV) * PP;
+    const bool vlive = v < qcols;
+    const int vrow = vlive ? v / a.group : 0;
+    const int vh = kvh * a.group + (vlive ? v % a.group : 0);
+    // every load first: the table's frequencies, the q-col's pairs and their scales
+    float fr[kAngles];
+#pragma unroll
+    for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[(int(threadIdx.x) + u * kWaves * 64) % HALF];
+    float x1[PP], x2[PP], s1[PP], s2[PP];
+    const float* qp = qrows + (size_t(vrow) * size_t(a.heads) + size_t(vh)) * D;
+#pragma unroll
+    for (int e = 0; e < PP; e += 2) {   // PP consecutive floats at a multiple of PP: 8-byte loads at least
+      const float2 t1 = *reinterpret_cast<const float2*>(qp + p0 + e);
+      const float2 t2 = *reinterpret_cast<const float2*>(qp + HALF + p0 + e);
+      x1[e] = t1.x, x1[e + 1] = t1.y;
+      x2[e] = t2.x, x2[e + 1] = t2.y;
+      if (a.qscale) {
+        const float* sp = a.qscale + size_t(vh) * D + p0 + e;
+        const float2 u1 = *reinterpret_cast<const float2*>(sp);
+        const float2 u2 = *reinterpret_cast<const float2*>(sp + HALF);
+        s1[e] = u1.x, s1[e + 1] = u1.y;
+        s2[e] = u2.x, s2[e + 1] = u2.y;
+      } else {
+        s1[e] = s1[e + 1] = s2[e] = s2[e + 1] = 1.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAngles; ++u) {
+      const int e = int(threadIdx.x) + u * kWaves * 64;
+      if (e < nrows * HALF) {
+        const float ang = float(a.pos0 + row0 + e / HALF) * fr[u];
+        scos[e] = cosf(ang);
+        ssin[e] = sinf(ang);
+      }
+    }
+    __syncthreads();
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < PP; ++e) {
+      const float cs = scos[vrow * HALF + p0 + e], sn = ssin[vrow * HALF + p0 + e];
+      const float o1 = x1[e] * cs - x2[e] * sn, o2 = x2[e] * cs + x1[e] * sn;
+      x1[e] = o1;
+      x2[e] = o2;
+      ss += o1 * o1 + o2 * o2;
+    }
+    // the sum over the q-col's TPV consecutive lanes (8 or 16: DPP within rows of 16)
+    ss += dpp<kDppXor1>(ss);
+    ss += dpp<kDppXor2>(ss);
+    ss += dpp<kDppHalfMirror>(ss);
+    if constexpr (TPV == 16) ss += dpp<kDppMirror>(ss);
+    const float f = inv_norm_of(ss);
+#pragma unroll
+    for (int e = 0; e < PP; e += 2) {
+      *reinterpret_cast<float2*>(sq + v * D + p0 + e) = make_float2((x1[e] * f) * s1[e], (x1[e + 1] * f) * s1[e + 1]);
+      *reinterpret_cast<float2*>(sq + v * D + HALF + p0 + e) =
+          make_float2((x2[e] * f) * s2[e], (x2[e + 1] * f) * s2[e + 1]);
     }
     __syncthreads();
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int qrow = qlive[qb] ? (qb * 16 + j) / a.group : 0;
-      float ss = 0.f;
-#pragma unroll
-      for (int c = 0; c < NC / 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int i = 32 * c + 8 * g + e;
-          const float cs = scos[qrow * HALF + i], sn = ssin[qrow * HALF + i];
-          const float x1 = xq[qb][c][e], x2 = xq[qb][c + NC / 2][e];
-          const float o1 = x1 * cs - x2 * sn, o2 = x2 * cs + x1 * sn;
-          xq[qb][c][e] = o1;
-          xq[qb][c + NC / 2][e] = o2;
-          ss += o1 * o1 + o2 * o2;
-        }
-      const float f = inv_norm_of(xor32_sum(xor16_sum(ss)));
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        float sc[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-        if (a.qscale) {
-          const float* sp = a.qscale + size_t(qh[qb]) * D + 32 * c + 8 * g;
-          const float4 u = *reinterpret_cast<const float4*>(sp);
-          const float4 w = *reinterpret_cast<const float4*>(sp + 4);
-          sc[0] = u.x, sc[1] = u.y, sc[2] = u.z, sc[3] = u.w, sc[4] = w.x, sc[5] = w.y, sc[6] = w.z, sc[7] = w.w;
-        }
+        const float* sp = sq + (qb * 16 + j) * D + 32 * c + 8 * g;
+        const float4 u = *reinterpret_cast<const float4*>(sp);
+        const float4 w = *reinterpret_cast<const float4*>(sp + 4);
+        float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xq[qb][c][e] = (xq[qb][c][e] * f) * sc[e];
+        for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? x[e] * a.scale2 : 0.f;
+        split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
+      }
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qc = qb * 16 + j;
+      const int qrow = qlive[qb] ? qc / a.group : 0;
+      const float* qp =
+          qrows + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (qlive[qb] ? qc % a.group : 0))) * D;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
+        const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
+        float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? x[e] * a.scale2 : 0.f;
+        split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
       }
     }
   }
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? xq[qb][c][e] * a.scale2 : 0.f;
-      split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
-    }
 
   ScanState<D, QB> st;
 #pragma unroll

@@ -152,13 +152,13 @@ void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype
   matmul_op(ws, nw, op_, m, y, y_off);
 }
 
-void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op) {
+void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op, float* copy) {
   XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
   XTG_CHECK(x_dtype == kXF32 || x_dtype == kXBF16, "matmul: unknown activation type %d", x_dtype);
   XTG_CHECK(x && op, "prep_x: NULL input or operand");
   XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(op) % 16 == 0,
             "prep_x: rows and operand must be 16-byte aligned");
-  timed([&] { return launch_prep_x(x, x_dtype, m, k, op, stream_); });
+  timed([&] { return launch_prep_x(x, x_dtype, m, k, op, stream_, copy); });
 }
 
 void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,

@@ -41,7 +41,7 @@ class Backend {
   void matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off);
   // the two halves of matmul_dev: the activation operand ([xop][8 row scales], op_bytes(k)) and the GEMV on it
   static size_t op_bytes(int k) { return op_group_bytes(k); }   // per 8 rows
-  void prep_x(const void* x, int x_dtype, int m, int k, void* op);
+  void prep_x(const void* x, int x_dtype, int m, int k, void* op, float* copy = nullptr);   // copy: FP32 rows too
   void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
                  const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]
 

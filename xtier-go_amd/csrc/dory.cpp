@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 
 #include "common.hpp"
 
@@ -188,19 +189,23 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
             (long long)c_.context);
   const int H = c_.hidden;
   const size_t bytes = size_t(m) * H * sizeof(float);
-  b_.copy(x, 0, x_, 0, bytes);
-  b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    b_.prep_x(x, XTG_X_F32, m, H, op_h_, x_);   // the rows' operand, and the rows into x_
+  } else {
+    b_.copy(x, 0, x_, 0, bytes);
+    b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
+  }
   size_t l = 0;
   for (; l < size_t(c_.n_in); ++l) sublayer(layers_[l], m, pos0, 0);
-  b_.copy(x_, 0, input_, 0, bytes);
-  b_.copy(x_, 0, state_, 0, bytes);
+  // the loops start from state = input = x: the first entry is justnorm(x + x) read in place, and input is kept
+  // only for later entries; the last exit writes x in place (x = state = justnorm(x))
+  if (c_.loops > 1) b_.copy(x_, 0, input_, 0, bytes);
   for (int i = 0; i < c_.loops; ++i) {
-    b_.add_norm(state_, input_, x_, m, H, op_h_);   // loop entry: x = justnorm(state + input)
+    const bool last = i == c_.loops - 1;
+    b_.add_norm(i == 0 ? x_ : state_, i == 0 ? x_ : input_, x_, m, H, op_h_);   // x = justnorm(state + input)
     for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r) sublayer(layers_[r], m, pos0, i);
-    // loop exit: state = justnorm(x); after the last loop x = state, whose operand the next projection reads
-    b_.add_norm(x_, nullptr, state_, m, H, i == c_.loops - 1 ? op_h_ : nullptr);
+    b_.add_norm(x_, nullptr, last ? x_ : state_, m, H, last ? op_h_ : nullptr);   // state = justnorm(x)
   }
-  b_.copy(state_, 0, x_, 0, bytes);
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0);
 }
 

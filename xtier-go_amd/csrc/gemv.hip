@@ -109,10 +109,12 @@ __device__ inline void load_chunk(const void* x, int x_dtype, int j, int k, int 
 // [2^14, 2^15); the scaled row is split into f16 high and low parts in MFMA B-operand order (columns 2 jj and
 // 2 jj + 1 of its group of 8 rows: row j is row jj = j % 8 of group j / 8, whose operand starts at
 // op + (j / 8) * op_group_bytes(k)). Rows up to 8192 wide make one read of x (chunks held in registers); wider
-// rows read x twice. Columns of rows >= m are not written: the GEMV and the GEMM never use them.
+// rows read x twice. Columns of rows >= m are not written: the GEMV and the GEMM never use them. copy (FP32 rows
+// only, or NULL): the rows are also written there as they are read.
 constexpr int kPrepThreads = 256, kPrepChunks = 4;
 __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __restrict__ x, int x_dtype, int k, int kt,
-                                                              char* __restrict__ op, size_t stride) {
+                                                              char* __restrict__ op, size_t stride,
+                                                              float* __restrict__ copy) {
   __shared__ float red[kPrepThreads / 64];
   const int row = blockIdx.x, tid = threadIdx.x;
   f16x8* __restrict__ xop = reinterpret_cast<f16x8*>(op + size_t(row / kMaxRows) * stride);
@@ -128,11 +130,27 @@ __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __rest
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
   }
+  if (copy) {
+#pragma unroll
+    for (int u = 0; u < kPrepChunks; ++u) {
+      const int c = tid + u * kPrepThreads;
+      if (c * 8 < k) {
+        float* d = copy + size_t(row) * size_t(k) + size_t(c) * 8;
+        *reinterpret_cast<float4*>(d) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+        *reinterpret_cast<float4*>(d + 4) = make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
+      }
+    }
+  }
   for (int c = tid + kPrepChunks * kPrepThreads; c < chunks; c += kPrepThreads) {
     float w[8];
     load_chunk(x, x_dtype, row, k, c, w);
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(w[i]));
+    if (copy && c * 8 < k) {
+      float* d = copy + size_t(row) * size_t(k) + size_t(c) * 8;
+      *reinterpret_cast<float4*>(d) = make_float4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<float4*>(d + 4) = make_float4(w[4], w[5], w[6], w[7]);
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -156,13 +174,15 @@ __global__ void __launch_bounds__(kPrepThreads) prep_x_kernel(const void* __rest
   }
 }
 
-std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream) {
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream, float* copy) {
   XTG_CHECK(m >= 1, "prep_x: %d rows", m);
   XTG_CHECK(k > 0 && k % 16 == 0, "prep_x: width %d (a multiple of 16)", k);
   XTG_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, "prep_x: activations at %p are not 16-byte aligned", x);
+  XTG_CHECK(!copy || (x_dtype == kXF32 && reinterpret_cast<uintptr_t>(copy) % 16 == 0),
+            "prep_x: a copy is of FP32 rows, 16-byte aligned");
   const int kt = (k + kTileK - 1) / kTileK;
   hipLaunchKernelGGL(prep_x_kernel, dim3(unsigned(m)), dim3(kPrepThreads), 0, stream, x, x_dtype, k, kt,
-                     static_cast<char*>(op), op_group_bytes(k));
+                     static_cast<char*>(op), op_group_bytes(k), copy);
   HIP_CHECK(hipGetLastError());
   return "prep_x_kernel";
 }

@@ -44,7 +44,8 @@ inline size_t op_group_bytes(int k) { return xop_bytes(k) + kMaxRows * sizeof(fl
 enum XDtype { kXF32 = 0, kXBF16 = 1 };
 // Launchers return the kernel's name (as rocprof prints it, without the namespace) for the profiler.
 // The operand of m >= 1 rows into op (ceil(m / 8) groups of op_group_bytes(k)).
-std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream);
+std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hipStream_t stream,
+                          float* copy = nullptr);
 
 struct GemvCall {
   const PackedNvfp4* w[4] = {nullptr, nullptr, nullptr, nullptr};

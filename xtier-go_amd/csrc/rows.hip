@@ -9,7 +9,8 @@
 //   slerp_norm:   x = justnorm(ya + lr * (yb - ya)), ya = justnorm(x), yb = justnorm(o) (kernels.cpp:177-189)
 //   swiglu_norm:  g = justnorm(silu(g * sg) * (u * su)) (kernels.cpp:225-234 then justnorm, dory.cpp:474-475)
 //   gate_norm:    a = justnorm(a * sigmoid(g * gs)) over all heads (dory.cpp:510-515)
-//   add_norm:     out = justnorm(a + b), or justnorm(a) without b (dory.cpp:532-541)
+//   add_norm:     out = justnorm(a + b), or justnorm(a) without b (dory.cpp:532-541); out may be a or b (each
+//                 thread reads its elements before it writes them)
 // The norms run one work-group of 512 threads per row with the whole row in registers (one read of each input,
 // the sums as block reductions), and can also write the row as the next projection's GEMV operand (the f16
 // high / low split prep_x_kernel makes), so no separate operand pass runs between a norm and its projection.
@@ -151,8 +152,7 @@ __global__ void __launch_bounds__(kNormThreads) gate_norm_kernel(const float* a_
 }
 
 template <int U>
-__global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_, const float* __restrict__ b_,
-                                                                 float* out,
+__global__ void __launch_bounds__(kNormThreads) add_norm_kernel(const float* a_, const float* b_, float* out,
                                                                  int w, int vec, f16x8* __restrict__ xop,
                                                                  float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
