@@ -261,6 +261,35 @@ def bf16_head_bench(pkg, wl, hip, reps):
     return out
 
 
+def sampling_bench(pkg, hip, reps):
+    """The device sampler on 131072-wide logits (the vocabulary), 1 and 8 rows: greedy (argmax), temperature only
+    (walk in index order), top_k 40 and top_p 0.9 (the full sort of the candidates), each call bracketed by
+    events on the backend's stream."""
+    n = 131072
+    rng = np.random.default_rng(51)
+    x = (rng.standard_normal((8, n)) * 3).astype(np.float32)
+    dx, dout = hip.array(x), hip.array(shape=(8,), dtype=np.int32)
+    out = {"n": n}
+    for label, p in (("greedy", dict(temperature=0.0)), ("temperature", dict(temperature=0.8)),
+                     ("top_k40", dict(temperature=0.8, top_k=40)), ("top_p0.9", dict(temperature=0.8, top_p=0.9))):
+        for m in (1, 8):
+            u = rng.random(m)
+            hip.sample(dx, m, n, u, dout, **p)
+            hip.finish()
+            hip.profile(True)
+            for _ in range(reps):
+                hip.sample(dx, m, n, u, dout, **p)
+            rep = hip.profile_report()
+            hip.profile(False)
+            name = [kk for kk in rep if kk in ("sample_kernel", "argmax_kernel")][0]
+            us = rep[name]["ms"] * 1e3 / rep[name]["calls"]
+            out["%s_m%d" % (label, m)] = {"kernel": name, "us": round(us, 2)}
+            log("sampling %s, %d row(s) of %d logits: %s %.1f us" % (label, m, n, name, us))
+    dx.free()
+    dout.free()
+    return out
+
+
 def prefill_run(pkg, hip, dev, w, rng, prompts):
     """Prompt processing on the 4B-shaped model (BF16 caches): xtg_hip_dory_prefill over n unit-norm rows from
     position 0 in chunks of 512 with logits for the last row only (the reference's Logits::Last), queued eagerly;
@@ -584,6 +613,7 @@ def main():
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
     bf16_head = bf16_head_bench(pkg, wl, hip, 10)
+    sampling = sampling_bench(pkg, hip, 20)
     prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
     prefill["attention_ctx4096"] = prefill_attention_bench(pkg, wl, hip, 512, 4096, 10)
 
@@ -628,6 +658,7 @@ def main():
                                  if all("traffic" in v for v in per_call.values()) else None)},
         "cpu_baseline": cpu,
         "bf16_lm_head": bf16_head,
+        "sampling": sampling,
         "prefill_gemm": prefill,
         "decode": decode,
     }

@@ -193,6 +193,21 @@ int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int
  * device logits [rows][n] into device out [rows] (int32): the first index of the largest value; NaNs never win, and
  * a NaN in element 0 gives 0, as the reference's scan does. Queued. */
 int xtg_hip_argmax(xtg_hip* h, const float* logits, int rows, int n, int32_t* out, char* err, int err_len);
+/* xtg::SamplingParams (engine/include/xtg/sampler.h:11-16), field for field. */
+typedef struct xtg_sampling {
+  float temperature; /* 0: greedy */
+  float top_p;
+  int top_k;         /* 0: off */
+  float min_p;
+} xtg_sampling;
+/* xtg::Sampler::sample (engine/src/sampler.cpp:40-94) per row of device logits [rows][n] (rows <= 8) into device
+ * out [rows] (int32). The random draw stays with the caller's generator: u [rows] (host) holds, per row, the
+ * value the reference's std::uniform_real_distribution<double>(0, total) scales by the total, i.e.
+ * std::generate_canonical<double, 53>(rng) from the Sampler's std::mt19937_64 (one draw per sampled row, none when
+ * temperature <= 0, which is argmax). Candidates are ordered by weight then index over the whole row, as the
+ * reference orders them wherever its result is defined. Queued. */
+int xtg_hip_sample(xtg_hip* h, const float* logits, int rows, int n, const xtg_sampling* p, const double* u,
+                   int32_t* out, char* err, int err_len);
 
 /* ----------------------------------------------------------------------------------- Dory decode step */
 

@@ -311,6 +311,99 @@ int xo_argmax(const float* x, int n) {
   return best;
 }
 
+/* engine/src/sampler.cpp:26-28: larger weight first, then smaller index (a strict total order on candidates) */
+typedef struct {
+  float w;
+  int i;
+} xo_cand;
+static int xo_more_likely_cmp(const void* pa, const void* pb) {
+  const xo_cand* a = (const xo_cand*)pa;
+  const xo_cand* b = (const xo_cand*)pb;
+  if (a->w > b->w || (a->w == b->w && a->i < b->i)) return -1;
+  if (b->w > a->w || (a->w == b->w && b->i < a->i)) return 1;
+  return 0;
+}
+
+static void xo_margin(double* m, double x, double boundary, double total) {
+  const double d = fabs(x - boundary) / (total > 0.0 ? total : 1.0);
+  if (d < *m) *m = d;
+}
+
+int xo_sample(const float* logits, int n, float temperature, float top_p, int top_k, float min_p, double u,
+              double* margin) {
+  /* engine/src/sampler.cpp:40-94 with r = u * total (uniform_real_distribution<double>(0, total) scales the
+     generator's generate_canonical draw u by the total). The candidates are fully sorted whenever a filter
+     applies: the reference's partial sorts order the same leading candidates, which are all its filters read
+     wherever its result is defined. margin (optional): the smallest distance, relative to the total, between r
+     (or the top_p target) and a running sum next to the chosen position. */
+  double mg = INFINITY;
+  if (temperature <= 0.f) {
+    if (margin) *margin = mg;
+    return xo_argmax(logits, n);
+  }
+  float mx = logits[0];
+  for (int i = 1; i < n; ++i) mx = mx < logits[i] ? logits[i] : mx; /* std::max(mx, logits[i]) */
+  const float inv_t = 1.f / temperature;
+  xo_cand* c = (xo_cand*)malloc(sizeof(xo_cand) * (size_t)n);
+  double total = 0.0;
+  for (int i = 0; i < n; ++i) {
+    const float w = expf((logits[i] - mx) * inv_t);
+    c[i].w = w;
+    c[i].i = i;
+    total += w;
+  }
+  int keep = n;
+  if (top_k > 0 && top_k < n) {
+    qsort(c, (size_t)n, sizeof(xo_cand), xo_more_likely_cmp);
+    keep = top_k;
+    total = 0.0;
+    for (int i = 0; i < keep; ++i) total += c[i].w;
+  } else if (top_p < 1.f || min_p > 0.f) {
+    qsort(c, (size_t)n, sizeof(xo_cand), xo_more_likely_cmp);
+  }
+  if (min_p > 0.f) {
+    const float floor_w = min_p * c[0].w;
+    int k = 0;
+    double t = 0.0;
+    while (k < keep && c[k].w >= floor_w) t += c[k++].w;
+    keep = k > 1 ? k : 1;
+    total = k ? t : (double)c[0].w;
+  }
+  if (top_p < 1.f) {
+    const double target = total * (double)top_p;
+    double cum = 0.0;
+    int k = 0;
+    while (k < keep) {
+      const double before = cum;
+      cum += c[k].w;
+      ++k;
+      if (cum >= target) {
+        xo_margin(&mg, target, before, total);
+        xo_margin(&mg, target, cum, total);
+        break;
+      }
+    }
+    keep = k > 1 ? k : 1;
+    total = cum;
+  }
+  const double r = u * total;
+  double cum = 0.0;
+  int token = c[keep - 1].i;
+  for (int i = 0; i < keep; ++i) {
+    const double before = cum;
+    cum += c[i].w;
+    if (r < cum) {
+      token = c[i].i;
+      xo_margin(&mg, r, before, total);
+      xo_margin(&mg, r, cum, total);
+      break;
+    }
+  }
+  free(c);
+  if (margin) *margin = mg;
+  return token;
+}
+
 void xo_add_norm(const float* a, const float* b, float* out, int rows, int width) {
   /* packs/dory/dory.cpp:532-541: loop entry x = justnorm(state + input); loop exit state = justnorm(x) */
   const size_t n = (size_t)rows * (size_t)width;

@@ -60,6 +60,8 @@ void xo_gate_norm(float* att, const float* gate, const float* gs, int rows, int 
 /* :532-541: out = justnorm(a + b) (b non-NULL) or justnorm(a); out may alias a */
 void xo_add_norm(const float* a, const float* b, float* out, int rows, int width);
 int xo_argmax(const float* x, int n);                                                      /* sampler.cpp:8-13 */
+int xo_sample(const float* logits, int n, float temperature, float top_p, int top_k, float min_p, double u,
+              double* margin);                                                             /* sampler.cpp:40-94 */
 
 /* --- Q/K producer: packs/dory/dory.cpp:481-490 (RoPE q and k, justnorm per head, q *= qscale) --- */
 void xo_qk_produce(float* q, float* k, int m, int heads, int kv_heads, int head_dim, int64_t pos0, float theta,

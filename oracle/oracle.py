@@ -71,6 +71,7 @@ _ORACLE_SIGS = [
     ("xo_gate_norm", None, [_P, _P, _P, _I, _I]),
     ("xo_add_norm", None, [_P, _P, _P, _I, _I]),
     ("xo_argmax", _I, [_P, _I]),
+    ("xo_sample", _I, [_P, _I, ctypes.c_float, ctypes.c_float, _I, ctypes.c_float, ctypes.c_double, _P]),
     ("xo_kv_create", _P, [_I, _I, _I64, _I, _I]),
     ("xo_kv_free", None, [_P]),
     ("xo_kv_slots", _I64, [_P]),
@@ -99,6 +100,7 @@ _REF_SIGS = [
     ("xr_matmul_bf16", _I, [_P, _I, _I, _P, _I, _P, _I]),
     ("xr_justnorm", None, [_P, _I, _I]),
     ("xr_argmax", _I, [_P, _I]),
+    ("xr_sample", _I, [_P, _I, ctypes.c_float, ctypes.c_float, _I, ctypes.c_float, ctypes.c_uint64, _P]),
     ("xr_slerp_residual", None, [_P, _P, _P, _I, _I]),
     ("xr_rope", None, [_P, _I, _I, _I, _I64, _F]),
     ("xr_swiglu_scaled", None, [_P, _P, _P, _P, _I, _I]),
@@ -234,6 +236,28 @@ def argmax(x, use_ref=False):
     x = np.atleast_2d(_f32(x))
     fn = ref().xr_argmax if use_ref else oracle().xo_argmax
     return np.array([fn(x[r].ctypes.data, x.shape[1]) for r in range(x.shape[0])], np.int32)
+
+
+def sample(x, u, temperature=1.0, top_p=1.0, top_k=0, min_p=0.0):
+    """xtg::Sampler::sample (sampler.cpp:40-94) of each row of x float32 [rows][n] with draws u [rows] ->
+    (tokens int32 [rows], margins float64 [rows]: how close, relative to the total, r or the top_p target came to
+    a running-sum boundary)."""
+    x = np.atleast_2d(_f32(x))
+    toks, margins = np.empty(x.shape[0], np.int32), np.empty(x.shape[0])
+    m = ctypes.c_double()
+    for r in range(x.shape[0]):
+        toks[r] = oracle().xo_sample(x[r].ctypes.data, x.shape[1], temperature, top_p, top_k, min_p, float(u[r]),
+                                     ctypes.byref(m))
+        margins[r] = m.value
+    return toks, margins
+
+
+def sample_ref(x, seed, temperature=1.0, top_p=1.0, top_k=0, min_p=0.0):
+    """The reference Sampler(seed) on one row x float32 [n] -> (token, the draw u it used)."""
+    x = _f32(x)
+    u = ctypes.c_double()
+    t = ref().xr_sample(x.ctypes.data, x.shape[-1], temperature, top_p, top_k, min_p, seed, ctypes.byref(u))
+    return t, u.value
 
 
 def add_norm(a, b=None):

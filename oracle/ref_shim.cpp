@@ -3,7 +3,9 @@
 // and, when present, as the CPU baseline. Calls go straight to xtg::matmul_nvfp4 / attention / KvCache / rope /
 // justnorm / slerp_residual / swiglu_scaled / f32_to_e4m3 / argmax (engine/include/xtg/{fp,kernels,kv,sampler}.h).
 #include <cstdint>
+#include <limits>
 #include <map>
+#include <random>
 #include <memory>
 #include <vector>
 
@@ -72,6 +74,20 @@ int xr_matmul_bf16(const uint16_t* w, int n_out, int k, const float* x, int m, f
 
 void xr_justnorm(float* x, int rows, int width) { xtg::justnorm(x, rows, width); }
 int xr_argmax(const float* x, int n) { return xtg::argmax(x, n); }
+// The reference Sampler seeded with `seed` samples one row; *u gets the draw its uniform_real_distribution made
+// (generate_canonical<double, 53> of a generator seeded alike), which a caller hands to a sampler that takes u.
+int xr_sample(const float* x, int n, float temperature, float top_p, int top_k, float min_p, uint64_t seed,
+              double* u) {
+  xtg::SamplingParams p;
+  p.temperature = temperature;
+  p.top_p = top_p;
+  p.top_k = top_k;
+  p.min_p = min_p;
+  xtg::Sampler s(seed);
+  std::mt19937_64 g(seed);
+  *u = std::generate_canonical<double, std::numeric_limits<double>::digits>(g);
+  return s.sample(x, n, p);
+}
 void xr_slerp_residual(float* a, const float* b, const float* lr, int rows, int width) {
   xtg::slerp_residual(a, b, lr, rows, width);
 }

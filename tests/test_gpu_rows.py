@@ -104,3 +104,36 @@ def test_argmax(hip, orc, rows, n):
     dx.free()
     dout.free()
     np.testing.assert_array_equal(got, orc.argmax(x))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 37, 1000, 5000, 131072])
+def test_sample(hip, orc, n):
+    """xtg::Sampler::sample (sampler.cpp:40-94) on the device with the same draws as the oracle (itself pinned
+    against the reference's Sampler): every filter combination over 8 rows at a time, ties planted, greedy rows
+    routed to argmax. The weights are FP32 exp values on both sides, so a token may differ only where r (or the
+    top_p target) lies within a rounding step of a running-sum boundary: a mismatch counts as one only if the
+    oracle's margin there exceeds 1e-6 of the total."""
+    rng = np.random.default_rng(n)
+    dout = hip.array(shape=(8,), dtype=np.int32)
+    checked = 0
+    for trial in range(12):
+        rows = int(rng.integers(1, 9))
+        x = (rng.standard_normal((rows, n)) * rng.choice([0.5, 2.0, 8.0])).astype(np.float32)
+        if trial % 3 == 0 and n > 3:
+            x[0, rng.integers(0, n, 3)] = x[0].max()   # ties among the most likely
+        params = dict(temperature=float(rng.choice([0.0, 0.3, 1.0, 2.0])),
+                      top_p=float(rng.choice([1.0, 0.9, 0.5, 0.05])),
+                      top_k=int(rng.choice([0, 1, 5, 40, n])), min_p=float(rng.choice([0.0, 0.05, 0.5])))
+        u = rng.random(rows)
+        dx = hip.array(x)
+        hip.sample(dx, rows, n, u, dout, **params)
+        got = dout.numpy()[:rows]
+        dx.free()
+        want, margin = orc.sample(x, u, **params)
+        for r in range(rows):
+            if got[r] != want[r]:
+                assert margin[r] < 1e-6, (n, params, r, int(got[r]), int(want[r]), float(margin[r]))
+            checked += 1
+    dout.free()
+    assert checked > 0

@@ -130,3 +130,54 @@ def test_argmax_vs_reference(orc):
     x[2, ::3] = np.nan
     x[3, 5000] = x[3, 90000] = x[3].max() + 1
     np.testing.assert_array_equal(orc.argmax(x, use_ref=True), orc.argmax(x))
+
+
+def test_sample_known_answers(orc):
+    """xtg::Sampler::sample (sampler.cpp:40-94) where the answer is fixed by the definition: temperature 0 is
+    argmax; top_k 1 and a tiny top_p keep only the most likely (ties: the smaller index); min_p 1 keeps the maxima
+    and their ties in index order; equal logits without a filter are walked in index order, so the draw u picks
+    index floor(u n); a single finite logit is always chosen."""
+    x = np.array([0.5, 2.0, 2.0, -1.0, 1.5], np.float32)
+    assert orc.sample(x[None], [0.9], temperature=0.0)[0][0] == 1
+    for u in (0.0, 0.5, 0.999):
+        assert orc.sample(x[None], [u], top_k=1)[0][0] == 1
+        assert orc.sample(x[None], [u], top_p=1e-4)[0][0] == 1
+    # min_p 1: the two maxima, index order, mass split evenly
+    assert orc.sample(x[None], [0.49], min_p=1.0)[0][0] == 1
+    assert orc.sample(x[None], [0.51], min_p=1.0)[0][0] == 2
+    flat = np.zeros((1, 1000), np.float32)
+    for u in (0.0, 0.1234, 0.5, 0.98765):
+        assert orc.sample(flat, [u])[0][0] == int(u * 1000)
+    one = np.full((1, 50), -np.inf, np.float32)
+    one[0, 17] = 3.0
+    for u in (0.0, 0.7):
+        assert orc.sample(one, [u], temperature=0.8, top_p=0.9)[0][0] == 17
+    # temperature: T -> 0 concentrates on the max; large T flattens towards index order
+    y = np.array([[0.0, 1.0]], np.float32)
+    assert orc.sample(y, [0.3], temperature=0.01)[0][0] == 1
+    assert orc.sample(y, [0.3], temperature=1e6)[0][0] == 0 and orc.sample(y, [0.7], temperature=1e6)[0][0] == 1
+
+
+def sample_params(rng, n):
+    return dict(temperature=float(rng.choice([0.0, 0.3, 1.0, 2.0])), top_p=float(rng.choice([1.0, 0.9, 0.5, 0.05])),
+                top_k=int(rng.choice([0, 1, 5, 40, n])), min_p=float(rng.choice([0.0, 0.05, 0.5])))
+
+
+@pytest.mark.skipif(not __import__("oracle").ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_sample_vs_reference(orc):
+    """The reference's own Sampler, seeded, against the oracle given the draw that Sampler made: every filter
+    combination, rows of 1 .. 5000 logits (past the reference's 1024-candidate sorted head) with planted ties, and
+    two 131072-wide rows."""
+    rng = np.random.default_rng(0)
+    for trial in range(300):
+        n = int(rng.choice([1, 7, 100, 1000, 5000]))
+        x = (rng.standard_normal(n) * rng.choice([0.5, 2, 8])).astype(np.float32)
+        if trial % 7 == 0:
+            x[rng.integers(0, n, 3)] = x.max()
+        params = sample_params(rng, n)
+        tr, u = orc.sample_ref(x, int(rng.integers(0, 2**63)), **params)
+        assert orc.sample(x[None], [u], **params)[0][0] == tr, (n, params)
+    for params in (dict(temperature=1.0), dict(temperature=0.7, top_p=0.95), dict(temperature=1.0, top_k=50)):
+        x = (rng.standard_normal(131072) * 3).astype(np.float32)
+        tr, u = orc.sample_ref(x, 12345, **params)
+        assert orc.sample(x[None], [u], **params)[0][0] == tr, params

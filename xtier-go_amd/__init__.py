@@ -33,6 +33,11 @@ class Bf16(ctypes.Structure):
     _fields_ = [("data", _P), ("n_out", _I), ("k", _I)]
 
 
+class Sampling(ctypes.Structure):
+    """xtg_sampling (the fields of xtg::SamplingParams, engine/include/xtg/sampler.h:11-16)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", _I), ("min_p", ctypes.c_float)]
+
+
 class AttnArgs(ctypes.Structure):
     """xtg_attn_args (the fields of xtg::AttnArgs, engine/include/xtg/kv.h:67-78)."""
     _fields_ = [("n_q", _I), ("pos0", ctypes.c_int64), ("heads", _I), ("kv_heads", _I), ("head_dim", _I),
@@ -87,6 +92,7 @@ SIGNATURES = [
     ("xtg_hip_gate_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_add_norm", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_argmax", _I, [_P, _P, _I, _I, _P] + _ERR),
+    ("xtg_hip_sample", _I, [_P, _P, _I, _I, ctypes.POINTER(Sampling), _P, _P] + _ERR),
     ("xtg_hip_dory_create", _P, [_P, ctypes.POINTER(DoryConfig), ctypes.POINTER(DoryLayer), ctypes.POINTER(Nvfp4),
                                  _P] + _ERR),
     ("xtg_hip_dory_destroy", None, [_P]),
@@ -405,6 +411,16 @@ class HipBackend:
         """out[r] (device int32) = the first index of the largest of logits[r][:n] (device)."""
         err = _errbuf()
         _check(lib().xtg_hip_argmax(self.h, _ptr(logits), rows, n, _ptr(out), err, len(err)), err)
+
+    def sample(self, logits, rows, n, u, out, temperature=1.0, top_p=1.0, top_k=0, min_p=0.0):
+        """out[r] (device int32) = xtg::Sampler::sample of logits[r][:n] (device) with the uniform draw u[r] in
+        [0, 1) (host; the reference's generate_canonical draw)."""
+        uu = np.ascontiguousarray(u, dtype=np.float64)
+        assert uu.shape == (rows,)
+        p = Sampling(temperature, top_p, top_k, min_p)
+        err = _errbuf()
+        _check(lib().xtg_hip_sample(self.h, _ptr(logits), rows, n, ctypes.byref(p), uu.ctypes.data, _ptr(out), err,
+                                    len(err)), err)
 
 
 class DorySession:

@@ -31,7 +31,7 @@ Backend::~Backend() {
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (auto& kv : bf16_weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_})
+  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_, sample_})
     if (p) (void)hipFree(p);
   for (DevKv* c : kvs_) {
     for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
@@ -562,6 +562,18 @@ void Backend::add_norm(const float* a, const float* b, float* out, int rows, int
 void Backend::argmax(const float* x, int rows, int n, int* out) {
   XTG_CHECK(x && out && rows >= 1 && n >= 1, "argmax: bad arguments");
   timed([&] { return launch_argmax(x, rows, n, out, stream_); });
+}
+
+void Backend::sample(const float* x, int rows, int n, float temperature, float top_p, int top_k, float min_p,
+                     const double* u, int* out) {
+  if (temperature <= 0.f) {   // greedy (sampler.cpp:41): no draw is used
+    argmax(x, rows, n, out);
+    return;
+  }
+  XTG_CHECK(x && out && u && rows >= 1 && n >= 1, "sample: bad arguments");
+  XTG_CHECK(rows <= kMaxSampleRows, "sample: %d rows (1..%d per call)", rows, kMaxSampleRows);
+  ensure(sample_, sample_size_, sample_scratch_bytes(rows, n));
+  timed([&] { return launch_sample(x, rows, n, temperature, top_p, top_k, min_p, u, out, sample_, stream_); });
 }
 
 hipEvent_t Backend::event() {

@@ -87,6 +87,10 @@ class Backend {
   void add_norm(const float* a, const float* b, float* out, int rows, int w, void* op = nullptr);
   // greedy decoding's token (xtg::argmax, sampler.cpp:8-13) of each of `rows` rows of n logits; device out int32
   void argmax(const float* x, int rows, int n, int* out);
+  // xtg::Sampler::sample (sampler.cpp:40-94) of each row with the caller's draws u[rows] (host, [0, 1): the
+  // generate_canonical the reference's uniform_real_distribution scales by the total); temperature <= 0: argmax
+  void sample(const float* x, int rows, int n, float temperature, float top_p, int top_k, float min_p,
+              const double* u, int* out);
   // 1 / theta^(2i/d) in FP32 computed on the host as engine/src/kernels.cpp:191-201 does, kept on the device
   const float* inv_freq(float theta, int d);
 
@@ -164,6 +168,8 @@ class Backend {
   size_t part_size_ = 0;
   void* kproc_ = nullptr;  // processed k rows of a decode step whose store follows the scan
   size_t kproc_size_ = 0;
+  void* sample_ = nullptr;   // sampling scratch: weights and the radix sort's buffers
+  size_t sample_size_ = 0;
   std::unordered_set<DevKv*> kvs_;
   std::vector<std::pair<std::pair<float, int>, float*>> inv_freq_;
   void* hx_ = nullptr;

@@ -261,6 +261,14 @@ int xtg_hip_argmax(xtg_hip* h, const float* logits, int rows, int n, int32_t* ou
   });
 }
 
+int xtg_hip_sample(xtg_hip* h, const float* logits, int rows, int n, const xtg_sampling* p, const double* u,
+                   int32_t* out, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && p, "sample: NULL handle or parameters");
+    h->b->sample(logits, rows, n, p->temperature, p->top_p, p->top_k, p->min_p, u, out);
+  });
+}
+
 struct xtg_hip_dory {
   xtg_hip* h;
   std::unique_ptr<xtg::hip::DorySession> s;

@@ -98,4 +98,12 @@ GemvShape gemv_bf16_shape(int kt, int nb, int m);
 std::string launch_gemv_bf16(const PackedBf16& w, const void* xop, int m, float* y, const float* col_scale,
                              hipStream_t stream);
 
+// ---- sampling (sample.hip) ----
+constexpr int kMaxSampleRows = 8;
+// xtg::Sampler::sample for rows of device logits [rows][n] with the caller's uniform draws u[rows] (host, [0, 1)),
+// temperature > 0; device tokens out[rows]. scratch: sample_scratch_bytes(rows, n) device bytes.
+size_t sample_scratch_bytes(int rows, int n);
+std::string launch_sample(const float* logits, int rows, int n, float temperature, float top_p, int top_k,
+                          float min_p, const double* u, int* out, void* scratch, hipStream_t stream);
+
 }  // namespace xtg::hip
