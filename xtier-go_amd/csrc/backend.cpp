@@ -561,6 +561,11 @@ void Backend::add_norm(const float* a, const float* b, float* out, int rows, int
 
 void Backend::argmax(const float* x, int rows, int n, int* out) {
   XTG_CHECK(x && out && rows >= 1 && n >= 1, "argmax: bad arguments");
+  if (rows <= kMaxSampleRows && n > 4096) {   // a vocabulary row: over slices, many work-groups a row
+    ensure(sample_, sample_size_, sample_scratch_bytes(rows, n));
+    timed([&] { return launch_argmax_slices(x, rows, n, out, sample_, stream_); });
+    return;
+  }
   timed([&] { return launch_argmax(x, rows, n, out, stream_); });
 }
 

@@ -105,5 +105,7 @@ constexpr int kMaxSampleRows = 8;
 size_t sample_scratch_bytes(int rows, int n);
 std::string launch_sample(const float* logits, int rows, int n, float temperature, float top_p, int top_k,
                           float min_p, const double* u, int* out, void* scratch, hipStream_t stream);
+// xtg::argmax over slices of the rows (rows <= kMaxSampleRows; scratch: sample_scratch_bytes(rows, n))
+std::string launch_argmax_slices(const float* logits, int rows, int n, int* out, void* scratch, hipStream_t stream);
 
 }  // namespace xtg::hip

@@ -16,18 +16,18 @@
 // the reference's left-to-right sums up to double rounding (a token can differ only when r lies within ~1e-15 of
 // a running-sum boundary).
 //
-// Design: one work-group of 1024 threads per row, everything in one launch, every pass over the row coalesced
-// (element i to thread i mod 1024). Running sums in a fixed order -- index order, or the sorted order -- go by
-// segments: each wave sums a contiguous segment, the segment sums run in order, and the wave whose segment holds
-// the crossing walks it in tiles of 64 with a wave scan.
-// With a filter, the candidates are the weights at or above a threshold tau that the kept prefix cannot go below:
-// every thread keeps its 4 most likely (weight, index) pairs during the weight pass; their union (4096 pairs,
-// sorted in LDS) gives tau -- its top_k-th value for top_k, the value where its running mass first reaches
-// total * top_p * (1 + 1e-6) for top_p, the floor for min_p (max(floor, that) with both) -- since the union is a
-// subset of the row, the row holds at least as much above tau. The candidates (at most kCand) are gathered, sorted
-// in LDS and filtered. When more than kCand weights lie at or above tau (a broad distribution under top_p or
-// min_p), the whole row is sorted instead by a stable LSD radix sort in scratch memory (8 passes of 4 bits,
-// contiguous chunks per thread): slower, the same result.
+// Design: three launches. Slices of 2048 logits (a work-group of 256 each): their maxima; then, with the row's max,
+// their weights, sums (fixed order), min_p counts and, with a filter, every thread's two most likely pairs (the
+// slice's 64 largest thread maxima sorted in LDS, and the largest second). Then
+// one work-group of 1024 threads per row: the slice sums in order give the total and, without a filter, the slice
+// where the running sum passes r, walked by hierarchical running sums (16 wave segments, 16 parts, tiles of 64).
+// With a filter, a threshold tau that the kept prefix cannot go below comes from the sorted union of the slices'
+// lists -- its top_k-th value for top_k, the value where its running mass first reaches total * top_p * (1 + 1e-6)
+// for top_p, the floor for min_p (max(floor, that) with both): the union is a subset of the row, so the row holds at
+// least as much above tau. When in every slice the 64th listed maximum and every thread's second lie below tau,
+// the union holds every weight >= tau, and the candidates are its sorted prefix; otherwise they are gathered from the row (at most 4096, sorted in LDS), or, past
+// that, the whole row is sorted by a stable LSD radix sort in scratch memory (8 passes of 4 bits): slower, the same
+// result. Greedy rows take the slices' first maxima (argmax_pick_kernel).
 #include <cfloat>
 #include <climits>
 #include <cmath>
@@ -119,17 +119,19 @@ __device__ inline double wave_range_sum(WF wf, int b, int e) {
 }
 
 // The first position i in [0, len) at which the running sum of wf(0 .. i) satisfies strict ? sum > r : sum >= r,
-// or len when none does; *at_sum: that running sum (the whole sum when none). Three levels: 16 segments (a wave
-// each), the crossing segment's 16 parts (a wave each), then the crossing part's tiles of 64 by one wave, the
-// crossing tile scanned. The sums of each level run in order. red: >= 20 doubles, sel: LDS int.
+// or len when none does; *at_sum: that running sum (the whole sum when none), both counted from base0. Three
+// levels: 16 segments (a wave each), the crossing segment's 16 parts (a wave each), then the crossing part's tiles
+// of 64 by one wave, the crossing tile scanned. The sums of each level run in order. red: >= 20 doubles, sel: LDS int.
 template <typename WF>
-__device__ inline int first_crossing(WF wf, int len, double r, bool strict, double* red, int* sel, double* at_sum) {
+__device__ inline int first_crossing(WF wf, int len, double r, bool strict, double* red, int* sel, double* at_sum,
+                                     double base0 = 0.0) {
   const int t = int(threadIdx.x), lane = t & 63, wave = t >> 6;
   constexpr int NW = kSampleThreads / 64;
   auto crosses = [&](double c) { return strict ? c > r : c >= r; };
-  // level 1 and 2: [lo, hi) split into NW parts of `part` elements; the first part whose running sum crosses
+  // level 1 and 2: [lo, hi) split into NW parts of `part` elements; the first part whose running sum (from base0)
+  // crosses
   int lo = 0, hi = len;
-  double base = 0.0;
+  double base = base0;
   for (int level = 0; level < 2; ++level) {
     const int part = ((hi - lo + NW - 1) / NW + 63) / 64 * 64;
     const int b = min(hi, lo + wave * part), e = min(hi, b + part);
@@ -233,232 +235,400 @@ __device__ inline void sort_pairs(float* cw, int* ci, int n2) {
 }
 }  // namespace
 
+// Per-row scratch (floats / ints / doubles laid out by SampleScratch): the weights, and per slice of kSlice logits
+// its max, argmax, weight sum, count and mass at or above the min_p floor, its 64 largest thread maxima in
+// candidate order (-1 weights past the slice's threads) and the largest second-most-likely weight of a thread.
+constexpr int kSlice = 2048, kSliceThreads = 256, kSliceTop = 64;
+constexpr int kCand = 4096;   // candidates sorted in LDS
+
 struct SampleArgs {
   const float* logits;   // [rows][n]
-  int n;
+  int n, slices;
   float temperature, top_p, min_p;
   int top_k;
   double u[kMaxSampleRows];
-  float* w;              // scratch [rows][n]
-  uint32_t* keys;        // scratch [rows][2][n]
-  int* idx;              // scratch [rows][2][n]
+  float* w;              // [rows][n]
+  float* smax;           // [rows][slices]
+  float* sbest;          // [rows][slices] argmax value, index in sbi
+  int* sbi;
+  double* ssum;          // [rows][slices]
+  double* sfl;           // [rows][slices] mass >= floor
+  int* snfl;             // [rows][slices] count >= floor
+  float* sw;             // [rows][slices][kSliceTop]: the slice's 64 largest thread maxima, in candidate order
+  int* si;
+  float* sm2;            // [rows][slices]: the largest second-most-likely weight of any thread of the slice
+  int lists;             // a filter applies: make the lists
+  uint32_t* keys;        // [rows][2][n] (the whole-row sort)
+  int* idx;
   int* out;              // [rows]
 };
 
-constexpr int kCand = 4096;   // candidates sorted in LDS (the union of the threads' top 4 has this many)
-constexpr int kTop = kCand / kSampleThreads;
-
-__global__ void __launch_bounds__(kSampleThreads) sample_kernel(const SampleArgs a) {
-  __shared__ double red[kSampleThreads / 64 + 4];   // >= 20
-  __shared__ uint32_t ured[kSampleThreads / 64 + 1];
-  __shared__ uint32_t hist[16 * kSampleThreads];   // the fallback sort's digit counts
-  __shared__ float cw[kCand];
-  __shared__ int ci[kCand];
-  __shared__ float fmx[kSampleThreads / 64];
-  __shared__ int sel, ccount;
-  __shared__ float tau_s;
-  const int row = int(blockIdx.x), t = int(threadIdx.x), n = a.n;
-  const float* l = a.logits + size_t(row) * size_t(n);
-  float* w = a.w + size_t(row) * size_t(n);
-
-  // the largest logit (std::max order is immaterial for finite rows), the weights, their total, each thread's
-  // 4 most likely, and (min_p) the count and mass at or above the floor min_p * w_max = min_p (w_max = exp(0))
-  float mx = -INFINITY;
-  for (int i0 = t; i0 < n; i0 += 8 * kSampleThreads) {   // eight loads in flight per thread
-    float v[8];
+// Slice maxima (the weights' reference point) and, for greedy decoding, each slice's first largest finite-or-inf
+// value (NaNs never win: xtg::argmax, sampler.cpp:8-13).
+__global__ void __launch_bounds__(kSliceThreads) slice_max_kernel(const SampleArgs a) {
+  __shared__ float sv[kSliceThreads / 64];
+  __shared__ int sx[kSliceThreads / 64];
+  __shared__ float sm[kSliceThreads / 64];
+  const int row = int(blockIdx.y), sl = int(blockIdx.x), t = int(threadIdx.x);
+  const float* l = a.logits + size_t(row) * size_t(a.n);
+  const int b = sl * kSlice, e = min(a.n, b + kSlice);
+  float v[kSlice / kSliceThreads];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = i0 + u * kSampleThreads < n ? l[i0 + u * kSampleThreads] : -INFINITY;
+  for (int u = 0; u < kSlice / kSliceThreads; ++u) {
+    const int i = b + t + u * kSliceThreads;
+    v[u] = i < e ? l[i] : -INFINITY;
+  }
+  float mx = -INFINITY, bv = -INFINITY;
+  int bi = INT_MAX;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) mx = fmaxf(mx, v[u]);
+  for (int u = 0; u < kSlice / kSliceThreads; ++u) {
+    const int i = b + t + u * kSliceThreads;
+    mx = fmaxf(mx, v[u]);
+    if (i < e && (v[u] > bv || (v[u] == bv && i < bi))) bv = v[u], bi = i;
   }
   mx = wave_max(mx);
-  if ((t & 63) == 0) fmx[t >> 6] = mx;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+  }
+  if ((t & 63) == 0) sv[t >> 6] = bv, sx[t >> 6] = bi, sm[t >> 6] = mx;
   __syncthreads();
-  mx = fmx[0];
-  for (int i = 1; i < kSampleThreads / 64; ++i) mx = fmaxf(mx, fmx[i]);
+  if (t == 0) {
+    for (int w = 1; w < kSliceThreads / 64; ++w) {
+      if (sv[w] > bv || (sv[w] == bv && sx[w] < bi)) bv = sv[w], bi = sx[w];
+      mx = fmaxf(mx, sm[w]);
+    }
+    a.smax[size_t(row) * a.slices + sl] = mx;
+    a.sbest[size_t(row) * a.slices + sl] = bv;
+    a.sbi[size_t(row) * a.slices + sl] = bi;
+  }
+}
+
+// The first largest over the slices (a NaN in element 0, or no element above -inf that is not NaN, gives 0).
+__global__ void __launch_bounds__(64) argmax_pick_kernel(const SampleArgs a) {
+  const int row = int(blockIdx.x), t = int(threadIdx.x);
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  for (int s = t; s < a.slices; s += 64) {
+    const float v = a.sbest[size_t(row) * a.slices + s];
+    const int i = a.sbi[size_t(row) * a.slices + s];
+    if (i != INT_MAX && (v > bv || (v == bv && i < bi))) bv = v, bi = i;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (oi != INT_MAX && (ov > bv || (ov == bv && oi < bi) || bi == INT_MAX)) bv = ov, bi = oi;
+  }
+  if (t == 0) {
+    const float x0 = a.logits[size_t(row) * size_t(a.n)];
+    a.out[row] = (x0 != x0 || bi == INT_MAX) ? 0 : bi;
+  }
+}
+
+// The slice's weights w = expf((l - max) * (1 / T)) (max over every slice), their sum in a fixed order, the count
+// and mass at or above the min_p floor (min_p * w_max, w_max = exp(0) = 1), and (with a filter) every thread's two
+// most likely pairs: the 64 largest of the threads' first ones in candidate order (256 sorted in LDS) and the
+// largest of their second ones. Any weight of the slice at or above a threshold above both is one of those 64.
+__global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const SampleArgs a) {
+  __shared__ float cw[kSliceThreads];
+  __shared__ int ci[kSliceThreads];
+  __shared__ double dred[kSliceThreads / 64][2];
+  __shared__ int ired[kSliceThreads / 64];
+  __shared__ float m2red[kSliceThreads / 64];
+  const int row = int(blockIdx.y), sl = int(blockIdx.x), t = int(threadIdx.x);
+  const float* l = a.logits + size_t(row) * size_t(a.n);
+  float* w = a.w + size_t(row) * size_t(a.n);
+  const int b = sl * kSlice, e = min(a.n, b + kSlice);
+  float mx = -INFINITY;
+  for (int s = 0; s < a.slices; ++s) mx = fmaxf(mx, a.smax[size_t(row) * a.slices + s]);
   const float inv_t = 1.f / a.temperature;
   const float floor_w = a.min_p * 1.0f;
-  float tw[kTop];
-  int ti[kTop];
+  float v[kSlice / kSliceThreads];
 #pragma unroll
-  for (int q = 0; q < kTop; ++q) tw[q] = -1.f, ti[q] = INT_MAX;
-  double s = 0.0, sfl = 0.0;
-  int nfl = 0;
-  for (int i0 = t; i0 < n; i0 += 8 * kSampleThreads) {
-    float v[8];
+  for (int u = 0; u < kSlice / kSliceThreads; ++u) {
+    const int i = b + t + u * kSliceThreads;
+    v[u] = i < e ? l[i] : 0.f;
+  }
+  double s = 0.0, sf = 0.0;
+  int nf = 0;
+  float w1 = -1.f, w2 = -1.f;
+  int i1 = INT_MAX, i2 = INT_MAX;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = i0 + u * kSampleThreads < n ? l[i0 + u * kSampleThreads] : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-    const int i = i0 + u * kSampleThreads;
-    if (i >= n) break;
-    const float x = expf((v[u] - mx) * inv_t);
-    w[i] = x;
-    s += double(x);
-    if (x >= floor_w) {
-      sfl += double(x);
-      ++nfl;
-    }
-    if (more_likely(x, i, tw[kTop - 1], ti[kTop - 1])) {   // insert, keeping the list in candidate order
-      float cwv = x;
-      int civ = i;
-#pragma unroll
-      for (int q = 0; q < kTop; ++q)
-        if (more_likely(cwv, civ, tw[q], ti[q])) {
-          const float tv = tw[q];
-          const int tiv = ti[q];
-          tw[q] = cwv;
-          ti[q] = civ;
-          cwv = tv;
-          civ = tiv;
-        }
-    }
+  for (int u = 0; u < kSlice / kSliceThreads; ++u) {
+    const int i = b + t + u * kSliceThreads;
+    if (i < e) {
+      const float x = expf((v[u] - mx) * inv_t);
+      w[i] = x;
+      s += double(x);
+      if (x >= floor_w) sf += double(x), ++nf;
+      if (more_likely(x, i, w1, i1)) {
+        w2 = w1, i2 = i1;
+        w1 = x, i1 = i;
+      } else if (more_likely(x, i, w2, i2)) {
+        w2 = x, i2 = i;
+      }
     }
   }
-  double total, t_floor;
-  block_exclusive(s, red, &total);
-  block_exclusive(sfl, red, &t_floor);
-  uint32_t n_floor;
-  block_exclusive<uint32_t>(uint32_t(nfl), ured, &n_floor);
-  __syncthreads();   // w complete
+  s = wave_sum_d(s);
+  sf = wave_sum_d(sf);
+  for (int o = 32; o >= 1; o >>= 1) nf += __shfl_xor(nf, o);
+  const float m2 = wave_max(w2);
+  if ((t & 63) == 0) dred[t >> 6][0] = s, dred[t >> 6][1] = sf, ired[t >> 6] = nf, m2red[t >> 6] = m2;
+  const size_t so = size_t(row) * a.slices + sl;
+  if (a.lists) {
+    cw[t] = w1;
+    ci[t] = i1;
+    for (int k = 2; k <= kSliceThreads; k <<= 1)
+      for (int jj = k >> 1; jj > 0; jj >>= 1) {
+        __syncthreads();
+        if (t < kSliceThreads / 2) {
+          const int lo = 2 * t - (t & (jj - 1)), hi = lo + jj;
+          const bool up = (lo & k) == 0;
+          const float wl = cw[lo], wh = cw[hi];
+          const int il = ci[lo], ih = ci[hi];
+          if (more_likely(wh, ih, wl, il) == up) {
+            cw[lo] = wh;
+            cw[hi] = wl;
+            ci[lo] = ih;
+            ci[hi] = il;
+          }
+        }
+      }
+    __syncthreads();
+    if (t < kSliceTop) {
+      a.sw[so * kSliceTop + t] = cw[t];
+      a.si[so * kSliceTop + t] = ci[t];
+    }
+  } else {
+    __syncthreads();
+  }
+  if (t == 0) {
+    double ts = 0.0, tf = 0.0;
+    int tn = 0;
+    float tm2 = -1.f;
+    for (int q = 0; q < kSliceThreads / 64; ++q)
+      ts += dred[q][0], tf += dred[q][1], tn += ired[q], tm2 = fmaxf(tm2, m2red[q]);
+    a.ssum[so] = ts;
+    a.sfl[so] = tf;
+    a.snfl[so] = tn;
+    a.sm2[so] = tm2;
+  }
+}
+
+// One work-group per row: the slices' sums in order, then the walk (index order, no filter) or the filters over
+// the candidates in order (sampler.cpp:44-94).
+__global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const SampleArgs a) {
+  __shared__ double red[kSampleThreads / 64 + 4];   // >= 20
+  __shared__ uint32_t ured[kSampleThreads / 64 + 1];
+  __shared__ uint32_t hist[16 * kSampleThreads];   // the whole-row sort's digit counts
+  __shared__ float cw[kCand];
+  __shared__ int ci[kCand];
+  __shared__ int sel, ccount, slices_ok;
+  __shared__ float tau_s;
+  __shared__ double base_s;
+  const int row = int(blockIdx.x), t = int(threadIdx.x), n = a.n, S = a.slices;
+  const float* w = a.w + size_t(row) * size_t(n);
+  const size_t so = size_t(row) * S;
+  const float floor_w = a.min_p * 1.0f;
+
+  // totals over the row: slice by slice, in order
+  if (t == 0) {
+    double tot = 0.0, tf = 0.0;
+    int nf = 0;
+    for (int q = 0; q < S; ++q) tot += a.ssum[so + q], tf += a.sfl[so + q], nf += a.snfl[so + q];
+    red[0] = tot;
+    red[1] = tf;
+    ccount = nf;
+  }
+  __syncthreads();
+  double total = red[0];
+  const double t_floor = red[1];
+  const int n_floor = ccount;
+  __syncthreads();
 
   const bool topk = a.top_k > 0 && a.top_k < n;
   if (!topk && a.top_p >= 1.f && a.min_p <= 0.f) {   // no filter: the candidates in index order
+    const double r = a.u[row] * total;
+    if (t == 0) {   // the slice where the running sum passes r, and the running sum before it
+      double c = 0.0;
+      int q = 0;
+      while (q < S - 1 && !(c + a.ssum[so + q] > r)) c += a.ssum[so + q++];
+      sel = q;
+      base_s = c;
+    }
+    __syncthreads();
+    const int q = sel;
+    const double c0 = base_s;
+    const int b = q * kSlice, len = min(n, b + kSlice) - b;
     double at;
-    const int i = first_crossing([&](int j) { return w[j]; }, n, a.u[row] * total, true, red, &sel, &at);
-    if (t == 0) a.out[row] = i < n ? i : n - 1;
+    const int i = first_crossing([&](int j) { return w[b + j]; }, len, r, true, red, &sel, &at, c0);
+    if (t == 0) a.out[row] = b + (i < len ? i : len - 1);   // past every crossing: the slice's (the row's) last
     return;
   }
 
-  // tau from the union of the threads' top 4 (sorted): the kept prefix lies at or above it
-#pragma unroll
-  for (int q = 0; q < kTop; ++q) {
-    cw[t * kTop + q] = tw[q];
-    ci[t * kTop + q] = ti[q];
-  }
-  sort_pairs(cw, ci, kCand);
-  if (t == 0) {
-    float tau = 0.f;
-    bool ok = true;
-    if (topk) {
-      ok = a.top_k <= kCand && cw[a.top_k - 1] >= 0.f;
-      tau = ok ? cw[a.top_k - 1] : 0.f;
-    } else {
-      if (a.top_p < 1.f) {
-        const double target = total * double(a.top_p) * (1.0 + 1e-6);
-        double c = 0.0;
-        int q = 0;
-        while (q < kCand && cw[q] >= 0.f && c < target) c += double(cw[q++]);
-        ok = c >= target;
-        tau = ok ? cw[q - 1] : 0.f;
-      }
-      if (a.min_p > 0.f) tau = fmaxf(tau, floor_w);
+  // tau from the slices' 64 most likely (their union, sorted): the kept prefix lies at or above it
+  const int U = S * kSliceTop;
+  int nc = INT_MAX;
+  float tau = -1.f;
+  if (U <= kCand) {
+    int n2 = 1;
+    while (n2 < U) n2 <<= 1;
+    for (int q = t; q < n2; q += kSampleThreads) {
+      cw[q] = q < U ? a.sw[so * kSliceTop + q] : -1.f;
+      ci[q] = q < U ? a.si[so * kSliceTop + q] : INT_MAX;
     }
-    tau_s = ok ? tau : -1.f;   // -1: no bound from the union
-    ccount = 0;
-  }
-  __syncthreads();
-  const float tau = tau_s;
-  // gather the candidates w >= tau (order-free: they are sorted next)
-  if (tau >= 0.f) {
-    for (int i0 = t; i0 < n; i0 += 8 * kSampleThreads) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = i0 + u * kSampleThreads < n ? w[i0 + u * kSampleThreads] : -1.f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (v[u] >= tau) {
-          const int pos = atomicAdd(&ccount, 1);
-          if (pos < kCand) {
-            cw[pos] = v[u];
-            ci[pos] = i0 + u * kSampleThreads;
-          }
+    sort_pairs(cw, ci, n2);
+    int qp = -1;   // top_p: the union's first position whose running mass reaches total * top_p * (1 + 1e-6)
+    if (!topk && a.top_p < 1.f) {
+      double at_unused;
+      const double target = total * double(a.top_p) * (1.0 + 1e-6);
+      qp = first_crossing([&](int j) { return fmaxf(cw[j], 0.f); }, U, target, false, red, &sel, &at_unused);
+    }
+    if (t == 0) {
+      float tv = 0.f;
+      bool ok = true;
+      if (topk) {
+        ok = a.top_k <= U && cw[a.top_k - 1] >= 0.f;
+        tv = ok ? cw[a.top_k - 1] : 0.f;
+      } else {
+        if (a.top_p < 1.f) {
+          ok = qp < U && cw[qp] >= 0.f;
+          tv = ok ? cw[qp] : 0.f;
         }
+        if (a.min_p > 0.f) tv = fmaxf(tv, floor_w);
+      }
+      tau_s = ok ? tv : -1.f;
+      slices_ok = 1;
+    }
+    __syncthreads();
+    tau = tau_s;
+    // every weight >= tau is a listed thread maximum when, in every slice, the 64th listed maximum and every
+    // thread's second most likely lie below tau
+    if (tau >= 0.f)
+      for (int q = t; q < S; q += kSampleThreads) {
+        const float last = a.sw[(so + q) * kSliceTop + kSliceTop - 1];
+        const float m2 = a.sm2[so + q];
+        if (!(last < tau) || !(m2 < tau)) slices_ok = 0;   // ties or runs at tau may continue past the lists
+      }
+    __syncthreads();
+    if (tau >= 0.f && slices_ok) {   // the candidates: the union's prefix at or above tau, already in order
+      if (t == 0) sel = U;
+      __syncthreads();
+      for (int q = t; q < U; q += kSampleThreads)
+        if (!(cw[q] >= tau)) atomicMin(&sel, q);
+      __syncthreads();
+      nc = sel;
+      __syncthreads();
     }
   }
-  __syncthreads();
-  const int nc = tau >= 0.f ? ccount : INT_MAX;
-  __syncthreads();
-
   const float* sw_l = cw;
   const int* si_l = ci;
   const uint32_t* ksrc = nullptr;
   const int* isrc = nullptr;
   int L;   // candidates available in order
-  if (nc <= kCand) {
-    int n2 = 1;
-    while (n2 < nc) n2 <<= 1;
-    for (int q = nc + t; q < n2; q += kSampleThreads) {
-      cw[q] = -1.f;
-      ci[q] = INT_MAX;
-    }
-    sort_pairs(cw, ci, n2);
+  if (nc != INT_MAX) {
     L = nc;
   } else {
-    // the whole row, stably sorted by (~bits(w), index), 4 bits a pass, contiguous chunks per thread
-    uint32_t* k0 = a.keys + size_t(row) * 2 * size_t(n);
-    uint32_t* k1 = k0 + n;
-    int* i0 = a.idx + size_t(row) * 2 * size_t(n);
-    int* i1 = i0 + n;
-    const int chunk = (n + kSampleThreads - 1) / kSampleThreads;
-    const int b = min(n, t * chunk), e = min(n, b + chunk);
-    uint32_t* kr = k0;
-    int* ir = i0;
-    uint32_t* kw = k1;
-    int* iw = i1;
-    for (int pass = 0; pass < 8; ++pass) {
-      const int sh = 4 * pass;
-      uint32_t cnt[16];
+    // gather every weight >= tau from the row (order-free, then sorted), or sort the whole row
+    if (t == 0) ccount = 0;
+    __syncthreads();
+    if (tau >= 0.f) {
+      for (int i0 = t; i0 < n; i0 += 8 * kSampleThreads) {
+        float v[8];
 #pragma unroll
-      for (int d = 0; d < 16; ++d) cnt[d] = 0;
-      for (int i = b; i < e; ++i) {
-        const uint32_t key = pass == 0 ? ~__float_as_uint(w[i]) : kr[i];
-        const uint32_t dg = (key >> sh) & 15u;
+        for (int u = 0; u < 8; ++u) v[u] = i0 + u * kSampleThreads < n ? w[i0 + u * kSampleThreads] : -1.f;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) cnt[d] += dg == uint32_t(d) ? 1u : 0u;
+        for (int u = 0; u < 8; ++u)
+          if (v[u] >= tau) {
+            const int pos = atomicAdd(&ccount, 1);
+            if (pos < kCand) {
+              cw[pos] = v[u];
+              ci[pos] = i0 + u * kSampleThreads;
+            }
+          }
       }
-      __syncthreads();   // hist free (the previous pass's scatter is done reading it)
-#pragma unroll
-      for (int d = 0; d < 16; ++d) hist[d * kSampleThreads + t] = cnt[d];
-      __syncthreads();
-      // exclusive scan of hist in (digit, thread) order: thread t owns entries 16 t .. 16 t + 15
-      uint32_t part = 0;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) part += hist[16 * t + q];
-      uint32_t tot_unused;
-      uint32_t run = block_exclusive<uint32_t>(part, ured, &tot_unused);
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const uint32_t c = hist[16 * t + q];
-        hist[16 * t + q] = run;
-        run += c;
-      }
-      __syncthreads();
-      uint32_t off[16];
-#pragma unroll
-      for (int d = 0; d < 16; ++d) off[d] = hist[d * kSampleThreads + t];
-      for (int i = b; i < e; ++i) {
-        const uint32_t key = pass == 0 ? ~__float_as_uint(w[i]) : kr[i];
-        const int id = pass == 0 ? i : ir[i];
-        const uint32_t dg = (key >> sh) & 15u;
-        uint32_t dst = 0;
-#pragma unroll
-        for (int d = 0; d < 16; ++d)
-          if (dg == uint32_t(d)) dst = off[d]++;
-        kw[dst] = key;
-        iw[dst] = id;
-      }
-      __syncthreads();   // the pass's output is complete before the next reads it
-      uint32_t* kt = kr;
-      kr = kw;
-      kw = pass == 0 ? k0 : kt;
-      int* it = ir;
-      ir = iw;
-      iw = pass == 0 ? i0 : it;
     }
-    ksrc = kr;
-    isrc = ir;
-    L = n;
+    __syncthreads();
+    nc = tau >= 0.f ? ccount : INT_MAX;
+    __syncthreads();
+    if (nc <= kCand) {
+      int n2 = 1;
+      while (n2 < nc) n2 <<= 1;
+      for (int q = nc + t; q < n2; q += kSampleThreads) {
+        cw[q] = -1.f;
+        ci[q] = INT_MAX;
+      }
+      sort_pairs(cw, ci, n2);
+      L = nc;
+    } else {
+      // the whole row, stably sorted by (~bits(w), index), 4 bits a pass, contiguous chunks per thread
+      uint32_t* k0 = a.keys + size_t(row) * 2 * size_t(n);
+      uint32_t* k1 = k0 + n;
+      int* i0 = a.idx + size_t(row) * 2 * size_t(n);
+      int* i1 = i0 + n;
+      const int chunk = (n + kSampleThreads - 1) / kSampleThreads;
+      const int b = min(n, t * chunk), e = min(n, b + chunk);
+      uint32_t* kr = k0;
+      int* ir = i0;
+      uint32_t* kw = k1;
+      int* iw = i1;
+      for (int pass = 0; pass < 8; ++pass) {
+        const int sh = 4 * pass;
+        uint32_t cnt[16];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) cnt[d] = 0;
+        for (int i = b; i < e; ++i) {
+          const uint32_t key = pass == 0 ? ~__float_as_uint(w[i]) : kr[i];
+          const uint32_t dg = (key >> sh) & 15u;
+#pragma unroll
+          for (int d = 0; d < 16; ++d) cnt[d] += dg == uint32_t(d) ? 1u : 0u;
+        }
+        __syncthreads();   // hist free (the previous pass's scatter is done reading it)
+#pragma unroll
+        for (int d = 0; d < 16; ++d) hist[d * kSampleThreads + t] = cnt[d];
+        __syncthreads();
+        // exclusive scan of hist in (digit, thread) order: thread t owns entries 16 t .. 16 t + 15
+        uint32_t part = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) part += hist[16 * t + q];
+        uint32_t tot_unused;
+        uint32_t run = block_exclusive<uint32_t>(part, ured, &tot_unused);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const uint32_t c = hist[16 * t + q];
+          hist[16 * t + q] = run;
+          run += c;
+        }
+        __syncthreads();
+        uint32_t off[16];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) off[d] = hist[d * kSampleThreads + t];
+        for (int i = b; i < e; ++i) {
+          const uint32_t key = pass == 0 ? ~__float_as_uint(w[i]) : kr[i];
+          const int id = pass == 0 ? i : ir[i];
+          const uint32_t dg = (key >> sh) & 15u;
+          uint32_t dst = 0;
+#pragma unroll
+          for (int d = 0; d < 16; ++d)
+            if (dg == uint32_t(d)) dst = off[d]++;
+          kw[dst] = key;
+          iw[dst] = id;
+        }
+        __syncthreads();   // the pass's output is complete before the next reads it
+        uint32_t* kt = kr;
+        kr = kw;
+        kw = pass == 0 ? k0 : kt;
+        int* it = ir;
+        ir = iw;
+        iw = pass == 0 ? i0 : it;
+      }
+      ksrc = kr;
+      isrc = ir;
+      L = n;
+    }
   }
   auto sw = [&](int j) { return ksrc ? __uint_as_float(~ksrc[j]) : sw_l[j]; };
   auto sidx = [&](int j) { return ksrc ? isrc[j] : si_l[j]; };
@@ -484,8 +654,8 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(const SampleArgs
       k = sel == INT_MAX ? lim : sel;
       __syncthreads();
       first_crossing(sw, k, INFINITY, true, red, &sel, &tk);
-    } else {   // every weight >= floor: counted over the row in the weight pass
-      k = int(n_floor);
+    } else {   // every weight >= floor: counted over the row with the weights
+      k = n_floor;
       tk = t_floor;
     }
     keep = max(1, k);
@@ -503,31 +673,91 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(const SampleArgs
   if (t == 0) a.out[row] = sidx(i < lim ? i : lim - 1);
 }
 
-size_t sample_scratch_bytes(int rows, int n) { return size_t(rows) * size_t(n) * (sizeof(float) + 4 * sizeof(uint32_t)); }
+namespace {
+struct SampleScratch {
+  size_t w, smax, sbest, sbi, ssum, sfl, snfl, sw, si, sm2, keys, idx, total;
+};
+SampleScratch scratch_layout(int rows, int n) {
+  const size_t S = size_t((n + kSlice - 1) / kSlice), R = size_t(rows), N = size_t(n);
+  SampleScratch o{};
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t p = at;
+    at += (bytes + 255) / 256 * 256;
+    return p;
+  };
+  o.ssum = take(R * S * 8);
+  o.sfl = take(R * S * 8);
+  o.w = take(R * N * 4);
+  o.smax = take(R * S * 4);
+  o.sbest = take(R * S * 4);
+  o.sbi = take(R * S * 4);
+  o.snfl = take(R * S * 4);
+  o.sw = take(R * S * kSliceTop * 4);
+  o.si = take(R * S * kSliceTop * 4);
+  o.sm2 = take(R * S * 4);
+  o.keys = take(R * 2 * N * 4);
+  o.idx = take(R * 2 * N * 4);
+  o.total = at;
+  return o;
+}
+
+SampleArgs sample_args(const float* logits, int rows, int n, void* scratch, int* out) {
+  const SampleScratch o = scratch_layout(rows, n);
+  char* base = static_cast<char*>(scratch);
+  SampleArgs a{};
+  a.logits = logits;
+  a.n = n;
+  a.slices = (n + kSlice - 1) / kSlice;
+  a.w = reinterpret_cast<float*>(base + o.w);
+  a.smax = reinterpret_cast<float*>(base + o.smax);
+  a.sbest = reinterpret_cast<float*>(base + o.sbest);
+  a.sbi = reinterpret_cast<int*>(base + o.sbi);
+  a.ssum = reinterpret_cast<double*>(base + o.ssum);
+  a.sfl = reinterpret_cast<double*>(base + o.sfl);
+  a.snfl = reinterpret_cast<int*>(base + o.snfl);
+  a.sw = reinterpret_cast<float*>(base + o.sw);
+  a.si = reinterpret_cast<int*>(base + o.si);
+  a.sm2 = reinterpret_cast<float*>(base + o.sm2);
+  a.keys = reinterpret_cast<uint32_t*>(base + o.keys);
+  a.idx = reinterpret_cast<int*>(base + o.idx);
+  a.out = out;
+  return a;
+}
+}  // namespace
+
+size_t sample_scratch_bytes(int rows, int n) { return scratch_layout(rows, n).total; }
 
 std::string launch_sample(const float* logits, int rows, int n, float temperature, float top_p, int top_k,
                           float min_p, const double* u, int* out, void* scratch, hipStream_t stream) {
   XTG_CHECK(rows >= 1 && rows <= kMaxSampleRows, "sample: %d rows (1..%d)", rows, kMaxSampleRows);
   XTG_CHECK(n >= 1, "sample: %d logits", n);
   XTG_CHECK(temperature > 0.f, "sample: temperature %g (greedy decoding is argmax)", double(temperature));
-  SampleArgs a{};
-  a.logits = logits;
-  a.n = n;
+  SampleArgs a = sample_args(logits, rows, n, scratch, out);
   a.temperature = temperature;
   a.top_p = top_p;
   a.min_p = min_p;
   a.top_k = top_k;
+  a.lists = (top_k > 0 && top_k < n) || top_p < 1.f || min_p > 0.f ? 1 : 0;
   for (int r = 0; r < rows; ++r) {
     XTG_CHECK(u[r] >= 0.0 && u[r] < 1.0, "sample: draw %g outside [0, 1)", u[r]);
     a.u[r] = u[r];
   }
-  a.w = static_cast<float*>(scratch);
-  a.keys = reinterpret_cast<uint32_t*>(a.w + size_t(rows) * size_t(n));
-  a.idx = reinterpret_cast<int*>(a.keys + size_t(rows) * 2 * size_t(n));
-  a.out = out;
-  hipLaunchKernelGGL(sample_kernel, dim3(unsigned(rows)), dim3(kSampleThreads), 0, stream, a);
+  const dim3 sg{unsigned(a.slices), unsigned(rows)};
+  hipLaunchKernelGGL(slice_max_kernel, sg, dim3(kSliceThreads), 0, stream, a);
+  hipLaunchKernelGGL(slice_weights_kernel, sg, dim3(kSliceThreads), 0, stream, a);
+  hipLaunchKernelGGL(sample_pick_kernel, dim3(unsigned(rows)), dim3(kSampleThreads), 0, stream, a);
   HIP_CHECK(hipGetLastError());
-  return "sample_kernel";
+  return "sample_pick_kernel";
+}
+
+std::string launch_argmax_slices(const float* logits, int rows, int n, int* out, void* scratch, hipStream_t stream) {
+  XTG_CHECK(rows >= 1 && rows <= kMaxSampleRows && n >= 1, "argmax: %d rows of %d", rows, n);
+  const SampleArgs a = sample_args(logits, rows, n, scratch, out);
+  hipLaunchKernelGGL(slice_max_kernel, dim3(unsigned(a.slices), unsigned(rows)), dim3(kSliceThreads), 0, stream, a);
+  hipLaunchKernelGGL(argmax_pick_kernel, dim3(unsigned(rows)), dim3(64), 0, stream, a);
+  HIP_CHECK(hipGetLastError());
+  return "argmax_pick_kernel";
 }
 
 }  // namespace xtg::hip
