@@ -1177,21 +1177,24 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
       for (int e = 0; e < 8; ++e) t[u][e] = 0.f;
     }
   }
-  float s = 0.f;
+  float s = 0.f, mx = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       t[u][e] = t[u][e] * (1.f / (1.f + expf(-gv[u][e] * sv[u][e])));
       s += t[u][e] * t[u][e];
+      mx = fmaxf(mx, fabsf(t[u][e]));
     }
-  const float f = inv_norm_of(block_sum<kMergeThreads>(s, red));
+  // the largest magnitude rides with the sum: max |t f| = fl(max |t| * f) for f > 0
+  block_sum_max<kMergeThreads>(s, mx, red);
+  const float f = inv_norm_of(s);
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[u][e] *= f;
   if (out) store_row<kMergeThreads, U>(out + size_t(row) * Q, Q, vec, t);
-  if (xop) emit_operand<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, red);
+  if (xop) emit_operand_mx<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, mx * f);
 }
 
 // ------------------------------------------------------------------------------------------------------- plan

@@ -102,6 +102,26 @@ __device__ inline float block_max(float v, float* red) {
   return s;
 }
 
+// A sum and a max over the work-group in one exchange; every thread gets both.
+template <int NT>
+__device__ inline void block_sum_max(float& s, float& m, float* red) {
+  s = wave_sum(s);
+  m = wave_max(m);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = s;
+    red[NT / 64 + (threadIdx.x >> 6)] = m;
+  }
+  __syncthreads();
+  s = 0.f;
+  m = red[NT / 64];
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) {
+    s += red[i];
+    m = fmaxf(m, red[NT / 64 + i]);
+  }
+}
+
 // justnorm's factor: x / sqrt(sum x^2 + 1e-6) as x * (1 / sqrt(...)) (engine/src/kernels.cpp:162-175)
 __device__ inline float inv_norm_of(float sumsq) { return 1.f / sqrtf(sumsq + 1e-6f); }
 
@@ -175,19 +195,14 @@ __device__ inline int operand_exponent(float mx) {
 // Row `row` of an operand of consecutive 8-row groups `stride` bytes apart (xop / xinv: group 0's operand and row
 // factors), from a row tile (values past w are zero): the work-group's max, then every chunk of the row's
 // kt = ceil(w / 128) k-tiles (zero chunks past w included). red: 2 * NT / 64 floats.
+// emit_operand with the row's largest magnitude mx already known (no reduction).
 template <int NT, int U>
-__device__ inline void emit_operand(const float (&v)[U][8], int w, int row, f16x8* xop, float* xinv, size_t stride,
-                                    float* red) {
+__device__ inline void emit_operand_mx(const float (&v)[U][8], int w, int row, f16x8* xop, float* xinv, size_t stride,
+                                       float mx) {
   const size_t off = size_t(row / kMaxRows) * stride;
   xop = reinterpret_cast<f16x8*>(reinterpret_cast<char*>(xop) + off);
   xinv = reinterpret_cast<float*>(reinterpret_cast<char*>(xinv) + off);
   const int j = row % kMaxRows;
-  float mx = 0.f;
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[u][e]));
-  mx = block_max<NT>(mx, red);
   const int ex = operand_exponent(mx);
   const float up = ldexpf(1.f, ex);
   if (threadIdx.x == 0) xinv[j] = ldexpf(1.f, -ex);
@@ -199,6 +214,17 @@ __device__ inline void emit_operand(const float (&v)[U][8], int w, int row, f16x
   }
   const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int c = int(threadIdx.x) + U * NT; c < chunks; c += NT) store_chunk(xop, j, c, zero, up);
+}
+
+template <int NT, int U>
+__device__ inline void emit_operand(const float (&v)[U][8], int w, int row, f16x8* xop, float* xinv, size_t stride,
+                                    float* red) {
+  float mx = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[u][e]));
+  emit_operand_mx<NT, U>(v, w, row, xop, xinv, stride, block_max<NT>(mx, red));
 }
 
 }  // namespace xtg::hip

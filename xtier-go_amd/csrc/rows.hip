@@ -58,17 +58,27 @@ __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q,
   }
 }
 
-// The normalised row t * f: written to out (if any) and as operand row j (if any).
+// The normalised row t * f: written to out (if any) and as operand row j (if any). The row's largest magnitude
+// rides with the norm's sum: scaling by f > 0 is monotone under rounding, so max |t f| = fl(max |t| * f) exactly,
+// and one exchange serves both.
 template <int U>
 __device__ inline void finish_row(float (&t)[U][8], float sumsq, int w, bool vec, float* out, f16x8* xop, float* xinv,
                                   size_t ostride, float* red) {
-  const float f = inv_norm_of(block_sum<kNormThreads>(sumsq, red));
+  float mx = 0.f;
+  if (xop) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(t[u][e]));
+  }
+  block_sum_max<kNormThreads>(sumsq, mx, red);
+  const float f = inv_norm_of(sumsq);
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) t[u][e] *= f;
   if (out) store_row<kNormThreads, U>(out, w, vec, t);
-  if (xop) emit_operand<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, ostride, red);
+  if (xop) emit_operand_mx<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, ostride, mx * f);
 }
 
 template <int U>
