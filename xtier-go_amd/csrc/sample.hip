@@ -511,7 +511,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
       for (int q = t; q < S; q += kSampleThreads) {
         const float last = a.sw[(so + q) * kSliceTop + kSliceTop - 1];
         const float m2 = a.sm2[so + q];
-        if (!(last < tau) || !(m2 < tau)) slices_ok = 0;   // ties or runs at tau may continue past the lists
+        if (!(last < tau) || !(m2 < tau)) atomicAnd(&slices_ok, 0);   // ties or runs at tau may continue past the lists
       }
     __syncthreads();
     if (tau >= 0.f && slices_ok) {   // the candidates: the union's prefix at or above tau, already in order
