@@ -191,7 +191,8 @@ int xtg_hip_add_norm(xtg_hip* h, const float* a, const float* b, float* out, int
                      int err_len);
 /* xtg::argmax (engine/include/xtg/sampler.h:29, engine/src/sampler.cpp:8-13), greedy decoding's token, per row of
  * device logits [rows][n] into device out [rows] (int32): the first index of the largest value; NaNs never win, and
- * a NaN in element 0 gives 0, as the reference's scan does. Queued. */
+ * a NaN in element 0 gives 0, as the reference's scan does. Queued. Up to 8 rows of more than 4096 logits use
+ * scratch memory that the first call of a shape sizes: make that call before a graph capture. */
 int xtg_hip_argmax(xtg_hip* h, const float* logits, int rows, int n, int32_t* out, char* err, int err_len);
 /* xtg::SamplingParams (engine/include/xtg/sampler.h:11-16), field for field. */
 typedef struct xtg_sampling {
@@ -205,7 +206,8 @@ typedef struct xtg_sampling {
  * value the reference's std::uniform_real_distribution<double>(0, total) scales by the total, i.e.
  * std::generate_canonical<double, 53>(rng) from the Sampler's std::mt19937_64 (one draw per sampled row, none when
  * temperature <= 0, which is argmax). Candidates are ordered by weight then index over the whole row, as the
- * reference orders them wherever its result is defined. Queued. */
+ * reference orders them wherever its result is defined. Queued; the first call of a shape sizes scratch memory
+ * (make it before a graph capture). */
 int xtg_hip_sample(xtg_hip* h, const float* logits, int rows, int n, const xtg_sampling* p, const double* u,
                    int32_t* out, char* err, int err_len);
 
