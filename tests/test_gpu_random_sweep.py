@@ -71,3 +71,45 @@ def test_random_sweep(hip, pkg, orc, wl):
                 if got[r] != want[r] and not margin[r] < 1e-6:
                     fails.append(("sample", rows, n, p, r, int(got[r]), int(want[r]), float(margin[r])))
     assert not fails, fails[:5]
+
+
+@pytest.mark.gpu
+def test_random_dory_configs(hip, orc, wl):
+    """The decode-step composition over random small configurations -- widths, head layouts (4/2, 8/2, 2/1, 4/4,
+    8/1 of 64 or 128), windows of 8-48 in rings of 4-64 slots more (some too short to store before the scan), one
+    or two loops, BF16 or FP8 caches -- through random calls: chunks of up to 40 rows, then steps of 1-8. Every
+    call's logits against the oracle's composition: rel-L2 <= 1e-3 and the same argmax per row."""
+    rng = np.random.default_rng(20261203)
+    fails = []
+    for _ in range(25):
+        heads, kvh = [(4, 2), (8, 2), (2, 1), (4, 4), (8, 1)][int(rng.integers(0, 5))]
+        window = int(rng.choice([8, 16, 48]))
+        cfg = dict(hidden=int(rng.choice([128, 256, 384])), ffn=int(rng.choice([256, 384, 512])), heads=heads,
+                   kv_heads=kvh, head_dim=int(rng.choice([64, 128])), vocab=int(rng.choice([500, 1000, 3000])),
+                   n_in=2, n_rec=int(rng.choice([2, 4])), n_out=2, loops=int(rng.integers(1, 3)), window=window,
+                   ring_slots=window + int(rng.choice([4, 16, 64])), theta_sliding=1e4, theta_full=1e6,
+                   kv_dtype=int(rng.integers(0, 2)))
+        context = 192
+        w = wl.DoryWeights(cfg, seed=int(rng.integers(0, 1 << 30)), context=context)
+        ref = orc.Dory(w, wl)
+        dev = hip.dory(w)
+        H, V = cfg["hidden"], cfg["vocab"]
+        dx, dl = hip.array(shape=(64, H)), hip.array(shape=(64, V))
+        pos = 0
+        seq = [int(rng.integers(1, 41)) for _ in range(int(rng.integers(1, 4)))] + \
+              [int(rng.integers(1, 9)) for _ in range(6)]
+        for m in seq:
+            x = rng.standard_normal((m, H)).astype(np.float32)
+            x /= np.linalg.norm(x, axis=1, keepdims=True)
+            dx.upload(np.concatenate([x, np.zeros((64 - m, H), np.float32)]))
+            dev.forward(dx, m, pos, dl)
+            got = dl.numpy()[:m]
+            want = ref.forward(x, pos)
+            e = float(np.linalg.norm(got.astype(np.float64) - want) / np.linalg.norm(want.astype(np.float64)))
+            if not (e <= 1e-3 and (got.argmax(1) == want.argmax(1)).all()):
+                fails.append((cfg, pos, m, e))
+            pos += m
+        dx.free()
+        dl.free()
+        dev.destroy()
+    assert not fails, fails[:3]
