@@ -107,6 +107,37 @@ def test_4b_decode_step(hip, model_4b, m):
     assert (got.argmax(1) == want.argmax(1)).all()
 
 
+@pytest.fixture(scope="module")
+def model_4b_32k(hip, orc, wl):
+    ctx = 32768
+    w = wl.DoryWeights(wl.DORY_4B, seed=8, context=ctx + 64)
+    ref = orc.Dory(w, wl)
+    dev = hip.dory(w)
+    fill_context(w, ctx, ref, dev, hip, np.random.default_rng(9))
+    yield w, ref, dev, ctx
+    dev.destroy()
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_4b_decode_step_32k(hip, model_4b_32k, m):
+    """Config 4 at a 32K context (the benchmark's longest): 32 splits per KV head on the global layers, the
+    sliding rings wrapped many times over."""
+    w, ref, dev, ctx = model_4b_32k
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(70 + m), m, H)
+    dx = hip.array(x)
+    dl = hip.array(shape=(m, V))
+    dev.forward(dx, m, ctx, dl)
+    got = dl.numpy()
+    want = ref.forward(x, ctx, threads=16)
+    dx.free()
+    dl.free()
+    e = rel_l2(got, want)
+    print("4B step at 32K m=%d: logits rel-L2 %.2e" % (m, e))
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
 def test_4b_graph_replay_matches_eager(hip, model_4b):
     """A captured step replays the eager step exactly, replay after replay, with eager work in between."""
     w, ref, dev, ctx = model_4b
