@@ -12,7 +12,8 @@
 //    Each k-tile (128 inputs) the work-group stages the groups' operand tile (4 KiB each) in LDS, double-buffered,
 //    in lane order (contiguous 16-byte writes and reads); each wave dequantises its RB weight tiles once and runs
 //    them against all GB groups: 4 RB GB matrix ops per k-tile per wave. The next k-tile's loads go out into
-//    registers before the current one's math and are written to LDS after it, one barrier per k-tile. (Direct
+//    registers before the current one's math and are written to LDS after it, one barrier per k-tile; within a
+//    k-tile, each 32-input step's operand fragments are read from LDS during the previous step's matrix ops. (Direct
 //    global-to-LDS loads would save those registers, but the compiler then waits for them before every LDS read
 //    of the current buffer, serialising the pipeline.)
 //  - Tiles are dealt so that work-group i, which runs on XCD i mod 8, gets a contiguous run of tiles: the
@@ -126,17 +127,29 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
     const XTile<GB> xn = load_x<GB>(a.op, a.op_stride, a.groups, g0, nxt, wave, lane);
     const WTile<RB> wn = load_w<RB>(tiles, nb, KT, rb0, nxt, lane);
     __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the math (the scheduler would sink them to their use)
+    // step s + 1's operand fragments are read from LDS while step s's matrix ops run (read just before their
+    // use, each pair of matrix ops would wait out an LDS round trip)
+    f16x8 Bn[kTileGroups];
+#pragma unroll
+    for (int g = 0; g < kTileGroups; ++g) Bn[g] = __builtin_bit_cast(f16x8, xs[cur][g][0][lane]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      f16x8 B[kTileGroups];
+#pragma unroll
+      for (int g = 0; g < kTileGroups; ++g) B[g] = Bn[g];
+      if (s < 3) {
+#pragma unroll
+        for (int g = 0; g < kTileGroups; ++g) Bn[g] = __builtin_bit_cast(f16x8, xs[cur][g][s + 1][lane]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       f16x8 A[RB];
 #pragma unroll
       for (int r = 0; r < RB; ++r) A[r] = dequant8(w.c[r][s], scale_pair(w.s[r], s >> 1));
 #pragma unroll
-      for (int g = 0; g < kTileGroups; ++g) {
-        const f16x8 B = __builtin_bit_cast(f16x8, xs[cur][g][s][lane]);
+      for (int g = 0; g < kTileGroups; ++g)
 #pragma unroll
-        for (int r = 0; r < RB; ++r) acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], B, acc[r][g], 0, 0, 0);
-      }
+        for (int r = 0; r < RB; ++r)
+          acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], B[g], acc[r][g], 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < GB; ++i) xs[cur ^ 1][i][wave][lane] = xn.v[i];
@@ -196,12 +209,13 @@ std::string launch_gemm(const GemvCall& c, hipStream_t stream) {
   };
   // measured on MI355X over the 4B-shaped projections at 64 .. 2048 rows: four groups per tile throughout; two
   // row-blocks per wave (34 % of the dense f16 peak on gate/up at 512 rows), four only with thousands of tiles
-  // (2048-row chunks of the wide projections), one when two would leave most CUs idle
+  // (2048-row chunks of the wide projections), one with fewer than 512 tiles of two (the 3072-wide o and down
+  // projections at 512 rows: 45 and 79 us against 46 and 83 us with two)
   const int gb = 4;
-  const int rb = tiles_for(4, 4) >= 2048 ? 4 : tiles_for(2, 4) >= 128 ? 2 : 1;
+  const int rb = tiles_for(4, 4) >= 2048 ? 4 : tiles_for(2, 4) >= 512 ? 2 : 1;
   if (const char* env = std::getenv("XTG_GEMM_SHAPE")) {
     int r = 0, g = 0;
-    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && (r == 1 || r == 2 || r == 4) && g == 4)
+    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && gemm_fn(r, g) != nullptr)
       return run_gemm(c, r, g, stream);
   }
   return run_gemm(c, rb, gb, stream);
