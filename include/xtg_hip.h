@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define XTG_HIP_ABI_VERSION 1
+#define XTG_HIP_ABI_VERSION 2
 
 typedef struct xtg_hip xtg_hip;
 typedef struct xtg_hip_kv xtg_hip_kv;
@@ -47,6 +47,9 @@ typedef struct xtg_bf16 {
 
 enum { XTG_X_F32 = 0, XTG_X_BF16 = 1 };   /* activation element type of the device matmul */
 enum { XTG_KV_BF16 = 0, XTG_KV_FP8 = 1 }; /* xtg::KvDtype (engine/include/xtg/kv.h:18) */
+/* The recurrent sublayers' KV mode (the pack's kv_mode option, packs/dory/dory.cpp:150-151): per_loop keeps one cache
+ * per loop; last_loop keeps one cache that only the last loop writes (dory.cpp:534-537). */
+enum { XTG_KV_PER_LOOP = 0, XTG_KV_LAST_LOOP = 1 };
 
 /* ------------------------------------------------------------------------------------------------ backend */
 
@@ -68,7 +71,8 @@ void* xtg_hip_stream(xtg_hip* h);
 int xtg_hip_prepare_nvfp4(xtg_hip* h, const xtg_nvfp4* w, char* err, int err_len);
 /* Drops the device copy prepared for `codes` (a weight whose host memory is about to be freed or reused). The
  * reference frees its device weights only with the backend (opencl.cpp:349-353); callers that recycle host
- * buffers need this to keep the codes-pointer key unambiguous. 0 also when nothing was prepared for it. */
+ * buffers need this to keep the codes-pointer key unambiguous. 0 also when nothing was prepared for it; -1 while a
+ * Dory session runs on the weight. */
 int xtg_hip_release_nvfp4(xtg_hip* h, const uint8_t* codes, char* err, int err_len);
 /* The device tile layout prepare() made for the weight keyed by `codes` (16 rows x 128 inputs per 1152-byte tile:
  * 1024 bytes of codes, lane l's 16 at 16 l, then lane l's two scales at 1024 + 2 l), copied to host memory; bytes
@@ -104,7 +108,7 @@ int xtg_hip_matmul_nvfp4_op(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void
 /* Replaces OpenClBackend::prepare(const Bf16Weight&) (opencl.h:33, opencl.cpp:516-521): copy the weight to the
  * device in the GEMV tile layout. Idempotent, keyed by w->data. n_out > 0 and k % 4 == 0 (as opencl.cpp:519). */
 int xtg_hip_prepare_bf16(xtg_hip* h, const xtg_bf16* w, char* err, int err_len);
-/* Drops the device copy prepared for `data` (0 also when there is none). */
+/* Drops the device copy prepared for `data` (0 also when there is none; -1 while a Dory session runs on it). */
 int xtg_hip_release_bf16(xtg_hip* h, const uint16_t* data, char* err, int err_len);
 /* Replaces xtg::matmul_bf16(ThreadPool&, w, x, m, y) (kernels.h:31, kernels.cpp:140-155) and the host
  * OpenClBackend::matmul(const Bf16Weight&, x, m, y) (opencl.h:35, opencl.cpp:602-628): y[m][n_out] =
@@ -217,11 +221,12 @@ int xtg_hip_sample(xtg_hip* h, const float* logits, int rows, int n, const xtg_s
 enum { XTG_DORY_MLP = 0, XTG_DORY_SLIDING = 1, XTG_DORY_FULL = 2 };
 typedef struct xtg_dory_config {
   int hidden, ffn, heads, kv_heads, head_dim, vocab;
-  int n_in, n_rec, n_out, loops;   /* input / recurrent / output sublayers; recurrent passes (per_loop caches) */
+  int n_in, n_rec, n_out, loops;   /* input / recurrent / output sublayers; recurrent passes */
   int window, ring_slots;          /* sliding window and the ring size of a sliding sublayer's cache */
   int64_t context;                 /* capacity of a full-attention cache */
   float theta_sliding, theta_full; /* RoPE theta per kind */
   int kv_dtype;                    /* XTG_KV_BF16 or XTG_KV_FP8 (dory.cpp:141, 159-161) for every cache */
+  int kv_mode;                     /* XTG_KV_PER_LOOP or XTG_KV_LAST_LOOP */
 } xtg_dory_config;
 /* One physical sublayer (dory.cpp:332-364) with the scale vectors already folded as the model constructor does
  * (qscale = (sqk * sqrt(d) / init_range)^2, gscale likewise, sg / su times sqrt(hidden), lr = |alpha * alpha_init /
@@ -288,11 +293,14 @@ int xtg_hip_finish(xtg_hip* h, char* err, int err_len);
 
 /* ------------------------------------------------------------------------------------------------- graphs */
 
-/* No counterpart in the reference (its OpenCL queue replays nothing): HIP graphs over the backend's stream, the
- * survey's graph_begin / end / replay. Every device call queued between begin and end is captured into one graph
- * instead of running; launch replays it on the stream. Weights must be prepared and scratch sized before the
- * capture (run the calls once first); blocking calls fail during a capture. `name` (may be NULL) is the graph's
- * entry in the profile report, where a profiled replay is timed as a whole. */
+/* No counterpart in the reference (its OpenCL queue replays nothing): HIP graphs over the backend's stream. Every
+ * device call queued between begin and end is captured into one graph instead of running; launch replays it on the
+ * stream. Weights must be prepared and scratch sized before the capture (run the calls once first); blocking calls
+ * fail during a capture. A graph replays its calls exactly as captured, arguments included. While any graph exists
+ * the backend frees no device memory a graph may address: scratch that a later, larger call outgrows, and weights,
+ * buffers and caches released meanwhile, are kept until the last graph is destroyed (the memory of the caller's
+ * own buffers is kept, but their contents are the caller's). `name` (may be NULL) is the graph's entry in the
+ * profile report, where a profiled replay is timed as a whole. */
 typedef struct xtg_hip_graph xtg_hip_graph;
 int xtg_hip_graph_begin(xtg_hip* h, char* err, int err_len);
 int xtg_hip_graph_end(xtg_hip* h, const char* name, xtg_hip_graph** out, char* err, int err_len);

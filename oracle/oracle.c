@@ -800,7 +800,8 @@ static int xo_recurrent(const xo_dory* d, int l) { return l >= d->c.n_in && l < 
 
 xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, const xo_nvfp4* head,
                         const float* logit_scale) {
-  /* the session's caches: packs/dory/dory.cpp:436-447 (per_loop: one cache per loop for recurrent sublayers) */
+  /* the session's caches: packs/dory/dory.cpp:436-447 (per_loop: one cache per loop for recurrent sublayers;
+   * last_loop: one) */
   xo_dory* d = (xo_dory*)calloc(1, sizeof(xo_dory));
   d->c = *c;
   d->layers = layers;
@@ -812,7 +813,7 @@ xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, co
   d->caches = (xo_kv**)calloc((size_t)d->n_attn * (size_t)c->loops, sizeof(xo_kv*));
   for (int l = 0; l < d->n_layers; ++l) {
     if (d->attn_of[l] < 0) continue;
-    int inst = xo_recurrent(d, l) ? c->loops : 1;
+    int inst = xo_recurrent(d, l) && c->kv_mode != XO_KV_LAST_LOOP ? c->loops : 1;
     for (int i = 0; i < inst; ++i)
       d->caches[(size_t)d->attn_of[l] * (size_t)c->loops + (size_t)i] =
           xo_kv_create(c->kv_heads, c->head_dim, c->context, layers[l].kind == XO_SLIDING ? c->ring_slots : 0,
@@ -909,7 +910,11 @@ int xo_dory_forward(xo_dory* d, const float* x, int m, int64_t pos0, float* logi
   for (int i = 0; i < c->loops; ++i) {
     for (size_t j = 0; j < n; ++j) xs[j] = state[j] + input[j];
     xo_justnorm(xs, m, H);
-    for (int r = c->n_in; r < c->n_in + c->n_rec; ++r) xo_sublayer(d, r, xs, m, pos0, i, 1, &s, threads);
+    /* last_loop: every loop attends to this chunk's own keys, the cache keeps the last loop's (dory.cpp:534-537) */
+    const int last_loop = c->kv_mode == XO_KV_LAST_LOOP;
+    const int store = !last_loop || i == c->loops - 1;
+    for (int r = c->n_in; r < c->n_in + c->n_rec; ++r)
+      xo_sublayer(d, r, xs, m, pos0, last_loop ? 0 : i, store, &s, threads);
     memcpy(state, xs, sizeof(float) * n);
     xo_justnorm(state, m, H);
   }

@@ -122,10 +122,13 @@ typedef struct xo_dory_config {
   int64_t context;                 /* linear cache capacity */
   float theta_sliding, theta_full;
   int kv_dtype;                    /* XO_KV_BF16 | XO_KV_FP8 for every cache (dory.cpp:141, 159-161) */
+  int kv_mode;                     /* XO_KV_PER_LOOP | XO_KV_LAST_LOOP (dory.cpp:150-151) */
 } xo_dory_config;
+enum { XO_KV_PER_LOOP = 0, XO_KV_LAST_LOOP = 1 };
 typedef struct xo_dory xo_dory;
-/* Layers and vectors are borrowed (they must outlive the model); per_loop KV mode: a recurrent attention sublayer
- * keeps one cache per loop (dory.cpp:436-447). */
+/* Layers and vectors are borrowed (they must outlive the model). KV modes (dory.cpp:436-447, 530-537): per_loop, a
+ * recurrent attention sublayer keeps one cache per loop; last_loop, one cache that only the last loop writes (every
+ * loop attends to it plus the chunk's own keys). */
 xo_dory* xo_dory_create(const xo_dory_config* c, const xo_dory_layer* layers, const xo_nvfp4* head,
                         const float* logit_scale);
 void xo_dory_free(xo_dory* d);

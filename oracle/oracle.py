@@ -33,7 +33,7 @@ class DoryConfig(ctypes.Structure):
     """xo_dory_config."""
     _fields_ = [(n, _I) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "n_in", "n_rec", "n_out",
                                   "loops", "window", "ring_slots")] + \
-               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F), ("kv_dtype", _I)]
+               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F), ("kv_dtype", _I), ("kv_mode", _I)]
 
 
 class DoryLayer(ctypes.Structure):
@@ -109,6 +109,13 @@ _REF_SIGS = [
     ("xr_kv_store", _I, [_P, _I64, _I, _P, _P]),
     ("xr_kv_load", None, [_P, _I, _I64, _I64, _P, _P]),
     ("xr_attention", _I, [ctypes.POINTER(AttnArgs), _I]),
+    ("xr_dory_open", _P, [ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.c_char_p, _I]),
+    ("xr_dory_close", None, [_P]),
+    ("xr_dory_forward", _I, [_P, _P, _I, _I, _P, ctypes.c_char_p, _I]),
+    ("xr_dory_n_past", _I64, [_P]),
+    ("xr_dory_rewind", _I, [_P, _I64]),
+    ("xr_dory_snapshot", None, [_P, _I]),
+    ("xr_dory_restore", _I, [_P, _I]),
 ]
 
 _oracle = None
@@ -391,3 +398,57 @@ class Dory:
         c.slots, c.ring = None, None
         c._borrowed = True
         return c
+
+
+class RefDory:
+    """The reference's own Dory pack (packs/dory/dory.cpp), compiled into oracle/_ref: load_model on a checkpoint
+    directory (config.json + model.safetensors) with launch options, then one session driven as the server drives it
+    (engine/include/xtg/model.h:31-63). Tokens in, logits out; positions advance with every forward."""
+
+    LOGITS = {"none": 0, "last": 1, "all": 2}
+
+    def __init__(self, path, options=None, threads=8):
+        import json
+        err = ctypes.create_string_buffer(512)
+        vocab = _I(0)
+        self.h = ref().xr_dory_open(path.encode(), json.dumps(options or {}).encode(), threads, ctypes.byref(vocab),
+                                    err, len(err))
+        if not self.h:
+            raise RuntimeError("reference Dory: " + err.value.decode())
+        self.vocab = vocab.value
+
+    def close(self):
+        if self.h:
+            ref().xr_dory_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, tokens, want="all"):
+        """Session::forward over `tokens`: logits [rows][vocab] of every row ("all"), the last ("last") or none."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = {"none": 0, "last": 1, "all": len(t)}[want]
+        out = np.empty((max(rows, 1), self.vocab), dtype=np.float32)
+        err = ctypes.create_string_buffer(512)
+        got = ref().xr_dory_forward(self.h, t.ctypes.data, len(t), self.LOGITS[want], out.ctypes.data, err, len(err))
+        if got < 0:
+            raise RuntimeError("reference Dory forward: " + err.value.decode())
+        assert got == rows, (got, rows)
+        return out[:rows]
+
+    @property
+    def n_past(self):
+        return int(ref().xr_dory_n_past(self.h))
+
+    def rewind(self, n):
+        return bool(ref().xr_dory_rewind(self.h, n))
+
+    def snapshot(self, slot):
+        ref().xr_dory_snapshot(self.h, slot)
+
+    def restore(self, slot):
+        return bool(ref().xr_dory_restore(self.h, slot))

@@ -1,20 +1,28 @@
 // extern "C" entry points into the reference engine's own CPU kernels, compiled from the reference sources by
 // oracle/Makefile into oracle/_ref/libxtgref.so. TEST INFRASTRUCTURE ONLY: used to pin the oracle restatement
 // and, when present, as the CPU baseline. Calls go straight to xtg::matmul_nvfp4 / attention / KvCache / rope /
-// justnorm / slerp_residual / swiglu_scaled / f32_to_e4m3 / argmax (engine/include/xtg/{fp,kernels,kv,sampler}.h).
+// justnorm / slerp_residual / swiglu_scaled / f32_to_e4m3 / argmax (engine/include/xtg/{fp,kernels,kv,sampler}.h),
+// and to the Dory pack's own CPU session (packs/dory/dory.cpp: load_model -> DoryModel -> DorySession::forward).
 #include <cstdint>
+#include <cstring>
 #include <limits>
 #include <map>
 #include <random>
 #include <memory>
+#include <string>
 #include <vector>
 
 #include "xtg/common.h"
 #include "xtg/fp.h"
 #include "xtg/kernels.h"
 #include "xtg/kv.h"
+#include "xtg/model.h"
 #include "xtg/sampler.h"
 #include "xtg/threadpool.h"
+
+namespace xtg {
+void register_builtin_packs();   // packs/packs.cpp
+}
 
 namespace {
 xtg::ThreadPool& pool_of(int threads) {
@@ -152,5 +160,61 @@ int xr_attention(const xr_attn_args* a, int threads) {
     return -1;
   }
 }
+
+// --- the Dory pack's CPU session (packs/dory/dory.cpp:304-578), as the server drives it (model.h:31-63) ---
+
+struct xr_dory {
+  std::unique_ptr<xtg::Model> model;
+  std::unique_ptr<xtg::Session> session;
+};
+
+static void put_err(const char* what, char* err, int err_len) {
+  if (err && err_len > 0) {
+    std::strncpy(err, what, size_t(err_len) - 1);
+    err[err_len - 1] = 0;
+  }
+}
+
+// load_model(dir, options) (engine/src/model.cpp:35-38) on a checkpoint directory, then one session. options is
+// the pack's launch-option JSON (dory.cpp:136-170), e.g. {"backend": "cpu", "kv_dtype": "bf16", "loops": 2}.
+void* xr_dory_open(const char* dir, const char* options, int threads, int* vocab, char* err, int err_len) {
+  try {
+    xtg::register_builtin_packs();
+    auto d = std::make_unique<xr_dory>();
+    d->model = xtg::load_model(dir, xtg::json::parse(options && *options ? options : "{}"), pool_of(threads));
+    d->session = d->model->new_session();
+    *vocab = d->model->info().vocab;
+    return d.release();
+  } catch (const std::exception& e) {
+    put_err(e.what(), err, err_len);
+    return nullptr;
+  }
+}
+
+void xr_dory_close(void* h) { delete static_cast<xr_dory*>(h); }
+
+// Session::forward(tokens, n, want, on_logits): the n tokens at positions n_past() .. ; logits receives the rows
+// on_logits hands over, in order (want 0 none, 1 the last row, 2 every row: xtg::Logits). Returns the rows written.
+int xr_dory_forward(void* h, const int32_t* tokens, int n, int want, float* logits, char* err, int err_len) {
+  try {
+    auto* d = static_cast<xr_dory*>(h);
+    const int vocab = d->model->info().vocab;
+    int rows = 0;
+    const xtg::Logits w = want == 2 ? xtg::Logits::All : want == 1 ? xtg::Logits::Last : xtg::Logits::None;
+    d->session->forward(tokens, n, w, [&](int, const float* lg) {
+      std::memcpy(logits + size_t(rows) * size_t(vocab), lg, size_t(vocab) * sizeof(float));
+      rows += 1;
+    });
+    return rows;
+  } catch (const std::exception& e) {
+    put_err(e.what(), err, err_len);
+    return -1;
+  }
+}
+
+int64_t xr_dory_n_past(void* h) { return static_cast<xr_dory*>(h)->session->n_past(); }
+int xr_dory_rewind(void* h, int64_t n) { return static_cast<xr_dory*>(h)->session->rewind(n) ? 1 : 0; }
+void xr_dory_snapshot(void* h, int slot) { static_cast<xr_dory*>(h)->session->snapshot(slot); }
+int xr_dory_restore(void* h, int slot) { return static_cast<xr_dory*>(h)->session->restore(slot) ? 1 : 0; }
 
 }  // extern "C"

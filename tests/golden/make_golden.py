@@ -112,6 +112,64 @@ def write_bf16():
         np.savez_compressed(os.path.join(HERE, "bf16_k%d.npz" % k), **arrays)
 
 
+# The Dory composition against the reference pack's own CPU session (packs/dory/dory.cpp:304-578, compiled into
+# oracle/_ref): a synthetic checkpoint written by tests/make_checkpoint.py (deterministic for a seed and variant; its
+# sha256 is kept with the vectors), driven through Session::forward with a schedule of calls. Each schedule entry is
+# (pos0, token offset, n): the session is rewound to pos0 when it stands elsewhere (speculative decoding's rewind,
+# dory.cpp:580-589), then forwards tokens[off:off + n] with logits for every row.
+DORY_SCHEDULE = ([(0, 0, 30)] +                                       # a prompt in one chunk
+                 [(p, p, 8) for p in range(30, 62, 8)] +              # 8-row verify steps
+                 [(p, p, 1) for p in range(62, 90)] +                 # single steps past the 64-slot ring's wrap
+                 [(90, 100, 8), (93, 93, 1)] +                        # 8 drafts, 3 accepted: rewind to 93
+                 [(p, p, 1) for p in range(94, 100)])
+DORY_TOKENS = 108
+# (name, checkpoint variant, seed, launch options); the options are the pack's (dory.cpp:136-170)
+DORY_CASES = [
+    ("tiny_bf16_per_loop", "tiny", 3, {"kv_dtype": "bf16", "kv_mode": "per_loop"}),
+    ("tiny_fp8_per_loop", "tiny", 3, {"kv_dtype": "fp8", "kv_mode": "per_loop"}),
+    ("tiny_bf16_last_loop", "tiny", 3, {"kv_dtype": "bf16", "kv_mode": "last_loop"}),
+    ("tiny_fp8_last_loop", "tiny", 3, {"kv_dtype": "fp8", "kv_mode": "last_loop"}),
+    ("tiny_fp8_loops1", "tiny", 3, {"kv_dtype": "fp8", "kv_mode": "per_loop", "loops": 1}),
+    ("d256_fp8_last_loop", "d256", 5, {"kv_dtype": "fp8"}),   # the checkpoint's (and the shipped card's) defaults
+    ("d256_bf16_per_loop", "d256", 5, {"kv_dtype": "bf16", "kv_mode": "per_loop"}),
+]
+
+
+def checkpoint(variant, seed, root="/tmp/xtg_golden_ckpt"):
+    import hashlib
+    import subprocess
+    d = os.path.join(root, "%s_%d" % (variant, seed))
+    if not os.path.exists(os.path.join(d, "model.safetensors")):
+        subprocess.run([sys.executable, os.path.join(ROOT, "tests", "make_checkpoint.py"), d, str(seed), variant],
+                       check=True)
+    with open(os.path.join(d, "model.safetensors"), "rb") as f:
+        return d, hashlib.sha256(f.read()).hexdigest()
+
+
+def write_dory():
+    """Logits of the reference's DorySession over DORY_SCHEDULE for each case: a third of the rows as they are, and
+    for every row its argmax, sum and sum of squares (float64)."""
+    import json
+    for name, variant, seed, opts in DORY_CASES:
+        d, sha = checkpoint(variant, seed)
+        options = dict({"backend": "cpu", "context": 256}, **opts)
+        r = orc.RefDory(d, options, threads=4)
+        tokens = np.random.default_rng(seed * 1000 + 7).integers(0, r.vocab, DORY_TOKENS).astype(np.int32)
+        rows = []
+        for pos0, off, n in DORY_SCHEDULE:
+            if r.n_past != pos0:
+                assert r.rewind(pos0), (name, pos0)
+            rows.append(r.forward(tokens[off:off + n]))
+        r.close()
+        logits = np.concatenate(rows).astype(np.float32)
+        keep = np.arange(0, len(logits), 3)
+        l64 = logits.astype(np.float64)
+        np.savez_compressed(os.path.join(HERE, "dory_%s.npz" % name), variant=variant, seed=seed, sha256=sha,
+                            options=json.dumps(options), schedule=np.array(DORY_SCHEDULE, np.int64),
+                            tokens=tokens, rows=keep, logits=logits[keep], argmax=logits.argmax(1),
+                            sums=l64.sum(1), sumsq=(l64 * l64).sum(1))
+
+
 def main():
     if not orc.ref_available():
         sys.exit("oracle/_ref/libxtgref.so is missing: run `make -C oracle ref` where the reference tree exists")
@@ -119,6 +177,8 @@ def main():
     if only:
         if "bf16" in only:
             write_bf16()
+        if "dory" in only:
+            write_dory()
         print("golden vectors written to", HERE)
         return
     write_bf16()
@@ -134,6 +194,7 @@ def main():
     for case in attention_cases():
         write_attention(*case)
     write_rows()
+    write_dory()
     print("golden vectors written to", HERE)
 
 

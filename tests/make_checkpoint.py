@@ -1,8 +1,10 @@
 """Writes a small synthetic Dory checkpoint in ModelOpt's W4A16_NVFP4 layout (config.json + model.safetensors), with
 the tensor names, dtypes and shapes the reference's DoryModel constructor reads (packs/dory/dory.cpp:77-134,
 316-364, 417-428). The file is written by the safetensors library from torch tensors, so the BF16 and F8_E4M3
-dtype tags are the library's own. Run as a separate process (python tests/make_checkpoint.py OUT_DIR SEED) so that
-torch's HIP runtime never shares a process with the kernel library.
+dtype tags are the library's own. Run as a separate process (python tests/make_checkpoint.py OUT_DIR SEED [VARIANT])
+so that torch's HIP runtime never shares a process with the kernel library. VARIANT "tiny" (the default: 4 q / 2 KV
+heads of 64) or "d256" (4 q heads over one KV head of 256, the real Dory 4B's head size and group of 4 q heads per
+KV head, docs/dory.md:13, with the shipped card's last_loop KV mode, configs/dory4b-nvfp4-sm8750/card.json).
 
 Raw values are drawn so that the folded vectors land where the synthetic models' do: qscale, gscale ~ U(0.5, 1.5),
 sg, su ~ U(5, 15), lr ~ U(0.02, 0.1), logit_scale ~ U(0.5, 1.5).
@@ -29,6 +31,11 @@ CONFIG = {
                         "full_attention": {"rope_type": "default", "rope_theta": 1000000.0}},
     "quantization_config": {"quant_algo": "W4A16_NVFP4"},
 }
+VARIANTS = {
+    "tiny": {},
+    "d256": {"hidden_size": 512, "intermediate_size": 1024, "num_attention_heads": 4, "num_key_value_heads": 1,
+             "head_dim": 256, "recurrent_kv_cache_mode": "last_loop"},
+}
 
 
 def layer_types(n):
@@ -42,11 +49,12 @@ def layer_types(n):
     return out
 
 
-def main(out_dir, seed):
+def main(out_dir, seed, variant="tiny"):
     import torch
     from safetensors.torch import save_file
 
-    c = dict(CONFIG, layer_types=layer_types(CONFIG["num_hidden_layers"]))
+    c = dict(CONFIG, **VARIANTS[variant])
+    c["layer_types"] = layer_types(c["num_hidden_layers"])
     H, F, V = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
     Q, KV = c["num_attention_heads"] * c["head_dim"], c["num_key_value_heads"] * c["head_dim"]
     ir, ai = c["initializer_range"], c["ngpt_alpha_init"]
@@ -102,4 +110,4 @@ def main(out_dir, seed):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1], int(sys.argv[2]) if len(sys.argv) > 2 else 0)
+    main(sys.argv[1], int(sys.argv[2]) if len(sys.argv) > 2 else 0, sys.argv[3] if len(sys.argv) > 3 else "tiny")

@@ -108,6 +108,36 @@ def test_4b_decode_step(hip, model_4b, m):
 
 
 @pytest.fixture(scope="module")
+def model_4b_8k(hip, orc, wl):
+    ctx = 8192
+    w = wl.DoryWeights(wl.DORY_4B, seed=81, context=ctx + 64)
+    ref = orc.Dory(w, wl)
+    dev = hip.dory(w)
+    fill_context(w, ctx, ref, dev, hip, np.random.default_rng(82))
+    yield w, ref, dev, ctx
+    dev.destroy()
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_4b_decode_step_8k(hip, model_4b_8k, m):
+    """Config 4 at an 8K context: 16 splits per KV head on the global layers."""
+    w, ref, dev, ctx = model_4b_8k
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(80 + m), m, H)
+    dx = hip.array(x)
+    dl = hip.array(shape=(m, V))
+    dev.forward(dx, m, ctx, dl)
+    got = dl.numpy()
+    want = ref.forward(x, ctx, threads=16)
+    dx.free()
+    dl.free()
+    e = rel_l2(got, want)
+    print("4B step at 8K m=%d: logits rel-L2 %.2e" % (m, e))
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+@pytest.fixture(scope="module")
 def model_4b_32k(hip, orc, wl):
     ctx = 32768
     w = wl.DoryWeights(wl.DORY_4B, seed=8, context=ctx + 64)

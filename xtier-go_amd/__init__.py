@@ -53,7 +53,7 @@ class DoryConfig(ctypes.Structure):
     """xtg_dory_config."""
     _fields_ = [(n, _I) for n in ("hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "n_in", "n_rec", "n_out",
                                   "loops", "window", "ring_slots")] + \
-               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F), ("kv_dtype", _I)]
+               [("context", _I64), ("theta_sliding", _F), ("theta_full", _F), ("kv_dtype", _I), ("kv_mode", _I)]
 
 
 class DoryLayer(ctypes.Structure):

@@ -26,6 +26,7 @@ DTYPES = {"F64": np.float64, "F32": np.float32, "F16": np.float16, "BF16": np.ui
 
 MLP, SLIDING, FULL = 0, 1, 2
 KV_BF16, KV_FP8 = 0, 1
+KV_MODES = {"per_loop": 0, "last_loop": 1}   # xtg_dory_config.kv_mode
 REWIND_SLACK = 16   # ring slots beyond the window (dory.cpp:43, 449)
 
 
@@ -137,15 +138,18 @@ class DoryCheckpoint:
     mapped file; the vectors are folded as the constructor folds them:
       logit_scale / init_range; qscale = (sqk * sqrt(head_dim) / init_range)^2; gscale = (s_gate * sqrt(gate_init) /
       init_range)^2; sg, su * sqrt(hidden); lr = |alpha * alpha_init / init_range|.
-    Options as the pack's (dory.cpp:136-170): loops (default n_recurrent_loops), kv_dtype (FP8 by default),
-    context (32768), ring_slots (window + 16 by default; the NPU layout uses window + 64)."""
+    Options as the pack's (dory.cpp:136-170): loops (default n_recurrent_loops), kv_mode ("per_loop" or
+    "last_loop"; default the checkpoint's recurrent_kv_cache_mode), kv_dtype (FP8 by default), context (32768),
+    ring_slots (window + 16 by default; the NPU layout uses window + 64)."""
 
-    def __init__(self, path, context=32768, kv_dtype=KV_FP8, loops=None, ring_slots=None):
+    def __init__(self, path, context=32768, kv_dtype=KV_FP8, loops=None, ring_slots=None, kv_mode=None):
         d = path if os.path.isdir(path) else os.path.dirname(path)
         with open(os.path.join(d, "config.json")) as f:
             k, kinds, theta = parse_config(json.load(f), d)
         loops = k["default_loops"] if loops is None else int(loops)
         _check(1 <= loops <= 4, "loops: %d (1..4)" % loops)
+        kv_mode = k["default_kv_mode"] if kv_mode is None else kv_mode
+        _check(kv_mode in KV_MODES, "kv_mode: %s (per_loop | last_loop)" % kv_mode)
         _check(256 <= context <= k["max_pos"], "context: %d (256..%d)" % (context, k["max_pos"]))
         self.st = SafeTensors(os.path.join(d, "model.safetensors"))
         H, F, V = k["hidden"], k["ffn"], k["vocab"]
@@ -155,7 +159,7 @@ class DoryCheckpoint:
                         vocab=V, n_in=k["n_in"], n_rec=k["n_rec"], n_out=k["n_out"], loops=loops,
                         window=k["window"], ring_slots=int(ring_slots or k["window"] + REWIND_SLACK),
                         theta_sliding=theta[SLIDING], theta_full=theta[FULL], context=int(context),
-                        kv_dtype=int(kv_dtype))
+                        kv_dtype=int(kv_dtype), kv_mode=KV_MODES[kv_mode])
         f32 = np.float32
         self.embed_table = self.st.get("backbone.embeddings.weight", "BF16", (V, H))
         self.head_bf16 = self.st.get("lm_head.weight", "BF16", (V, H))

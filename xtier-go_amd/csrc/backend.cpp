@@ -33,6 +33,7 @@ Backend::~Backend() {
   for (void* p : allocs_) (void)hipFree(p);
   for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_, sample_})
     if (p) (void)hipFree(p);
+  for (void* p : retired_) (void)hipFree(p);
   for (DevKv* c : kvs_) {
     for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
                     static_cast<void*>(c->slot_pos)})
@@ -53,13 +54,55 @@ void Backend::ensure(void*& buf, size_t& size, size_t need) {
   XTG_CHECK(!capturing_, "scratch of %zu bytes needed during graph capture (run the calls once before capturing)",
             need);
   if (buf) {
-    HIP_CHECK(hipStreamSynchronize(stream_));   // queued work may still read the old buffer
-    HIP_CHECK(hipFree(buf));
+    dev_free(buf);   // queued work, or a graph, may still read the old buffer
     buf = nullptr;
     size = 0;
   }
   HIP_CHECK(hipMalloc(&buf, need));
   size = need;
+}
+
+void Backend::dev_free(void* p) {
+  if (!p) return;
+  if (!graphs_.empty()) {
+    retired_.push_back(p);
+    return;
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  HIP_CHECK(hipFree(p));
+}
+
+void Backend::hold(const void* key, bool owned) {
+  XTG_CHECK(weights_.count(static_cast<const uint8_t*>(key)) || bf16_weights_.count(static_cast<const uint16_t*>(key)),
+            "hold: no weight prepared for %p", key);
+  Hold& h = holds_[key];
+  h.count += 1;
+  h.owned = h.owned || owned;
+}
+
+void Backend::unhold(const void* key) {
+  auto it = holds_.find(key);
+  if (it == holds_.end()) return;
+  if (--it->second.count > 0) return;
+  const bool owned = it->second.owned;
+  holds_.erase(it);
+  if (owned) drop_weight(key);
+}
+
+void Backend::drop_weight(const void* key) {
+  auto it = weights_.find(static_cast<const uint8_t*>(key));
+  if (it != weights_.end()) {
+    dev_free(it->second.tiles);
+    weight_bytes_ -= it->second.bytes;
+    weights_.erase(it);
+    return;
+  }
+  auto jt = bf16_weights_.find(static_cast<const uint16_t*>(key));
+  if (jt != bf16_weights_.end()) {
+    dev_free(jt->second.tiles);
+    weight_bytes_ -= jt->second.bytes;
+    bf16_weights_.erase(jt);
+  }
 }
 
 const PackedNvfp4& Backend::prepare(const xtg_nvfp4& w) {
@@ -112,12 +155,9 @@ void Backend::read_tiles(const uint8_t* codes, void* out, size_t bytes) {
 
 void Backend::release_weight(const uint8_t* codes) {
   XTG_CHECK(!capturing_, "release_nvfp4: not during a graph capture");
-  auto it = weights_.find(codes);
-  if (it == weights_.end()) return;
-  HIP_CHECK(hipStreamSynchronize(stream_));   // queued launches may still read it
-  HIP_CHECK(hipFree(it->second.tiles));
-  weight_bytes_ -= it->second.bytes;
-  weights_.erase(it);
+  XTG_CHECK(!holds_.count(codes), "release_nvfp4: weight %p is in use by a Dory session",
+            static_cast<const void*>(codes));
+  drop_weight(codes);
 }
 
 void Backend::matmul_dev(const xtg_nvfp4* ws, int nw, const void* x, int x_dtype, int m, float* y, size_t y_off) {
@@ -223,12 +263,8 @@ const PackedBf16& Backend::prepare(const xtg_bf16& w) {
 
 void Backend::release_bf16(const uint16_t* data) {
   XTG_CHECK(!capturing_, "release_bf16: not during a graph capture");
-  auto it = bf16_weights_.find(data);
-  if (it == bf16_weights_.end()) return;
-  HIP_CHECK(hipStreamSynchronize(stream_));   // queued launches may still read it
-  HIP_CHECK(hipFree(it->second.tiles));
-  weight_bytes_ -= it->second.bytes;
-  bf16_weights_.erase(it);
+  XTG_CHECK(!holds_.count(data), "release_bf16: weight %p is in use by a Dory session", static_cast<const void*>(data));
+  drop_weight(data);
 }
 
 void Backend::matmul_bf16_dev(const xtg_bf16& w, const void* x, int x_dtype, int m, float* y, size_t y_off,
@@ -311,10 +347,9 @@ void Backend::kv_destroy(DevKv* c) {
   auto it = kvs_.find(c);
   if (it == kvs_.end()) return;
   XTG_CHECK(!capturing_, "kv_destroy: not during a graph capture");
-  HIP_CHECK(hipStreamSynchronize(stream_));
   for (void* p : {c->k, c->v, static_cast<void*>(c->kscale), static_cast<void*>(c->vscale),
                   static_cast<void*>(c->slot_pos)})
-    if (p) HIP_CHECK(hipFree(p));
+    dev_free(p);
   kvs_.erase(it);
   delete c;
 }
@@ -467,7 +502,7 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
 
 void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
                         float* k, const float* v, const float* qscale, const float* g, const float* gscale,
-                        float* out, void* op) {
+                        float* out, void* op, bool store) {
   XTG_CHECK(kvs_.count(c), "attention step: unknown cache");
   XTG_CHECK(m >= 1 && pos0 >= 0, "attention step: %d rows at %lld", m, pos0);
   XTG_CHECK(pos0 + m < (1LL << 31), "attention step: position %lld beyond the 32-bit slot positions", pos0 + m);
@@ -487,15 +522,15 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
     timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, m, heads, window, scale, part, stream_); });
     if (p.splits > 0)
       timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
-    timed([&] { return launch_kv_store(*c, pos0, m, k, v, stream_); });
+    if (store) timed([&] { return launch_kv_store(*c, pos0, m, k, v, stream_); });
     timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
     return;
   }
   // storing before the scan hides nothing the scan should see: a linear cache's new slots are masked as
   // positions >= pos0, and a ring of window + m - 1 slots or more only drops positions outside every row's window
-  const bool store_first = !c->ring || (window > 0 && c->slots >= (long long)window + m - 1);
+  const bool store_first = store && (!c->ring || (window > 0 && c->slots >= (long long)window + m - 1));
   float* kout = nullptr;   // the processed k rows, for a store after the scan
-  if (!store_first) {
+  if (store && !store_first) {
     ensure(kproc_, kproc_size_, size_t(m) * size_t(c->kv_heads) * size_t(c->head_dim) * sizeof(float));
     kout = static_cast<float*>(kproc_);
   }
@@ -512,7 +547,7 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
     if (p.splits > 0)
       timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
   }
-  if (!store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
+  if (store && !store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
   timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
 
@@ -634,6 +669,11 @@ void Backend::graph_destroy(hipGraphExec_t g) {
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipGraphExecDestroy(g));
   graphs_.erase(it);
+  if (graphs_.empty()) {   // nothing can address the retired memory any more
+    std::vector<void*> r;
+    r.swap(retired_);
+    for (void* p : r) HIP_CHECK(hipFree(p));
+  }
 }
 
 std::string Backend::profile_report() {
@@ -702,9 +742,8 @@ void Backend::release(void* p) {
   XTG_CHECK(!capturing_, "release: not during a graph capture");
   auto it = allocs_.find(p);
   XTG_CHECK(it != allocs_.end(), "release: %p was not allocated by this backend", p);
-  HIP_CHECK(hipStreamSynchronize(stream_));
-  HIP_CHECK(hipFree(p));
   allocs_.erase(it);
+  dev_free(p);
 }
 
 void Backend::write(void* dst, size_t offset, const void* src, size_t bytes) {

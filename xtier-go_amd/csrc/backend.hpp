@@ -32,7 +32,13 @@ class Backend {
   // opencl.h:32 prepare(): idempotent, keyed by w.codes
   const PackedNvfp4& prepare(const xtg_nvfp4& w);
   bool has_weight(const uint8_t* codes) const { return weights_.count(codes) != 0; }
+  // drops the device copy; refused while a Dory session holds the weight
   void release_weight(const uint8_t* codes);
+  // Dory sessions hold the prepared weights they run on (NVFP4 codes or BF16 data as the key). A session that found
+  // the weight unprepared owns it: the device copy goes once the last holder lets go and some holder owned it, so
+  // a session's teardown never frees weights another session still runs on.
+  void hold(const void* key, bool owned);
+  void unhold(const void* key);
   // the prepared tiles of the weight keyed by codes, to host memory (bytes = their size)
   void read_tiles(const uint8_t* codes, void* out, size_t bytes);
   // opencl.h:34 host matmul: upload, compute, read back (up to kHostPassRows rows per pass)
@@ -73,9 +79,10 @@ class Backend {
   // and this call's keys, the store of k / v into the cache, then out (optional) and op (optional, the
   // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)). Up to 8 rows (a decode or verify step)
   // in one fused producer; more (a prefill chunk): k is rewritten too, and the steps run as separate launches.
+  // store = false leaves the cache as it was (a last_loop session's earlier loops, packs/dory/dory.cpp:534-537).
   void attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
                  float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
-                 void* op);
+                 void* op, bool store = true);
   // the row kernels of the decode step (rows.hip); device memory. op (optional): also write the result rows as a
   // GEMV / GEMM operand of ceil(rows / 8) groups of op_bytes(w) bytes.
   void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
@@ -115,6 +122,8 @@ class Backend {
 
   // HIP graphs over the backend's stream: begin/end capture every launch queued in between into one graph,
   // launch() replays it. Scratch buffers must already be large enough (run the calls once before capturing).
+  // While any graph exists, device memory the backend would free (scratch outgrown by a later call, released
+  // weights, buffers and caches) is kept, since a graph may address it, and freed when the last graph goes.
   void graph_begin();
   hipGraphExec_t graph_end(const std::string& name);   // name: the graph's entry in the profile report
   void graph_launch(hipGraphExec_t g);
@@ -136,6 +145,15 @@ class Backend {
 
  private:
   void ensure(void*& buf, size_t& size, size_t need);
+  // frees device memory now (after queued work), or retires it until no graph exists
+  void dev_free(void* p);
+  void drop_weight(const void* key);
+  struct Hold {
+    int count = 0;
+    bool owned = false;
+  };
+  std::unordered_map<const void*, Hold> holds_;
+  std::vector<void*> retired_;
   void clear_kv(DevKv* c);
   void snapshot(const DevKv* c, void* out);   // kv_bytes(c) host bytes
   hipEvent_t event();

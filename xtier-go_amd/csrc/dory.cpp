@@ -24,7 +24,8 @@ float* DorySession::upload(const float* v, size_t n) {
 void DorySession::prepare(const xtg_nvfp4& w) {
   const bool fresh = w.codes && !b_.has_weight(w.codes);
   b_.prepare(w);
-  if (fresh) prepared_.push_back(w.codes);
+  b_.hold(w.codes, fresh);
+  held_.push_back(w.codes);
 }
 
 DorySession::DorySession(Backend& b, const xtg_dory_config& c, const xtg_dory_layer* layers, const xtg_nvfp4& head,
@@ -43,6 +44,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
   const int n_layers = c.n_in + c.n_rec + c.n_out;
   XTG_CHECK(n_layers > 0 && c.loops >= 1, "dory: %d sublayers, %d loops", n_layers, c.loops);
   XTG_CHECK(c.heads % c.kv_heads == 0 && c.head_dim % 2 == 0, "dory: unsupported attention shape");
+  XTG_CHECK(c.kv_mode == XTG_KV_PER_LOOP || c.kv_mode == XTG_KV_LAST_LOOP, "dory: kv_mode %d (per_loop | last_loop)",
+            c.kv_mode);
   const int H = c.hidden, Q = c.heads * c.head_dim, KV = c.kv_heads * c.head_dim, F = c.ffn;
   layers_.resize(size_t(n_layers));
   for (int l = 0; l < n_layers; ++l) {
@@ -65,8 +68,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
       L.qscale = upload(L.w.qscale, size_t(Q));
       L.gscale = upload(L.w.gscale, size_t(Q));
       L.attn = n_attn_++;
-      // the session's caches (dory.cpp:436-447): per_loop, one per loop for a recurrent sublayer
-      const int inst = L.recurrent ? c.loops : 1;
+      // the session's caches (dory.cpp:436-447): per_loop, one per loop for a recurrent sublayer; last_loop, one
+      const int inst = L.recurrent && c.kv_mode == XTG_KV_PER_LOOP ? c.loops : 1;
       for (int i = 0; i < c.loops; ++i)
         caches_.push_back(i < inst ? b_.kv_create(c.kv_heads, c.head_dim, c.context,
                                                    L.w.kind == XTG_DORY_SLIDING ? c.ring_slots : 0, c.kv_dtype)
@@ -106,15 +109,13 @@ void DorySession::release_all() {
     for (DevKv* c : caches_)
       if (c) b_.kv_destroy(c);
     for (void* p : owned_) b_.release(p);
-    for (const uint8_t* codes : prepared_) b_.release_weight(codes);
-    for (const uint16_t* data : prepared_bf16_) b_.release_bf16(data);
+    for (const void* key : held_) b_.unhold(key);
   } catch (...) {
   }
   caches_.clear();
   snaps_.clear();
   owned_.clear();
-  prepared_.clear();
-  prepared_bf16_.clear();
+  held_.clear();
 }
 
 DorySession::~DorySession() { release_all(); }
@@ -153,11 +154,16 @@ void DorySession::set_head_bf16(const xtg_bf16& head) {
             "dory: BF16 LM head %dx%d for hidden %d, vocab %d", head.n_out, head.k, c_.hidden, c_.vocab);
   const bool fresh = !b_.has_bf16(head.data);
   b_.prepare(head);
-  if (fresh) prepared_bf16_.push_back(head.data);
+  b_.hold(head.data, fresh);
+  held_.push_back(head.data);
+  if (head_bf16_.data) {   // the head it replaces
+    b_.unhold(head_bf16_.data);
+    held_.erase(std::find(held_.begin(), held_.end(), static_cast<const void*>(head_bf16_.data)));
+  }
   head_bf16_ = head;
 }
 
-void DorySession::sublayer(Layer& L, int m, long long pos0, int inst) {
+void DorySession::sublayer(Layer& L, int m, long long pos0, int inst, bool store) {
   // packs/dory/dory.cpp:467-518; x's GEMV operand is in op_h_ on entry and on exit
   const int H = c_.hidden, Q = c_.heads * c_.head_dim, KV = c_.kv_heads * c_.head_dim, F = c_.ffn;
   if (L.w.kind == XTG_DORY_MLP) {
@@ -177,7 +183,7 @@ void DorySession::sublayer(Layer& L, int m, long long pos0, int inst) {
   const bool sliding = L.w.kind == XTG_DORY_SLIDING;
   const float scale = 1.f / std::sqrt(float(c_.head_dim));
   b_.attn_step(this->cache(L.attn, inst), m, pos0, c_.heads, sliding ? c_.window : 0, scale,
-               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_);
+               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_, store);
   b_.matmul_op(&L.w.o, 1, op_q_, m, o_, 0);
   b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
 }
@@ -196,17 +202,20 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
     b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
   }
   size_t l = 0;
-  for (; l < size_t(c_.n_in); ++l) sublayer(layers_[l], m, pos0, 0);
+  for (; l < size_t(c_.n_in); ++l) sublayer(layers_[l], m, pos0, 0, true);
   // the loops start from state = input = x: the first entry is justnorm(x + x) read in place, and input is kept
   // only for later entries; the last exit writes x in place (x = state = justnorm(x))
   if (c_.loops > 1) b_.copy(x_, 0, input_, 0, bytes);
   for (int i = 0; i < c_.loops; ++i) {
     const bool last = i == c_.loops - 1;
     b_.add_norm(i == 0 ? x_ : state_, i == 0 ? x_ : input_, x_, m, H, op_h_);   // x = justnorm(state + input)
-    for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r) sublayer(layers_[r], m, pos0, i);
+    // last_loop: every loop attends to the chunk's own keys, the cache keeps the last loop's (dory.cpp:534-537)
+    const bool per_loop = c_.kv_mode == XTG_KV_PER_LOOP;
+    for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r)
+      sublayer(layers_[r], m, pos0, per_loop ? i : 0, per_loop || last);
     b_.add_norm(x_, nullptr, last ? x_ : state_, m, H, last ? op_h_ : nullptr);   // state = justnorm(x)
   }
-  for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0);
+  for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0, true);
 }
 
 void DorySession::head(int r0, int rows, float* logits) {

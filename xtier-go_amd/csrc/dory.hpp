@@ -48,7 +48,7 @@ class DorySession {
     float* su = nullptr;
     float* lr = nullptr;
   };
-  void sublayer(Layer& L, int m, long long pos0, int inst);
+  void sublayer(Layer& L, int m, long long pos0, int inst, bool store);
   void run_chunk(const float* x, int m, long long pos0);
   void head(int r0, int rows, float* logits);
   float* upload(const float* v, size_t n);
@@ -66,10 +66,9 @@ class DorySession {
   std::vector<DevKv*> caches_;   // [attn][loops]
   std::vector<std::vector<DevKv*>> snaps_;   // [slot][ring caches in caches_ order]
   std::vector<void*> owned_;     // device vectors and scratch
-  // weights this session prepared (their device copies go with it: the host arrays that key them may be freed
-  // and their addresses reused once the session is gone)
-  std::vector<const uint8_t*> prepared_;
-  std::vector<const uint16_t*> prepared_bf16_;
+  // the weights this session holds on the backend, once per use (a weight it found unprepared goes with the last
+  // session holding it: the host arrays that key it may be freed and their addresses reused once it is gone)
+  std::vector<const void*> held_;
   // scratch for up to 512 rows (one chunk)
   float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
         *o_ = nullptr;

@@ -211,7 +211,7 @@ def dory_structs(w, nvfp4_type, layer_type, config_type):
     c = w.cfg
     cfg = config_type(c["hidden"], c["ffn"], c["heads"], c["kv_heads"], c["head_dim"], c["vocab"], c["n_in"],
                       c["n_rec"], c["n_out"], c["loops"], c["window"], c["ring_slots"], c["context"],
-                      c["theta_sliding"], c["theta_full"], c.get("kv_dtype", 0))
+                      c["theta_sliding"], c["theta_full"], c.get("kv_dtype", 0), c.get("kv_mode", 0))
     return cfg, arr, nv(w.head) if w.head is not None else zero
 
 
