@@ -168,6 +168,15 @@ typedef struct xtg_attn_args {
  * keys t - window + 1 .. t. The cache is read only; which slots a row sees is decided from the positions stored
  * in them (for a ring: npu/xtg_npu.cpp:236-258). Queued. head_dim 64 or 128, at most 8 q heads per KV head. */
 int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len);
+/* No counterpart in the reference: xtg_hip_attention for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and results; it
+ * allocates nothing: the split partials go to one fixed device array of XTG_HIP_ATTN_SCRATCH_BYTES per device, held
+ * from the library's load until the process ends, and no profiling events are made. A call whose partials exceed it
+ * fails (-1, the sizes in err) before anything is queued: decode and verify calls fit (8 rows over 8 KV heads of 128
+ * take about 2 MB), long prefill chunks may not. Every such call on a device shares that array, so calls that overlap
+ * on one device (two backends' streams) race; calls queued on one backend's stream run in order. */
+#define XTG_HIP_ATTN_SCRATCH_BYTES (16u << 20)
+int xtg_hip_attention_noalloc(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len);
 
 /* ----------------------------------------------------------------------------------------- row kernels */
 

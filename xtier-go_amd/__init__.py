@@ -86,6 +86,7 @@ SIGNATURES = [
     ("xtg_hip_nvfp4_tiles", _I, [_P, _P, _P, _SZ] + _ERR),
     ("xtg_hip_kv_release", _I, [_P, _P] + _ERR),
     ("xtg_hip_attention", _I, [_P, ctypes.POINTER(AttnArgs)] + _ERR),
+    ("xtg_hip_attention_noalloc", _I, [_P, ctypes.POINTER(AttnArgs)] + _ERR),
     ("xtg_hip_qk_rope_norm", _I, [_P, _P, _P, _I, _I, _I, _I, _I64, _F, _P] + _ERR),
     ("xtg_hip_slerp_residual", _I, [_P, _P, _P, _P, _I, _I] + _ERR),
     ("xtg_hip_swiglu_norm", _I, [_P, _P, _P, _P, _P, _I, _I] + _ERR),
@@ -378,6 +379,14 @@ class HipBackend:
                      _ptr(out))
         err = _errbuf()
         _check(lib().xtg_hip_attention(self.h, ctypes.byref(a), err, len(err)), err)
+
+    def attention_noalloc(self, cache, q, k, v, out, n_q, pos0, heads, window=0, scale=None):
+        """The same call with its partials in the device's fixed scratch (xtg_hip_attention_noalloc)."""
+        sc = float(np.float32(1) / np.sqrt(np.float32(cache.head_dim))) if scale is None else float(scale)
+        a = AttnArgs(n_q, pos0, heads, cache.kv_heads, cache.head_dim, window, sc, _ptr(q), _ptr(k), _ptr(v), cache.h,
+                     _ptr(out))
+        err = _errbuf()
+        _check(lib().xtg_hip_attention_noalloc(self.h, ctypes.byref(a), err, len(err)), err)
 
     # ---- the Dory decode step
     def dory(self, weights):

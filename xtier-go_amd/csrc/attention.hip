@@ -38,7 +38,9 @@
 #include <climits>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "attention.hpp"
 #include "common.hpp"
@@ -1241,6 +1243,33 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
     p.splits = 0;
   }
   return p;
+}
+
+// ------------------------------------------------------------------------------------------ fixed scratch
+
+// The attention call that allocates nothing keeps its split partials here: one array per device, of
+// kAttnScratchBytes, shared by every such call on that device (each call writes every partial it reads). Host code
+// never passes the array's name to a kernel: in host code it is a stand-in, not a device address. The address each
+// device holds it at comes from hipGetSymbolAddress, looked up once per device with that device current.
+static __device__ __align__(256) float scratch[kAttnScratchBytes / sizeof(float)];
+
+void* attn_scratch_ptr(int device) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;   // per device
+  std::lock_guard<std::mutex> lock(mu);
+  XTG_CHECK(device >= 0, "attention scratch: device %d", device);
+  if (size_t(device) >= ptrs.size()) ptrs.resize(size_t(device) + 1, nullptr);
+  if (!ptrs[size_t(device)]) {
+    int cur = -1;
+    HIP_CHECK(hipGetDevice(&cur));
+    XTG_CHECK(cur == device, "attention scratch: device %d is not the current device (%d is)", device, cur);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    XTG_CHECK(e == hipSuccess && p != nullptr, "attention scratch: hipGetSymbolAddress failed on device %d: %s",
+              device, hipGetErrorString(e));
+    ptrs[size_t(device)] = p;
+  }
+  return ptrs[size_t(device)];
 }
 
 // ------------------------------------------------------------------------------------------------- launchers

@@ -65,6 +65,12 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblo
 std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
                               hipStream_t stream);
 
+// The split partials of the attention call that allocates nothing live in a fixed device array of this many bytes
+// per device (attention.hip), loaded with the code object and held until the process ends. attn_scratch_ptr(device)
+// is its device address on `device`, which must be the current device; the first call per device looks it up.
+constexpr size_t kAttnScratchBytes = size_t(16) << 20;
+void* attn_scratch_ptr(int device);
+
 constexpr int kProdRows = 8, kProdGroup = 8;   // the producer's rows per call and q heads per KV head
 
 // The decode step's producer (packs/dory/dory.cpp:482-490 and the cache store of :507): in one launch per

@@ -16,6 +16,7 @@ Backend::Backend(int device) : device_(device) {
   XTG_CHECK(device >= 0 && device < count, "no HIP device %d (%d present)", device, count);
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  attn_scratch_ = attn_scratch_ptr(device);   // with the device current, once per device
 }
 
 Backend::~Backend() {
@@ -482,14 +483,34 @@ void Backend::kv_copy(const DevKv* src, DevKv* dst) {
                            hipMemcpyDeviceToDevice, stream_));
 }
 
-void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
-                        const float* k, const float* v, float* out) {
+void Backend::check_attention(const DevKv* c, int n_q, long long pos0, const float* q, const float* k, const float* v,
+                              const float* out) const {
   XTG_CHECK(kvs_.count(const_cast<DevKv*>(c)), "attention: unknown cache");
   XTG_CHECK(n_q >= 1 && pos0 >= 0, "attention: %d rows at %lld", n_q, pos0);
   XTG_CHECK(q && k && v && out, "attention: NULL argument");
   for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
                         static_cast<const void*>(out)})
     XTG_CHECK(reinterpret_cast<uintptr_t>(p) % 16 == 0, "attention: arguments must be 16-byte aligned");
+}
+
+void Backend::attention_noalloc(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale,
+                                const float* q, const float* k, const float* v, float* out) {
+  check_attention(c, n_q, pos0, q, k, v, out);
+  const AttnPlan p = attn_plan(*c, n_q, heads, pos0, window);
+  const size_t need = p.part_floats() * sizeof(float);
+  XTG_CHECK(need <= kAttnScratchBytes,
+            "attention_noalloc: %d rows over %d KV heads (%d key splits) need %zu bytes of partials; the fixed scratch "
+            "holds %zu",
+            n_q, c->kv_heads, p.splits, need, kAttnScratchBytes);
+  float* part = static_cast<float*>(attn_scratch_);
+  launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_);
+  if (p.splits > 0) launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_);
+  launch_attn_merge(p, n_q, heads, part, out, stream_);
+}
+
+void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
+                        const float* k, const float* v, float* out) {
+  check_attention(c, n_q, pos0, q, k, v, out);
   const AttnPlan p = attn_plan(*c, n_q, heads, pos0, window);
   ensure(part_, part_size_, p.part_floats() * sizeof(float));
   float* part = static_cast<float*>(part_);

@@ -74,6 +74,10 @@ class Backend {
   // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
+  // The same with the split partials in the device's fixed scratch (attn_scratch_ptr): allocates nothing, creates no
+  // profiling events; refuses a call whose partials exceed kAttnScratchBytes.
+  void attention_noalloc(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
+                         const float* k, const float* v, float* out);
   // The attention half of a Dory sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
   // k / v [m][kv_heads][d], g [m][heads * d]: RoPE + norms of q (rewritten) and k, the attention over the cache
   // and this call's keys, the store of k / v into the cache, then out (optional) and op (optional, the
@@ -145,6 +149,9 @@ class Backend {
 
  private:
   void ensure(void*& buf, size_t& size, size_t need);
+  void check_attention(const DevKv* c, int n_q, long long pos0, const float* q, const float* k, const float* v,
+                       const float* out) const;
+  void* attn_scratch_ = nullptr;   // this device's fixed attention scratch (device address)
   // frees device memory now (after queued work), or retires it until no graph exists
   void dev_free(void* p);
   void drop_weight(const void* key);

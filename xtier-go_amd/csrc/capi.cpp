@@ -15,6 +15,8 @@ struct xtg_hip {
   std::unique_ptr<xtg::hip::Backend> b;
 };
 
+static_assert(XTG_HIP_ATTN_SCRATCH_BYTES == xtg::hip::kAttnScratchBytes, "the header's scratch size is the kernel's");
+
 namespace {
 void put_err(char* err, int err_len, const char* msg) {
   if (err && err_len > 0) {
@@ -211,6 +213,17 @@ int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len
               "attention: %d KV heads of %d for a cache of %d of %d", a->kv_heads, a->head_dim, c->kv_heads,
               c->head_dim);
     h->b->attention(c, a->n_q, a->pos0, a->heads, a->window, a->scale, a->q, a->k, a->v, a->out);
+  });
+}
+
+int xtg_hip_attention_noalloc(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h && a && a->cache, "attention_noalloc: NULL argument");
+    const auto* c = reinterpret_cast<const xtg::hip::DevKv*>(a->cache);
+    XTG_CHECK(a->kv_heads == c->kv_heads && a->head_dim == c->head_dim,
+              "attention_noalloc: %d KV heads of %d for a cache of %d of %d", a->kv_heads, a->head_dim, c->kv_heads,
+              c->head_dim);
+    h->b->attention_noalloc(c, a->n_q, a->pos0, a->heads, a->window, a->scale, a->q, a->k, a->v, a->out);
   });
 }
 
