@@ -124,6 +124,32 @@ def test_decode_global_cache_fp8(hip, orc, ctx, n_q):
     assert rel_l2(out, ref) <= 1e-5
 
 
+# The real Dory 4B's attention (docs/dory.md:13): 16 q heads over 4 KV heads of 256. (cached, n_q, window, FP8):
+# decode and verify steps over global caches, a prefill chunk, sliding windows over rings of window + 16 slots
+# (the CPU session's ring, packs/dory/dory.cpp:43, 449), a call with nothing cached.
+D256 = [(4096, 1, 0, 0), (4096, 8, 0, 0), (4096, 1, 0, 1), (8192, 8, 0, 1), (300, 37, 0, 0), (1500, 300, 0, 1),
+        (3000, 8, 1024, 1), (3000, 1, 1024, 0), (0, 20, 0, 0), (700, 5, 64, 1)]
+
+
+@pytest.mark.parametrize("cached,n_q,window,fp8", D256)
+def test_head_dim_256(hip, orc, cached, n_q, window, fp8):
+    rng = np.random.default_rng(256 + cached + n_q + window + fp8)
+    out, ref, exact = run_case(hip, orc, cached, n_q, window, 16, 4, 256, None, rng, unit=True, fp8=bool(fp8),
+                               ring=window + 16 if window else 0)
+    assert rel_l2(out, ref) <= 1e-5
+    if exact is not None:
+        assert np.max(np.abs(out - exact)) < 2e-5
+
+
+@pytest.mark.parametrize("n_q", [1, 8])
+def test_head_dim_256_sharp(hip, orc, n_q):
+    """A sharp softmax (q x 30) at 256 dims over an FP8 cache of 900 keys."""
+    rng = np.random.default_rng(2560 + n_q)
+    out, ref, exact = run_case(hip, orc, 900, n_q, 0, 16, 4, 256, None, rng, unit=True, qmul=30.0, fp8=True)
+    assert rel_l2(out, ref) <= 5e-5
+    assert rel_l2(out, exact) <= max(3 * rel_l2(ref, exact), 1e-5)
+
+
 @pytest.mark.parametrize("n_q", [1, 5, 16])
 def test_head_dim_128_group_8_fp8(hip, orc, n_q):
     """Eight q heads per KV head (two q-blocks per MFMA pass at 4+ rows), FP8, a sharp softmax, 700 cached keys."""
@@ -361,6 +387,8 @@ def test_errors(hip, pkg):
             dc.destroy()
     with pytest.raises(pkg.XtgError, match="head_dim"):
         hip.kv_cache(2, 96, 32)
+    with pytest.raises(pkg.XtgError, match="head_dim"):
+        hip.kv_cache(2, 512, 32)
 
 
 @pytest.mark.parametrize("dtype", [0, 1])

@@ -22,8 +22,6 @@ def ckroot(tmp_path_factory):
 @pytest.mark.parametrize("name", dg.CASES)
 def test_device_session_matches_reference_session(name, hip, ck, ckroot):
     g = dg.load(name)
-    if g["variant"] == "d256":
-        pytest.skip("heads of 256 dims are not built yet")
     d, sha = dg.checkpoint_dir(ckroot, g["variant"], int(g["seed"]))
     assert sha == g["sha256"], "tests/make_checkpoint.py no longer writes the checkpoint the vectors were made on"
     c = dg.open_checkpoint(ck, d, g["options"])

@@ -63,6 +63,21 @@ def test_attention_vs_naive(orc, cached, n_q, window, fp8):
     assert np.max(np.abs(out - ref)) < 2e-5
 
 
+@pytest.mark.parametrize("cached,n_q,window,fp8", [(300, 1, 0, 0), (200, 9, 0, 1), (500, 3, 64, 1)])
+def test_attention_head_dim_256(orc, cached, n_q, window, fp8):
+    """The real Dory 4B's heads (16 q over 4 KV heads of 256, docs/dory.md:13): FP64 and the compiled reference."""
+    rng = np.random.default_rng(256)
+    K, V, q, cache, Kc, Vc = build_case(orc, cached, n_q, window, fp8, rng, heads=16, kvh=4, d=256)
+    out = orc.attention(q, K[cached:], V[cached:], cache, cached, 16, 4, 256, window=window, scale=0.7, pool_size=4)
+    assert np.max(np.abs(out - naive_attention(q, Kc, Vc, cached, 16, 4, 256, window, 0.7))) < 2e-5
+    if orc.ref_available():
+        rng = np.random.default_rng(256)
+        K2, V2, q2, cache_r, _, _ = build_case(orc, cached, n_q, window, fp8, rng, heads=16, kvh=4, d=256, use_ref=True)
+        ref = orc.attention(q2, K2[cached:], V2[cached:], cache_r, cached, 16, 4, 256, window=window, scale=0.7,
+                            pool_size=4)
+        assert np.max(np.abs(out - ref)) <= 1e-6
+
+
 def test_naive_catches_causal_slip(orc):
     rng = np.random.default_rng(43)
     K, V, q, cache, Kc, Vc = build_case(orc, 100, 37, 0, 0, rng)

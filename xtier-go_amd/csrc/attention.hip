@@ -200,12 +200,12 @@ std::string launch_kv_store(const DevKv& c, long long pos, int n, const float* k
     const dim3 grid{unsigned((waves + 3) / 4)}, block{256};
     auto* ck = static_cast<uint8_t*>(c.k);
     auto* cv = static_cast<uint8_t*>(c.v);
-    if (c.head_dim == 64)
-      hipLaunchKernelGGL(kv_store_fp8_kernel<64>, grid, block, 0, stream, k, v, ck, cv, c.kscale, c.vscale,
-                         c.slot_pos, pos, first, n, c.kv_heads, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
-    else
-      hipLaunchKernelGGL(kv_store_fp8_kernel<128>, grid, block, 0, stream, k, v, ck, cv, c.kscale, c.vscale,
-                         c.slot_pos, pos, first, n, c.kv_heads, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
+#define XTG_STORE8(D)                                                                                        \
+  if (c.head_dim == D)                                                                                      \
+    hipLaunchKernelGGL(kv_store_fp8_kernel<D>, grid, block, 0, stream, k, v, ck, cv, c.kscale, c.vscale,     \
+                       c.slot_pos, pos, first, n, c.kv_heads, (long long)c.slots, c.ring ? 1 : 0, c.slots_pad);
+    XTG_STORE8(64) XTG_STORE8(128) XTG_STORE8(256)
+#undef XTG_STORE8
     HIP_CHECK(hipGetLastError());
     return strf("kv_store_fp8_kernel<%d>", c.head_dim);
   }
@@ -271,21 +271,52 @@ struct KvTile {
   int4 p0, p1;
 };
 
+// Tile t's K operands and slot positions, and its V operands (the two halves of a tile load).
 template <int D>
-__device__ inline void load_tile(KvTile<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
-                                 const int* __restrict__ slot_pos, int t, int lane) {
-  constexpr int NC = D / 32, ND = D / 16;
-  const size_t ktile = size_t(2 * NC) * 64, vtile = size_t(ND) * 64;
+__device__ inline void load_tile_k(KvTile<D>& T, const uint4* __restrict__ kb, const int* __restrict__ slot_pos, int t,
+                                   int lane) {
+  constexpr int NC = D / 32;
+  const size_t ktile = size_t(2 * NC) * 64;
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int c = 0; c < NC; ++c) T.k[b][c] = kb[size_t(t) * ktile + size_t(b * NC + c) * 64 + size_t(lane)];
-#pragma unroll
-  for (int dd = 0; dd < ND; ++dd) T.v[dd] = vb[size_t(t) * vtile + size_t(dd) * 64 + size_t(lane)];
   const int g = lane >> 4;
   T.p0 = *reinterpret_cast<const int4*>(slot_pos + t * kTile + 4 * g);
   T.p1 = *reinterpret_cast<const int4*>(slot_pos + t * kTile + 16 + 4 * g);
 }
+
+template <int D>
+__device__ inline void load_tile_v(KvTile<D>& T, const uint4* __restrict__ vb, int t, int lane) {
+  constexpr int ND = D / 16;
+  const size_t vtile = size_t(ND) * 64;
+#pragma unroll
+  for (int dd = 0; dd < ND; ++dd) T.v[dd] = vb[size_t(t) * vtile + size_t(dd) * 64 + size_t(lane)];
+}
+
+template <int D>
+__device__ inline void load_tile(KvTile<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
+                                 const int* __restrict__ slot_pos, int t, int lane) {
+  load_tile_k<D>(T, kb, slot_pos, t, lane);
+  load_tile_v<D>(T, vb, t, lane);
+}
+
+// The q operand of a scan, B of the score products: column block qb, 32-dim chunk c, BF16 term t (split3). Heads of
+// up to 128 dims keep it in registers; larger heads keep it in the work-group's LDS, where all 4 waves read it (they
+// scan the same q-cols), as [qb][c][t][64 lanes] x 16 bytes.
+template <int D, int QB>
+struct QRegs {
+  bf16x8 q[QB][D / 32][3];
+  __device__ bf16x8 get(int qb, int c, int t) const { return q[qb][c][t]; }
+};
+template <int D, int QB>
+struct QLds {
+  const bf16x8* base;
+  int lane;
+  __device__ bf16x8 get(int qb, int c, int t) const { return base[((qb * (D / 32) + c) * 3 + t) * 64 + lane]; }
+};
+template <int D>
+constexpr bool q_in_lds() { return D > 128; }
 
 // The online-softmax state of the lane's column in each q-block (the same in the 4 lanes of a column).
 template <int D, int QB>
@@ -296,25 +327,23 @@ struct ScanState {
 
 // One tile for every q-block: scores (three MFMA terms), mask, online softmax, P.V (two terms). lo[qb]: the
 // lane's column sees stored positions lo .. pos0 - 1 (INT_MAX for a column with no query).
-template <int D, int QB>
-__device__ inline void scan_tile(const KvTile<D>& T, const bf16x8 (&qop)[QB][D / 32][3], const int (&lo)[QB],
-                                 ScanState<D, QB>& st, int pos0) {
+template <int D, int QB, class QS>
+__device__ inline void scan_tile(const KvTile<D>& T, const QS& qop, const int (&lo)[QB], ScanState<D, QB>& st,
+                                 int pos0) {
   constexpr int NC = D / 32, ND = D / 16;
   const int kpos[8] = {T.p0.x, T.p0.y, T.p0.z, T.p0.w, T.p1.x, T.p1.y, T.p1.z, T.p1.w};
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    f32x4 s[2];
+    f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      s[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const bf16x8 A = __builtin_bit_cast(bf16x8, T.k[b][c]);
+      for (int term = 0; term < 3; ++term) {
+        const bf16x8 B = qop.get(qb, c, term);   // each operand read once per tile, for both key blocks
 #pragma unroll
-        for (int term = 0; term < 3; ++term)
-          s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, qop[qb][c][term], s[b], 0, 0, 0);
+        for (int b = 0; b < 2; ++b)
+          s[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, T.k[b][c]), B, s[b], 0, 0, 0);
       }
-    }
     // mask, then the column's max over its 4 lanes x 8 keys
     float sc[8];
     float mx = -INFINITY;
@@ -358,6 +387,77 @@ __device__ inline void scan_tile(const KvTile<D>& T, const bf16x8 (&qop)[QB][D /
   }
 }
 
+// scan_tile for BF16 heads of more than 128 dims, where two whole tiles do not fit the registers: one tile is
+// held, and reloaded in a skew. Once the scores have used this tile's K and positions, next_k(T) loads the next
+// tile's into their registers, to land during this tile's softmax and P.V; once P.V has used V, next_v(T) loads the
+// next tile's V, to land during the next scores. Each load then has about half a tile's work to land behind, and a
+// wave keeps 16 KB in flight as the 128-dim scan's double buffer does.
+template <int D, int QB, class QS, class LK, class LV>
+__device__ inline void scan_tile_skewed(KvTile<D>& T, const QS& qop, const int (&lo)[QB], ScanState<D, QB>& st,
+                                        int pos0, LK&& next_k, LV&& next_v) {
+  constexpr int NC = D / 32, ND = D / 16;
+  f32x4 s[QB][2];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    s[qb][0] = s[qb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int term = 0; term < 3; ++term) {
+        const bf16x8 B = qop.get(qb, c, term);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, T.k[b][c]), B, s[qb][b], 0, 0, 0);
+      }
+  }
+  const int kpos[8] = {T.p0.x, T.p0.y, T.p0.z, T.p0.w, T.p1.x, T.p1.y, T.p1.z, T.p1.w};
+  next_k(T);
+  bf16x8 phi[QB], plo[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    float sc[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sc[e] = kpos[e] >= lo[qb] && kpos[e] < pos0 ? s[qb][e >> 2][e & 3] : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = xor32_max(xor16_max(mx));
+    const float m_new = fmaxf(st.m[qb], mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = exp2_fast(st.m[qb] - m_ref);
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = exp2_fast(sc[e] - m_ref);
+      ps += p[e];
+    }
+    ps = xor32_sum(xor16_sum(ps));
+    st.l[qb] = st.l[qb] * corr + ps;
+    st.m[qb] = m_new;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 h = to_bf16(p[e]);
+      phi[qb][e] = h;
+      plo[qb][e] = to_bf16(p[e] - of_bf16(h));
+    }
+    if (__ballot(corr != 1.f)) {
+#pragma unroll
+      for (int dd = 0; dd < ND; ++dd) st.acc[qb][dd] *= corr;
+    }
+  }
+#pragma unroll
+  for (int dd = 0; dd < ND; ++dd) {
+    const bf16x8 A = __builtin_bit_cast(bf16x8, T.v[dd]);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      st.acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, phi[qb], st.acc[qb][dd], 0, 0, 0);
+      st.acc[qb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, plo[qb], st.acc[qb][dd], 0, 0, 0);
+    }
+  }
+  next_v(T);
+}
+
 // The FP8 form of a tile: K as two 16-slot blocks of D / 64 lane loads (two operands each), V as D / 32 loads, the
 // positions and the key and value scales of the lane's 8 keys.
 template <int D>
@@ -368,25 +468,46 @@ struct KvTile8 {
   float4 ks0, ks1, vs0, vs1;
 };
 
+// An FP8 tile's halves: K codes, slot positions and key scales; V codes and value scales.
 template <int D>
-__device__ inline void load_tile(KvTile8<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
-                                 const int* __restrict__ slot_pos, const float* __restrict__ ks,
-                                 const float* __restrict__ vs, int t, int lane) {
-  constexpr int NP = D / 64, NV = D / 32;
+__device__ inline void load_tile_k(KvTile8<D>& T, const uint4* __restrict__ kb, const int* __restrict__ slot_pos,
+                                   const float* __restrict__ ks, int t, int lane) {
+  constexpr int NP = D / 64;
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int c = 0; c < NP; ++c) T.k[b][c] = kb[(size_t(2 * t + b) * NP + size_t(c)) * 64 + size_t(lane)];
-#pragma unroll
-  for (int dp = 0; dp < NV; ++dp) T.v[dp] = vb[(size_t(t) * NV + size_t(dp)) * 64 + size_t(lane)];
   const int at = t * kTile + 4 * (lane >> 4);
   T.p0 = *reinterpret_cast<const int4*>(slot_pos + at);
   T.p1 = *reinterpret_cast<const int4*>(slot_pos + at + 16);
   T.ks0 = *reinterpret_cast<const float4*>(ks + at);
   T.ks1 = *reinterpret_cast<const float4*>(ks + at + 16);
+}
+
+template <int D>
+__device__ inline void load_tile_v(KvTile8<D>& T, const uint4* __restrict__ vb, const float* __restrict__ vs, int t,
+                                   int lane) {
+  constexpr int NV = D / 32;
+#pragma unroll
+  for (int dp = 0; dp < NV; ++dp) T.v[dp] = vb[(size_t(t) * NV + size_t(dp)) * 64 + size_t(lane)];
+  const int at = t * kTile + 4 * (lane >> 4);
   T.vs0 = *reinterpret_cast<const float4*>(vs + at);
   T.vs1 = *reinterpret_cast<const float4*>(vs + at + 16);
 }
+
+template <int D>
+__device__ inline void load_tile(KvTile8<D>& T, const uint4* __restrict__ kb, const uint4* __restrict__ vb,
+                                 const int* __restrict__ slot_pos, const float* __restrict__ ks,
+                                 const float* __restrict__ vs, int t, int lane) {
+  load_tile_k<D>(T, kb, slot_pos, ks, t, lane);
+  load_tile_v<D>(T, vb, vs, t, lane);
+}
+
+// A tile reload that does nothing (the double-buffered scans load whole tiles themselves).
+struct NoLoad {
+  template <class T>
+  __device__ void operator()(T&) const {}
+};
 
 // 8 E4M3 codes (two dwords, element 0 in the low byte) as 8 BF16 values, exactly.
 __device__ inline bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
@@ -399,10 +520,12 @@ __device__ inline bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
 
 // scan_tile for an FP8 tile: each K and V operand is converted once and used for every q-block; the raw scores are
 // multiplied by their key's scale before the mask, and the softmax weights by their value's scale on the way into
-// the P.V product (the running sum takes them unscaled).
-template <int D, int QB>
-__device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D / 32][3], const int (&lo)[QB],
-                                 ScanState<D, QB>& st, int pos0) {
+// the P.V product (the running sum takes them unscaled). next_k / next_v: the skewed reload of scan_tile_skewed
+// (heads of more than 128 dims), after the scores (K codes, positions, key scales) and after P.V (V codes, value
+// scales).
+template <int D, int QB, class QS, class LK = NoLoad, class LV = NoLoad>
+__device__ inline void scan_tile(KvTile8<D>& T, const QS& qop, const int (&lo)[QB], ScanState<D, QB>& st, int pos0,
+                                 LK&& next_k = LK{}, LV&& next_v = LV{}) {
   constexpr int NP = D / 64, NV = D / 32;
   const int kpos[8] = {T.p0.x, T.p0.y, T.p0.z, T.p0.w, T.p1.x, T.p1.y, T.p1.z, T.p1.w};
   const float ks[8] = {T.ks0.x, T.ks0.y, T.ks0.z, T.ks0.w, T.ks1.x, T.ks1.y, T.ks1.z, T.ks1.w};
@@ -420,10 +543,11 @@ __device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D 
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int term = 0; term < 3; ++term) {
-          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, qop[qb][2 * c][term], s[qb][b], 0, 0, 0);
-          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, qop[qb][2 * c + 1][term], s[qb][b], 0, 0, 0);
+          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, qop.get(qb, 2 * c, term), s[qb][b], 0, 0, 0);
+          s[qb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, qop.get(qb, 2 * c + 1, term), s[qb][b], 0, 0, 0);
         }
     }
+  next_k(T);   // kpos and ks are copies: the next tile's K half may land in T
   bf16x8 phi[QB], plo[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -473,14 +597,28 @@ __device__ inline void scan_tile(const KvTile8<D>& T, const bf16x8 (&qop)[QB][D 
       x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, plo[qb], x1, 0, 0, 0);
     }
   }
+  next_v(T);
 }
 
-// LDS of a scan work-group: the wave merge, then (raw q rows) the rows' RoPE cosines and sines.
+// LDS of a scan work-group. Heads of up to 128 dims: the wave merge, then (raw q rows) the processed q-cols and the
+// rows' RoPE cosines and sines. Larger heads: the q operand first, then one region that holds the processed q-cols
+// and the RoPE table before the scan and the wave merge after it; the merge runs in passes of 128 dims.
+template <int D>
+constexpr int scan_merge_passes() { return D > 128 ? D / 128 : 1; }
 template <int D, int QB>
-constexpr int scan_merge_floats() { return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16) * 64 * 4; }
+constexpr int scan_qop_floats() { return q_in_lds<D>() ? QB * (D / 32) * 3 * 64 * 4 : 0; }
+template <int D, int QB>
+constexpr int scan_merge_floats() {
+  return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16 / scan_merge_passes<D>()) * 64 * 4;
+}
+template <int D, int QB, bool RAWQ>
+constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * D + 2 * kProdRows * (D / 2) : 0; }
+template <int D, int QB>
+constexpr int scan_sq_offset() { return q_in_lds<D>() ? scan_qop_floats<D, QB>() : scan_merge_floats<D, QB>(); }
 template <int D, int QB, bool RAWQ>
 constexpr int scan_lds_floats() {
-  return scan_merge_floats<D, QB>() + (RAWQ ? QB * 16 * D + 2 * kProdRows * (D / 2) : 0);
+  return q_in_lds<D>() ? scan_qop_floats<D, QB>() + std::max(scan_merge_floats<D, QB>(), scan_rawq_floats<D, QB, RAWQ>())
+                       : scan_merge_floats<D, QB>() + scan_rawq_floats<D, QB, RAWQ>();
 }
 
 // One scan work-group (KV head, split) of a row block. RAWQ: q arrives as the projection wrote it, and the work-group
@@ -521,12 +659,31 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
       load_tile<D>(T, kbase, vbase, a.slot_pos, tt, lane);
   };
   int t = t_begin + wave;
-  Tile A, B;
+  // heads of more than 128 dims hold one tile, reloaded in a skew (scan_tile_skewed); else two alternate
+  constexpr bool SKEW = D > 128;
+  Tile A;
+  std::conditional_t<SKEW, char, Tile> B;
   load(A, min(t, t_last));
 
   // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale * log2(e),
   // three terms. lo: the first stored position the column sees.
-  bf16x8 qop[QB][NC][3];
+  constexpr bool QL = q_in_lds<D>();
+  std::conditional_t<QL, QLds<D, QB>, QRegs<D, QB>> qop;
+  bf16x8* qlds = reinterpret_cast<bf16x8*>(lds);   // QL: the operand's LDS region
+  // QL: each wave builds the chunks c = wave (mod 4) of every q-block into LDS; else every wave all of them
+  auto put = [&](int qb, int c, const float (&x)[8]) {
+    if constexpr (QL) {
+      bf16x8 t0, t1, t2;
+      split3(x, t0, t1, t2);
+      qlds[((qb * NC + c) * 3 + 0) * 64 + lane] = t0;
+      qlds[((qb * NC + c) * 3 + 1) * 64 + lane] = t1;
+      qlds[((qb * NC + c) * 3 + 2) * 64 + lane] = t2;
+    } else {
+      split3(x, qop.q[qb][c][0], qop.q[qb][c][1], qop.q[qb][c][2]);
+    }
+  };
+  constexpr int c_step = QL ? kWaves : 1;
+  const int c_first = QL ? wave : 0;
   int lo[QB];
   bool qlive[QB];
 #pragma unroll
@@ -542,7 +699,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     constexpr int PP = HALF / TPV;        // RoPE pairs per thread
     constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
     static_assert(PP % 2 == 0 && TPV * QB * 16 == kWaves * 64, "q-col split");
-    float* sq = lds + scan_merge_floats<D, QB>();   // processed q-cols [QB * 16][D]
+    float* sq = lds + scan_sq_offset<D, QB>();   // processed q-cols [QB * 16][D]
     float* scos = sq + QB * 16 * D;
     float* ssin = scos + kProdRows * HALF;
     const int nrows = min(a.rpb, a.n_q - row0);
@@ -607,14 +764,14 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int c = c_first; c < NC; c += c_step) {
         const float* sp = sq + (qb * 16 + j) * D + 32 * c + 8 * g;
         const float4 u = *reinterpret_cast<const float4*>(sp);
         const float4 w = *reinterpret_cast<const float4*>(sp + 4);
         float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? x[e] * a.scale2 : 0.f;
-        split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
+        put(qb, c, x);
       }
   } else {
 #pragma unroll
@@ -624,15 +781,20 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
       const float* qp =
           qrows + (size_t(qrow) * size_t(a.heads) + size_t(kvh * a.group + (qlive[qb] ? qc % a.group : 0))) * D;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int c = c_first; c < NC; c += c_step) {
         const float4 u = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g);
         const float4 w = *reinterpret_cast<const float4*>(qp + 32 * c + 8 * g + 4);
         float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = qlive[qb] ? x[e] * a.scale2 : 0.f;
-        split3(x, qop[qb][c][0], qop[qb][c][1], qop[qb][c][2]);
+        put(qb, c, x);
       }
     }
+  }
+  if constexpr (QL) {
+    qop.base = qlds;
+    qop.lane = lane;
+    __syncthreads();   // the operand complete in LDS
   }
 
   ScanState<D, QB> st;
@@ -643,50 +805,76 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
 #pragma unroll
     for (int dd = 0; dd < ND; ++dd) st.acc[qb][dd] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  while (t < t_end) {
-    load(B, min(t + kWaves, t_last));
-    scan_tile<D, QB>(A, qop, lo, st, a.pos0);
-    t += kWaves;
-    if (t >= t_end) break;
-    load(A, min(t + kWaves, t_last));
-    scan_tile<D, QB>(B, qop, lo, st, a.pos0);
-    t += kWaves;
+  if constexpr (SKEW) {
+    (void)B;
+    while (t < t_end) {
+      const int tn = min(t + kWaves, t_last);
+      __asm__ volatile("" ::: "memory");   // keeps the q operand's LDS reads inside the loop
+      if constexpr (F8)
+        scan_tile<D, QB>(
+            A, qop, lo, st, a.pos0, [&](Tile& T) { load_tile_k<D>(T, kbase, a.slot_pos, ksb, tn, lane); },
+            [&](Tile& T) { load_tile_v<D>(T, vbase, vsb, tn, lane); });
+      else
+        scan_tile_skewed<D, QB>(
+            A, qop, lo, st, a.pos0, [&](Tile& T) { load_tile_k<D>(T, kbase, a.slot_pos, tn, lane); },
+            [&](Tile& T) { load_tile_v<D>(T, vbase, tn, lane); });
+      t += kWaves;
+    }
+  } else {
+    while (t < t_end) {
+      load(B, min(t + kWaves, t_last));
+      if constexpr (QL) __asm__ volatile("" ::: "memory");
+      scan_tile<D, QB>(A, qop, lo, st, a.pos0);
+      t += kWaves;
+      if (t >= t_end) break;
+      load(A, min(t + kWaves, t_last));
+      if constexpr (QL) __asm__ volatile("" ::: "memory");
+      scan_tile<D, QB>(B, qop, lo, st, a.pos0);
+      t += kWaves;
+    }
   }
 
   // merge the 4 waves' states in LDS: (max, sum) as [wave][qb][2][16 cols], then accumulators
-  // [wave][qb][dd][64 lanes][4]
-  float* ml = lds;
-  float* accs = lds + kWaves * QB * 2 * 16;
+  // [wave][qb][dd][64 lanes][4], NDP dim blocks at a time (one pass for heads of up to 128 dims)
+  constexpr int MP = scan_merge_passes<D>(), NDP = ND / MP;
+  float* ml = lds + scan_qop_floats<D, QB>();
+  float* accs = ml + kWaves * QB * 2 * 16;   // QL: the region the q-cols were processed in (read before the barrier
+                                             // that completed the operand)
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    if (g == 0) {
-      ml[((wave * QB + qb) * 2 + 0) * 16 + j] = st.m[qb];
-      ml[((wave * QB + qb) * 2 + 1) * 16 + j] = st.l[qb];
-    }
+  for (int pass = 0; pass < MP; ++pass) {
+    if (pass > 0) __syncthreads();   // the previous pass's reads are done
 #pragma unroll
-    for (int dd = 0; dd < ND; ++dd)
-      *reinterpret_cast<f32x4*>(accs + ((size_t(wave * QB + qb) * ND + dd) * 64 + lane) * 4) = st.acc[qb][dd];
-  }
-  __syncthreads();
-  // wave w finishes q-block w: the partial (max, sum, accumulator[D]) of each live q-col
-  for (int qb = wave; qb < QB; qb += kWaves) {
-    const int qc = qb * 16 + j;
-    float M = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[((w * QB + qb) * 2 + 0) * 16 + j]);
-    float L = 0.f, f[kWaves];
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = ml[((w * QB + qb) * 2 + 0) * 16 + j];
-      f[w] = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
-      L += f[w] * ml[((w * QB + qb) * 2 + 1) * 16 + j];
+    for (int qb = 0; qb < QB; ++qb) {
+      if (g == 0 && pass == 0) {
+        ml[((wave * QB + qb) * 2 + 0) * 16 + j] = st.m[qb];
+        ml[((wave * QB + qb) * 2 + 1) * 16 + j] = st.l[qb];
+      }
+#pragma unroll
+      for (int dd = 0; dd < NDP; ++dd)
+        *reinterpret_cast<f32x4*>(accs + ((size_t(wave * QB + qb) * NDP + dd) * 64 + lane) * 4) =
+            st.acc[qb][pass * NDP + dd];
     }
-    if (qc >= qcols) continue;
-    const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(split)) * size_t(a.qpad) + size_t(qc);
-    if (g == 0) *reinterpret_cast<float2*>(ml_out + rec * 2) = make_float2(M, L);
-    for (int dd = 0; dd < ND; ++dd) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int w = 0; w < kWaves; ++w)
-        s += f[w] * *reinterpret_cast<const f32x4*>(accs + ((size_t(w * QB + qb) * ND + dd) * 64 + lane) * 4);
-      *reinterpret_cast<f32x4*>(acc_out + rec * D + 16 * dd + 4 * g) = s;
+    __syncthreads();
+    // wave w finishes q-block w: the partial (max, sum, accumulator[D]) of each live q-col
+    for (int qb = wave; qb < QB; qb += kWaves) {
+      const int qc = qb * 16 + j;
+      float M = -INFINITY;
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[((w * QB + qb) * 2 + 0) * 16 + j]);
+      float L = 0.f, f[kWaves];
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = ml[((w * QB + qb) * 2 + 0) * 16 + j];
+        f[w] = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
+        L += f[w] * ml[((w * QB + qb) * 2 + 1) * 16 + j];
+      }
+      if (qc >= qcols) continue;
+      const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(split)) * size_t(a.qpad) + size_t(qc);
+      if (g == 0 && pass == 0) *reinterpret_cast<float2*>(ml_out + rec * 2) = make_float2(M, L);
+      for (int dd = 0; dd < NDP; ++dd) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kWaves; ++w)
+          s += f[w] * *reinterpret_cast<const f32x4*>(accs + ((size_t(w * QB + qb) * NDP + dd) * 64 + lane) * 4);
+        *reinterpret_cast<f32x4*>(acc_out + rec * D + 16 * (pass * NDP + dd) + 4 * g) = s;
+      }
     }
   }
 }
@@ -702,14 +890,18 @@ __global__ void __launch_bounds__(kWaves * 64) attn_scan_kernel(const ScanArgs a
 // The online-softmax state of one q-col over own keys j0 .. j1 - 1 (kv.cpp:214-243 with this call's FP32 rows),
 // computed by one wave. Scores: lane (key slot kk = lane / 8, part p = lane % 8) dots D / 8 dims of q with the same
 // dims of key jb + kk, the 8 lanes of a slot add up with three DPP steps, and each slot's score is read out as a
-// wave-uniform value. Outputs: lane l holds dims l mod (D / 2) and that + D / 2 (a0, a1). q at qp, key / value
-// rows at kb + j * stride, vb + j * stride; every load index is clamped into the rows, so none sits behind a
-// branch. Scores are in the base-2 domain (scale2 = scale * log2 e).
+// wave-uniform value. Outputs: lane l holds the OWN_NA<D> dims (l mod OWN_STRIDE<D>) + OWN_STRIDE<D> u (a[u]). q at
+// qp, key / value rows at kb + j * stride, vb + j * stride; every load index is clamped into the rows, so none sits
+// behind a branch. Scores are in the base-2 domain (scale2 = scale * log2 e).
+template <int D>
+constexpr int own_na() { return D / 64 > 2 ? D / 64 : 2; }
+template <int D>
+constexpr int own_stride() { return D / own_na<D>(); }
 template <int D>
 __device__ inline void own_state(const float* qp, const float* kb, const float* vb, size_t stride, int j0, int j1,
-                                 float scale2, float& M, float& L, float& a0, float& a1) {
-  constexpr int P = D / 8;
-  const int lane = threadIdx.x & 63, slot = lane >> 3, part = lane & 7, l = lane & (D / 2 - 1);
+                                 float scale2, float& M, float& L, float (&a)[own_na<D>()]) {
+  constexpr int P = D / 8, NA = own_na<D>(), SD = own_stride<D>();
+  const int lane = threadIdx.x & 63, slot = lane >> 3, part = lane & 7, l = lane & (SD - 1);
   float q[P];
 #pragma unroll
   for (int e = 0; e < P; e += 4) {
@@ -724,12 +916,12 @@ __device__ inline void own_state(const float* qp, const float* kb, const float* 
       const float4 t = *reinterpret_cast<const float4*>(kr + e);
       dot += q[e] * t.x + q[e + 1] * t.y + q[e + 2] * t.z + q[e + 3] * t.w;
     }
-    float v0[8], v1[8];
+    float vv[8][NA];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const size_t r = size_t(min(jb + u, j1 - 1)) * stride;
-      v0[u] = vb[r + l];
-      v1[u] = vb[r + l + D / 2];
+#pragma unroll
+      for (int n = 0; n < NA; ++n) vv[u][n] = vb[r + l + n * SD];
     }
     dot += dpp<kDppXor1>(dot);
     dot += dpp<kDppXor2>(dot);
@@ -744,25 +936,27 @@ __device__ inline void own_state(const float* qp, const float* kb, const float* 
     const float mn = fmaxf(M, bm);   // finite: the batch holds at least one key
     const float corr = exp2_fast(M - mn);
     L *= corr;
-    a0 *= corr;
-    a1 *= corr;
+#pragma unroll
+    for (int n = 0; n < NA; ++n) a[n] *= corr;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float w = exp2_fast(sj[u] - mn);   // 0 for a slot past j1 (score -inf)
       L += w;
-      a0 += w * v0[u];
-      a1 += w * v1[u];
+#pragma unroll
+      for (int n = 0; n < NA; ++n) a[n] += w * vv[u][n];
     }
     M = mn;
   }
 }
 
-__device__ inline void write_partial(float* acc, float* ml, size_t rec, int d, float M, float L, float a0, float a1) {
+template <int D>
+__device__ inline void write_partial(float* acc, float* ml, size_t rec, float M, float L,
+                                     const float (&a)[own_na<D>()]) {
   const int l = threadIdx.x & 63;
   if (l == 0) *reinterpret_cast<float2*>(ml + rec * 2) = make_float2(M, L);
-  if (l < d / 2) {
-    acc[rec * d + l] = a0;
-    acc[rec * d + l + d / 2] = a1;
+  if (l < own_stride<D>()) {
+#pragma unroll
+    for (int n = 0; n < own_na<D>(); ++n) acc[rec * D + l + n * own_stride<D>()] = a[n];
   }
 }
 
@@ -926,6 +1120,7 @@ constexpr int prod_lds_floats() { return (kProdGroup + 2 * kProdRows) * D + 2 * 
 template <int D, int VPW>
 __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* lds) {
   constexpr int HALF = D / 2;
+  constexpr int PR = HALF > 64 ? HALF / 64 : 1;   // RoPE pairs (i, i + HALF) per lane: i = l + 64 u
   constexpr int kT = kWaves * 64;
   float* sq = lds;
   float* sk = sq + kProdGroup * D;
@@ -941,7 +1136,7 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
   const long long slot_r = a.ring ? (a.pos0 + r) % a.slots : a.pos0 + r;
 
   // every load first, each at an index clamped into its buffer (no load behind a branch)
-  float x1[VPW], x2[VPW], s1[VPW], s2[VPW];
+  float x1[VPW][PR], x2[VPW][PR], s1[VPW][PR], s2[VPW][PR];
 #pragma unroll
   for (int it = 0; it < VPW; ++it) {
     const int idx = min(wave + it * kWaves, nv - 1);
@@ -949,12 +1144,15 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
     const int h = kvh * a.group + (is_q ? idx : 0);
     const float* p = is_q ? a.q + (size_t(r) * size_t(a.heads) + size_t(h)) * D
                           : a.k + (size_t(j0 + idx - a.group) * size_t(a.kv_heads) + size_t(kvh)) * D;
-    x1[it] = p[l];
-    x2[it] = p[l + HALF];
-    s1[it] = s2[it] = 1.f;
-    if (a.qscale && is_q) {
-      s1[it] = a.qscale[size_t(h) * D + l];
-      s2[it] = a.qscale[size_t(h) * D + l + HALF];
+#pragma unroll
+    for (int u = 0; u < PR; ++u) {
+      x1[it][u] = p[l + 64 * u];
+      x2[it][u] = p[l + 64 * u + HALF];
+      s1[it][u] = s2[it][u] = 1.f;
+      if (a.qscale && is_q) {
+        s1[it][u] = a.qscale[size_t(h) * D + l + 64 * u];
+        s2[it][u] = a.qscale[size_t(h) * D + l + 64 * u + HALF];
+      }
     }
   }
   constexpr int kAngles = (kProdRows * HALF + kT - 1) / kT;
@@ -997,35 +1195,51 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
     const int ic = min(idx, nv - 1);
     const bool is_q = ic < a.group;
     const int t = is_q ? nk - 1 : ic - a.group;   // table row: row r for q, row j0 + t for k
-    const float c = scos[t * HALF + l], s = ssin[t * HALF + l];
-    float o1 = x1[it] * c - x2[it] * s;
-    float o2 = x2[it] * c + x1[it] * s;
-    const float f = inv_norm_of(wave_sum(on ? o1 * o1 + o2 * o2 : 0.f));
-    o1 *= f;
-    o2 *= f;
+    float o1[PR], o2[PR], ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < PR; ++u) {
+      const float c = scos[t * HALF + l + 64 * u], s = ssin[t * HALF + l + 64 * u];
+      o1[u] = x1[it][u] * c - x2[it][u] * s;
+      o2[u] = x2[it][u] * c + x1[it][u] * s;
+      ss += o1[u] * o1[u] + o2[u] * o2[u];
+    }
+    const float f = inv_norm_of(wave_sum(on ? ss : 0.f));
+#pragma unroll
+    for (int u = 0; u < PR; ++u) {
+      o1[u] *= f;
+      o2[u] *= f;
+    }
     if (live && on && is_q) {   // q: times qscale, into LDS (and back in place)
-      o1 *= s1[it];
-      o2 *= s2[it];
-      if (a.write_q) {
-        float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + ic)) * D;
-        p[lane] = o1;
-        p[lane + HALF] = o2;
-      }
-      sq[ic * D + lane] = o1;
-      sq[ic * D + lane + HALF] = o2;
-    } else if (live && on) {   // k row j0 + t into LDS; row r's to kout and the cache
-      sk[t * D + lane] = o1;
-      sk[t * D + lane + HALF] = o2;
-      if (t == nk - 1) {
-        if (a.kout) {
-          float* p = a.kout + (size_t(r) * size_t(a.kv_heads) + size_t(kvh)) * D;
-          p[lane] = o1;
-          p[lane + HALF] = o2;
+      float* p = a.q + (size_t(r) * size_t(a.heads) + size_t(kvh * a.group + ic)) * D;
+#pragma unroll
+      for (int u = 0; u < PR; ++u) {
+        const int i = lane + 64 * u;
+        o1[u] *= s1[it][u];
+        o2[u] *= s2[it][u];
+        if (a.write_q) {
+          p[i] = o1[u];
+          p[i + HALF] = o2[u];
         }
-        if (a.store && !a.fp8) {
-          uint16_t* ck = static_cast<uint16_t*>(a.ck);
-          ck[k_index(kvh, int(slot_r), lane, a.slots_pad, D)] = f32_to_bf16_bits(o1);
-          ck[k_index(kvh, int(slot_r), lane + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2);
+        sq[ic * D + i] = o1[u];
+        sq[ic * D + i + HALF] = o2[u];
+      }
+    } else if (live && on) {   // k row j0 + t into LDS; row r's to kout and the cache
+#pragma unroll
+      for (int u = 0; u < PR; ++u) {
+        const int i = lane + 64 * u;
+        sk[t * D + i] = o1[u];
+        sk[t * D + i + HALF] = o2[u];
+        if (t == nk - 1) {
+          if (a.kout) {
+            float* p = a.kout + (size_t(r) * size_t(a.kv_heads) + size_t(kvh)) * D;
+            p[i] = o1[u];
+            p[i + HALF] = o2[u];
+          }
+          if (a.store && !a.fp8) {
+            uint16_t* ck = static_cast<uint16_t*>(a.ck);
+            ck[k_index(kvh, int(slot_r), i, a.slots_pad, D)] = f32_to_bf16_bits(o1[u]);
+            ck[k_index(kvh, int(slot_r), i + HALF, a.slots_pad, D)] = f32_to_bf16_bits(o2[u]);
+          }
         }
       }
     }
@@ -1042,12 +1256,12 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
 
   // own keys: q-col (r, hg) sees keys j0 .. r
   for (int hg = wave; hg < a.group; hg += kWaves) {
-    float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
-    own_state<D>(sq + hg * D, sk, sv, D, 0, nk, a.scale * kLog2e, M, L, a0, a1);
+    float M = -INFINITY, L = 0.f, acc[own_na<D>()] = {};
+    own_state<D>(sq + hg * D, sk, sv, D, 0, nk, a.scale * kLog2e, M, L, acc);
     const int blk = r / a.rpb, qc = (r % a.rpb) * a.group + hg;
     const size_t rec = size_t(blk) * a.blk_records + (size_t(kvh) * size_t(a.splits1) + size_t(a.splits)) * size_t(a.qpad) +
                        size_t(qc);
-    write_partial(a.acc, a.ml, rec, D, M, L, a0, a1);
+    write_partial<D>(a.acc, a.ml, rec, M, L, acc);
   }
 }
 
@@ -1202,7 +1416,8 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
 // ------------------------------------------------------------------------------------------------------- plan
 
 AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window) {
-  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "attention: head_dim %d (64 or 128)", c.head_dim);
+  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "attention: head_dim %d (64, 128 or 256)",
+            c.head_dim);
   XTG_CHECK(heads % c.kv_heads == 0, "attention: %d heads over %d KV heads", heads, c.kv_heads);
   const int group = heads / c.kv_heads;
   XTG_CHECK(group <= 8, "attention: %d query heads per KV head (at most 8)", group);
@@ -1282,8 +1497,19 @@ ScanFn scan_fn(int d, int qb, bool f8) {
   if (d == D && qb == Q && f8 == F) return attn_scan_kernel<D, Q, F>;
   XTG_CASE(64, 1, false) XTG_CASE(64, 2, false) XTG_CASE(128, 1, false) XTG_CASE(128, 2, false)
   XTG_CASE(64, 1, true) XTG_CASE(64, 2, true) XTG_CASE(128, 1, true) XTG_CASE(128, 2, true)
+  XTG_CASE(256, 1, false) XTG_CASE(256, 2, false) XTG_CASE(256, 1, true) XTG_CASE(256, 2, true)
 #undef XTG_CASE
   return nullptr;
+}
+
+// LDS bytes of a scan launch (raw q rows: the fused decode step's)
+size_t scan_lds_bytes(int d, int qb, bool rawq) {
+#define XTG_LDS(D, Q)                                                                             \
+  if (d == D && qb == Q)                                                                          \
+    return size_t(rawq ? scan_lds_floats<D, Q, true>() : scan_lds_floats<D, Q, false>()) * sizeof(float);
+  XTG_LDS(64, 1) XTG_LDS(64, 2) XTG_LDS(128, 1) XTG_LDS(128, 2) XTG_LDS(256, 1) XTG_LDS(256, 2)
+#undef XTG_LDS
+  fail("attention: no scan for head_dim %d and %d column blocks", d, qb);
 }
 
 // The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks (gfx950
@@ -1410,8 +1636,7 @@ std::string launch_attn_scan(const DevKv& c, const AttnPlan& p, int b0, int nblo
   const int qb = (nr * p.group + 15) / 16;
   ScanFn fn = scan_fn(c.head_dim, qb, c.fp8);
   XTG_CHECK(fn != nullptr, "attention: no kernel for head_dim %d and %d column blocks", c.head_dim, qb);
-  const int nd = c.head_dim / 16;
-  const size_t lds = (size_t(kWaves) * qb * 2 * 16 + size_t(kWaves) * qb * nd * 64 * 4) * sizeof(float);
+  const size_t lds = scan_lds_bytes(c.head_dim, qb, false);
   allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(c.kv_heads * p.splits), unsigned(nblocks)), dim3(kWaves * 64), lds, stream, a);
   HIP_CHECK(hipGetLastError());
@@ -1446,8 +1671,10 @@ std::string launch_attn_own(const AttnPlan& p, int b0, int nblocks, const float*
   const dim3 grid{unsigned((waves + 3) / 4)}, block{256};
   if (p.d == 64)
     hipLaunchKernelGGL(attn_own_mfma_kernel<64>, grid, block, 0, stream, a);
-  else
+  else if (p.d == 128)
     hipLaunchKernelGGL(attn_own_mfma_kernel<128>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(attn_own_mfma_kernel<256>, grid, block, 0, stream, a);
   HIP_CHECK(hipGetLastError());
   return strf("attn_own_mfma_kernel<%d>", p.d);
 }
@@ -1457,8 +1684,10 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
   const MergeArgs a = merge_args(p, heads, part);
   if (p.d == 64)
     hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(unsigned(n_q)), dim3(kMergeThreads), 0, stream, a, out);
-  else
+  else if (p.d == 128)
     hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(unsigned(n_q)), dim3(kMergeThreads), 0, stream, a, out);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(unsigned(n_q)), dim3(kMergeThreads), 0, stream, a, out);
   HIP_CHECK(hipGetLastError());
   return strf("attn_merge_kernel<%d>", p.d);
 }
@@ -1472,9 +1701,9 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const
   const dim3 grid{unsigned(c.kv_heads * m)}, block{unsigned(kWaves * 64)};
 #define XTG_PROD(D, V) \
   if (c.head_dim == D && vpw == V) hipLaunchKernelGGL((qk_produce_kernel<D, V>), grid, block, 0, stream, a);
-  XTG_PROD(64, 2) XTG_PROD(64, 4) XTG_PROD(128, 2) XTG_PROD(128, 4)
+  XTG_PROD(64, 2) XTG_PROD(64, 4) XTG_PROD(128, 2) XTG_PROD(128, 4) XTG_PROD(256, 2) XTG_PROD(256, 4)
 #undef XTG_PROD
-  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "producer: head_dim %d", c.head_dim);
+  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "producer: head_dim %d", c.head_dim);
   HIP_CHECK(hipGetLastError());
   return strf("qk_produce_kernel<%d, %d>", c.head_dim, vpw);
 }
@@ -1490,7 +1719,7 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
   XTG_CHECK(attn_step_fuses(p, m), "attention step: %d rows in %d blocks, %d splits: no fused launch", m, p.blocks,
             p.splits);
   XTG_CHECK(p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
-  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128, "attention step: head_dim %d", c.head_dim);
+  XTG_CHECK(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "attention step: head_dim %d", c.head_dim);
   XTG_CHECK(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(qscale) % 16 == 0,
             "attention step: q and qscale must be 16-byte aligned");
   ScanArgs a = scan_args(c, p, 0, q, m, heads, pos0, window, scale, part);
@@ -1505,7 +1734,7 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
 #define XTG_STEP(D, Q, F, V)                                                                                   \
   if (!done && c.head_dim == D && qb == Q && c.fp8 == F && vpw == V) {                                         \
     auto fn = attn_step_kernel<D, Q, F, V>;                                                                    \
-    const size_t lds = size_t(std::max(scan_lds_floats<D, Q, true>(), prod_lds_floats<D>())) * sizeof(float);   \
+    const size_t lds = std::max(scan_lds_bytes(D, Q, true), size_t(prod_lds_floats<D>()) * sizeof(float));     \
     allow_lds(reinterpret_cast<const void*>(fn), lds);                                                         \
     hipLaunchKernelGGL(fn, grid, block, lds, stream, a, pa);                                                   \
     done = true;                                                                                               \
@@ -1513,7 +1742,7 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
 #define XTG_STEP_D(D) \
   XTG_STEP(D, 1, false, 2) XTG_STEP(D, 1, false, 4) XTG_STEP(D, 2, false, 2) XTG_STEP(D, 2, false, 4) \
   XTG_STEP(D, 1, true, 2) XTG_STEP(D, 1, true, 4) XTG_STEP(D, 2, true, 2) XTG_STEP(D, 2, true, 4)
-  XTG_STEP_D(64) XTG_STEP_D(128)
+  XTG_STEP_D(64) XTG_STEP_D(128) XTG_STEP_D(256)
 #undef XTG_STEP_D
 #undef XTG_STEP
   XTG_CHECK(done, "attention step: no kernel for head_dim %d, %d column blocks, %d rows per wave", c.head_dim, qb,
@@ -1545,6 +1774,7 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
     u = U;                                                                                                  \
   }
   XTG_GATE(64, 1) XTG_GATE(64, 2) XTG_GATE(64, 4) XTG_GATE(128, 1) XTG_GATE(128, 2) XTG_GATE(128, 4)
+  XTG_GATE(256, 1) XTG_GATE(256, 2) XTG_GATE(256, 4)
 #undef XTG_GATE
   XTG_CHECK(u != 0, "attention gate: %d heads of %d", heads, p.d);
   HIP_CHECK(hipGetLastError());

@@ -301,7 +301,8 @@ void Backend::matmul_bf16(const xtg_bf16& w, const float* x, int m, float* y) {
 DevKv* Backend::kv_create(int kv_heads, int head_dim, long long slots, int ring, int dtype) {
   XTG_CHECK(!capturing_, "kv_create: not during a graph capture");
   XTG_CHECK(dtype == XTG_KV_BF16 || dtype == XTG_KV_FP8, "kv_create: unknown KV dtype %d", dtype);
-  XTG_CHECK(head_dim == 64 || head_dim == 128, "kv_create: head_dim %d (64 or 128)", head_dim);
+  XTG_CHECK(head_dim == 64 || head_dim == 128 || head_dim == 256, "kv_create: head_dim %d (64, 128 or 256)",
+            head_dim);
   XTG_CHECK(kv_heads > 0, "kv_create: %d KV heads", kv_heads);
   const long long n = ring > 0 ? ring : slots;   // kv.cpp:42-44: ring > 0 gives a ring of `ring` slots
   XTG_CHECK(n > 0 && n < (1LL << 30), "kv_create: %lld slots", n);

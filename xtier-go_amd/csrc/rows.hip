@@ -26,7 +26,7 @@ namespace xtg::hip {
 constexpr int kNormThreads = 512;
 constexpr int kNormRed = 2 * kNormThreads / 64;
 
-// One wave per (row, head): thread i holds the pair (i, i + d/2); d <= 128.
+// One wave per (row, head): thread t holds the pairs (i, i + d/2) for i = t + 64 u < d/2; d <= 256.
 __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q, float* __restrict__ k, int m,
                                                           int heads, int kv_heads, int d, long long pos0,
                                                           const float* __restrict__ inv_freq,
@@ -36,25 +36,33 @@ __global__ void __launch_bounds__(64) qk_rope_norm_kernel(float* __restrict__ q,
   const bool is_q = hh < heads;
   const int h = is_q ? hh : hh - heads;
   float* v = is_q ? q + (size_t(row) * heads + h) * d : k + (size_t(row) * kv_heads + h) * d;
-  const int half = d / 2, i = threadIdx.x;
-  float o1 = 0.f, o2 = 0.f;
-  if (i < half) {
-    const float ang = float(pos0 + row) * inv_freq[i];
-    const float c = cosf(ang), s = sinf(ang);
-    const float x1 = v[i], x2 = v[i + half];
-    o1 = x1 * c - x2 * s;
-    o2 = x2 * c + x1 * s;
-  }
-  const float f = inv_norm_of(wave_sum(o1 * o1 + o2 * o2));
-  if (i < half) {
-    o1 *= f;
-    o2 *= f;
-    if (is_q && qscale) {
-      o1 *= qscale[h * d + i];
-      o2 *= qscale[h * d + i + half];
+  const int half = d / 2;
+  float o1[2] = {0.f, 0.f}, o2[2] = {0.f, 0.f}, ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = int(threadIdx.x) + 64 * u;
+    if (i < half) {
+      const float ang = float(pos0 + row) * inv_freq[i];
+      const float c = cosf(ang), s = sinf(ang);
+      const float x1 = v[i], x2 = v[i + half];
+      o1[u] = x1 * c - x2 * s;
+      o2[u] = x2 * c + x1 * s;
+      ss += o1[u] * o1[u] + o2[u] * o2[u];
     }
-    v[i] = o1;
-    v[i + half] = o2;
+  }
+  const float f = inv_norm_of(wave_sum(ss));
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = int(threadIdx.x) + 64 * u;
+    if (i < half) {
+      float a = o1[u] * f, b = o2[u] * f;
+      if (is_q && qscale) {
+        a *= qscale[h * d + i];
+        b *= qscale[h * d + i + half];
+      }
+      v[i] = a;
+      v[i + half] = b;
+    }
   }
 }
 
@@ -285,7 +293,7 @@ Operand operand_of(void* op, int rows, int w) {
 
 std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0,
                                 const float* inv_freq, const float* qscale, hipStream_t stream) {
-  XTG_CHECK(d % 2 == 0 && d <= 128, "rope: head_dim %d (even, at most 128)", d);
+  XTG_CHECK(d % 2 == 0 && d <= 256, "rope: head_dim %d (even, at most 256)", d);
   hipLaunchKernelGGL(qk_rope_norm_kernel, dim3(unsigned(m * (heads + kv_heads))), dim3(64), 0, stream, q, k, m, heads,
                      kv_heads, d, pos0, inv_freq, qscale);
   HIP_CHECK(hipGetLastError());
