@@ -59,28 +59,240 @@ def call_bytes(ws, m):
     return sum(n * k // 2 + n * k // 16 + 4 for n, _ in ws) + 2 * m * k + 4 * m * sum(n for n, _ in ws)
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline rows."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(base, xs, seconds):
-    """The reference's CPU matmul_nvfp4 (or the oracle) over the step's 6 calls, until `seconds` have passed."""
+    """The reference's CPU matmul_nvfp4 (or the oracle) over the step's 6 calls, until `seconds` have passed, on
+    all the host's threads; then the same on one thread for a quarter of that time."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     use_ref = orc.ref_available()
-    threads = os.cpu_count() or 1
     ws_by = {name: [(w.codes, w.scales, w.glob) for w in base[name]] for name, _ in SHAPES}
     calls = [(name, m) for m in ROWS for name, _ in SHAPES]
-    orc.matmul_nvfp4(ws_by[calls[0][0]], xs[calls[0]], threads=threads, use_ref=use_ref)   # warm-up
-    done, nbytes, t0 = 0, 0, time.perf_counter()
-    while True:
-        for name, m in calls:
-            orc.matmul_nvfp4(ws_by[name], xs[(name, m)], threads=threads, use_ref=use_ref)
-            nbytes += call_bytes(dict(SHAPES)[name], m)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(nbytes / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "reference" if use_ref else "port",
+
+    def run(threads, secs):
+        orc.matmul_nvfp4(ws_by[calls[0][0]], xs[calls[0]], threads=threads, use_ref=use_ref)   # warm-up
+        done, nbytes, t0 = 0, 0, time.perf_counter()
+        while True:
+            for name, m in calls:
+                orc.matmul_nvfp4(ws_by[name], xs[(name, m)], threads=threads, use_ref=use_ref)
+                nbytes += call_bytes(dict(SHAPES)[name], m)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= secs:
+                return nbytes / el / 1e9, done, el
+
+    threads = os.cpu_count() or 1
+    gbs, done, el = run(threads, seconds)
+    gbs1, done1, el1 = run(1, seconds / 4)
+    model = cpu_model()
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads,
+            "kind": "reference" if use_ref else "port", "cpu": model,
             "sample": "%d passes over the step's 6 calls (QKV 5120, gate/up 2x8192, down 3072x8192 at M=1 and M=8, "
-                      "same weights and inputs, one weight copy), %.1f s on %d threads" % (done, el, threads)}
+                      "same weights and inputs, one weight copy), %.1f s on %d threads of %s" % (done, el, threads,
+                                                                                                 model),
+            "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                              "sample": "%d passes, %.1f s on one thread" % (done1, el1)}}
+
+
+# Configs 0 and 1 launch by launch: config 0's 3072x3072 GEMV and config 1's projections, including the QKV widths
+# 6144 (32 q + 2 x 8 KV heads of 128) and 10240 (the fused q/k/v/g), at every verify batch size.
+SWEEP = [("square3072", [(3072, 3072)]), ("qkv5120", [(5120, 3072)]), ("qkv6144", [(6144, 3072)]),
+         ("qkvg10240", [(10240, 3072)]), ("gateup2x8192", [(8192, 3072), (8192, 3072)]),
+         ("down3072x8192", [(3072, 8192)])]
+SWEEP_ROWS = (1, 2, 4, 8)
+
+
+def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
+    """Per (shape, rows): a graph of one xtg_hip_matmul_nvfp4_dev call (one GEMV launch) per weight copy, the copies
+    rotating over >= 1 GiB so each launch streams from HBM, replayed `reps` times between events on the backend's
+    stream; per launch: microseconds, algorithmic GB/s (call_bytes) and the fraction of the HBM peak. Config 0's
+    shape also on the CPU: the reference's matmul_nvfp4 on all threads and on one, on the same weights and row."""
+    rng = np.random.default_rng(20261205)
+    out = {}
+    for name, shapes in SWEEP:
+        base = [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes]
+        one = sum(w.codes.nbytes + w.scales.nbytes for w in base)
+        copies = max(2, -(-(1 << 30) // one) + 1)
+        sets = [[pkg.Weight(w.codes.copy(), w.scales.copy(), w.glob) for w in base] for _ in range(copies)]
+        for ws in sets:
+            for w in ws:
+                hip.prepare(w)
+        k = shapes[0][1]
+        xb = wl.unit_rows_bf16(rng, 8, k)
+        dx = hip.array(xb)
+        dy = hip.array(shape=(8 * sum(n for n, _ in shapes) + 64,))
+        for m in SWEEP_ROWS:
+            hip.matmul_dev(sets[0], dx, pkg.X_BF16, m, dy)   # sizes what the call needs before the capture
+            hip.finish()
+            hip.graph_begin()
+            for ws in sets:
+                hip.matmul_dev(ws, dx, pkg.X_BF16, m, dy)
+            label = "sweep_%s_m%d" % (name, m)
+            g = hip.graph_end(label)
+            hip.graph_launch(g)
+            hip.finish()
+            hip.profile(True)
+            for _ in range(reps):
+                hip.graph_launch(g)
+            t = hip.profile_report()[label]
+            hip.profile(False)
+            hip.graph_destroy(g)
+            us = t["ms"] * 1e3 / (t["calls"] * copies)
+            b = call_bytes(shapes, m)
+            out["%s_m%d" % (name, m)] = {"us_per_launch": round(us, 3), "bytes": b, "gbs": round(b / us / 1e3, 1),
+                                         "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log("GEMV sweep %-14s (%d copies): %s" % (name, copies, ", ".join(
+            "M=%d %.2f us %.0f GB/s" % (m, out["%s_m%d" % (name, m)]["us_per_launch"], out["%s_m%d" % (name, m)]["gbs"])
+            for m in SWEEP_ROWS)))
+        if name == "square3072" and cpu_seconds > 0:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle as orc
+            use_ref = orc.ref_available()
+            w = [(base[0].codes, base[0].scales, base[0].glob)]
+            x = wl.bf16_to_f32(xb[:1])
+            cpu = {}
+            for threads, secs in ((os.cpu_count() or 1, cpu_seconds), (1, cpu_seconds)):
+                orc.matmul_nvfp4(w, x, threads=threads, use_ref=use_ref)
+                n, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < secs:
+                    orc.matmul_nvfp4(w, x, threads=threads, use_ref=use_ref)
+                    n += 1
+                el = (time.perf_counter() - t0) / n
+                cpu["threads%d" % threads] = {"us": round(el * 1e6, 1), "gbs": round(call_bytes(shapes, 1) / el / 1e9, 3),
+                                              "calls": n}
+            cpu["kind"] = "reference" if use_ref else "port"
+            cpu["cpu"] = cpu_model()
+            out["square3072_cpu"] = cpu
+            log("config 0 on the CPU (%s): %s" % (cpu["kind"], ", ".join(
+                "%s %.1f us" % (kk, v["us"]) for kk, v in cpu.items() if kk.startswith("threads"))))
+        dx.free()
+        dy.free()
+        for ws in sets:
+            for w in ws:
+                hip.release_weight(w)
+        del sets
+    return out
+
+
+def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
+    """Configs 2 and 3 through xtg_hip_attention (own-key, scan and merge launches, each between events on the
+    backend's stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
+    - config 2: global caches of 4K / 8K / 32K positions, 1 and 8 new rows at positions ctx ..;
+    - config 3: a 1088-slot ring after 40000 decoded positions (slots hold 38912 .. 39999), window 1024, 1 and 8
+      rows at 40000 ..; the q / k producer (RoPE, per-head norm, qscale) timed beside it (xtg_hip_qk_rope_norm).
+    BF16 and FP8 caches. Each call reads one of `copies` caches with the same contents, rotating over >= 1 GiB so
+    every call streams the cache from HBM. Algorithmic bytes: the visible K and V (ctx positions, or the whole ring)
+    at 2 bytes (BF16) or 1 byte plus a 4-byte scale per (position, head) for each of K and V (FP8), plus q, the new k
+    and v, and out in FP32; the roofline fraction is that over the scan launch's time (the launch that streams the
+    cache). The reference's CPU attention (oracle/_ref) on the same inputs beside it."""
+    heads, kvh, d = 32, 8, 128
+    rng = np.random.default_rng(61)
+    out = {}
+    cases = [("ctx%d" % c, c, 0, 0) for c in (4096, 8192, 32768)] + [("ring1088", 40000, 1088, 1024)]
+    for fp8 in (False, True):
+        for label, ctx, ring, window in cases:
+            lo = ctx - ring if ring else 0
+            n_pos = ctx - lo
+            K = wl.unit_heads(rng, (n_pos, kvh), d)
+            V = wl.unit_heads(rng, (n_pos, kvh), d)
+            dK, dV = hip.array(K), hip.array(V)
+            per_pos = kvh * (2 * d + (8 if fp8 else 0)) if fp8 else kvh * d * 4
+            cache_bytes = (ring if ring else ctx) * per_pos
+            copies = max(2, -(-(1 << 30) // cache_bytes) + 1)
+            caches = []
+            for _ in range(copies):
+                c = hip.kv_cache(kvh, d, ctx + 8, ring=ring, dtype=1 if fp8 else 0)
+                for p in range(0, n_pos, 8192):
+                    n = min(8192, n_pos - p)
+                    c.store(lo + p, n, dK.ptr + p * kvh * d * 4, dV.ptr + p * kvh * d * 4)
+                caches.append(c)
+            hip.finish()
+            for n_q in (1, 8):
+                q = wl.unit_heads(rng, (n_q, heads), d)
+                kn = wl.unit_heads(rng, (n_q, kvh), d)
+                vn = wl.unit_heads(rng, (n_q, kvh), d)
+                dq, dk, dv, do = hip.array(q), hip.array(kn), hip.array(vn), hip.array(shape=(n_q, heads, d))
+                qs = hip.array(rng.uniform(0.5, 1.5, heads * d).astype(np.float32))
+                for c in caches[:2]:
+                    hip.attention(c, dq, dk, dv, do, n_q, ctx, heads, window=window)
+                hip.finish()
+                hip.profile(True)
+                for _ in range(reps):
+                    for c in caches:
+                        if ring:
+                            hip.qk_rope_norm(dq, dk, n_q, heads, kvh, d, ctx, 1e6, qs)
+                        hip.attention(c, dq, dk, dv, do, n_q, ctx, heads, window=window)
+                rep = hip.profile_report()
+                hip.profile(False)
+                calls = reps * copies
+                kern = {kk: round(v["ms"] * 1e3 / v["calls"], 3) for kk, v in rep.items()}
+                scan = [kk for kk in rep if kk.startswith("attn_scan_kernel")][0]
+                attn_us = sum(v["ms"] for kk, v in rep.items() if kk.startswith("attn_")) * 1e3 / calls
+                visible = ring if ring else ctx
+                b = visible * per_pos + 4 * d * (2 * heads * n_q + 2 * kvh * n_q)
+                key = "%s_%s_q%d" % ("fp8" if fp8 else "bf16", label, n_q)
+                out[key] = {"copies": copies, "bytes": b, "kernels_us": kern, "attention_us": round(attn_us, 3),
+                            "scan_gbs": round(b / kern[scan] / 1e3, 1),
+                            "frac": round(b / kern[scan] / 1e3 / HBM_PEAK_GBS, 4),
+                            "call_gbs": round(b / attn_us / 1e3, 1)}
+                log("attention %-4s %-9s n_q=%d: scan %.2f us (%.0f GB/s, %.1f%% of HBM peak), call %.2f us%s"
+                    % ("FP8" if fp8 else "BF16", label, n_q, kern[scan], b / kern[scan] / 1e3,
+                       b / kern[scan] / 1e3 / HBM_PEAK_GBS * 100, attn_us,
+                       (", producer %.2f us" % kern["qk_rope_norm_kernel"]) if ring else ""))
+                for a in (dq, dk, dv, do, qs):
+                    a.free()
+            for c in caches:
+                c.destroy()
+            dK.free()
+            dV.free()
+    if cpu_seconds > 0:
+        out["cpu"] = cpu_attention(wl, rng, cpu_seconds)
+    return out
+
+
+def cpu_attention(wl, rng, seconds):
+    """The reference's CPU attention (engine/src/kv.cpp:166-286, oracle/_ref; the oracle's restatement when that is
+    absent) on config 2 at 4K (1 and 8 rows) and config 3's ring (8 rows), BF16 caches, on all threads and on one."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    use_ref = orc.ref_available()
+    heads, kvh, d = 32, 8, 128
+    out = {"kind": "reference" if use_ref else "port", "cpu": cpu_model()}
+    per = seconds / 6
+    for label, ctx, ring, window, n_q in (("ctx4096_q1", 4096, 0, 0, 1), ("ctx4096_q8", 4096, 0, 0, 8),
+                                           ("ring1088_q8", 40000, 1088, 1024, 8)):
+        lo = ctx - ring if ring else 0
+        cache = orc.KvCache(kvh, d, ctx + 8, ring=ring, fp8=False, use_ref=use_ref)
+        for p in range(lo, ctx, 1024):
+            n = min(1024, ctx - p)
+            cache.store(p, wl.unit_heads(rng, (n, kvh), d), wl.unit_heads(rng, (n, kvh), d))
+        q = wl.unit_heads(rng, (n_q, heads), d)
+        k, v = wl.unit_heads(rng, (n_q, kvh), d), wl.unit_heads(rng, (n_q, kvh), d)
+        b = (ring if ring else ctx) * kvh * d * 4 + 4 * d * (2 * heads * n_q + 2 * kvh * n_q)
+        for threads in (os.cpu_count() or 1, 1):
+            orc.attention(q, k, v, cache, ctx, heads, kvh, d, window=window, pool_size=threads, threads=threads)
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < per or n == 0:
+                orc.attention(q, k, v, cache, ctx, heads, kvh, d, window=window, pool_size=threads, threads=threads)
+                n += 1
+            el = (time.perf_counter() - t0) / n
+            out["%s_threads%d" % (label, threads)] = {"us": round(el * 1e6, 1), "gbs": round(b / el / 1e9, 3),
+                                                      "calls": n}
+        del cache
+    log("attention on the CPU (%s): %s" % (out["kind"], ", ".join(
+        "%s %.0f us" % (kk, v["us"]) for kk, v in out.items() if isinstance(v, dict))))
+    return out
 
 
 COPY_BYTES = 256 << 20
@@ -612,6 +824,8 @@ def main():
         cpu = cpu_baseline(base, xs, args.cpu_seconds)
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
+    sweep = gemv_sweep(pkg, wl, hip, 5, 0 if args.no_cpu else 1.0)
+    attention = decode_attention_bench(pkg, wl, hip, 3, 0 if args.no_cpu else 6.0)
     bf16_head = bf16_head_bench(pkg, wl, hip, 10)
     sampling = sampling_bench(pkg, hip, 20)
     prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
@@ -657,6 +871,8 @@ def main():
                      "traffic": (int(sum(v["traffic"] for v in per_call.values()) / len(per_call))
                                  if all("traffic" in v for v in per_call.values()) else None)},
         "cpu_baseline": cpu,
+        "gemv_sweep": sweep,
+        "decode_attention": attention,
         "bf16_lm_head": bf16_head,
         "sampling": sampling,
         "prefill_gemm": prefill,

@@ -62,7 +62,8 @@ def fill_context(w, ctx, oracle_model, dev_model, hip, rng):
             continue
         lo = 0 if kind == 2 else max(0, ctx - ring)
         recurrent = c["n_in"] <= l < c["n_in"] + c["n_rec"]
-        for inst in range(c["loops"] if recurrent else 1):   # per-loop caches of a recurrent sublayer
+        per_loop = c.get("kv_mode", 0) == 0
+        for inst in range(c["loops"] if recurrent and per_loop else 1):   # per-loop caches of a recurrent sublayer
             oc = oracle_model.cache(a, inst)
             dc = dev_model.cache(a, inst)
             for p in range(lo, ctx, 1024):
@@ -103,6 +104,37 @@ def test_4b_decode_step(hip, model_4b, m):
     dl.free()
     e = rel_l2(got, want)
     print("4B step m=%d: logits rel-L2 %.2e" % (m, e))
+    assert e <= 1e-3
+    assert (got.argmax(1) == want.argmax(1)).all()
+
+
+@pytest.fixture(scope="module")
+def model_real(hip, orc, wl):
+    ctx = 4096
+    w = wl.DoryWeights(wl.DORY_REAL, seed=91, context=ctx + 64)
+    ref = orc.Dory(w, wl)
+    dev = hip.dory(w)
+    fill_context(w, ctx, ref, dev, hip, np.random.default_rng(92))
+    yield w, ref, dev, ctx
+    dev.destroy()
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_real_dory_shape_step(hip, model_real, m):
+    """The real Dory 4B's shape (hidden 2560, FFN 7168, 16 q / 4 KV heads of 256, 72 sublayers, two loops, FP8
+    caches in last_loop mode, BF16 head) at a 4K context: a decode and a verify step against the oracle."""
+    w, ref, dev, ctx = model_real
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    x = unit_rows(np.random.default_rng(90 + m), m, H)
+    dx = hip.array(x)
+    dl = hip.array(shape=(m, V))
+    dev.forward(dx, m, ctx, dl)
+    got = dl.numpy()
+    want = ref.forward(x, ctx, threads=16)
+    dx.free()
+    dl.free()
+    e = rel_l2(got, want)
+    print("real Dory shape, step m=%d at 4K: logits rel-L2 %.2e" % (m, e))
     assert e <= 1e-3
     assert (got.argmax(1) == want.argmax(1)).all()
 

@@ -123,6 +123,13 @@ MLP, SLIDING, FULL = 0, 1, 2
 # sublayer global and the others sliding (window 1024 in a 1088-slot ring), vocab 131072 with an NVFP4 head.
 DORY_4B = dict(hidden=3072, ffn=8192, heads=32, kv_heads=8, head_dim=128, vocab=131072, n_in=4, n_rec=40, n_out=4,
                loops=1, window=1024, ring_slots=1088, theta_sliding=1e6, theta_full=1e6)
+# The real Dory 4B's shape (docs/dory.md:12-15 of the reference): hidden 2560, FFN 7168, 16 q / 4 KV heads of 256,
+# 16 input / 40 recurrent / 16 output sublayers (9 of the 36 attention sublayers global), two loops, sliding window
+# 1024 in the CPU session's ring of window + 16 slots (packs/dory/dory.cpp:43, 449), RoPE theta 1e4 sliding / 1e7
+# global, FP8 caches in last_loop mode (the shipped card's defaults) and a BF16 LM head over 131072.
+DORY_REAL = dict(hidden=2560, ffn=7168, heads=16, kv_heads=4, head_dim=256, vocab=131072, n_in=16, n_rec=40,
+                 n_out=16, loops=2, window=1024, ring_slots=1040, theta_sliding=1e4, theta_full=1e7, kv_dtype=1,
+                 kv_mode=1, bf16_head=True)
 # A small model with the same structure for parity tests (two loops exercise the per-loop caches).
 DORY_TINY = dict(hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, n_in=2, n_rec=4, n_out=2,
                  loops=2, window=48, ring_slots=64, theta_sliding=1e4, theta_full=1e6)
@@ -158,6 +165,9 @@ class DoryWeights:
         def layer(i):   # every sublayer (and the head, i = len) draws from its own stream of the seed
             rng = np.random.default_rng([seed, i])
             if i == len(self.kinds):
+                if cfg.get("bf16_head"):   # a BF16 head as a checkpoint's lm_head.weight: N(0,1) rounded to BF16
+                    w = f32_to_bf16(rng.standard_normal((cfg["vocab"], H), dtype=np.float32))
+                    return w, rng.uniform(0.5, 1.5, cfg["vocab"]).astype(np.float32)
                 return nvfp4_weight(rng, cfg["vocab"], H), rng.uniform(0.5, 1.5, cfg["vocab"]).astype(np.float32)
             kind = self.kinds[i]
             L = {"kind": kind, "lr": rng.uniform(0.02, 0.1, H).astype(np.float32)}
@@ -179,12 +189,15 @@ class DoryWeights:
             parts = list(ex.map(layer, range(len(self.kinds) + 1)))
         self.layers = parts[:-1]
         self.head, self.logit_scale = parts[-1]
+        self.head_bf16 = None
+        if cfg.get("bf16_head"):
+            self.head_bf16, self.head = self.head, None
 
     def n_attn(self):
         return sum(1 for k in self.kinds if k != MLP)
 
     def weight_bytes(self):
-        b = self.head[0].nbytes + self.head[1].nbytes
+        b = self.head[0].nbytes + self.head[1].nbytes if self.head is not None else self.head_bf16.nbytes
         for L in self.layers:
             for name in ("q", "k", "v", "g", "o", "gate", "up", "down"):
                 if name in L:
