@@ -105,7 +105,7 @@ def cpu_baseline(base, xs, seconds):
                               "sample": "%d passes, %.1f s on one thread" % (done1, el1)}}
 
 
-# Configs 0 and 1 launch by launch: config 0's 3072x3072 GEMV and config 1's projections, including the QKV widths
+# The NVFP4 GEMV workloads launch by launch: the 3072x3072 GEMV and the 4B layer's projections, including the QKV widths
 # 6144 (32 q + 2 x 8 KV heads of 128) and 10240 (the fused q/k/v/g), at every verify batch size.
 SWEEP = [("square3072", [(3072, 3072)]), ("qkv5120", [(5120, 3072)]), ("qkv6144", [(6144, 3072)]),
          ("qkvg10240", [(10240, 3072)]), ("gateup2x8192", [(8192, 3072), (8192, 3072)]),
@@ -116,7 +116,7 @@ SWEEP_ROWS = (1, 2, 4, 8)
 def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
     """Per (shape, rows): a graph of one xtg_hip_matmul_nvfp4_dev call (one GEMV launch) per weight copy, the copies
     rotating over >= 1 GiB so each launch streams from HBM, replayed `reps` times between events on the backend's
-    stream; per launch: microseconds, algorithmic GB/s (call_bytes) and the fraction of the HBM peak. Config 0's
+    stream; per launch: microseconds, algorithmic GB/s (call_bytes) and the fraction of the HBM peak. The 3072x3072
     shape also on the CPU: the reference's matmul_nvfp4 on all threads and on one, on the same weights and row."""
     rng = np.random.default_rng(20261205)
     out = {}
@@ -174,7 +174,7 @@ def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
             cpu["kind"] = "reference" if use_ref else "port"
             cpu["cpu"] = cpu_model()
             out["square3072_cpu"] = cpu
-            log("config 0 on the CPU (%s): %s" % (cpu["kind"], ", ".join(
+            log("3072x3072 GEMV on the CPU (%s): %s" % (cpu["kind"], ", ".join(
                 "%s %.1f us" % (kk, v["us"]) for kk, v in cpu.items() if kk.startswith("threads"))))
         dx.free()
         dy.free()
@@ -186,10 +186,10 @@ def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
 
 
 def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
-    """Configs 2 and 3 through xtg_hip_attention (own-key, scan and merge launches, each between events on the
-    backend's stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
-    - config 2: global caches of 4K / 8K / 32K positions, 1 and 8 new rows at positions ctx ..;
-    - config 3: a 1088-slot ring after 40000 decoded positions (slots hold 38912 .. 39999), window 1024, 1 and 8
+    """Decode attention over global caches and sliding rings through xtg_hip_attention (own-key, scan and merge
+    launches, each between events on the backend's stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
+    - global caches of 4K / 8K / 32K positions, 1 and 8 new rows at positions ctx ..;
+    - a 1088-slot ring after 40000 decoded positions (slots hold 38912 .. 39999), window 1024, 1 and 8
       rows at 40000 ..; the q / k producer (RoPE, per-head norm, qscale) timed beside it (xtg_hip_qk_rope_norm).
     BF16 and FP8 caches. Each call reads one of `copies` caches with the same contents, rotating over >= 1 GiB so
     every call streams the cache from HBM. Algorithmic bytes: the visible K and V (ctx positions, or the whole ring)
@@ -263,7 +263,8 @@ def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
 
 def cpu_attention(wl, rng, seconds):
     """The reference's CPU attention (engine/src/kv.cpp:166-286, oracle/_ref; the oracle's restatement when that is
-    absent) on config 2 at 4K (1 and 8 rows) and config 3's ring (8 rows), BF16 caches, on all threads and on one."""
+    absent) on the 4K global cache (1 and 8 rows) and the 1088-slot ring (8 rows), BF16 caches, on all threads and
+    on one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     use_ref = orc.ref_available()
@@ -541,7 +542,7 @@ def prefill_run(pkg, hip, dev, w, rng, prompts):
 
 
 def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
-    """Config 4: the synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
+    """The synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
     row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
     synthetic context of unit-norm K / V rows; a replay re-decodes position ctx, so every replay is the same step."""
     ctx_max = max(contexts)

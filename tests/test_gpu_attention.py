@@ -110,7 +110,8 @@ def test_prefill_rows(hip, orc, cached, n_q, window, fp8):
 @pytest.mark.parametrize("ctx", [4096, 8192, 32768])
 @pytest.mark.parametrize("n_q", [1, 8])
 def test_decode_global_cache(hip, orc, ctx, n_q):
-    """Config 2: 32 q / 8 KV heads of 128, unit-norm K / V / q, BF16 cache of ctx positions, 1 or 8 new rows."""
+    """Global-cache decode attention: 32 q / 8 KV heads of 128, unit-norm K / V / q, BF16 cache of ctx positions,
+    1 or 8 new rows."""
     rng = np.random.default_rng(ctx + n_q)
     out, ref, _ = run_case(hip, orc, ctx, n_q, 0, 32, 8, 128, None, rng, unit=True)
     assert rel_l2(out, ref) <= 1e-5
@@ -118,7 +119,7 @@ def test_decode_global_cache(hip, orc, ctx, n_q):
 
 @pytest.mark.parametrize("ctx,n_q", [(4096, 1), (4096, 8), (32768, 1), (32768, 8)])
 def test_decode_global_cache_fp8(hip, orc, ctx, n_q):
-    """Config 2's shapes over an FP8 cache (the reference Dory's default KV dtype, dory.cpp:141)."""
+    """The global-cache shapes over an FP8 cache (the reference Dory's default KV dtype, dory.cpp:141)."""
     rng = np.random.default_rng(ctx + n_q + 1)
     out, ref, _ = run_case(hip, orc, ctx, n_q, 0, 32, 8, 128, None, rng, unit=True, fp8=True)
     assert rel_l2(out, ref) <= 1e-5
@@ -202,8 +203,8 @@ def test_decode_sharp_softmax(hip, orc, qmul):
 
 @pytest.mark.parametrize("window,fp8", [(1024, False), (1088, False), (1024, True)])
 def test_ring_wrapped_config3(hip, orc, wl, window, fp8):
-    """Config 3: a 1088-slot ring after 40000 positions (holding 38912..39999), 8 rows at 40000..40007, q and k
-    produced by RoPE (theta 1e6) -> per-head norm -> q * qscale ~ U(0.5, 1.5); the mask is rebuilt from the stored
+    """The sliding-window ring: a 1088-slot ring after 40000 positions (holding 38912..39999), 8 rows at
+    40000..40007, q and k produced by RoPE (theta 1e6) -> per-head norm -> q * qscale ~ U(0.5, 1.5); the mask is rebuilt from the stored
     slot positions. Compared with the oracle's position form and its slot form."""
     rng = np.random.default_rng(window)
     heads, kvh, d, ring, pos0, n_q = 32, 8, 128, 1088, 40000, 8

@@ -230,6 +230,36 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
     timed([&] { return launch_gemm(c, stream_); });
 }
 
+int Backend::matmul_fused(const xtg_nvfp4* ws, int nw, FusedGemv f, const void* op, int m, float* y) {
+  XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
+  XTG_CHECK(m == 1, "fused matmul: %d rows (one)", m);
+  XTG_CHECK(y, "matmul: NULL output");
+  if (f.in == kInOp && f.out == kOutPlain) {   // nothing rides on it: the plain GEMV
+    matmul_op(ws, nw, op, m, y, 0);
+    return 0;
+  }
+  const int k = ws[0].k;
+  GemvCall& c = f.c;
+  c.nw = nw;
+  size_t off = 0;
+  for (int i = 0; i < nw; ++i) {
+    XTG_CHECK(ws[i].k == k, "matmul: input widths differ (%d, %d)", ws[i].k, k);
+    c.w[i] = &prepare(ws[i]);
+    c.y_off[i] = off;
+    if (f.out != kOutSwiglu) off += size_t(m) * size_t(ws[i].n_out);
+  }
+  c.y = y;
+  c.m = m;
+  c.k = k;
+  if (f.in == kInOp) {
+    XTG_CHECK(op, "fused matmul: no operand");
+    c.xop = op;
+    c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
+  }
+  timed([&] { return launch_gemv_fused(f, stream_); });
+  return fused_gemv_groups(f);
+}
+
 // ------------------------------------------------------------------------------------------------ BF16 path
 
 const PackedBf16& Backend::prepare(const xtg_bf16& w) {

@@ -50,6 +50,10 @@ class Backend {
   void prep_x(const void* x, int x_dtype, int m, int k, void* op, float* copy = nullptr);   // copy: FP32 rows too
   void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
                  const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]
+  // The one-token decode step's projections with its norms riding on them (kernels.hpp FusedGemv; m = 1): the weights,
+  // m and the output y (consecutive [m][n_i] blocks; one [m][n] block for a SwiGLU pair) go into f.c; with kInOp,
+  // op is the prepared operand. Returns the launch's work-group count: the records a consumer takes.
+  int matmul_fused(const xtg_nvfp4* ws, int nw, FusedGemv f, const void* op, int m, float* y);
 
   // opencl.h:33, 35, 56: the BF16 weight path (keyed by w.data)
   const PackedBf16& prepare(const xtg_bf16& w);

@@ -3,6 +3,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <utility>
 
 #include "common.hpp"
 
@@ -90,6 +92,11 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
   };
   const size_t R = kChunkRows;
   x_ = scratch(R * H);
+  x2_ = scratch(R * H);
+  part_s_ = scratch(size_t(kMaxFusedGroups) * 5);
+  part_h_ = scratch(size_t(kMaxFusedGroups));
+  // XTG_DECODE_UNFUSED=1 runs one-token steps on the separate norm launches (the prefill path's), for comparison
+  fused_ = !std::getenv("XTG_DECODE_UNFUSED");
   input_ = scratch(R * H);
   state_ = scratch(R * H);
   proj_ = scratch(R * size_t(2 * Q + 2 * KV));
@@ -188,6 +195,78 @@ void DorySession::sublayer(Layer& L, int m, long long pos0, int inst, bool store
   b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
 }
 
+void DorySession::materialize(int m) {
+  if (!pend_) return;
+  b_.slerp_norm(x_, o_, pend_lr_, m, c_.hidden, op_h_);
+  pend_ = false;
+}
+
+void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, bool store) {
+  // packs/dory/dory.cpp:467-518 for one token: the slerp closing the previous sublayer is made by this sublayer's
+  // first projection, the SwiGLU norm by the down projection, and this sublayer's slerp is left to the next
+  const int Q = c_.heads * c_.head_dim, KV = c_.kv_heads * c_.head_dim;
+  auto input_side = [&](FusedGemv& f) {
+    if (!pend_) return;   // op_h_ holds x's operand
+    f.in = kInSlerp;
+    f.in_x = x_;
+    f.in_o = o_;
+    f.in_lr = pend_lr_;
+    f.in_part = part_s_;
+    f.in_groups = pend_groups_;
+    f.in_xout = x2_;
+  };
+  auto took_input = [&] {
+    if (!pend_) return;
+    std::swap(x_, x2_);   // the projection wrote the new residual
+    pend_ = false;
+  };
+  if (L.w.kind == XTG_DORY_MLP) {
+    const xtg_nvfp4 gu[2] = {L.w.gate, L.w.up};
+    FusedGemv g;
+    input_side(g);
+    g.out = kOutSwiglu;
+    g.out_sg = L.sg;
+    g.out_su = L.su;
+    g.out_part = part_h_;
+    const int groups = b_.matmul_fused(gu, 2, g, op_h_, m, gu_);   // h = silu(g sg) (u su) [m][F]
+    took_input();
+    FusedGemv d;
+    d.in = kInNorm;   // justnorm(h) as the operand
+    d.in_x = gu_;
+    d.in_part = part_h_;
+    d.in_groups = groups;
+    d.out = kOutSlerp;
+    d.out_x = x_;
+    d.out_lr = L.lr;
+    d.out_part = part_s_;
+    pend_groups_ = b_.matmul_fused(&L.w.down, 1, d, nullptr, m, o_);
+    pend_ = true;
+    pend_lr_ = L.lr;
+    return;
+  }
+  const xtg_nvfp4 qkvg[4] = {L.w.q, L.w.k, L.w.v, L.w.g};
+  FusedGemv p;
+  input_side(p);
+  b_.matmul_fused(qkvg, 4, p, op_h_, m, proj_);   // q [m][Q] | k [m][KV] | v [m][KV] | g [m][Q]
+  took_input();
+  float* q = proj_;
+  float* k = proj_ + size_t(m) * Q;
+  float* v = k + size_t(m) * KV;
+  float* g = v + size_t(m) * KV;
+  const bool sliding = L.w.kind == XTG_DORY_SLIDING;
+  const float scale = 1.f / std::sqrt(float(c_.head_dim));
+  b_.attn_step(this->cache(L.attn, inst), m, pos0, c_.heads, sliding ? c_.window : 0, scale,
+               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_, store);
+  FusedGemv o;
+  o.out = kOutSlerp;
+  o.out_x = x_;
+  o.out_lr = L.lr;
+  o.out_part = part_s_;
+  pend_groups_ = b_.matmul_fused(&L.w.o, 1, o, op_q_, m, o_);
+  pend_ = true;
+  pend_lr_ = L.lr;
+}
+
 void DorySession::run_chunk(const float* x, int m, long long pos0) {
   // packs/dory/dory.cpp:520-544 from the embedding rows; x's operand is in op_h_ on exit
   XTG_CHECK(m >= 1 && m <= kChunkRows, "dory: %d rows per chunk (1..%d)", m, kChunkRows);
@@ -201,8 +280,17 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
     b_.copy(x, 0, x_, 0, bytes);
     b_.prep_x(x_, XTG_X_F32, m, H, op_h_);
   }
+  const bool fused = fused_ && m == 1;   // several rows take the separate norm launches
+  pend_ = false;
+  auto run = [&](Layer& L, int inst, bool store) {
+    if (fused)
+      sublayer_decode(L, m, pos0, inst, store);
+    else
+      sublayer(L, m, pos0, inst, store);
+  };
   size_t l = 0;
-  for (; l < size_t(c_.n_in); ++l) sublayer(layers_[l], m, pos0, 0, true);
+  for (; l < size_t(c_.n_in); ++l) run(layers_[l], 0, true);
+  materialize(m);
   // the loops start from state = input = x: the first entry is justnorm(x + x) read in place, and input is kept
   // only for later entries; the last exit writes x in place (x = state = justnorm(x))
   if (c_.loops > 1) b_.copy(x_, 0, input_, 0, bytes);
@@ -212,10 +300,12 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
     // last_loop: every loop attends to the chunk's own keys, the cache keeps the last loop's (dory.cpp:534-537)
     const bool per_loop = c_.kv_mode == XTG_KV_PER_LOOP;
     for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r)
-      sublayer(layers_[r], m, pos0, per_loop ? i : 0, per_loop || last);
+      run(layers_[r], per_loop ? i : 0, per_loop || last);
+    materialize(m);
     b_.add_norm(x_, nullptr, last ? x_ : state_, m, H, last ? op_h_ : nullptr);   // state = justnorm(x)
   }
-  for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) sublayer(layers_[l], m, pos0, 0, true);
+  for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) run(layers_[l], 0, true);
+  materialize(m);
 }
 
 void DorySession::head(int r0, int rows, float* logits) {

@@ -49,6 +49,11 @@ class DorySession {
     float* lr = nullptr;
   };
   void sublayer(Layer& L, int m, long long pos0, int inst, bool store);
+  // the same for a decode or verify step (m <= 8) with the slerp and SwiGLU norms riding on the projections: after
+  // it the residual awaits its slerp (pend_), which the next sublayer's first projection (or materialize) makes
+  void sublayer_decode(Layer& L, int m, long long pos0, int inst, bool store);
+  // the awaited slerp as a launch of its own: x_ and op_h_ hold the residual's rows afterwards
+  void materialize(int m);
   void run_chunk(const float* x, int m, long long pos0);
   void head(int r0, int rows, float* logits);
   float* upload(const float* v, size_t n);
@@ -69,9 +74,15 @@ class DorySession {
   // the weights this session holds on the backend, once per use (a weight it found unprepared goes with the last
   // session holding it: the host arrays that key it may be freed and their addresses reused once it is gone)
   std::vector<const void*> held_;
-  // scratch for up to 512 rows (one chunk)
-  float *x_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
+  // scratch for up to 512 rows (one chunk); x_ / x2_ trade places when a projection writes the next residual
+  float *x_ = nullptr, *x2_ = nullptr, *input_ = nullptr, *state_ = nullptr, *proj_ = nullptr, *gu_ = nullptr,
         *o_ = nullptr;
+  // the fused one-token path: records of the slerp's and the SwiGLU's partial sums (kernels.hpp FusedGemv), and
+  // the residual awaiting its slerp (of o_ with pend_lr_, pend_groups_ records in part_s_)
+  float *part_s_ = nullptr, *part_h_ = nullptr;
+  bool fused_ = true, pend_ = false;
+  const float* pend_lr_ = nullptr;
+  int pend_groups_ = 0;
   // GEMV operands, each written by the kernel that produces its rows: x's (K = hidden; by the slerp / loop norms
   // or, for the first sublayer, prep_x), the gated attention's (K = heads * head_dim), the SwiGLU's (K = ffn)
   void* op_h_ = nullptr;

@@ -530,3 +530,404 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
 }
 
 }  // namespace xtg::hip
+
+// ----------------------------------------------------------------------------- fused decode-step projections
+
+namespace xtg::hip {
+
+struct FusedArgs {
+  GemvArgs g;
+  int in_groups;
+  const float* in_x;
+  const float* in_o;
+  const float* in_lr;
+  const float* in_part;
+  float* in_xout;
+  const float* out_x;
+  const float* out_lr;
+  const float* out_sg;
+  const float* out_su;
+  float* out_part;
+};
+
+// Unit rows take the operand exponent 2^14 (|x| <= 1 keeps |x 2^14| below f16's maximum).
+constexpr float kRowsUp = 16384.f, kRowsDown = 1.f / 16384.f;
+
+// LDS of a fused launch, in floats: the waves' accumulators [S][R][64][4], then each wave's staging of one
+// k-tile's live operand columns [S][4 steps][8 entries][8 f16].
+struct FusedLds {
+  int red, stage, total;
+  __host__ __device__ FusedLds(int S, int R, int in) {
+    red = 0;
+    stage = red + S * R * 256;
+    total = stage + (in != kInOp ? S * 128 : 0);
+  }
+};
+
+// Lanes of one wave passing values through LDS: a wave's LDS operations execute in issue order, so keeping the
+// compiler's order is enough.
+__device__ inline void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The row values one lane reads for the operand of a k-tile: inputs l and l + 64 of the tile, and lr of those
+// inputs; indices clamped into the row, so every load is issued before anything waits.
+struct TileRow {
+  float x[2], o[2], lr[2];
+};
+
+template <int IN>
+__device__ inline void load_row(const FusedArgs& f, int k, int kt, bool kt_ok, int lane, TileRow& r) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int kg = kt * kTileK + lane + 64 * h;
+    const int kc = kt_ok && kg < k ? kg : 0;
+    r.lr[h] = IN == kInSlerp ? f.in_lr[kc] : 0.f;
+    r.x[h] = f.in_x[kc];
+    r.o[h] = IN == kInSlerp ? f.in_o[kc] : 0.f;
+  }
+}
+
+// One k-tile's operand from the row into a wave's staging area, in operand order (input kk of column c at step
+// (kk / 8) % 4, entry 4 c + kk / 32, element kk % 8; the 8 entries of the two live columns per step), with the
+// row's factors fac. Work-group 0 also writes the slerp's x_new to in_xout.
+template <int IN>
+__device__ inline void stage_row(const FusedArgs& f, int k, int kt, bool kt_ok, int lane, const float (&fac)[3],
+                                 const TileRow& r, _Float16* st16) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int kk = lane + 64 * h, kg = kt * kTileK + kk;
+    const bool valid = kt_ok && kg < k;
+    float v;
+    if constexpr (IN == kInSlerp) {
+      const float ya = r.x[h] * fac[0], yb = r.o[h] * fac[1];
+      v = (ya + r.lr[h] * (yb - ya)) * fac[2];
+      if (valid && blockIdx.x == 0 && f.in_xout) f.in_xout[kg] = v;
+    } else {
+      v = r.x[h] * fac[0];
+    }
+    v = valid ? v : 0.f;
+    const float sc = v * kRowsUp;
+    const _Float16 hi = (_Float16)sc;
+    const _Float16 lo = (_Float16)(sc - (float)hi);
+    const int g = kk >> 5, t = (kk >> 3) & 3, e8 = kk & 7;
+    st16[(t * 8 + g) * 8 + e8] = hi;       // column 0: entry g
+    st16[(t * 8 + 4 + g) * 8 + e8] = lo;   // column 1: entry 4 + g
+  }
+}
+
+// The GEMV of gemv_kernel (prepared-operand form) for one activation row with the fused input and output sides of
+// kernels.hpp. The row's factors come from the producer's P records, laid out [Q][P]: every wave adds
+// them lane-strided, then across its lanes (the same order in every wave and work-group: identical factors), so
+// the launch has no barrier before its math. Every global load the prologue needs goes out first, the L2-resident
+// ones (records, row values, epilogue inputs) ahead of the weights from HBM (a wave's loads retire in order), and
+// none behind a branch (the compiler's wait counts after a branch assume its loads were not issued), so the
+// prologue waits for them alone. Every thread reaches every barrier.
+template <int R, int T, int MAXT, int IN, int OUT>
+__global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
+  const GemvArgs& a = f.g;
+  extern __shared__ f32x4 red[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  constexpr bool PAIR = OUT == kOutSwiglu;
+  constexpr int RB = PAIR ? R / 2 : R;   // row-blocks per weight: PAIR takes RB of gate and the same RB of up
+  static_assert(!PAIR || R % 2 == 0, "paired row-blocks");
+  constexpr bool ROWS = IN != kInOp;
+  constexpr int Q = IN == kInSlerp ? 5 : 1;   // quantities per record (input side)
+  constexpr int NI = Q == 5 ? 3 : 8;          // records per quantity a lane holds from the start (P <= 64 NI)
+  int wi = 0;
+  if constexpr (!PAIR)
+    while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+  const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * RB;
+  const int KT = a.kt, kt0 = wave * T;
+  const FusedLds L(S, R, IN);
+  float* ldsf = reinterpret_cast<float*>(red);
+
+  const int col = lane & 15, grp = lane >> 4;
+  const bool live_col = col < 2;   // the row's high and low operand columns
+  const int entry = 4 * col + grp;
+  const int P = f.in_groups;
+  // the records through a buffer resource: a load past them returns zero
+  const __amdgpu_buffer_rsrc_t rres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(f.in_part), (short)0, ROWS ? Q * P * 4 : 0, 0x00020000);
+  auto record = [&](int q, int p) {
+    const uint32_t off = p < P ? uint32_t((q * P + p) * 4) : 0x80000000u;
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, int(off), 0, 0));
+  };
+  float rv[ROWS ? Q : 1][ROWS ? NI : 1];
+  TileRow rows[ROWS ? T : 1];
+  if constexpr (ROWS) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) rv[q][i] = record(q, lane + 64 * i);
+#pragma unroll
+    for (int u = 0; u < T; ++u) load_row<IN>(f, a.k, kt0 + u, kt0 + u < KT, lane, rows[u]);
+  }
+  // the epilogue's inputs of this thread's output (below): sg, su (PAIR) or x, lr (slerp)
+  float ep_a = 0.f, ep_b = 0.f;
+  if constexpr (OUT != kOutPlain) {
+    const int b = rb0 + (int(threadIdx.x) >> 4), w0 = PAIR ? 0 : wi;
+    const int o_i = b * kTileRows + (int(threadIdx.x) & 15), n = a.n[w0];
+    const int oc = int(threadIdx.x) < RB * 16 && o_i < n ? o_i : 0;
+    ep_a = PAIR ? f.out_sg[oc] : f.out_x[oc];
+    ep_b = PAIR ? f.out_su[oc] : f.out_lr[oc];
+  }
+  uint4 xb[T][4];
+  uint4 cw[T][R];
+  uint32_t sw[T][R];
+  // the prepared operand through a buffer resource (zero past it: k-tiles past k, columns past the row)
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4*>(a.xop), (short)0, IN == kInOp ? KT * 4096 : 0, 0x00020000);
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    const int kt = kt0 + u;
+    const bool ok = kt < KT;
+    if constexpr (IN == kInOp) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t off = ok && live_col ? uint32_t(((kt * 4 + t) * 64 + entry) * 16) : 0x80000000u;
+        xb[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, int(off), 0, 0));
+      }
+    }
+    // an absent weight tile (past the last row-block or past k) loads a tile of the same weight, clamped: past
+    // the last row-block its results are not stored, past k its products meet zero operand columns
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int w = PAIR ? (r < RB ? 0 : 1) : wi;
+      const int b = rb0 + (PAIR && r >= RB ? r - RB : r);
+      const int bc = b < a.nb[w] ? b : a.nb[w] - 1, ktc = ok ? kt : KT - 1;
+      const uint8_t* tile = a.tiles[w] + (size_t(bc) * size_t(KT) + size_t(ktc)) * kTileBytes;
+      const u32x4 c4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + 16 * lane));
+      cw[u][r] = make_uint4(c4[0], c4[1], c4[2], c4[3]);
+      sw[u][r] = uint32_t(__builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(tile + 1024 + 2 * lane)));
+    }
+  }
+
+  if constexpr (ROWS) {
+    float sq[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) v += rv[q][i];
+      for (int p0 = 64 * NI; p0 < P; p0 += 64) v += record(q, p0 + lane);
+      sq[q] = wave_sum(v);
+    }
+    float fac[3] = {inv_norm_of(sq[0]), 0.f, 0.f};
+    if constexpr (IN == kInSlerp) {
+      fac[1] = inv_norm_of(sq[1]);
+      fac[2] = inv_norm_of(fac[0] * fac[0] * sq[2] + 2.f * fac[0] * fac[1] * sq[3] + fac[1] * fac[1] * sq[4]);
+    }
+    _Float16* st16 = reinterpret_cast<_Float16*>(ldsf + L.stage) + size_t(wave) * 256;
+    const uint4* st4 = reinterpret_cast<const uint4*>(st16);
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+      const int kt = kt0 + u;
+      stage_row<IN>(f, a.k, kt, kt < KT, lane, fac, rows[u], st16);
+      wave_lds_order();
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xb[u][t] = live_col ? st4[t * 8 + entry] : make_uint4(0, 0, 0, 0);
+      wave_lds_order();
+    }
+  }
+
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const f16x2 s0 = scale_pair(sw[u][r], 0), s1 = scale_pair(sw[u][r], 1);
+      const uint32_t words[4] = {cw[u][r].x, cw[u][r].y, cw[u][r].z, cw[u][r].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f16x8 A = dequant8(words[t], t < 2 ? s0 : s1);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(f16x8, xb[u][t]), acc[r], 0, 0, 0);
+      }
+    }
+  }
+
+  // The waves' accumulators added in LDS in a fixed order by the first RB * 16 threads (all in wave 0), one output
+  // each: row 4 gg + e of row-block r (of each weight, PAIR), i = 16 r + 4 gg + e; then the work-group's record,
+  // each quantity added over those threads by wave_sum.
+#pragma unroll
+  for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  if (wave != 0) return;
+  float q[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  if (int(threadIdx.x) < RB * 16) {
+    const int r = int(threadIdx.x) >> 4, gg = (int(threadIdx.x) >> 2) & 3, e = int(threadIdx.x) & 3;
+    const int b = rb0 + r, w0 = PAIR ? 0 : wi, n = a.n[w0], o_i = b * kTileRows + 4 * gg + e;
+    // accumulator row 4 gg + e: lanes 16 gg (high column) and 16 gg + 1 (low), element e
+    auto sum_of = [&](int rr) {
+      const float* rf = ldsf + size_t(rr * 64 + 16 * gg) * 4 + e;
+      float v[16];
+#pragma unroll
+      for (int w = 0; w < 16; ++w) v[w] = w < S ? rf[w * R * 256] + rf[w * R * 256 + 4] : 0.f;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 16; ++w)
+        if (w < S) sum += v[w];
+      return sum;
+    };
+    const float fscale = IN == kInOp ? (a.xinv ? a.xinv[0] : 1.f) : kRowsDown;
+    if (b < a.nb[w0] && o_i < n) {
+      float* yp = a.y + a.y_off[w0];
+      if constexpr (PAIR) {
+        const float z = (sum_of(r) * (a.global[0] * fscale)) * ep_a;
+        const float hv = z / (1.f + expf(-z)) * ((sum_of(r + RB) * (a.global[1] * fscale)) * ep_b);
+        yp[o_i] = hv;
+        q[0] = hv * hv;
+      } else {
+        const float* cs = a.col_scale[wi];
+        const float sv = sum_of(r) * (a.global[wi] * fscale);
+        const float o = cs ? sv * cs[o_i] : sv;
+        yp[o_i] = o;
+        if constexpr (OUT == kOutSlerp) {
+          const float x = ep_a, lr = ep_b, ol = 1.f - lr;
+          q[0] = x * x;
+          q[1] = o * o;
+          q[2] = (ol * ol) * (x * x);
+          q[3] = (ol * lr) * (x * o);
+          q[4] = (lr * lr) * (o * o);
+        }
+      }
+    }
+  }
+  if constexpr (OUT != kOutPlain) {
+    constexpr int QO = OUT == kOutSlerp ? 5 : 1;
+#pragma unroll
+    for (int i = 0; i < QO; ++i) {
+      const float t = wave_sum(q[i]);
+      if (lane == 0) f.out_part[size_t(i) * gridDim.x + blockIdx.x] = t;
+    }
+  }
+}
+
+namespace {
+using FusedFn = void (*)(const FusedArgs);
+
+template <int R, int T, int IN, int OUT>
+FusedFn fused_pick(int threads) {
+  return threads <= 512 ? gemv_fused_kernel<R, T, 512, IN, OUT> : gemv_fused_kernel<R, T, 1024, IN, OUT>;
+}
+
+// the combinations the decode step makes: qkvg (slerp rows in), gate / up (slerp rows in, SwiGLU out), down (norm
+// rows in, slerp records out), o (prepared operand in, slerp records out); R row-blocks (per weight when paired);
+// two k-tiles per wave up to K = 4096, four above (the plain GEMV's k-split)
+FusedFn fused_fn(int r, int t, int threads, int in, int out) {
+#define XTG_F(R, T, IN, OUT) \
+  if (r == R && t == T && in == IN && out == OUT) return fused_pick<R, T, IN, OUT>(threads);
+  XTG_F(1, 2, kInSlerp, kOutPlain) XTG_F(2, 2, kInSlerp, kOutPlain) XTG_F(4, 2, kInSlerp, kOutPlain)
+  XTG_F(2, 2, kInSlerp, kOutSwiglu) XTG_F(4, 2, kInSlerp, kOutSwiglu) XTG_F(2, 2, kInOp, kOutSwiglu)
+  XTG_F(1, 2, kInNorm, kOutSlerp) XTG_F(2, 2, kInNorm, kOutSlerp) XTG_F(1, 4, kInNorm, kOutSlerp)
+  XTG_F(1, 2, kInOp, kOutSlerp) XTG_F(2, 2, kInOp, kOutSlerp) XTG_F(1, 4, kInOp, kOutSlerp)
+  XTG_F(1, 4, kInSlerp, kOutPlain) XTG_F(2, 4, kInSlerp, kOutSwiglu)
+#undef XTG_F
+  return nullptr;
+}
+
+// The launch shape: the plain GEMV's k-split (so a fused projection sums every output in the order the plain
+// launch does), T k-tiles of 2 or 4 (the fused kernels are made for those); the row-blocks as the plain GEMV picks
+// them, at least one pair when paired.
+GemvShape fused_shape(const FusedGemv& f) {
+  int nbs[4];
+  for (int i = 0; i < f.c.nw; ++i) nbs[i] = f.c.w[i]->nb;
+  GemvShape sh = gemv_shape(f.c.w[0]->kt, nbs, f.c.nw, f.c.m, false);
+  if (f.out == kOutSwiglu) sh.r = sh.r >= 4 ? 4 : 2;   // one or two pairs
+  if (f.out == kOutSlerp || f.in == kInNorm) sh.r = std::min(sh.r, 2);
+  return sh;
+}
+}  // namespace
+
+int fused_gemv_groups(const FusedGemv& f) {
+  const GemvShape sh = fused_shape(f);
+  if (f.out == kOutSwiglu) return (f.c.w[0]->nb + sh.r / 2 - 1) / (sh.r / 2);
+  int wgs = 0;
+  for (int i = 0; i < f.c.nw; ++i) wgs += (f.c.w[i]->nb + sh.r - 1) / sh.r;
+  return wgs;
+}
+
+std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
+  const GemvCall& c = f.c;
+  XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
+  XTG_CHECK(c.m == 1, "fused gemv: %d rows (one)", c.m);
+  XTG_CHECK(f.in != kInOp || c.xop, "fused gemv: no operand");
+  XTG_CHECK(f.in == kInOp || (f.in_x && f.in_part && f.in_groups > 0 && c.k > 0 && c.k % 16 == 0 &&
+                              (f.in == kInNorm || (f.in_o && f.in_lr))),
+            "fused gemv: rows, records and width for the built operand");
+  XTG_CHECK(f.out != kOutSwiglu || (c.nw == 2 && c.w[0]->n == c.w[1]->n && f.out_sg && f.out_su && f.out_part),
+            "fused gemv: SwiGLU pairs two weights of one shape");
+  XTG_CHECK(f.out != kOutSlerp || (c.nw == 1 && f.out_x && f.out_lr && f.out_part && !c.col_scale[0]),
+            "fused gemv: slerp records come from one weight");
+  XTG_CHECK(f.in == kInOp || f.in_groups <= kMaxFusedGroups, "fused gemv: records of %d work-groups (at most %d)",
+            f.in_groups, kMaxFusedGroups);
+  FusedArgs a{};
+  const int kt = c.w[0]->kt;
+  for (int i = 0; i < c.nw; ++i) XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
+  const GemvShape sh = fused_shape(f);
+  XTG_CHECK(sh.t == 2 || sh.t == 4, "fused gemv: %d k-tiles per wave", sh.t);
+  const int rb = f.out == kOutSwiglu ? sh.r / 2 : sh.r;
+  int wgs = 0;
+  for (int i = 0; i < c.nw; ++i) {
+    a.g.tiles[i] = c.w[i]->tiles;
+    a.g.nb[i] = c.w[i]->nb;
+    a.g.n[i] = c.w[i]->n;
+    a.g.global[i] = c.w[i]->global;
+    a.g.y_off[i] = (long long)c.y_off[i];
+    a.g.col_scale[i] = c.col_scale[i];
+    if (f.out != kOutSwiglu || i == 0) wgs += (c.w[i]->nb + rb - 1) / rb;
+    a.g.wg_end[i] = wgs;
+  }
+  for (int i = c.nw; i < 4; ++i) a.g.wg_end[i] = wgs;
+  a.g.nw = c.nw;
+  a.g.kt = kt;
+  a.g.m = c.m;
+  a.g.xop = static_cast<const uint4*>(c.xop);
+  a.g.xinv = c.xinv;
+  a.g.k = c.k;
+  a.g.y = c.y;
+  a.in_groups = f.in_groups;
+  a.in_x = f.in_x;
+  a.in_o = f.in_o;
+  a.in_lr = f.in_lr;
+  a.in_part = f.in_part;
+  a.in_xout = f.in_xout;
+  a.out_x = f.out_x;
+  a.out_lr = f.out_lr;
+  a.out_sg = f.out_sg;
+  a.out_su = f.out_su;
+  a.out_part = f.out_part;
+  XTG_CHECK(wgs == fused_gemv_groups(f), "fused gemv: %d work-groups", wgs);
+  XTG_CHECK(f.out == kOutPlain || wgs <= kMaxFusedGroups, "fused gemv: %d work-groups' records (at most %d)", wgs,
+            kMaxFusedGroups);
+  XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
+  const int threads = sh.s * 64;
+  FusedFn fn = fused_fn(sh.r, sh.t, threads, f.in, f.out);
+  XTG_CHECK(fn != nullptr, "fused gemv: no kernel for R=%d T=%d (in %d, out %d)", sh.r, sh.t, f.in, f.out);
+  const size_t lds = size_t(FusedLds(sh.s, sh.r, f.in).total) * sizeof(float);
+  if (lds > 65536) {
+    static thread_local const void* raised[64] = {};
+    bool done = false;
+    for (const void* p : raised) done = done || p == reinterpret_cast<const void*>(fn);
+    if (!done) {
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(lds)));
+      for (const void*& p : raised)
+        if (!p) {
+          p = reinterpret_cast<const void*>(fn);
+          break;
+        }
+    }
+  }
+  hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
+  HIP_CHECK(hipGetLastError());
+  static const char* kIn[] = {"op", "slerp", "norm"};
+  static const char* kOut[] = {"plain", "slerp", "swiglu"};
+  return strf("gemv_fused_kernel<%d, %d, %d, %s, %s>", sh.r, sh.t, threads <= 512 ? 512 : 1024, kIn[f.in],
+              kOut[f.out]);
+}
+
+}  // namespace xtg::hip

@@ -69,6 +69,46 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream);
 // whether launch_gemv takes c's raw rows for its shape (otherwise prepare the operand first)
 bool gemv_takes_raw(const GemvCall& c);
 
+// ---- the one-token decode step's projections with the nGPT norms riding on them (gemv.hip) ----
+//
+// A norm over a whole row needs every output of the projection that made the row, so as a kernel of its own it
+// costs a dependent launch per norm. Here the producing GEMV writes, besides its outputs, one record of partial
+// sums per work-group over the outputs it owns (records [Q quantities][groups]), and the consuming GEMV adds the
+// P records in a fixed order (every work-group the same order: bit-identical factors) and builds its operand lane
+// by lane from the row. Rows of unit norm take a fixed operand exponent (2^14: |x| <= 1), so no row maximum is
+// needed. One activation row (m = 1).
+//   input side:  kInOp     the prepared operand (c.xop / c.xinv)
+//                kInSlerp  x_new = (ya + lr (yb - ya)) f2, ya = x fa, yb = o fb (kernels.cpp:177-189), the three
+//                          factors from kOutSlerp records: fa = 1/sqrt(sum x^2 + 1e-6), fb likewise of o, and f2 of
+//                          sum t^2 = fa^2 sum (1-lr)^2 x^2 + 2 fa fb sum (1-lr) lr x o + fb^2 sum lr^2 o^2; work-group
+//                          0 also writes x_new to in_xout (the next residual)
+//                kInNorm   h r, r = 1/sqrt(sum h^2 + 1e-6) from kOutSwiglu records
+//   output side: kOutPlain
+//                kOutSlerp  y as usual, plus records of sum x^2, o^2, (1-lr)^2 x^2, (1-lr) lr x o, lr^2 o^2 over the
+//                           group's outputs o (out_x: the residual [n], out_lr [n]); one weight
+//                kOutSwiglu two weights (gate, up) of equal shape, the same row-blocks of both in one work-group:
+//                           y = h = silu(g sg) (u su) [n] (kernels.cpp:225-234) and records of sum h^2
+enum { kInOp = 0, kInSlerp = 1, kInNorm = 2 };
+enum { kOutPlain = 0, kOutSlerp = 1, kOutSwiglu = 2 };
+struct FusedGemv {
+  GemvCall c;                        // weights, y, m = 1, k (kInOp: c.xop / c.xinv)
+  int in = kInOp, out = kOutPlain;
+  const float* in_x = nullptr;       // kInSlerp: x [k]; kInNorm: h [k]
+  const float* in_o = nullptr;       // kInSlerp: o [k]
+  const float* in_lr = nullptr;      // kInSlerp: lr [k]
+  const float* in_part = nullptr;    // the producing launch's records
+  int in_groups = 0;                 // their number (fused_gemv_groups of that launch)
+  float* in_xout = nullptr;          // kInSlerp: where x_new goes
+  const float* out_x = nullptr;      // kOutSlerp
+  const float* out_lr = nullptr;
+  const float* out_sg = nullptr;     // kOutSwiglu
+  const float* out_su = nullptr;
+  float* out_part = nullptr;         // kOutSlerp / kOutSwiglu: the records (5 or 1 x kMaxFusedGroups floats)
+};
+int fused_gemv_groups(const FusedGemv& f);
+constexpr int kMaxFusedGroups = 1024;   // work-groups of a launch whose records a consumer takes
+std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream);
+
 // ---- NVFP4 GEMM for prefill chunks of m > 8 rows (gemm.hip) ----
 // The same weights and call description (c.xop: group 0 of ceil(m / 8) operand groups of op_group_bytes(k);
 // c.xinv unused), any m >= 1; y[i] blocks as in the GEMV.
