@@ -1413,6 +1413,36 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
   if (xop) emit_operand_mx<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, mx * f);
 }
 
+// The one-token step's gate with its norm left to the o-projection: one wave per head merges the head's partials
+// (lane l: dims 8 l .. 8 l + 7), applies a * sigmoid(g * gs) (dory.cpp:509-512) and writes the gated head to y,
+// and its sum of squares to rec[head] (wave_sum: the same order every call), from which the o-projection's
+// operand takes the justnorm (dory.cpp:513-515).
+template <int D>
+__global__ void __launch_bounds__(64) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
+                                                             const float* __restrict__ gs, float* __restrict__ y,
+                                                             float* __restrict__ rec) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  float s = 0.f;
+  if (lane < D / 8) {
+    const int c = h * (D / 8) + lane;
+    float t[8];
+    merge_chunk<D, 12>(a, 0, c, t);
+    const float4 g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      t[e] = t[e] * (1.f / (1.f + expf(-gv[e] * sv[e])));
+      s += t[e] * t[e];
+    }
+    *reinterpret_cast<float4*>(y + 8 * c) = make_float4(t[0], t[1], t[2], t[3]);
+    *reinterpret_cast<float4*>(y + 8 * c + 4) = make_float4(t[4], t[5], t[6], t[7]);
+  }
+  s = wave_sum(s);
+  if (lane == 0) rec[h] = s;
+}
+
 // ------------------------------------------------------------------------------------------------------- plan
 
 AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window) {
@@ -1779,6 +1809,25 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
   XTG_CHECK(u != 0, "attention gate: %d heads of %d", heads, p.d);
   HIP_CHECK(hipGetLastError());
   return strf("attn_gate_kernel<%d, %d>", p.d, u);
+}
+
+std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* part, const float* g, const float* gs,
+                                   float* y, float* rec, hipStream_t stream) {
+  XTG_CHECK(p.blocks == 1, "attention gate by heads: one query row");
+  auto al = [](const void* x) { return reinterpret_cast<uintptr_t>(x) % 16 == 0; };
+  XTG_CHECK(g && gs && y && rec && al(g) && al(gs) && al(y), "attention gate by heads: 16-byte aligned rows");
+  const MergeArgs a = merge_args(p, heads, part);
+  const dim3 grid{unsigned(heads)}, block{64u};
+  if (p.d == 64)
+    hipLaunchKernelGGL((attn_gate_heads_kernel<64>), grid, block, 0, stream, a, g, gs, y, rec);
+  else if (p.d == 128)
+    hipLaunchKernelGGL((attn_gate_heads_kernel<128>), grid, block, 0, stream, a, g, gs, y, rec);
+  else if (p.d == 256)
+    hipLaunchKernelGGL((attn_gate_heads_kernel<256>), grid, block, 0, stream, a, g, gs, y, rec);
+  else
+    XTG_CHECK(false, "attention gate by heads: head_dim %d", p.d);
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_gate_heads_kernel<%d>", p.d);
 }
 
 }  // namespace xtg::hip

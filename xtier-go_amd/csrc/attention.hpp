@@ -94,5 +94,9 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
 // heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).
 std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,
                              float* out, void* op, hipStream_t stream);
+// The same for one row with the justnorm left to the consumer: y [heads * d] = the gated merge before its norm, and
+// rec [heads] = each head's sum of squares (the records a kInNorm projection takes, kernels.hpp FusedGemv).
+std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* part, const float* g, const float* gs,
+                                   float* y, float* rec, hipStream_t stream);
 
 }  // namespace xtg::hip

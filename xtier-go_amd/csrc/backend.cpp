@@ -554,8 +554,9 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
 
 void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
                         float* k, const float* v, const float* qscale, const float* g, const float* gscale,
-                        float* out, void* op, bool store) {
+                        float* out, void* op, bool store, float* gate_rec) {
   XTG_CHECK(kvs_.count(c), "attention step: unknown cache");
+  XTG_CHECK(!gate_rec || (m == 1 && out && !op), "attention step: the gate's records take one row, out and no operand");
   XTG_CHECK(m >= 1 && pos0 >= 0, "attention step: %d rows at %lld", m, pos0);
   XTG_CHECK(pos0 + m < (1LL << 31), "attention step: position %lld beyond the 32-bit slot positions", pos0 + m);
   XTG_CHECK(c->ring || pos0 + m <= c->slots, "attention step: context full (%lld + %d > %lld slots)", pos0, m,
@@ -600,7 +601,10 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
       timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, m, heads, pos0, window, scale, part, stream_); });
   }
   if (store && !store_first) timed([&] { return launch_kv_store(*c, pos0, m, kout, v, stream_); });
-  timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
+  if (gate_rec)
+    timed([&] { return launch_attn_gate_heads(p, heads, part, g, gscale, out, gate_rec, stream_); });
+  else
+    timed([&] { return launch_attn_gate(p, m, heads, part, g, gscale, out, op, stream_); });
 }
 
 // ---------------------------------------------------------------------------------------------- row kernels

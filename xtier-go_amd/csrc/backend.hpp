@@ -88,9 +88,11 @@ class Backend {
   // o-projection's operand) = justnorm(attention * sigmoid(g * gscale)). Up to 8 rows (a decode or verify step)
   // in one fused producer; more (a prefill chunk): k is rewritten too, and the steps run as separate launches.
   // store = false leaves the cache as it was (a last_loop session's earlier loops, packs/dory/dory.cpp:534-537).
+  // gate_rec (one row only): out gets the gated attention before its justnorm and gate_rec [heads] each head's sum
+  // of squares, the records of a kInNorm o-projection (kernels.hpp FusedGemv); op must be NULL.
   void attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,
                  float* k, const float* v, const float* qscale, const float* g, const float* gscale, float* out,
-                 void* op, bool store = true);
+                 void* op, bool store = true, float* gate_rec = nullptr);
   // the row kernels of the decode step (rows.hip); device memory. op (optional): also write the result rows as a
   // GEMV / GEMM operand of ceil(rows / 8) groups of op_bytes(w) bytes.
   void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,

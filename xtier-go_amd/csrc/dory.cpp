@@ -95,6 +95,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
   x2_ = scratch(R * H);
   part_s_ = scratch(size_t(kMaxFusedGroups) * 5);
   part_h_ = scratch(size_t(kMaxFusedGroups));
+  part_a_ = scratch(size_t(c.heads));
+  att_ = scratch(size_t(c.heads) * size_t(c.head_dim));
   // XTG_DECODE_UNFUSED=1 runs one-token steps on the separate norm launches (the prefill path's), for comparison
   fused_ = !std::getenv("XTG_DECODE_UNFUSED");
   input_ = scratch(R * H);
@@ -255,14 +257,20 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
   float* g = v + size_t(m) * KV;
   const bool sliding = L.w.kind == XTG_DORY_SLIDING;
   const float scale = 1.f / std::sqrt(float(c_.head_dim));
+  // the gate's justnorm rides on the o-projection: att_ holds the gated heads, part_a_ their sums of squares
   b_.attn_step(this->cache(L.attn, inst), m, pos0, c_.heads, sliding ? c_.window : 0, scale,
-               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_, store);
+               sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, att_, nullptr, store,
+               part_a_);
   FusedGemv o;
+  o.in = kInNorm;
+  o.in_x = att_;
+  o.in_part = part_a_;
+  o.in_groups = c_.heads;
   o.out = kOutSlerp;
   o.out_x = x_;
   o.out_lr = L.lr;
   o.out_part = part_s_;
-  pend_groups_ = b_.matmul_fused(&L.w.o, 1, o, op_q_, m, o_);
+  pend_groups_ = b_.matmul_fused(&L.w.o, 1, o, nullptr, m, o_);
   pend_ = true;
   pend_lr_ = L.lr;
 }

@@ -80,6 +80,7 @@ class DorySession {
   // the fused one-token path: records of the slerp's and the SwiGLU's partial sums (kernels.hpp FusedGemv), and
   // the residual awaiting its slerp (of o_ with pend_lr_, pend_groups_ records in part_s_)
   float *part_s_ = nullptr, *part_h_ = nullptr;
+  float *part_a_ = nullptr, *att_ = nullptr;   // the attention gate's per-head records and gated heads
   bool fused_ = true, pend_ = false;
   const float* pend_lr_ = nullptr;
   int pend_groups_ = 0;
