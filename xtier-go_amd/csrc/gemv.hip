@@ -390,8 +390,21 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
     const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7, ln = gg * 16 + 2 * jj;
     if (rb0 + r >= nb) continue;
+    // the S <= 16 waves in order, the reads in batches of 4 with clamped indices (no wait between them)
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < S; ++w) sum += red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 1];
+#pragma unroll
+    for (int w0 = 0; w0 < 16; w0 += 4) {
+      if (w0 >= S) break;
+      f32x4 v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = w0 + i < S ? w0 + i : S - 1;
+        v[i] = red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 1];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (w0 + i < S) sum += v[i];
+    }
     store_rows(a, wi, rb0 + r, gg, jj, sum);
   }
 }
@@ -552,6 +565,26 @@ struct FusedArgs {
 
 // Unit rows take the operand exponent 2^14 (|x| <= 1 keeps |x 2^14| below f16's maximum).
 constexpr float kRowsUp = 16384.f, kRowsDown = 1.f / 16384.f;
+
+// sum over the S <= 16 waves of (p[w R 256] + p[w R 256 + hl]) in wave order; the reads go out in batches of 8 with
+// their indices clamped into [0, S) (a branch per read would wait for each before the next)
+template <int R>
+__device__ inline float wave_sums(const float* p, int S, int hl) {
+  float sum = 0.f;
+#pragma unroll
+  for (int w0 = 0; w0 < 16; w0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int w = w0 + i < S ? w0 + i : S - 1;
+      v[i] = p[w * R * 256] + p[w * R * 256 + hl];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (w0 + i < S) sum += v[i];
+  }
+  return sum;
+}
 
 // LDS of a fused launch, in floats: the waves' accumulators [S][R][64][4], then each wave's staging of one
 // k-tile's live operand columns [S][4 steps][8 entries][8 f16].
@@ -761,17 +794,7 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
     const int r = int(threadIdx.x) >> 4, gg = (int(threadIdx.x) >> 2) & 3, e = int(threadIdx.x) & 3;
     const int b = rb0 + r, w0 = PAIR ? 0 : wi, n = a.n[w0], o_i = b * kTileRows + 4 * gg + e;
     // accumulator row 4 gg + e: lanes 16 gg (high column) and 16 gg + 1 (low), element e
-    auto sum_of = [&](int rr) {
-      const float* rf = ldsf + size_t(rr * 64 + 16 * gg) * 4 + e;
-      float v[16];
-#pragma unroll
-      for (int w = 0; w < 16; ++w) v[w] = w < S ? rf[w * R * 256] + rf[w * R * 256 + 4] : 0.f;
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < 16; ++w)
-        if (w < S) sum += v[w];
-      return sum;
-    };
+    auto sum_of = [&](int rr) { return wave_sums<R>(ldsf + size_t(rr * 64 + 16 * gg) * 4 + e, S, 4); };
     const float fscale = IN == kInOp ? (a.xinv ? a.xinv[0] : 1.f) : kRowsDown;
     if (b < a.nb[w0] && o_i < n) {
       float* yp = a.y + a.y_off[w0];
