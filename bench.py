@@ -646,6 +646,14 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
                               "hbm_gbs": round((w.weight_bytes() + kv8) / (ms / 1e3) / 1e9, 1)}
         log("decode ctx %5d, FP8 caches: M=1 %.3f ms/token (%.0f tok/s)" % (ctx, ms, 1e3 / ms))
     if dev8:
+        # per-kernel breakdown of one eager FP8 step at the largest context (events around every launch)
+        hip.profile(True)
+        dev8.forward(dx, 1, ctx_max, dl)
+        rep = hip.profile_report()
+        hip.profile(False)
+        results["kernels_fp8_ctx%d_m1_eager" % ctx_max] = {
+            k: {"calls": v["calls"], "us": round(v["ms"] * 1e3, 1)} for k, v in
+            sorted(rep.items(), key=lambda kv: -kv[1]["ms"])}
         dev8.destroy()
     results["fp8_kv_m1"] = fp8
     results["prepare"] = {"bytes": w.weight_bytes(), "s": round(prep_s, 3), "gbs": round(w.weight_bytes() / prep_s / 1e9, 2)}

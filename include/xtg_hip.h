@@ -305,7 +305,9 @@ int xtg_hip_finish(xtg_hip* h, char* err, int err_len);
 /* No counterpart in the reference (its OpenCL queue replays nothing): HIP graphs over the backend's stream. Every
  * device call queued between begin and end is captured into one graph instead of running; launch replays it on the
  * stream. Weights must be prepared and scratch sized before the capture (run the calls once first); blocking calls
- * fail during a capture. A graph replays its calls exactly as captured, arguments included. While any graph exists
+ * fail during a capture. A graph replays its calls exactly as captured, arguments included: a captured decode step
+ * is the step at its captured position (RoPE angles, cache slots and scan plan are arguments), so a decode loop
+ * captures one graph per position or runs eagerly. While any graph exists
  * the backend frees no device memory a graph may address: scratch that a later, larger call outgrows, and weights,
  * buffers and caches released meanwhile, are kept until the last graph is destroyed (the memory of the caller's
  * own buffers is kept, but their contents are the caller's). `name` (may be NULL) is the graph's entry in the

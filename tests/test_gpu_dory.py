@@ -257,6 +257,38 @@ def test_4b_graph_replay_matches_eager(hip, model_4b):
     dl.free()
 
 
+def test_graph_per_position(hip, wl):
+    """A captured step is the step at the captured position (its RoPE angles, cache slots and scan plan are launch
+    arguments), so a decode loop captures one graph per position: twin sessions with the same history, one eager,
+    one replaying a graph captured at each new position, give identical logits token after token."""
+    w = wl.DoryWeights(wl.DORY_TINY, seed=21, context=128)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    eager, graphed = hip.dory(w), hip.dory(w)
+    rng = np.random.default_rng(22)
+    dx = hip.array(shape=(8, H))
+    la, lb = hip.array(shape=(8, V)), hip.array(shape=(8, V))
+    for p in range(0, 24, 8):
+        dx.upload(unit_rows(rng, 8, H))
+        eager.forward(dx, 8, p, la)
+        graphed.forward(dx, 8, p, lb)
+    for p in range(24, 30):
+        dx.upload(np.concatenate([unit_rows(rng, 1, H), np.zeros((7, H), np.float32)]))
+        eager.forward(dx, 1, p, la)
+        hip.graph_begin()
+        graphed.forward(dx, 1, p, lb)
+        g = hip.graph_end("step_at_%d" % p)
+        hip.graph_launch(g)
+        np.testing.assert_array_equal(lb.numpy()[:1], la.numpy()[:1])
+        hip.graph_launch(g)   # a second replay at the same position rewrites the same slots
+        np.testing.assert_array_equal(lb.numpy()[:1], la.numpy()[:1])
+        hip.graph_destroy(g)
+    dx.free()
+    la.free()
+    lb.free()
+    eager.destroy()
+    graphed.destroy()
+
+
 def sharpened(w, seed=9):
     """q scaled up 40x and lr ~ U(0.3, 0.7): attention that depends on positions and masks (see
     tests/test_oracle_dory.py)."""
