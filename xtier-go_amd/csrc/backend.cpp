@@ -255,6 +255,9 @@ int Backend::matmul_fused(const xtg_nvfp4* ws, int nw, FusedGemv f, const void* 
     XTG_CHECK(op, "fused matmul: no operand");
     c.xop = op;
     c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
+  } else if (f.in == kInSlerp) {
+    XTG_CHECK(op, "fused matmul: no operand");
+    c.xop = op;   // the producer's linear-form operand, its factors in f.in_ia / f.in_ib
   }
   timed([&] { return launch_gemv_fused(f, stream_); });
   return fused_gemv_groups(f);

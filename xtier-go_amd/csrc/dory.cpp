@@ -15,6 +15,27 @@ constexpr int kChunkRows = 512;   // rows of one run_chunk: the reference's pref
 constexpr int kMaxSnapshots = 64;
 }
 
+namespace {
+// 2^e with |v 2^e| <= 2^14 for every |v| <= bound (an f16 operand part's headroom; 1 for bound 0)
+float operand_factor(double bound) {
+  if (!(bound > 0.0)) return 1.f;
+  int p = 0;
+  (void)std::frexp(bound, &p);   // bound < 2^p
+  return std::ldexp(1.f, std::max(-60, std::min(60, 14 - p)));
+}
+
+// The largest |w| of an NVFP4 weight: |global| * 6 (E2M1's largest) * its largest E4M3 scale (the codes' order
+// follows the magnitudes'; a NaN code counts as 448, E4M3's largest finite value).
+double max_abs_weight(const xtg_nvfp4& w) {
+  int top = 0;
+  const size_t n = size_t(w.n_out) * size_t(w.k / 16);
+  for (size_t i = 0; i < n; ++i) top = std::max(top, int(w.scales[i] & 0x7f));
+  const int e = top >> 3, m = top & 7;
+  const double scale = top >= 0x7e ? 448.0 : e == 0 ? std::ldexp(double(m), -9) : std::ldexp(1.0 + m / 8.0, e - 7);
+  return std::fabs(double(w.global)) * 6.0 * scale;
+}
+}  // namespace
+
 float* DorySession::upload(const float* v, size_t n) {
   XTG_CHECK(v, "dory: a per-layer vector is NULL");
   float* p = static_cast<float*>(b_.alloc(n * sizeof(float)));
@@ -55,6 +76,19 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
     L.w = layers[l];
     L.recurrent = l >= c.n_in && l < c.n_in + c.n_rec;
     L.lr = upload(L.w.lr, size_t(H));
+    // the fused one-token path's operand of the next projection in the slerp's linear form: a = (1 - lr) x with
+    // |x_i| <= 1 (a unit row), b = lr o with |o_i| <= |W_i| |u| <= sqrt(K) max |w| (u, the projection's operand, a
+    // unit row); a little margin for rounding
+    {
+      const xtg_nvfp4& wo = L.w.kind == XTG_DORY_MLP ? L.w.down : L.w.o;
+      double la = 0.0, lb = 0.0;
+      for (int i = 0; i < H; ++i) {
+        la = std::max(la, std::fabs(1.0 - double(L.w.lr[i])));
+        lb = std::max(lb, std::fabs(double(L.w.lr[i])));
+      }
+      L.lin_a = operand_factor(la * 1.01);
+      L.lin_b = operand_factor(lb * std::sqrt(double(wo.k)) * max_abs_weight(wo) * 1.01);
+    }
     if (L.w.kind == XTG_DORY_MLP) {
       for (const xtg_nvfp4* w : {&L.w.gate, &L.w.up, &L.w.down}) prepare(*w);
       XTG_CHECK(L.w.gate.n_out == F && L.w.up.n_out == F && L.w.gate.k == H && L.w.down.k == F && L.w.down.n_out == H,
@@ -108,6 +142,14 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
     const int k = op == &op_q_ ? Q : op == &op_f_ ? F : H;
     *op = b_.alloc(Backend::op_bytes(k) * (op == &op_last_ ? 1 : size_t(kChunkRows / 8)));
     owned_.push_back(*op);
+  }
+  // the slerp's linear-form operand (K = hidden): its entries past hidden and past the four live columns are never
+  // written and stay zero
+  op_lin_ = b_.alloc(xop_bytes(H));
+  owned_.push_back(op_lin_);
+  {
+    const std::vector<uint8_t> zeros(xop_bytes(H), 0);
+    b_.write(op_lin_, 0, zeros.data(), zeros.size());
   }
 }
 
@@ -209,13 +251,32 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
   const int Q = c_.heads * c_.head_dim, KV = c_.kv_heads * c_.head_dim;
   auto input_side = [&](FusedGemv& f) {
     if (!pend_) return;   // op_h_ holds x's operand
-    f.in = kInSlerp;
+    f.in = kInSlerp;      // op_lin_ holds the slerp's linear-form operand
     f.in_x = x_;
     f.in_o = o_;
     f.in_lr = pend_lr_;
     f.in_part = part_s_;
     f.in_groups = pend_groups_;
     f.in_xout = x2_;
+    f.in_ia = 1.f / pend_a_;
+    f.in_ib = 1.f / pend_b_;
+  };
+  const void* in_op = pend_ ? op_lin_ : op_h_;
+  auto slerp_side = [&](FusedGemv& f) {
+    f.out = kOutSlerp;
+    f.out_x = x_;
+    f.out_lr = L.lr;
+    f.out_part = part_s_;
+    f.out_op = op_lin_;
+    f.out_ea = L.lin_a;
+    f.out_eb = L.lin_b;
+  };
+  auto pending = [&](int groups) {
+    pend_groups_ = groups;
+    pend_ = true;
+    pend_lr_ = L.lr;
+    pend_a_ = L.lin_a;
+    pend_b_ = L.lin_b;
   };
   auto took_input = [&] {
     if (!pend_) return;
@@ -230,26 +291,21 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
     g.out_sg = L.sg;
     g.out_su = L.su;
     g.out_part = part_h_;
-    const int groups = b_.matmul_fused(gu, 2, g, op_h_, m, gu_);   // h = silu(g sg) (u su) [m][F]
+    const int groups = b_.matmul_fused(gu, 2, g, in_op, m, gu_);   // h = silu(g sg) (u su) [m][F]
     took_input();
     FusedGemv d;
     d.in = kInNorm;   // justnorm(h) as the operand
     d.in_x = gu_;
     d.in_part = part_h_;
     d.in_groups = groups;
-    d.out = kOutSlerp;
-    d.out_x = x_;
-    d.out_lr = L.lr;
-    d.out_part = part_s_;
-    pend_groups_ = b_.matmul_fused(&L.w.down, 1, d, nullptr, m, o_);
-    pend_ = true;
-    pend_lr_ = L.lr;
+    slerp_side(d);
+    pending(b_.matmul_fused(&L.w.down, 1, d, nullptr, m, o_));
     return;
   }
   const xtg_nvfp4 qkvg[4] = {L.w.q, L.w.k, L.w.v, L.w.g};
   FusedGemv p;
   input_side(p);
-  b_.matmul_fused(qkvg, 4, p, op_h_, m, proj_);   // q [m][Q] | k [m][KV] | v [m][KV] | g [m][Q]
+  b_.matmul_fused(qkvg, 4, p, in_op, m, proj_);   // q [m][Q] | k [m][KV] | v [m][KV] | g [m][Q]
   took_input();
   float* q = proj_;
   float* k = proj_ + size_t(m) * Q;
@@ -266,13 +322,8 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
   o.in_x = att_;
   o.in_part = part_a_;
   o.in_groups = c_.heads;
-  o.out = kOutSlerp;
-  o.out_x = x_;
-  o.out_lr = L.lr;
-  o.out_part = part_s_;
-  pend_groups_ = b_.matmul_fused(&L.w.o, 1, o, nullptr, m, o_);
-  pend_ = true;
-  pend_lr_ = L.lr;
+  slerp_side(o);
+  pending(b_.matmul_fused(&L.w.o, 1, o, nullptr, m, o_));
 }
 
 void DorySession::run_chunk(const float* x, int m, long long pos0) {

@@ -47,6 +47,7 @@ class DorySession {
     float* sg = nullptr;
     float* su = nullptr;
     float* lr = nullptr;
+    float lin_a = 1.f, lin_b = 1.f;   // 2^ea, 2^eb of the slerp's linear-form operand (kernels.hpp kInSlerp)
   };
   void sublayer(Layer& L, int m, long long pos0, int inst, bool store);
   // the same for a decode or verify step (m <= 8) with the slerp and SwiGLU norms riding on the projections: after
@@ -83,6 +84,7 @@ class DorySession {
   float *part_a_ = nullptr, *att_ = nullptr;   // the attention gate's per-head records and gated heads
   bool fused_ = true, pend_ = false;
   const float* pend_lr_ = nullptr;
+  float pend_a_ = 1.f, pend_b_ = 1.f;   // its linear-form operand's factors, the operand in op_lin_
   int pend_groups_ = 0;
   // GEMV operands, each written by the kernel that produces its rows: x's (K = hidden; by the slerp / loop norms
   // or, for the first sublayer, prep_x), the gated attention's (K = heads * head_dim), the SwiGLU's (K = ffn)
@@ -90,6 +92,7 @@ class DorySession {
   void* op_q_ = nullptr;
   void* op_f_ = nullptr;
   void* op_last_ = nullptr;   // one row's operand (K = hidden), for the head of a chunk's last row
+  void* op_lin_ = nullptr;    // the fused one-token path's slerp operand (K = hidden; kernels.hpp kInSlerp)
 };
 
 }  // namespace xtg::hip

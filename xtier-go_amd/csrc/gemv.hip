@@ -556,44 +556,28 @@ struct FusedArgs {
   const float* in_lr;
   const float* in_part;
   float* in_xout;
+  float in_ia, in_ib;
   const float* out_x;
   const float* out_lr;
   const float* out_sg;
   const float* out_su;
   float* out_part;
+  _Float16* out_op;
+  float out_ea, out_eb;
 };
 
 // Unit rows take the operand exponent 2^14 (|x| <= 1 keeps |x 2^14| below f16's maximum).
 constexpr float kRowsUp = 16384.f, kRowsDown = 1.f / 16384.f;
 
-// sum over the S <= 16 waves of (p[w R 256] + p[w R 256 + hl]) in wave order; the reads go out in batches of 8 with
-// their indices clamped into [0, S) (a branch per read would wait for each before the next)
-template <int R>
-__device__ inline float wave_sums(const float* p, int S, int hl) {
-  float sum = 0.f;
-#pragma unroll
-  for (int w0 = 0; w0 < 16; w0 += 8) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int w = w0 + i < S ? w0 + i : S - 1;
-      v[i] = p[w * R * 256] + p[w * R * 256 + hl];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (w0 + i < S) sum += v[i];
-  }
-  return sum;
-}
-
-// LDS of a fused launch, in floats: the waves' accumulators [S][R][64][4], then each wave's staging of one
-// k-tile's live operand columns [S][4 steps][8 entries][8 f16].
+// LDS of a fused launch, in floats: each wave's high + low column sums [S][R][NCP column pairs][4 gg][4 e] (NCP:
+// 2 for kInSlerp's a and b, else 1), then each wave's staging of one k-tile's live operand columns [S][4 steps]
+// [8 entries][8 f16].
 struct FusedLds {
   int red, stage, total;
   __host__ __device__ FusedLds(int S, int R, int in) {
     red = 0;
-    stage = red + S * R * 256;
-    total = stage + (in != kInOp ? S * 128 : 0);
+    stage = red + S * R * (in == kInSlerp ? 2 : 1) * 16;
+    total = stage + (in == kInNorm ? S * 128 : 0);
   }
 };
 
@@ -604,42 +588,29 @@ __device__ inline void wave_lds_order() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// The row values one lane reads for the operand of a k-tile: inputs l and l + 64 of the tile, and lr of those
-// inputs; indices clamped into the row, so every load is issued before anything waits.
+// The row values one lane reads for the kInNorm operand of a k-tile: inputs l and l + 64 of the tile; indices
+// clamped into the row, so every load is issued before anything waits.
 struct TileRow {
-  float x[2], o[2], lr[2];
+  float x[2];
 };
 
-template <int IN>
 __device__ inline void load_row(const FusedArgs& f, int k, int kt, bool kt_ok, int lane, TileRow& r) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int kg = kt * kTileK + lane + 64 * h;
-    const int kc = kt_ok && kg < k ? kg : 0;
-    r.lr[h] = IN == kInSlerp ? f.in_lr[kc] : 0.f;
-    r.x[h] = f.in_x[kc];
-    r.o[h] = IN == kInSlerp ? f.in_o[kc] : 0.f;
+    r.x[h] = f.in_x[kt_ok && kg < k ? kg : 0];
   }
 }
 
-// One k-tile's operand from the row into a wave's staging area, in operand order (input kk of column c at step
-// (kk / 8) % 4, entry 4 c + kk / 32, element kk % 8; the 8 entries of the two live columns per step), with the
-// row's factors fac. Work-group 0 also writes the slerp's x_new to in_xout.
-template <int IN>
-__device__ inline void stage_row(const FusedArgs& f, int k, int kt, bool kt_ok, int lane, const float (&fac)[3],
-                                 const TileRow& r, _Float16* st16) {
+// One k-tile's kInNorm operand (h r) from the row into a wave's staging area, in operand order (input kk of column
+// c at step (kk / 8) % 4, entry 4 c + kk / 32, element kk % 8; the 8 entries of the two live columns per step).
+__device__ inline void stage_row(int k, int kt, bool kt_ok, int lane, float r_fac, const TileRow& r,
+                                 _Float16* st16) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int kk = lane + 64 * h, kg = kt * kTileK + kk;
     const bool valid = kt_ok && kg < k;
-    float v;
-    if constexpr (IN == kInSlerp) {
-      const float ya = r.x[h] * fac[0], yb = r.o[h] * fac[1];
-      v = (ya + r.lr[h] * (yb - ya)) * fac[2];
-      if (valid && blockIdx.x == 0 && f.in_xout) f.in_xout[kg] = v;
-    } else {
-      v = r.x[h] * fac[0];
-    }
+    float v = r.x[h] * r_fac;
     v = valid ? v : 0.f;
     const float sc = v * kRowsUp;
     const _Float16 hi = (_Float16)sc;
@@ -651,21 +622,26 @@ __device__ inline void stage_row(const FusedArgs& f, int k, int kt, bool kt_ok, 
 }
 
 // The GEMV of gemv_kernel (prepared-operand form) for one activation row with the fused input and output sides of
-// kernels.hpp. The row's factors come from the producer's P records, laid out [Q][P]: every wave adds
-// them lane-strided, then across its lanes (the same order in every wave and work-group: identical factors), so
-// the launch has no barrier before its math. Every global load the prologue needs goes out first, the L2-resident
-// ones (records, row values, epilogue inputs) ahead of the weights from HBM (a wave's loads retire in order), and
-// none behind a branch (the compiler's wait counts after a branch assume its loads were not issued), so the
-// prologue waits for them alone. Every thread reaches every barrier.
+// kernels.hpp. The row's factors come from the producer's P records, laid out [Q][P]: a wave adds them
+// lane-strided, then across its lanes (the same order in every wave and work-group: identical factors). kInNorm
+// needs them before its math (every wave makes them itself, so the launch has no barrier before its math);
+// kInSlerp only in the epilogue, where wave 0 makes them. Every global load the launch needs goes out first, the
+// L2-resident ones (records, row values, epilogue inputs) ahead of the weights from HBM (a wave's loads retire in
+// order), and none behind a branch (the compiler's wait counts after a branch assume its loads were not issued).
+// Every thread reaches every barrier. Two k-tiles per wave (K <= 4096, at most 16 waves) is kept to 80 registers,
+// so two work-groups of 12 waves (K = 3072) share a CU: the decode step's projections of 320 and 512 work-groups
+// then run in one round over the 256 CUs.
 template <int R, int T, int MAXT, int IN, int OUT>
-__global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
+__global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(T == 2 ? 6 : 1)))
+gemv_fused_kernel(const FusedArgs f) {
   const GemvArgs& a = f.g;
   extern __shared__ f32x4 red[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
   constexpr bool PAIR = OUT == kOutSwiglu;
   constexpr int RB = PAIR ? R / 2 : R;   // row-blocks per weight: PAIR takes RB of gate and the same RB of up
   static_assert(!PAIR || R % 2 == 0, "paired row-blocks");
-  constexpr bool ROWS = IN != kInOp;
+  constexpr bool RECS = IN != kInOp;          // factors from the producer's records
+  constexpr bool STAGE = IN == kInNorm;       // the operand built from the row in the prologue
   constexpr int Q = IN == kInSlerp ? 5 : 1;   // quantities per record (input side)
   constexpr int NI = Q == 5 ? 3 : 8;          // records per quantity a lane holds from the start (P <= 64 NI)
   int wi = 0;
@@ -677,46 +653,39 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
   float* ldsf = reinterpret_cast<float*>(red);
 
   const int col = lane & 15, grp = lane >> 4;
-  const bool live_col = col < 2;   // the row's high and low operand columns
+  // the live operand columns: the row's high and low parts; kInSlerp: those of a (0, 1) and of b (2, 3)
+  const bool live_col = col < (IN == kInSlerp ? 4 : 2);
   const int entry = 4 * col + grp;
   const int P = f.in_groups;
   // the records through a buffer resource: a load past them returns zero
   const __amdgpu_buffer_rsrc_t rres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(f.in_part), (short)0, ROWS ? Q * P * 4 : 0, 0x00020000);
+      const_cast<float*>(f.in_part), (short)0, RECS ? Q * P * 4 : 0, 0x00020000);
   auto record = [&](int q, int p) {
     const uint32_t off = p < P ? uint32_t((q * P + p) * 4) : 0x80000000u;
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, int(off), 0, 0));
   };
-  float rv[ROWS ? Q : 1][ROWS ? NI : 1];
-  TileRow rows[ROWS ? T : 1];
-  if constexpr (ROWS) {
+  float rv[RECS ? Q : 1][RECS ? NI : 1];
+  TileRow rows[STAGE ? T : 1];
+  // kInNorm makes its factor before its math: the records and the row go out first
+  if constexpr (STAGE) {
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
       for (int i = 0; i < NI; ++i) rv[q][i] = record(q, lane + 64 * i);
 #pragma unroll
-    for (int u = 0; u < T; ++u) load_row<IN>(f, a.k, kt0 + u, kt0 + u < KT, lane, rows[u]);
-  }
-  // the epilogue's inputs of this thread's output (below): sg, su (PAIR) or x, lr (slerp)
-  float ep_a = 0.f, ep_b = 0.f;
-  if constexpr (OUT != kOutPlain) {
-    const int b = rb0 + (int(threadIdx.x) >> 4), w0 = PAIR ? 0 : wi;
-    const int o_i = b * kTileRows + (int(threadIdx.x) & 15), n = a.n[w0];
-    const int oc = int(threadIdx.x) < RB * 16 && o_i < n ? o_i : 0;
-    ep_a = PAIR ? f.out_sg[oc] : f.out_x[oc];
-    ep_b = PAIR ? f.out_su[oc] : f.out_lr[oc];
+    for (int u = 0; u < T; ++u) load_row(f, a.k, kt0 + u, kt0 + u < KT, lane, rows[u]);
   }
   uint4 xb[T][4];
   uint4 cw[T][R];
   uint32_t sw[T][R];
   // the prepared operand through a buffer resource (zero past it: k-tiles past k, columns past the row)
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint4*>(a.xop), (short)0, IN == kInOp ? KT * 4096 : 0, 0x00020000);
+      const_cast<uint4*>(a.xop), (short)0, STAGE ? 0 : KT * 4096, 0x00020000);
 #pragma unroll
   for (int u = 0; u < T; ++u) {
     const int kt = kt0 + u;
     const bool ok = kt < KT;
-    if constexpr (IN == kInOp) {
+    if constexpr (!STAGE) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t off = ok && live_col ? uint32_t(((kt * 4 + t) * 64 + entry) * 16) : 0x80000000u;
@@ -737,7 +706,8 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
     }
   }
 
-  if constexpr (ROWS) {
+  // the row's factors from the records: fa, fb, f2 (kInSlerp) or r (kInNorm, in fac[0])
+  auto factors = [&](float (&fac)[3]) {
     float sq[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
@@ -747,17 +717,22 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
       for (int p0 = 64 * NI; p0 < P; p0 += 64) v += record(q, p0 + lane);
       sq[q] = wave_sum(v);
     }
-    float fac[3] = {inv_norm_of(sq[0]), 0.f, 0.f};
+    fac[0] = inv_norm_of(sq[0]);
+    fac[1] = fac[2] = 0.f;
     if constexpr (IN == kInSlerp) {
       fac[1] = inv_norm_of(sq[1]);
       fac[2] = inv_norm_of(fac[0] * fac[0] * sq[2] + 2.f * fac[0] * fac[1] * sq[3] + fac[1] * fac[1] * sq[4]);
     }
+  };
+  if constexpr (STAGE) {
+    float fac[3];
+    factors(fac);
     _Float16* st16 = reinterpret_cast<_Float16*>(ldsf + L.stage) + size_t(wave) * 256;
     const uint4* st4 = reinterpret_cast<const uint4*>(st16);
 #pragma unroll
     for (int u = 0; u < T; ++u) {
       const int kt = kt0 + u;
-      stage_row<IN>(f, a.k, kt, kt < KT, lane, fac, rows[u], st16);
+      stage_row(a.k, kt, kt < KT, lane, fac[0], rows[u], st16);
       wave_lds_order();
 #pragma unroll
       for (int t = 0; t < 4; ++t) xb[u][t] = live_col ? st4[t * 8 + entry] : make_uint4(0, 0, 0, 0);
@@ -782,30 +757,93 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
     }
   }
 
-  // The waves' accumulators added in LDS in a fixed order by the first RB * 16 threads (all in wave 0), one output
-  // each: row 4 gg + e of row-block r (of each weight, PAIR), i = 16 r + 4 gg + e; then the work-group's record,
-  // each quantity added over those threads by wave_sum.
+  // Wave 0 loads what only the epilogue needs now, while the other waves finish: the records (kInSlerp), the
+  // x_new elements' inputs (work-group j writes its share of the row) and this thread's output's sg, su (PAIR)
+  // or x, lr (slerp).
+  const int xn_per = (a.k + int(gridDim.x) - 1) / int(gridDim.x), xn0 = int(blockIdx.x) * xn_per;
+  float sx = 0.f, so = 0.f, sl = 0.f, ep_a = 0.f, ep_b = 0.f;
+  if (wave == 0) {
+    if constexpr (IN == kInSlerp) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) rv[q][i] = record(q, lane + 64 * i);
+      const int kc = lane < xn_per && xn0 + lane < a.k ? xn0 + lane : 0;
+      sx = f.in_x[kc];
+      so = f.in_o[kc];
+      sl = f.in_lr[kc];
+    }
+    if constexpr (OUT != kOutPlain) {
+      const int b = rb0 + (int(threadIdx.x) >> 4), w0 = PAIR ? 0 : wi;
+      const int o_i = b * kTileRows + (int(threadIdx.x) & 15), n = a.n[w0];
+      const int oc = int(threadIdx.x) < RB * 16 && o_i < n ? o_i : 0;
+      ep_a = PAIR ? f.out_sg[oc] : f.out_x[oc];
+      ep_b = PAIR ? f.out_su[oc] : f.out_lr[oc];
+    }
+  }
+  // Each wave adds its high and low columns (lanes l and l ^ 1) and stores the column pairs' sums; then the first
+  // RB * 16 threads (all in wave 0) add the waves' sums in a fixed order, one output each: row 4 gg + e of
+  // row-block r (of each weight, PAIR), i = 16 r + 4 gg + e; then the work-group's record, each quantity added over
+  // those threads by wave_sum.
+  constexpr int NCP = IN == kInSlerp ? 2 : 1;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    f32x4 v = acc[r];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += dpp<kDppXor1>(v[e]);
+    const int c = lane & 15;
+    if ((c & 1) == 0 && c < 2 * NCP)
+      *reinterpret_cast<f32x4*>(ldsf + (((wave * R + r) * NCP + (c >> 1)) * 4 + (lane >> 4)) * 4) = v;
+  }
   __syncthreads();
   if (wave != 0) return;
+  // kInSlerp: y = global (f2 fa 2^-ea (W a) + f2 fb 2^-eb (W b)), and this work-group's share of x_new
+  float ca = 0.f, cb = 0.f;
+  if constexpr (IN == kInSlerp) {
+    float fac[3];
+    factors(fac);
+    ca = fac[2] * fac[0] * f.in_ia;
+    cb = fac[2] * fac[1] * f.in_ib;
+    if (f.in_xout && lane < xn_per && xn0 + lane < a.k) {
+      const float ya = sx * fac[0], yb = so * fac[1];
+      f.in_xout[xn0 + lane] = (ya + sl * (yb - ya)) * fac[2];
+    }
+  }
   float q[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
   if (int(threadIdx.x) < RB * 16) {
     const int r = int(threadIdx.x) >> 4, gg = (int(threadIdx.x) >> 2) & 3, e = int(threadIdx.x) & 3;
     const int b = rb0 + r, w0 = PAIR ? 0 : wi, n = a.n[w0], o_i = b * kTileRows + 4 * gg + e;
-    // accumulator row 4 gg + e: lanes 16 gg (high column) and 16 gg + 1 (low), element e
-    auto sum_of = [&](int rr) { return wave_sums<R>(ldsf + size_t(rr * 64 + 16 * gg) * 4 + e, S, 4); };
-    const float fscale = IN == kInOp ? (a.xinv ? a.xinv[0] : 1.f) : kRowsDown;
+    // accumulator row 4 gg + e of row-block rr: column pair cp's sums, one per wave
+    auto pair_sum = [&](int rr, int cp) {
+      const float* p = ldsf + ((rr * NCP + cp) * 4 + gg) * 4 + e;
+      float sum = 0.f;
+#pragma unroll
+      for (int w0 = 0; w0 < 16; w0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = p[(w0 + i < S ? w0 + i : S - 1) * R * NCP * 16];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (w0 + i < S) sum += v[i];
+      }
+      return sum;
+    };
+    auto sum_of = [&](int rr) {
+      if constexpr (IN == kInSlerp)
+        return ca * pair_sum(rr, 0) + cb * pair_sum(rr, 1);
+      else
+        return pair_sum(rr, 0) * (IN == kInOp ? (a.xinv ? a.xinv[0] : 1.f) : kRowsDown);
+    };
     if (b < a.nb[w0] && o_i < n) {
       float* yp = a.y + a.y_off[w0];
       if constexpr (PAIR) {
-        const float z = (sum_of(r) * (a.global[0] * fscale)) * ep_a;
-        const float hv = z / (1.f + expf(-z)) * ((sum_of(r + RB) * (a.global[1] * fscale)) * ep_b);
+        const float z = (sum_of(r) * a.global[0]) * ep_a;
+        const float hv = z / (1.f + expf(-z)) * ((sum_of(r + RB) * a.global[1]) * ep_b);
         yp[o_i] = hv;
         q[0] = hv * hv;
       } else {
         const float* cs = a.col_scale[wi];
-        const float sv = sum_of(r) * (a.global[wi] * fscale);
+        const float sv = sum_of(r) * a.global[wi];
         const float o = cs ? sv * cs[o_i] : sv;
         yp[o_i] = o;
         if constexpr (OUT == kOutSlerp) {
@@ -815,6 +853,18 @@ __global__ void __launch_bounds__(MAXT) gemv_fused_kernel(const FusedArgs f) {
           q[2] = (ol * ol) * (x * x);
           q[3] = (ol * lr) * (x * o);
           q[4] = (lr * lr) * (o * o);
+          if (f.out_op) {
+            // the consumer's operand in the linear form of the slerp: a = (1 - lr) x at 2^ea, b = lr o at 2^eb,
+            // high and low f16 parts in columns 0, 1 (a) and 2, 3 (b) of input o_i
+            const int kt = o_i >> 7, kk = o_i & 127, t = (kk >> 3) & 3, g = kk >> 5, e8 = kk & 7;
+            _Float16* op = f.out_op + size_t((kt * 4 + t) * 64 + g) * 8 + size_t(e8);
+            const float av = ol * x * f.out_ea, bv = lr * o * f.out_eb;
+            const _Float16 ah = (_Float16)av, bh = (_Float16)bv;
+            op[0] = ah;
+            op[4 * 8] = (_Float16)(av - (float)ah);
+            op[8 * 8] = bh;
+            op[12 * 8] = (_Float16)(bv - (float)bh);
+          }
         }
       }
     }
@@ -877,10 +927,10 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   const GemvCall& c = f.c;
   XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
   XTG_CHECK(c.m == 1, "fused gemv: %d rows (one)", c.m);
-  XTG_CHECK(f.in != kInOp || c.xop, "fused gemv: no operand");
+  XTG_CHECK(f.in == kInNorm || c.xop, "fused gemv: no operand");
   XTG_CHECK(f.in == kInOp || (f.in_x && f.in_part && f.in_groups > 0 && c.k > 0 && c.k % 16 == 0 &&
                               (f.in == kInNorm || (f.in_o && f.in_lr))),
-            "fused gemv: rows, records and width for the built operand");
+            "fused gemv: rows, records and width for the input side");
   XTG_CHECK(f.out != kOutSwiglu || (c.nw == 2 && c.w[0]->n == c.w[1]->n && f.out_sg && f.out_su && f.out_part),
             "fused gemv: SwiGLU pairs two weights of one shape");
   XTG_CHECK(f.out != kOutSlerp || (c.nw == 1 && f.out_x && f.out_lr && f.out_part && !c.col_scale[0]),
@@ -918,12 +968,19 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   a.in_lr = f.in_lr;
   a.in_part = f.in_part;
   a.in_xout = f.in_xout;
+  a.in_ia = f.in_ia;
+  a.in_ib = f.in_ib;
+  a.out_op = static_cast<_Float16*>(f.out_op);
+  a.out_ea = f.out_ea;
+  a.out_eb = f.out_eb;
   a.out_x = f.out_x;
   a.out_lr = f.out_lr;
   a.out_sg = f.out_sg;
   a.out_su = f.out_su;
   a.out_part = f.out_part;
   XTG_CHECK(wgs == fused_gemv_groups(f), "fused gemv: %d work-groups", wgs);
+  XTG_CHECK(f.in != kInSlerp || (c.k + wgs - 1) / wgs <= 64, "fused gemv: x_new of %d inputs over %d work-groups",
+            c.k, wgs);
   XTG_CHECK(f.out == kOutPlain || wgs <= kMaxFusedGroups, "fused gemv: %d work-groups' records (at most %d)", wgs,
             kMaxFusedGroups);
   XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);

@@ -74,18 +74,23 @@ bool gemv_takes_raw(const GemvCall& c);
 // A norm over a whole row needs every output of the projection that made the row, so as a kernel of its own it
 // costs a dependent launch per norm. Here the producing GEMV writes, besides its outputs, one record of partial
 // sums per work-group over the outputs it owns (records [Q quantities][groups]), and the consuming GEMV adds the
-// P records in a fixed order (every work-group the same order: bit-identical factors) and builds its operand lane
-// by lane from the row. Rows of unit norm take a fixed operand exponent (2^14: |x| <= 1), so no row maximum is
-// needed. One activation row (m = 1).
+// P records in a fixed order (every work-group the same order: bit-identical factors). One activation row (m = 1).
 //   input side:  kInOp     the prepared operand (c.xop / c.xinv)
-//                kInSlerp  x_new = (ya + lr (yb - ya)) f2, ya = x fa, yb = o fb (kernels.cpp:177-189), the three
-//                          factors from kOutSlerp records: fa = 1/sqrt(sum x^2 + 1e-6), fb likewise of o, and f2 of
-//                          sum t^2 = fa^2 sum (1-lr)^2 x^2 + 2 fa fb sum (1-lr) lr x o + fb^2 sum lr^2 o^2; work-group
-//                          0 also writes x_new to in_xout (the next residual)
-//                kInNorm   h r, r = 1/sqrt(sum h^2 + 1e-6) from kOutSwiglu records
+//                kInSlerp  W x_new with x_new = (ya + lr (yb - ya)) f2, ya = x fa, yb = o fb (kernels.cpp:177-189),
+//                          taken in its linear form f2 (fa W a + fb W b), a = (1 - lr) x, b = lr o: the producer
+//                          writes a and b as an operand (c.xop: high and low f16 parts of a 2^ea in columns 0, 1 and
+//                          of b 2^eb in 2, 3; in_ia = 2^-ea, in_ib = 2^-eb), so the math waits for no factor; the
+//                          factors come from kOutSlerp records in the epilogue: fa = 1/sqrt(sum x^2 + 1e-6), fb
+//                          likewise of o, f2 of sum t^2 = fa^2 sum (1-lr)^2 x^2 + 2 fa fb sum (1-lr) lr x o + fb^2
+//                          sum lr^2 o^2; each work-group also writes its share of x_new to in_xout (the next residual)
+//                          from in_x, in_o, in_lr
+//                kInNorm   h r, r = 1/sqrt(sum h^2 + 1e-6) from kOutSwiglu records, built from the row h (in_x) lane
+//                          by lane (unit norm: a fixed operand exponent 2^14, |h r| <= 1)
 //   output side: kOutPlain
 //                kOutSlerp  y as usual, plus records of sum x^2, o^2, (1-lr)^2 x^2, (1-lr) lr x o, lr^2 o^2 over the
-//                           group's outputs o (out_x: the residual [n], out_lr [n]); one weight
+//                           group's outputs o (out_x: the residual [n], out_lr [n]); one weight; with out_op, the
+//                           kInSlerp operand of a = (1 - lr) x and b = lr o at out_ea = 2^ea, out_eb = 2^eb (exponents
+//                           that keep |a 2^ea|, |b 2^eb| <= 2^14; the buffer's entries for inputs past n stay zero)
 //                kOutSwiglu two weights (gate, up) of equal shape, the same row-blocks of both in one work-group:
 //                           y = h = silu(g sg) (u su) [n] (kernels.cpp:225-234) and records of sum h^2
 enum { kInOp = 0, kInSlerp = 1, kInNorm = 2 };
@@ -99,11 +104,14 @@ struct FusedGemv {
   const float* in_part = nullptr;    // the producing launch's records
   int in_groups = 0;                 // their number (fused_gemv_groups of that launch)
   float* in_xout = nullptr;          // kInSlerp: where x_new goes
+  float in_ia = 1.f, in_ib = 1.f;    // kInSlerp: 2^-ea, 2^-eb
   const float* out_x = nullptr;      // kOutSlerp
   const float* out_lr = nullptr;
   const float* out_sg = nullptr;     // kOutSwiglu
   const float* out_su = nullptr;
   float* out_part = nullptr;         // kOutSlerp / kOutSwiglu: the records (5 or 1 x kMaxFusedGroups floats)
+  void* out_op = nullptr;            // kOutSlerp: the consumer's kInSlerp operand (xop_bytes(n) bytes), or NULL
+  float out_ea = 1.f, out_eb = 1.f;  // its factors 2^ea, 2^eb
 };
 int fused_gemv_groups(const FusedGemv& f);
 constexpr int kMaxFusedGroups = 1024;   // work-groups of a launch whose records a consumer takes
