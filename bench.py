@@ -11,10 +11,13 @@ streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed 
 rotation phase), so host launch cost does not set the pace.
 
 value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
-roofline: the GEMV kernel alone (the whole call). For each (shape, rows) a graph of one call per weight copy is
-replayed between two HIP events on the backend's stream; achieved = algorithmic bytes of those launches / their
-time, against the 8 TB/s HBM peak. traffic: HBM bytes per launch (mean over the 6 calls) from
-rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known size
+roofline: the dominant kernel, the GEMV instantiation that moves the largest share of the step's bytes (each call
+is one launch; the launch shape follows the call's shape, so the calls map onto three instantiations; the fused
+gate/up one carries 55 % of the bytes). For each
+(shape, rows) a graph of one call per weight copy is replayed between two HIP events on the backend's stream;
+achieved = algorithmic bytes of the dominant kernel's launches / their time, against the 8 TB/s HBM peak
+(all_calls_*: the same over all 6 calls). traffic: that kernel's HBM bytes per launch from rocprofv3 FETCH_SIZE /
+WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known size
 (profiles/gemv_layer_projections_traffic_pmc.md).
 cpu_baseline: the reference engine's own CPU matmul_nvfp4 (oracle/_ref, compiled from the reference sources)
 on the same shapes and inputs on this host's cores, or the oracle restatement when that library is absent.
@@ -802,17 +805,33 @@ def main():
             hip.graph_launch(g)
     rep = hip.profile_report()
     hip.profile(False)
+    # the kernel that serves each call: one eager call each, named by the profile report
+    kernel_of = {}
+    for name, m in calls:
+        hip.profile(True)
+        hip.matmul_dev(sets[0][name], dx[(name, m)], pkg.X_BF16, m, dy)
+        names = [k for k in hip.profile_report() if k.startswith("gemv_kernel")]
+        hip.profile(False)
+        kernel_of["%s_m%d" % (name, m)] = names[0]
     tot_bytes, tot_s = 0, 0.0
+    by_kernel = {}
     for name, m in calls:
         t = rep["gemv_%s_m%d" % (name, m)]
         launches = t["calls"] * copies
         us = t["ms"] * 1e3 / launches
         b = call_bytes(dict(SHAPES)[name], m)
-        per_call["%s_m%d" % (name, m)] = {"us_per_launch": round(us, 3), "bytes": b, "gbs": round(b / us / 1e3, 1),
-                                          "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        key = "%s_m%d" % (name, m)
+        per_call[key] = {"kernel": kernel_of[key], "us_per_launch": round(us, 3), "bytes": b,
+                         "gbs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         tot_bytes += b * launches
         tot_s += t["ms"] / 1e3
-    achieved = tot_bytes / tot_s / 1e9
+        kb = by_kernel.setdefault(kernel_of[key], {"bytes": 0.0, "s": 0.0, "calls": []})
+        kb["bytes"] += b * launches
+        kb["s"] += t["ms"] / 1e3
+        kb["calls"].append(key)
+    all_achieved = tot_bytes / tot_s / 1e9
+    dominant = max(by_kernel, key=lambda k: by_kernel[k]["bytes"])
+    achieved = by_kernel[dominant]["bytes"] / by_kernel[dominant]["s"] / 1e9
     traffic = measured_traffic()
     if traffic:
         for key, v in per_call.items():
@@ -823,8 +842,11 @@ def main():
         keys = ["%s_m%d" % (name, m) for name, _ in SHAPES]
         by_m["m%d" % m] = round(sum(per_call[k]["bytes"] for k in keys) /
                                 sum(per_call[k]["us_per_launch"] for k in keys) / 1e3, 1)
-    log("GEMV kernel: %.1f GB/s (%.1f%% of HBM peak) averaged over the 6 shapes; M=1 %.1f, M=8 %.1f GB/s"
-        % (achieved, achieved / HBM_PEAK_GBS * 100, by_m["m1"], by_m["m8"]))
+    log("GEMV: dominant kernel %s (%s, %.0f%% of the step's bytes, %.0f%% of its kernel time) %.1f GB/s (%.1f%% "
+        "of HBM peak); all 6 calls %.1f GB/s (%.1f%%); M=1 %.1f, M=8 %.1f GB/s"
+        % (dominant, " + ".join(by_kernel[dominant]["calls"]), 100 * by_kernel[dominant]["bytes"] / tot_bytes,
+           100 * by_kernel[dominant]["s"] / tot_s, achieved,
+           achieved / HBM_PEAK_GBS * 100, all_achieved, all_achieved / HBM_PEAK_GBS * 100, by_m["m1"], by_m["m8"]))
     for k, v in per_call.items():
         log("  %-22s %7.3f us  %7.1f GB/s" % (k, v["us_per_launch"], v["gbs"]))
 
@@ -875,10 +897,16 @@ def main():
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     # HBM bytes per launch, averaged over the 6 calls as achieved is (algorithmic: the mean of
-                     # per_call bytes); per-call values in config.per_call
-                     "traffic": (int(sum(v["traffic"] for v in per_call.values()) / len(per_call))
-                                 if all("traffic" in v for v in per_call.values()) else None)},
+                     # the dominant kernel's HBM bytes per launch (the mean over its calls, as achieved is);
+                     # per-call values in config.per_call
+                     "traffic": (int(sum(per_call[k]["traffic"] for k in by_kernel[dominant]["calls"]) /
+                                     len(by_kernel[dominant]["calls"]))
+                                 if all("traffic" in per_call[k] for k in by_kernel[dominant]["calls"]) else None),
+                     "kernel": dominant, "kernel_calls": by_kernel[dominant]["calls"],
+                     "kernel_byte_share": round(by_kernel[dominant]["bytes"] / tot_bytes, 4),
+                     "kernel_time_share": round(by_kernel[dominant]["s"] / tot_s, 4),
+                     "all_calls_achieved": round(all_achieved, 1),
+                     "all_calls_frac": round(all_achieved / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
         "gemv_sweep": sweep,
         "decode_attention": attention,

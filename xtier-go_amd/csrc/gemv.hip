@@ -384,12 +384,18 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     }
     return;
   }
+  // each wave adds its high and low columns (lanes l and l ^ 1) and stores row j's sums at [wave][r][j][gg]
 #pragma unroll
-  for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
+  for (int r = 0; r < R; ++r) {
+    f32x4 v = acc[r];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += dpp<kDppXor1>(v[e]);
+    if ((col & 1) == 0 && (col >> 1) < a.m) red[((wave * R + r) * kMaxRows + (col >> 1)) * 4 + grp] = v;
+  }
   __syncthreads();
   for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
-    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7, ln = gg * 16 + 2 * jj;
-    if (rb0 + r >= nb) continue;
+    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7;
+    if (rb0 + r >= nb || jj >= a.m) continue;
     // the S <= 16 waves in order, the reads in batches of 4 with clamped indices (no wait between them)
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -397,10 +403,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
       if (w0 >= S) break;
       f32x4 v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int w = w0 + i < S ? w0 + i : S - 1;
-        v[i] = red[(w * R + r) * 64 + ln] + red[(w * R + r) * 64 + ln + 1];
-      }
+      for (int i = 0; i < 4; ++i) v[i] = red[(((w0 + i < S ? w0 + i : S - 1) * R + r) * kMaxRows + jj) * 4 + gg];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (w0 + i < S) sum += v[i];
@@ -535,7 +538,7 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   const int threads = sh.s * 64;
   GemvFn fn = gemv_fn(sh.r, sh.t, threads, xr);
   XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d%s", sh.r, sh.t, xr ? " on raw rows" : "");
-  const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * 64 * sizeof(f32x4) : 0;
+  const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * kMaxRows * 4 * sizeof(f32x4) : 0;
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, threads <= 512 ? 512 : 1024)
