@@ -319,7 +319,8 @@ def measured_traffic():
 
 def pmc_pass(pkg, wl):
     """Counter pass: the copy first (known bytes read and written once), then the GEMV calls, each followed by a
-    finish so dispatches stay apart. Kernel dispatch order: copy, then one gemv_kernel per call."""
+    finish so dispatches stay apart, then 4 launches of the NVFP4 LM head. Kernel dispatch order: copy, one
+    gemv_kernel per call (24), then prep_x_kernel + gemv_kernel per head launch."""
     hip = pkg.HipBackend(0)
     src, dst = hip.alloc(COPY_BYTES), hip.alloc(COPY_BYTES)
     hip.copy(src, dst, COPY_BYTES)
@@ -346,6 +347,21 @@ def pmc_pass(pkg, wl):
                 hip.finish()
                 i += 1
             dx.free()
+    for s in sets:
+        for ws in s.values():
+            for w in ws:
+                hip.release_weight(w)
+    # then the 4B-shaped model's NVFP4 LM head (131072 x 3072, one FP32 row prepared by prep_x_kernel), two weight
+    # copies read in turn, 4 launches
+    heads = [pkg.Weight(*wl.nvfp4_weight(rng, 131072, 3072)) for _ in range(2)]
+    for w in heads:
+        hip.prepare(w)
+    x = rng.standard_normal((1, 3072)).astype(np.float32)
+    dx = hip.array(x)
+    dh = hip.array(shape=(131072,))
+    for i in range(4):
+        hip.matmul_dev([heads[i % 2]], dx, pkg.X_F32, 1, dh)
+        hip.finish()
     hip.release(src)
     hip.release(dst)
     hip.close()
