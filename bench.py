@@ -727,6 +727,9 @@ def main():
                          "or also the FP8 caches of the reference Dory's default (M=1; the default)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step measurement (for profiling it); prints its own JSON line")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
+                         "left out of the JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels are one GPU's share of a "
@@ -871,15 +874,17 @@ def main():
         cpu = cpu_baseline(base, xs, args.cpu_seconds)
         log("CPU baseline (%s, %d threads): %.2f GB/s" % (cpu["kind"], cpu["cores"], cpu["value"]))
 
-    sweep = gemv_sweep(pkg, wl, hip, 5, 0 if args.no_cpu else 1.0)
-    attention = decode_attention_bench(pkg, wl, hip, 3, 0 if args.no_cpu else 6.0)
-    bf16_head = bf16_head_bench(pkg, wl, hip, 10)
-    sampling = sampling_bench(pkg, hip, 20)
-    prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
-    prefill["attention_ctx4096"] = prefill_attention_bench(pkg, wl, hip, 512, 4096, 10)
+    sweep = attention = bf16_head = sampling = prefill = None
+    if not args.gemv_only:
+        sweep = gemv_sweep(pkg, wl, hip, 5, 0 if args.no_cpu else 1.0)
+        attention = decode_attention_bench(pkg, wl, hip, 3, 0 if args.no_cpu else 6.0)
+        bf16_head = bf16_head_bench(pkg, wl, hip, 10)
+        sampling = sampling_bench(pkg, hip, 20)
+        prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
+        prefill["attention_ctx4096"] = prefill_attention_bench(pkg, wl, hip, 512, 4096, 10)
 
     decode = None
-    if not args.no_decode:
+    if not args.no_decode and not args.gemv_only:
         for name in list(base):   # the projection bench's weights are no longer needed
             for s in sets:
                 for w in s[name]:
