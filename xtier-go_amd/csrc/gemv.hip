@@ -573,16 +573,27 @@ struct FusedArgs {
 constexpr float kRowsUp = 16384.f, kRowsDown = 1.f / 16384.f;
 
 // LDS of a fused launch, in floats: each wave's high + low column sums [S][R][NCP column pairs][4 gg][4 e] (NCP:
-// 2 for kInSlerp's a and b, else 1), then each wave's staging of one k-tile's live operand columns [S][4 steps]
-// [8 entries][8 f16].
+// 2 for kInSlerp's a and b, else 1), their totals over the waves [R][NCP][16], then each wave's staging of one
+// k-tile's live operand columns [S][4 steps][8 entries][8 f16].
 struct FusedLds {
-  int red, stage, total;
+  int red, sums, stage, total;
   __host__ __device__ FusedLds(int S, int R, int in) {
+    const int ncp = in == kInSlerp ? 2 : 1;
     red = 0;
-    stage = red + S * R * (in == kInSlerp ? 2 : 1) * 16;
+    sums = red + S * R * ncp * 16;   // then the waves' totals, [R][NCP][16]
+    stage = sums + R * ncp * 16;
     total = stage + (in == kInNorm ? S * 128 : 0);
   }
 };
+
+// A work-group barrier for LDS only: the waves' LDS writes are complete and visible after it, but their outstanding
+// global loads are not waited for (__syncthreads' fence waits for every vector memory operation, so loads issued
+// just before it for the epilogue would hold the whole work-group).
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // Lanes of one wave passing values through LDS: a wave's LDS operations execute in issue order, so keeping the
 // compiler's order is enough.
@@ -798,8 +809,26 @@ gemv_fused_kernel(const FusedArgs f) {
     if ((c & 1) == 0 && c < 2 * NCP)
       *reinterpret_cast<f32x4*>(ldsf + (((wave * R + r) * NCP + (c >> 1)) * 4 + (lane >> 4)) * 4) = v;
   }
-  __syncthreads();
+  lds_barrier();
   if (wave != 0) return;
+  // the waves' sums added in wave order, one (row-block, column pair, row) per lane (the factors below do not
+  // depend on them, so the two interleave)
+  float* tot = ldsf + L.sums;
+  for (int u = lane; u < R * NCP * 16; u += 64) {
+    const int rr = u / (NCP * 16), cp = (u / 16) % NCP, gg = (u >> 2) & 3, e = u & 3;
+    const float* p = ldsf + ((rr * NCP + cp) * 4 + gg) * 4 + e;
+    float sum = 0.f;
+#pragma unroll
+    for (int w0 = 0; w0 < 16; w0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = p[(w0 + i < S ? w0 + i : S - 1) * R * NCP * 16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (w0 + i < S) sum += v[i];
+    }
+    tot[u] = sum;
+  }
   // kInSlerp: y = global (f2 fa 2^-ea (W a) + f2 fb 2^-eb (W b)), and this work-group's share of x_new
   float ca = 0.f, cb = 0.f;
   if constexpr (IN == kInSlerp) {
@@ -812,25 +841,13 @@ gemv_fused_kernel(const FusedArgs f) {
       f.in_xout[xn0 + lane] = (ya + sl * (yb - ya)) * fac[2];
     }
   }
+  wave_lds_order();   // the totals are in
   float q[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
   if (int(threadIdx.x) < RB * 16) {
     const int r = int(threadIdx.x) >> 4, gg = (int(threadIdx.x) >> 2) & 3, e = int(threadIdx.x) & 3;
     const int b = rb0 + r, w0 = PAIR ? 0 : wi, n = a.n[w0], o_i = b * kTileRows + 4 * gg + e;
-    // accumulator row 4 gg + e of row-block rr: column pair cp's sums, one per wave
-    auto pair_sum = [&](int rr, int cp) {
-      const float* p = ldsf + ((rr * NCP + cp) * 4 + gg) * 4 + e;
-      float sum = 0.f;
-#pragma unroll
-      for (int w0 = 0; w0 < 16; w0 += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = p[(w0 + i < S ? w0 + i : S - 1) * R * NCP * 16];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (w0 + i < S) sum += v[i];
-      }
-      return sum;
-    };
+    // accumulator row 4 gg + e of row-block rr: column pair cp's total over the waves
+    auto pair_sum = [&](int rr, int cp) { return tot[(rr * NCP + cp) * 16 + 4 * gg + e]; };
     auto sum_of = [&](int rr) {
       if constexpr (IN == kInSlerp)
         return ca * pair_sum(rr, 0) + cb * pair_sum(rr, 1);
