@@ -809,10 +809,24 @@ gemv_fused_kernel(const FusedArgs f) {
     if ((c & 1) == 0 && c < 2 * NCP)
       *reinterpret_cast<f32x4*>(ldsf + (((wave * R + r) * NCP + (c >> 1)) * 4 + (lane >> 4)) * 4) = v;
   }
+  // kInSlerp: y = global (f2 fa 2^-ea (W a) + f2 fb 2^-eb (W b)), and this work-group's share of x_new; wave 0
+  // works them out before the barrier, while the other waves may still be loading
+  float ca = 0.f, cb = 0.f;
+  if constexpr (IN == kInSlerp) {
+    if (wave == 0) {
+      float fac[3];
+      factors(fac);
+      ca = fac[2] * fac[0] * f.in_ia;
+      cb = fac[2] * fac[1] * f.in_ib;
+      if (f.in_xout && lane < xn_per && xn0 + lane < a.k) {
+        const float ya = sx * fac[0], yb = so * fac[1];
+        f.in_xout[xn0 + lane] = (ya + sl * (yb - ya)) * fac[2];
+      }
+    }
+  }
   lds_barrier();
   if (wave != 0) return;
-  // the waves' sums added in wave order, one (row-block, column pair, row) per lane (the factors below do not
-  // depend on them, so the two interleave)
+  // the waves' sums added in wave order, one (row-block, column pair, row) per lane
   float* tot = ldsf + L.sums;
   for (int u = lane; u < R * NCP * 16; u += 64) {
     const int rr = u / (NCP * 16), cp = (u / 16) % NCP, gg = (u >> 2) & 3, e = u & 3;
@@ -828,18 +842,6 @@ gemv_fused_kernel(const FusedArgs f) {
         if (w0 + i < S) sum += v[i];
     }
     tot[u] = sum;
-  }
-  // kInSlerp: y = global (f2 fa 2^-ea (W a) + f2 fb 2^-eb (W b)), and this work-group's share of x_new
-  float ca = 0.f, cb = 0.f;
-  if constexpr (IN == kInSlerp) {
-    float fac[3];
-    factors(fac);
-    ca = fac[2] * fac[0] * f.in_ia;
-    cb = fac[2] * fac[1] * f.in_ib;
-    if (f.in_xout && lane < xn_per && xn0 + lane < a.k) {
-      const float ya = sx * fac[0], yb = so * fac[1];
-      f.in_xout[xn0 + lane] = (ya + sl * (yb - ya)) * fac[2];
-    }
   }
   wave_lds_order();   // the totals are in
   float q[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
