@@ -611,8 +611,12 @@ template <int D, int QB>
 constexpr int scan_merge_floats() {
   return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16 / scan_merge_passes<D>()) * 64 * 4;
 }
+// Row stride of the processed q-cols in LDS: D + 4 floats. The operand build reads 16 q-cols at one dim offset
+// per instruction; at a stride of D (a multiple of the bank count) those 16 reads share one bank.
+template <int D>
+constexpr int sq_stride() { return D + 4; }
 template <int D, int QB, bool RAWQ>
-constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * D + 2 * kProdRows * (D / 2) : 0; }
+constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * sq_stride<D>() + 2 * kProdRows * (D / 2) : 0; }
 template <int D, int QB>
 constexpr int scan_sq_offset() { return q_in_lds<D>() ? scan_qop_floats<D, QB>() : scan_merge_floats<D, QB>(); }
 template <int D, int QB, bool RAWQ>
@@ -663,7 +667,9 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   constexpr bool SKEW = D > 128;
   Tile A;
   std::conditional_t<SKEW, char, Tile> B;
-  load(A, min(t, t_last));
+  // raw q: the tile's loads go out right after the few q loads, so the q processing waits only for those (loads
+  // complete in order); otherwise first
+  if constexpr (!RAWQ) load(A, min(t, t_last));
 
   // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale * log2(e),
   // three terms. lo: the first stored position the column sees.
@@ -699,8 +705,9 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     constexpr int PP = HALF / TPV;        // RoPE pairs per thread
     constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
     static_assert(PP % 2 == 0 && TPV * QB * 16 == kWaves * 64, "q-col split");
-    float* sq = lds + scan_sq_offset<D, QB>();   // processed q-cols [QB * 16][D]
-    float* scos = sq + QB * 16 * D;
+    constexpr int SQS = sq_stride<D>();
+    float* sq = lds + scan_sq_offset<D, QB>();   // processed q-cols [QB * 16][SQS]
+    float* scos = sq + QB * 16 * SQS;
     float* ssin = scos + kProdRows * HALF;
     const int nrows = min(a.rpb, a.n_q - row0);
     const int v = int(threadIdx.x) / TPV, p0 = (int(threadIdx.x) % TPV) * PP;
@@ -729,6 +736,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
         s1[e] = s1[e + 1] = s2[e] = s2[e + 1] = 1.f;
       }
     }
+    load(A, min(t, t_last));
 #pragma unroll
     for (int u = 0; u < kAngles; ++u) {
       const int e = int(threadIdx.x) + u * kWaves * 64;
@@ -756,8 +764,8 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     const float f = inv_norm_of(ss);
 #pragma unroll
     for (int e = 0; e < PP; e += 2) {
-      *reinterpret_cast<float2*>(sq + v * D + p0 + e) = make_float2((x1[e] * f) * s1[e], (x1[e + 1] * f) * s1[e + 1]);
-      *reinterpret_cast<float2*>(sq + v * D + HALF + p0 + e) =
+      *reinterpret_cast<float2*>(sq + v * SQS + p0 + e) = make_float2((x1[e] * f) * s1[e], (x1[e + 1] * f) * s1[e + 1]);
+      *reinterpret_cast<float2*>(sq + v * SQS + HALF + p0 + e) =
           make_float2((x2[e] * f) * s2[e], (x2[e + 1] * f) * s2[e + 1]);
     }
     __syncthreads();
@@ -765,7 +773,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int c = c_first; c < NC; c += c_step) {
-        const float* sp = sq + (qb * 16 + j) * D + 32 * c + 8 * g;
+        const float* sp = sq + (qb * 16 + j) * SQS + 32 * c + 8 * g;
         const float4 u = *reinterpret_cast<const float4*>(sp);
         const float4 w = *reinterpret_cast<const float4*>(sp + 4);
         float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
