@@ -1301,25 +1301,26 @@ __global__ void __launch_bounds__(kWaves * 64) attn_step_kernel(const ScanArgs a
 
 constexpr int kMergeThreads = 512;
 
-// The merged output of one q-col for 8 dims dd .. dd + 7 over its S1 records rec0 + s * qpad (kv.cpp:262-285:
-// splits with a zero sum are skipped, weights 2^(m_s - max) with the maxima in base-2 units, the sum's reciprocal
-// applied last). The running
-// maximum is updated once per batch of B records, whose loads are all in flight together.
+// The online-softmax state (running maximum M in base-2 units, sum L, unnormalised output o) of one q-col for 8 dims
+// dd .. dd + 7 over the records rec0 + s * qpad, s = s0, s0 + ds, ... < S1 (kv.cpp:262-285: splits with a zero sum
+// are skipped, weights 2^(m_s - max)). The running maximum is updated once per batch of B records, whose loads are
+// all in flight together.
 template <int D, int B>
-__device__ inline void merge8(const float* __restrict__ acc, const float* __restrict__ ml, size_t rec0, int qpad,
-                              int S1, int dd, float out[8]) {
-  float M = -INFINITY, L = 0.f, o[8];
+__device__ inline void merge8_state(const float* __restrict__ acc, const float* __restrict__ ml, size_t rec0, int qpad,
+                                    int s0, int ds, int S1, int dd, float& M, float& L, float (&o)[8]) {
+  M = -INFINITY;
+  L = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
-  for (int s0 = 0; s0 < S1; s0 += B) {
+  for (int sb = s0; sb < S1; sb += B * ds) {
     float2 w2[B];
     float4 x0[B], x1[B];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       w2[u] = make_float2(-INFINITY, 0.f);
       x0[u] = x1[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (s0 + u < S1) {
-        const size_t rec = rec0 + size_t(s0 + u) * size_t(qpad);
+      if (sb + u * ds < S1) {
+        const size_t rec = rec0 + size_t(sb + u * ds) * size_t(qpad);
         w2[u] = *reinterpret_cast<const float2*>(ml + rec * 2);
         x0[u] = *reinterpret_cast<const float4*>(acc + rec * D + dd);
         x1[u] = *reinterpret_cast<const float4*>(acc + rec * D + dd + 4);
@@ -1345,6 +1346,14 @@ __device__ inline void merge8(const float* __restrict__ acc, const float* __rest
       }
     M = mn;
   }
+}
+
+// The merged output over all S1 records (the sum's reciprocal applied last).
+template <int D, int B>
+__device__ inline void merge8(const float* __restrict__ acc, const float* __restrict__ ml, size_t rec0, int qpad,
+                              int S1, int dd, float out[8]) {
+  float M, L, o[8];
+  merge8_state<D, B>(acc, ml, rec0, qpad, 0, 1, S1, dd, M, L, o);
   const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] = o[e] * inv;
@@ -1357,13 +1366,17 @@ struct MergeArgs {
 };
 
 // Chunk c (dims 8c .. 8c + 7 of the row's heads * D outputs) of query row `row`.
+// The first record of chunk c (dims 8c .. 8c + 7 of the row's heads * D outputs) of query row `row`.
+template <int D>
+__device__ inline size_t chunk_rec0(const MergeArgs& a, int row, int c) {
+  const int h = 8 * c / D;
+  const int blk = row / a.rpb, qc = (row % a.rpb) * a.group + h % a.group;
+  return ((size_t(blk) * size_t(a.kv_heads) + size_t(h / a.group)) * size_t(a.splits1)) * size_t(a.qpad) + size_t(qc);
+}
+
 template <int D, int B>
 __device__ inline void merge_chunk(const MergeArgs& a, int row, int c, float out[8]) {
-  const int e0 = 8 * c, h = e0 / D, dd = e0 % D;
-  const int blk = row / a.rpb, qc = (row % a.rpb) * a.group + h % a.group;
-  const size_t rec0 = ((size_t(blk) * size_t(a.kv_heads) + size_t(h / a.group)) * size_t(a.splits1)) * size_t(a.qpad) +
-                      size_t(qc);
-  merge8<D, B>(a.acc, a.ml, rec0, a.qpad, a.splits1, dd, out);
+  merge8<D, B>(a.acc, a.ml, chunk_rec0<D>(a, row, c), a.qpad, a.splits1, (8 * c) % D, out);
 }
 
 // One work-group per query row: out[row][heads][D].
@@ -1421,34 +1434,54 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
   if (xop) emit_operand_mx<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, mx * f);
 }
 
-// The one-token step's gate with its norm left to the o-projection: one wave per head merges the head's partials
-// (lane l: dims 8 l .. 8 l + 7), applies a * sigmoid(g * gs) (dory.cpp:509-512) and writes the gated head to y,
-// and its sum of squares to rec[head] (wave_sum: the same order every call), from which the o-projection's
+// The one-token step's gate with its norm left to the o-projection: one wave per head. Lane l = (part p, chunk c)
+// with CH = D / 8 chunks of 8 dims and P = 64 / CH parts: part p merges the head's records s = p, p + P, ... (up to
+// 8 of them per batch, all loads in flight together), the parts' states are combined across lanes (exchanges of
+// lanes l ^ CH, l ^ 2 CH, ...: the same order every call), and part 0 applies a * sigmoid(g * gs)
+// (dory.cpp:509-512), writes the gated head to y and its sum of squares to rec[head], from which the o-projection's
 // operand takes the justnorm (dory.cpp:513-515).
+template <int CH>
+__device__ inline float xor_parts_max(float v) {
+  if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
+  if constexpr (CH <= 16) v = xor16_max(v);
+  return xor32_max(v);
+}
+template <int CH>
+__device__ inline float xor_parts_sum(float v) {
+  if constexpr (CH <= 8) v += __shfl_xor(v, 8);
+  if constexpr (CH <= 16) v = xor16_sum(v);
+  return xor32_sum(v);
+}
+
 template <int D>
 __global__ void __launch_bounds__(64) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
                                                              const float* __restrict__ gs, float* __restrict__ y,
                                                              float* __restrict__ rec) {
-  const int h = blockIdx.x, lane = threadIdx.x;
-  float s = 0.f;
-  if (lane < D / 8) {
-    const int c = h * (D / 8) + lane;
-    float t[8];
-    merge_chunk<D, 12>(a, 0, c, t);
-    const float4 g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
-    const float4 s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
-    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  constexpr int CH = D / 8, P = 64 / CH;
+  static_assert(CH >= 8 && CH <= 32, "8 to 32 chunks per head");
+  const int h = blockIdx.x, lane = threadIdx.x, c = h * CH + lane % CH, p = lane / CH;
+  const float4 g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
+  float M, L, o[8];
+  merge8_state<D, 8>(a.acc, a.ml, chunk_rec0<D>(a, 0, c), a.qpad, p, P, a.splits1, (8 * c) % D, M, L, o);
+  const float Mh = xor_parts_max<CH>(M);
+  const float f = M == -INFINITY ? 0.f : exp2_fast(M - Mh);
+  const float Lh = xor_parts_sum<CH>(L * f);
+  const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
+  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float t[8], ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      t[e] = t[e] * (1.f / (1.f + expf(-gv[e] * sv[e])));
-      s += t[e] * t[e];
-    }
+  for (int e = 0; e < 8; ++e) {
+    t[e] = (xor_parts_sum<CH>(o[e] * f) * inv) * (1.f / (1.f + expf(-gv[e] * sv[e])));
+    ss += t[e] * t[e];
+  }
+  if (p == 0) {
     *reinterpret_cast<float4*>(y + 8 * c) = make_float4(t[0], t[1], t[2], t[3]);
     *reinterpret_cast<float4*>(y + 8 * c + 4) = make_float4(t[4], t[5], t[6], t[7]);
   }
-  s = wave_sum(s);
-  if (lane == 0) rec[h] = s;
+  ss = wave_sum(p == 0 ? ss : 0.f);
+  if (lane == 0) rec[h] = ss;
 }
 
 // ------------------------------------------------------------------------------------------------------- plan
