@@ -49,10 +49,12 @@ def test_tiny_model_many_steps(hip, orc, wl):
     print("tiny model: worst logits rel-L2 %.2e over %d positions" % (worst, pos))
 
 
-def test_one_token_steps_fused_and_separate(hip, orc, wl, monkeypatch):
+@pytest.mark.parametrize("loops", [2, 1])
+def test_one_token_steps_fused_and_separate(hip, orc, wl, monkeypatch, loops):
     """One-token steps run their norms inside the projections (records of partial sums); XTG_DECODE_UNFUSED=1 takes
-    the separate norm launches instead. Both against the oracle, and against each other, over the same calls."""
-    w = wl.DoryWeights(wl.DORY_TINY, seed=13, context=128)
+    the separate norm launches instead. Both against the oracle, and against each other, over the same calls. With
+    one loop the loop's entry and exit norms ride on the next projection too."""
+    w = wl.DoryWeights(dict(wl.DORY_TINY, loops=loops), seed=13, context=128)
     H, V = w.cfg["hidden"], w.cfg["vocab"]
     ref = orc.Dory(w, wl)
     fused = hip.dory(w)

@@ -242,7 +242,10 @@ void DorySession::sublayer(Layer& L, int m, long long pos0, int inst, bool store
 void DorySession::materialize(int m) {
   if (!pend_) return;
   b_.slerp_norm(x_, o_, pend_lr_, m, c_.hidden, op_h_);
+  if (pend_post_ == kPostAddNorm) b_.add_norm(x_, x_, x_, m, c_.hidden, op_h_);
+  if (pend_post_ == kPostNorm) b_.add_norm(x_, nullptr, x_, m, c_.hidden, op_h_);
   pend_ = false;
+  pend_post_ = kPostNone;
 }
 
 void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, bool store) {
@@ -260,6 +263,7 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
     f.in_xout = x2_;
     f.in_ia = 1.f / pend_a_;
     f.in_ib = 1.f / pend_b_;
+    f.in_post = pend_post_;
   };
   const void* in_op = pend_ ? op_lin_ : op_h_;
   auto slerp_side = [&](FusedGemv& f) {
@@ -282,6 +286,7 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
     if (!pend_) return;
     std::swap(x_, x2_);   // the projection wrote the new residual
     pend_ = false;
+    pend_post_ = kPostNone;
   };
   if (L.w.kind == XTG_DORY_MLP) {
     const xtg_nvfp4 gu[2] = {L.w.gate, L.w.up};
@@ -349,19 +354,31 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
   };
   size_t l = 0;
   for (; l < size_t(c_.n_in); ++l) run(layers_[l], 0, true);
-  materialize(m);
-  // the loops start from state = input = x: the first entry is justnorm(x + x) read in place, and input is kept
-  // only for later entries; the last exit writes x in place (x = state = justnorm(x))
-  if (c_.loops > 1) b_.copy(x_, 0, input_, 0, bytes);
+  // One loop and a slerp pending: the loop's entry and exit norms ride on the next projection (in_post), since
+  // neither state nor input is read again. Otherwise they run on the materialized residual.
+  const bool fold = c_.loops == 1 && c_.n_rec > 0;
+  if (fold && pend_) {
+    pend_post_ = kPostAddNorm;
+  } else {
+    materialize(m);
+    // the loops start from state = input = x: the first entry is justnorm(x + x) read in place, and input is kept
+    // only for later entries; the last exit writes x in place (x = state = justnorm(x))
+    if (c_.loops > 1) b_.copy(x_, 0, input_, 0, bytes);
+    b_.add_norm(x_, x_, x_, m, H, op_h_);   // x = justnorm(state + input), state = input = x
+  }
   for (int i = 0; i < c_.loops; ++i) {
     const bool last = i == c_.loops - 1;
-    b_.add_norm(i == 0 ? x_ : state_, i == 0 ? x_ : input_, x_, m, H, op_h_);   // x = justnorm(state + input)
+    if (i > 0) b_.add_norm(state_, input_, x_, m, H, op_h_);   // x = justnorm(state + input)
     // last_loop: every loop attends to the chunk's own keys, the cache keeps the last loop's (dory.cpp:534-537)
     const bool per_loop = c_.kv_mode == XTG_KV_PER_LOOP;
     for (size_t r = size_t(c_.n_in); r < size_t(c_.n_in + c_.n_rec); ++r)
       run(layers_[r], per_loop ? i : 0, per_loop || last);
-    materialize(m);
-    b_.add_norm(x_, nullptr, last ? x_ : state_, m, H, last ? op_h_ : nullptr);   // state = justnorm(x)
+    if (fold && pend_ && pend_post_ == kPostNone) {
+      pend_post_ = kPostNorm;   // x = state = justnorm(x)
+    } else {
+      materialize(m);
+      b_.add_norm(x_, nullptr, last ? x_ : state_, m, H, last ? op_h_ : nullptr);   // state = justnorm(x)
+    }
   }
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) run(layers_[l], 0, true);
   materialize(m);

@@ -86,6 +86,7 @@ class DorySession {
   const float* pend_lr_ = nullptr;
   float pend_a_ = 1.f, pend_b_ = 1.f;   // its linear-form operand's factors, the operand in op_lin_
   int pend_groups_ = 0;
+  int pend_post_ = 0;   // a loop boundary's norm of the slerped residual, folded into the consumer (kPost*)
   // GEMV operands, each written by the kernel that produces its rows: x's (K = hidden; by the slerp / loop norms
   // or, for the first sublayer, prep_x), the gated attention's (K = heads * head_dim), the SwiGLU's (K = ffn)
   void* op_h_ = nullptr;

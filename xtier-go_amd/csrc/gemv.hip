@@ -560,6 +560,7 @@ struct FusedArgs {
   const float* in_part;
   float* in_xout;
   float in_ia, in_ib;
+  int in_post;
   const float* out_x;
   const float* out_lr;
   const float* out_sg;
@@ -720,7 +721,8 @@ gemv_fused_kernel(const FusedArgs f) {
     }
   }
 
-  // the row's factors from the records: fa, fb, f2 (kInSlerp) or r (kInNorm, in fac[0])
+  // the row's factors from the records: fa, fb, f2 (kInSlerp; with in_post's norm folded into f2) or r (kInNorm, in
+  // fac[0])
   auto factors = [&](float (&fac)[3]) {
     float sq[Q];
 #pragma unroll
@@ -735,7 +737,12 @@ gemv_fused_kernel(const FusedArgs f) {
     fac[1] = fac[2] = 0.f;
     if constexpr (IN == kInSlerp) {
       fac[1] = inv_norm_of(sq[1]);
-      fac[2] = inv_norm_of(fac[0] * fac[0] * sq[2] + 2.f * fac[0] * fac[1] * sq[3] + fac[1] * fac[1] * sq[4]);
+      const float t2 = fac[0] * fac[0] * sq[2] + 2.f * fac[0] * fac[1] * sq[3] + fac[1] * fac[1] * sq[4];
+      fac[2] = inv_norm_of(t2);
+      if (f.in_post != kPostNone) {
+        const float x2 = fac[2] * fac[2] * t2;   // sum x_new^2
+        fac[2] *= f.in_post == kPostAddNorm ? 2.f * inv_norm_of(4.f * x2) : inv_norm_of(x2);
+      }
     }
   };
   if constexpr (STAGE) {
@@ -992,6 +999,7 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   a.in_xout = f.in_xout;
   a.in_ia = f.in_ia;
   a.in_ib = f.in_ib;
+  a.in_post = f.in_post;
   a.out_op = static_cast<_Float16*>(f.out_op);
   a.out_ea = f.out_ea;
   a.out_eb = f.out_eb;

@@ -83,7 +83,9 @@ bool gemv_takes_raw(const GemvCall& c);
 //                          factors come from kOutSlerp records in the epilogue: fa = 1/sqrt(sum x^2 + 1e-6), fb
 //                          likewise of o, f2 of sum t^2 = fa^2 sum (1-lr)^2 x^2 + 2 fa fb sum (1-lr) lr x o + fb^2
 //                          sum lr^2 o^2; each work-group also writes its share of x_new to in_xout (the next residual)
-//                          from in_x, in_o, in_lr
+//                          from in_x, in_o, in_lr. in_post folds one more row norm of x_new into f2 (sum x_new^2 =
+//                          f2^2 sum t^2): kPostAddNorm x_new := justnorm(x_new + x_new) (a loop's entry with state
+//                          = input), kPostNorm x_new := justnorm(x_new) (a loop's exit)
 //                kInNorm   h r, r = 1/sqrt(sum h^2 + 1e-6) from kOutSwiglu records, built from the row h (in_x) lane
 //                          by lane (unit norm: a fixed operand exponent 2^14, |h r| <= 1)
 //   output side: kOutPlain
@@ -95,6 +97,7 @@ bool gemv_takes_raw(const GemvCall& c);
 //                           y = h = silu(g sg) (u su) [n] (kernels.cpp:225-234) and records of sum h^2
 enum { kInOp = 0, kInSlerp = 1, kInNorm = 2 };
 enum { kOutPlain = 0, kOutSlerp = 1, kOutSwiglu = 2 };
+enum { kPostNone = 0, kPostAddNorm = 1, kPostNorm = 2 };
 struct FusedGemv {
   GemvCall c;                        // weights, y, m = 1, k (kInOp: c.xop / c.xinv)
   int in = kInOp, out = kOutPlain;
@@ -105,6 +108,7 @@ struct FusedGemv {
   int in_groups = 0;                 // their number (fused_gemv_groups of that launch)
   float* in_xout = nullptr;          // kInSlerp: where x_new goes
   float in_ia = 1.f, in_ib = 1.f;    // kInSlerp: 2^-ea, 2^-eb
+  int in_post = 0;                   // kInSlerp: kPostNone, kPostAddNorm or kPostNorm
   const float* out_x = nullptr;      // kOutSlerp
   const float* out_lr = nullptr;
   const float* out_sg = nullptr;     // kOutSwiglu
