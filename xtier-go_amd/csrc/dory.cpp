@@ -331,7 +331,7 @@ void DorySession::sublayer_decode(Layer& L, int m, long long pos0, int inst, boo
   pending(b_.matmul_fused(&L.w.o, 1, o, nullptr, m, o_));
 }
 
-void DorySession::run_chunk(const float* x, int m, long long pos0) {
+void DorySession::run_chunk(const float* x, int m, long long pos0, bool keep_pending) {
   // packs/dory/dory.cpp:520-544 from the embedding rows; x's operand is in op_h_ on exit
   XTG_CHECK(m >= 1 && m <= kChunkRows, "dory: %d rows per chunk (1..%d)", m, kChunkRows);
   XTG_CHECK(pos0 >= 0 && pos0 + m <= c_.context, "context full: %lld + %d > %lld tokens", pos0, m,
@@ -381,7 +381,7 @@ void DorySession::run_chunk(const float* x, int m, long long pos0) {
     }
   }
   for (l = size_t(c_.n_in + c_.n_rec); l < layers_.size(); ++l) run(layers_[l], 0, true);
-  materialize(m);
+  if (!keep_pending) materialize(m);
 }
 
 void DorySession::head(int r0, int rows, float* logits) {
@@ -395,6 +395,26 @@ void DorySession::head(int r0, int rows, float* logits) {
     return;
   }
   XTG_CHECK(head_.codes, "dory: no LM head (pass an NVFP4 head to create or set a BF16 one)");
+  if (pend_) {   // one row whose last slerp is pending: it rides on the head's projection, which writes x too
+    XTG_CHECK(r0 == 0 && rows == 1, "dory: a pending slerp for head rows %d .. %d", r0, r0 + rows - 1);
+    FusedGemv f;
+    f.in = kInSlerp;
+    f.in_x = x_;
+    f.in_o = o_;
+    f.in_lr = pend_lr_;
+    f.in_part = part_s_;
+    f.in_groups = pend_groups_;
+    f.in_xout = x2_;
+    f.in_ia = 1.f / pend_a_;
+    f.in_ib = 1.f / pend_b_;
+    f.in_post = pend_post_;
+    f.c.col_scale[0] = logit_scale_;
+    b_.matmul_fused(&head_, 1, f, op_lin_, 1, logits);
+    std::swap(x_, x2_);
+    pend_ = false;
+    pend_post_ = kPostNone;
+    return;
+  }
   const void* op = op_h_;   // the chunk's operand when the rows are all of it, else the rows' own
   if (r0 != 0) {
     XTG_CHECK(rows == 1, "dory: head rows %d .. %d of a chunk", r0, r0 + rows - 1);
@@ -406,7 +426,7 @@ void DorySession::head(int r0, int rows, float* logits) {
 
 void DorySession::forward(const float* x, int m, long long pos0, float* logits) {
   // one chunk, then the head over all its rows (dory.cpp:566-576 with Logits::All)
-  run_chunk(x, m, pos0);
+  run_chunk(x, m, pos0, m == 1 && !head_bf16_.data && head_.codes);
   head(0, m, logits);
 }
 

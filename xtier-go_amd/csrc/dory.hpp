@@ -55,7 +55,8 @@ class DorySession {
   void sublayer_decode(Layer& L, int m, long long pos0, int inst, bool store);
   // the awaited slerp as a launch of its own: x_ and op_h_ hold the residual's rows afterwards
   void materialize(int m);
-  void run_chunk(const float* x, int m, long long pos0);
+  // keep_pending: a one-row chunk's last slerp is left for the head's projection (head() makes it)
+  void run_chunk(const float* x, int m, long long pos0, bool keep_pending = false);
   void head(int r0, int rows, float* logits);
   float* upload(const float* v, size_t n);
   void build(const xtg_dory_layer* layers, const float* logit_scale);

@@ -940,6 +940,11 @@ GemvShape fused_shape(const FusedGemv& f) {
   GemvShape sh = gemv_shape(f.c.w[0]->kt, nbs, f.c.nw, f.c.m, false);
   if (f.out == kOutSwiglu) sh.r = sh.r >= 4 ? 4 : 2;   // one or two pairs
   if (f.out == kOutSlerp || f.in == kInNorm) sh.r = std::min(sh.r, 2);
+  if (sh.t != 2 && sh.t != 4) {   // a k-split the fused kernels are not made for (a wide head's three k-tiles)
+    sh.t = f.c.w[0]->kt <= 32 ? 2 : 4;
+    sh.s = (f.c.w[0]->kt + sh.t - 1) / sh.t;
+    sh.r = std::min(sh.r, 4);
+  }
   return sh;
 }
 }  // namespace
