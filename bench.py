@@ -374,8 +374,10 @@ def prefill_gemm_bench(pkg, wl, hip, rows, reps):
     """The NVFP4 GEMM on a prefill chunk: one 4B-shaped layer's projections (q/k/v/g 10240x3072, fused gate/up
     2x8192x3072, o 3072x4096, down 3072x8192) at `rows` rows of FP32 activations, operand prepared once, each
     launch bracketed by events. Compute-bound: reported against the dense f16 matrix-core peak with the
-    algorithmic 2 m n k flops (the kernel issues twice that: each activation is a high and a low f16 part)."""
+    algorithmic 2 m n k flops (the default two-part operand issues twice that: each activation is a high and a low
+    f16 part; with XTG_GEMM_PARTS=1 in the environment, the single-part operand issues them once)."""
     rng = np.random.default_rng(41)
+    parts = 1 if os.environ.get("XTG_GEMM_PARTS") == "1" else 2   # matrix ops issued per useful one
     calls = [("qkvg10240", [(10240, 3072)]), ("gateup2x8192", [(8192, 3072), (8192, 3072)]),
              ("o3072x4096", [(3072, 4096)]), ("down3072x8192", [(3072, 8192)])]
     out = {"rows": rows, "per_call": {}}
@@ -408,7 +410,7 @@ def prefill_gemm_bench(pkg, wl, hip, rows, reps):
         tot_us += us
         log("prefill GEMM %s at %d rows: %s %.1f us, %.1f TFLOP/s (%.1f%% of the dense f16 peak; matrix-core "
             "issue %.1f%%)" % (name, rows, kname, us, flops / us / 1e6, flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS * 100,
-                               2 * flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS * 100))
+                               parts * flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS * 100))
         for a in (dx, dy, op):
             a.free()
         for w in ws:
@@ -416,7 +418,7 @@ def prefill_gemm_bench(pkg, wl, hip, rows, reps):
     achieved = tot_flops / tot_us / 1e6
     out["roofline"] = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                        "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                       "issue_frac": round(2 * achieved / MFMA_F16_PEAK_TFLOPS, 4)}
+                       "issue_frac": round(parts * achieved / MFMA_F16_PEAK_TFLOPS, 4), "operand_parts": parts}
     return out
 
 
@@ -881,6 +883,13 @@ def main():
         bf16_head = bf16_head_bench(pkg, wl, hip, 10)
         sampling = sampling_bench(pkg, hip, 20)
         prefill = prefill_gemm_bench(pkg, wl, hip, 512, 10)
+        # the single-part operand (XTG_GEMM_PARTS=1: f16 activations, half the matrix ops; not the default)
+        os.environ["XTG_GEMM_PARTS"] = "1"
+        try:
+            prefill["single_part"] = {str(r): prefill_gemm_bench(pkg, wl, hip, r, 10) for r in (512, 2048)}
+        finally:
+            del os.environ["XTG_GEMM_PARTS"]
+        prefill["rows2048"] = prefill_gemm_bench(pkg, wl, hip, 2048, 5)
         prefill["attention_ctx4096"] = prefill_attention_bench(pkg, wl, hip, 512, 4096, 10)
 
     decode = None

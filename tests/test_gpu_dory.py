@@ -474,12 +474,14 @@ def test_bf16_head_and_fp8_caches(hip, orc, wl):
     assert (got.argmax(1) == want.argmax(1)).all()
 
 
-@pytest.mark.parametrize("kv_dtype,sharp", [(0, False), (0, True), (1, False)])
-def test_tiny_prefill_chunks_then_steps(hip, pkg, orc, wl, kv_dtype, sharp):
+@pytest.mark.parametrize("kv_dtype,sharp,parts", [(0, False, "2"), (0, True, "2"), (1, False, "2"), (0, False, "1")])
+def test_tiny_prefill_chunks_then_steps(hip, pkg, orc, wl, monkeypatch, kv_dtype, sharp, parts):
     """The prefill path (chunks of more than 8 rows: GEMM projections, the many-row attention with its own-key
     tiles, the store after the scan) on the tiny model: prefill() over 700 rows in chunks of 512 + 188 with
     logits for every row, then four one-row steps, against the oracle's chunks of the same sizes. The 64-slot
-    rings take whole chunks (a ring keeps a chunk's last 64 rows)."""
+    rings take whole chunks (a ring keeps a chunk's last 64 rows). parts = 1: the GEMMs take the single-part
+    operand (XTG_GEMM_PARTS=1)."""
+    monkeypatch.setenv("XTG_GEMM_PARTS", parts)
     w = wl.DoryWeights(dict(wl.DORY_TINY, kv_dtype=kv_dtype), seed=31 + kv_dtype, context=800)
     if sharp:
         w = sharpened(w, seed=32)
@@ -509,8 +511,8 @@ def test_tiny_prefill_chunks_then_steps(hip, pkg, orc, wl, kv_dtype, sharp):
     got = np.concatenate(got)
     e = rel_l2(got, want)
     bar, decided = noise_bar(run_oracle, x, want) if sharp else (1e-3, np.ones(len(want), bool))
-    print("tiny prefill 512 + 188 rows then steps (KV dtype %d, sharp %s): logits rel-L2 %.2e (bar %.2e), %d of %d "
-          "rows decided" % (kv_dtype, sharp, e, bar, decided.sum(), len(decided)))
+    print("tiny prefill 512 + 188 rows then steps (KV dtype %d, sharp %s, %s parts): logits rel-L2 %.2e (bar %.2e), %d "
+          "of %d rows decided" % (kv_dtype, sharp, parts, e, bar, decided.sum(), len(decided)))
     assert e <= bar
     assert (got.argmax(1) == want.argmax(1))[decided].all()
 

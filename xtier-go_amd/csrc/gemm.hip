@@ -7,7 +7,10 @@
 // Design (MI355X; compute-bound once a chunk has tens of rows):
 //  - Operands as in the GEMV: weights in the prepared 16 x 128 tiles, dequantised exactly to f16 in registers;
 //    activations in 8-row groups of the GEMV's operand (each row as f16 high and low parts, columns 2 r and
-//    2 r + 1), so v_mfma_f32_16x16x32_f16 keeps ~22 bits of every activation and accumulates in FP32.
+//    2 r + 1), so v_mfma_f32_16x16x32_f16 keeps ~22 bits of every activation and accumulates in FP32. With
+//    XTG_GEMM_PARTS=1 (or GemvCall::parts = 1) a pair of groups feeds one matrix op with the 16 rows' high parts
+//    only: half the matrix ops and operand bytes per output, f16 activations (rel-L2 ~2e-4 against FP32, the
+//    precision class of the reference's FP16 GPU prefill GEMM); the default keeps both parts.
 //  - A work-group of 4 waves owns 4 RB row-blocks (64 RB output rows) and GB activation groups (8 GB rows).
 //    Each k-tile (128 inputs) the work-group stages the groups' operand tile (4 KiB each) in LDS, double-buffered,
 //    in lane order (contiguous 16-byte writes and reads); each wave dequantises its RB weight tiles once and runs
@@ -71,6 +74,20 @@ __device__ inline XTile<GB> load_x(const char* op, size_t stride, int groups, in
   return r;
 }
 
+// The same for the single-part operand of group pairs p0 .. p0 + GP - 1 (16 rows each): lane L = (kgrp, row) of
+// wave w fetches the high part of row (L & 15) of the pair, chunk L >> 4 of step w, from its 8-row group, and stores
+// it at lane slot L. The low parts are never read.
+template <int GP>
+__device__ inline XTile<GP> load_x1(const char* op, size_t stride, int groups, int p0, int kt, int wave, int lane) {
+  XTile<GP> r;
+  const int row = lane & 15;
+  const size_t at = (size_t(kt) * 4 + size_t(wave)) * 64 + size_t(8 * (row & 7) + (lane >> 4));
+#pragma unroll
+  for (int i = 0; i < GP; ++i)
+    r.v[i] = reinterpret_cast<const uint4*>(op + size_t(min(2 * (p0 + i) + (row >> 3), groups - 1)) * stride)[at];
+  return r;
+}
+
 // Row-blocks rb0 .. rb0 + RB - 1 of k-tile kt (a row-block past the last reloads the last one).
 template <int RB>
 __device__ inline WTile<RB> load_w(const uint8_t* tiles, int nb, int kt_count, int rb0, int kt, int lane) {
@@ -84,9 +101,12 @@ __device__ inline WTile<RB> load_w(const uint8_t* tiles, int nb, int kt_count, i
   return w;
 }
 
-// RB row-blocks per wave, GB activation groups per work-group tile, OCC work-groups per CU the registers are
-// budgeted for (one: up to 512 VGPRs and AGPRs per lane)
-template <int RB, int GB, int OCC>
+// RB row-blocks per wave, GB operand blocks per work-group tile, OCC work-groups per CU the registers are
+// budgeted for (one: up to 512 VGPRs and AGPRs per lane). PARTS = 2: a block is an 8-row group's high and low f16
+// parts (~22 bits of each activation); PARTS = 1: a block is a pair of groups, 16 rows of their high parts only
+// (11 bits: the f16 precision of the reference's GPU prefill GEMM, engine/src/opencl.cpp:232-269), half the matrix
+// ops and operand bytes per row.
+template <int RB, int GB, int OCC, int PARTS>
 __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmArgs a) {
   constexpr int kTileGroups = GB;
   __shared__ uint4 xs[2][kTileGroups][4][64];   // [buffer][group][step][lane], 8 GB KiB
@@ -103,7 +123,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
   const int lt = t - (wi ? a.tile_end[wi - 1] : 0);
   const int ntile = lt / a.mtiles, mtile = lt % a.mtiles;
   const int rb0 = ntile * (kGemmWaves * RB) + wave * RB;
-  const int g0 = mtile * kTileGroups;
+  const int g0 = mtile * kTileGroups;   // PARTS = 1: the first pair
   const int nb = a.nb[wi], KT = a.kt;
   const uint8_t* __restrict__ tiles = a.tiles[wi];
 
@@ -113,9 +133,15 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
 #pragma unroll
     for (int g = 0; g < kTileGroups; ++g) acc[r][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  auto xload = [&](int kt) {
+    if constexpr (PARTS == 1)
+      return load_x1<GB>(a.op, a.op_stride, a.groups, g0, kt, wave, lane);
+    else
+      return load_x<GB>(a.op, a.op_stride, a.groups, g0, kt, wave, lane);
+  };
   WTile<RB> w = load_w<RB>(tiles, nb, KT, rb0, 0, lane);
   {
-    const XTile<GB> x0 = load_x<GB>(a.op, a.op_stride, a.groups, g0, 0, wave, lane);
+    const XTile<GB> x0 = xload(0);
 #pragma unroll
     for (int i = 0; i < GB; ++i) xs[0][i][wave][lane] = x0.v[i];
   }
@@ -124,7 +150,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
     const int cur = kt & 1;
     const int nxt = min(kt + 1, KT - 1);   // the last k-tile reloads itself: no branch around the loads
     // the next k-tile's loads, in flight during this one's math
-    const XTile<GB> xn = load_x<GB>(a.op, a.op_stride, a.groups, g0, nxt, wave, lane);
+    const XTile<GB> xn = xload(nxt);
     const WTile<RB> wn = load_w<RB>(tiles, nb, KT, rb0, nxt, lane);
     __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the math (the scheduler would sink them to their use)
     // step s + 1's operand fragments are read from LDS while step s's matrix ops run (read just before their
@@ -156,11 +182,34 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
     w = wn;
   }
 
-  // lane (grp, col) holds rows 4 grp .. 4 grp + 3 of its row-block for operand column col; columns 2 j and
-  // 2 j + 1 (neighbour lanes) are row j's high and low parts
+  // lane (grp, col) holds rows 4 grp .. 4 grp + 3 of its row-block for operand column col; PARTS = 2: columns 2 j
+  // and 2 j + 1 (neighbour lanes) are row j's high and low parts; PARTS = 1: column col is row col of the pair
   const int n = a.n[wi];
   const float glob = a.global[wi];
   const float* cs = a.col_scale[wi];
+  if constexpr (PARTS == 1) {
+#pragma unroll
+    for (int g = 0; g < kTileGroups; ++g) {
+      const int gi = 2 * (g0 + g) + (col >> 3);
+      const int mrow = gi * kMaxRows + (col & 7);
+      const bool row_ok = gi < a.groups && mrow < a.m;
+      const float xinv =
+          row_ok ? reinterpret_cast<const float*>(a.op + size_t(gi) * a.op_stride + a.xop_bytes)[col & 7] : 0.f;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const f32x4 v = acc[r][g];
+        if (row_ok && rb0 + r < nb) {
+          const int n0 = (rb0 + r) * kTileRows + 4 * grp;
+          float* yp = a.y + a.y_off[wi] + (long long)mrow * n;
+          const float f = glob * xinv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n0 + e < n) yp[n0 + e] = cs ? (v[e] * f) * cs[n0 + e] : v[e] * f;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < kTileGroups; ++g) {
     const int gi = g0 + g;
@@ -186,23 +235,29 @@ __global__ void __launch_bounds__(kGemmWaves * 64, OCC) gemm_kernel(const GemmAr
 }
 
 using GemmFn = void (*)(const GemmArgs);
-static GemmFn gemm_fn(int rb, int gb) {
-#define XTG_GEMM(R, G, O) \
-  if (rb == R && gb == G) return gemm_kernel<R, G, O>;
-  XTG_GEMM(4, 4, 2) XTG_GEMM(2, 4, 2) XTG_GEMM(1, 4, 2)
+static GemmFn gemm_fn(int rb, int gb, int parts) {
+#define XTG_GEMM(R, G, O, P) \
+  if (rb == R && gb == G && parts == P) return gemm_kernel<R, G, O, P>;
+  XTG_GEMM(4, 4, 2, 2) XTG_GEMM(2, 4, 2, 2) XTG_GEMM(1, 4, 2, 2)
+  XTG_GEMM(4, 4, 2, 1) XTG_GEMM(2, 4, 2, 1) XTG_GEMM(1, 4, 2, 1) XTG_GEMM(4, 2, 2, 1) XTG_GEMM(2, 2, 2, 1)
+  XTG_GEMM(1, 2, 2, 1)
 #undef XTG_GEMM
   return nullptr;
 }
 
-static std::string run_gemm(const GemvCall& c, int rb, int gb, hipStream_t stream);
+static std::string run_gemm(const GemvCall& c, int rb, int gb, int parts, hipStream_t stream);
 
 std::string launch_gemm(const GemvCall& c, hipStream_t stream) {
   XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemm: %d weights (1..4)", c.nw);
   XTG_CHECK(c.m >= 1, "gemm: %d rows", c.m);
+  int parts = c.parts;
+  if (const char* env = std::getenv("XTG_GEMM_PARTS")) parts = std::atoi(env);
+  XTG_CHECK(parts == 1 || parts == 2, "gemm: %d operand parts (1 or 2)", parts);
   const int groups = (c.m + kMaxRows - 1) / kMaxRows;
+  const int blocks = parts == 1 ? (groups + 1) / 2 : groups;   // operand blocks: groups, or pairs of them
   // launch shape (XTG_GEMM_SHAPE=RB,GB fixes it, for experiments)
   auto tiles_for = [&](int r, int g) {
-    const int mt = (groups + g - 1) / g;
+    const int mt = (blocks + g - 1) / g;
     long t = 0;
     for (int i = 0; i < c.nw; ++i) t += long((c.w[i]->nb + kGemmWaves * r - 1) / (kGemmWaves * r)) * mt;
     return t;
@@ -211,20 +266,29 @@ std::string launch_gemm(const GemvCall& c, hipStream_t stream) {
   // row-blocks per wave (34 % of the dense f16 peak on gate/up at 512 rows), four only with thousands of tiles
   // (2048-row chunks of the wide projections), one with fewer than 512 tiles of two (the 3072-wide o and down
   // projections at 512 rows: 45 and 79 us against 46 and 83 us with two)
-  const int gb = 4;
-  const int rb = tiles_for(4, 4) >= 2048 ? 4 : tiles_for(2, 4) >= 512 ? 2 : 1;
+  int gb = 4;
+  int rb = tiles_for(4, 4) >= 2048 ? 4 : tiles_for(2, 4) >= 512 ? 2 : 1;
+  // single part (blocks of 16 rows), measured likewise (512 / 2048 rows): four row-blocks and four pairs on the
+  // wide projections at 2048 rows and gate/up at 512 (198 / 319 / 76 us), four and two on o and down at 2048
+  // (85 / 152 us), two and two below that (q/k/v/g 62 us, o 35 us, down 61 us at 512 rows); eight pairs were 2-4x
+  // slower at every size
+  if (parts == 1) {
+    gb = tiles_for(4, 4) >= 512 ? 4 : 2;
+    rb = gb == 4 || tiles_for(4, 2) >= 768 ? 4 : 2;
+  }
   if (const char* env = std::getenv("XTG_GEMM_SHAPE")) {
     int r = 0, g = 0;
-    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && gemm_fn(r, g) != nullptr)
-      return run_gemm(c, r, g, stream);
+    if (std::sscanf(env, "%d,%d", &r, &g) == 2 && gemm_fn(r, g, parts) != nullptr)
+      return run_gemm(c, r, g, parts, stream);
   }
-  return run_gemm(c, rb, gb, stream);
+  return run_gemm(c, rb, gb, parts, stream);
 }
 
-static std::string run_gemm(const GemvCall& c, int rb, int gb, hipStream_t stream) {
+static std::string run_gemm(const GemvCall& c, int rb, int gb, int parts, hipStream_t stream) {
   const int kt = c.w[0]->kt;
   const int groups = (c.m + kMaxRows - 1) / kMaxRows;
-  const int mtiles = (groups + gb - 1) / gb;
+  const int blocks = parts == 1 ? (groups + 1) / 2 : groups;
+  const int mtiles = (blocks + gb - 1) / gb;
   GemmArgs a{};
   int end = 0;
   for (int i = 0; i < c.nw; ++i) {
@@ -249,11 +313,11 @@ static std::string run_gemm(const GemvCall& c, int rb, int gb, hipStream_t strea
   a.xop_bytes = xop_bytes(c.w[0]->k);
   a.y = c.y;
   const dim3 grid{unsigned(end)}, block{unsigned(kGemmWaves * 64)};
-  const GemmFn fn = gemm_fn(rb, gb);
-  XTG_CHECK(fn != nullptr, "gemm: no kernel for RB=%d GB=%d", rb, gb);
+  const GemmFn fn = gemm_fn(rb, gb, parts);
+  XTG_CHECK(fn != nullptr, "gemm: no kernel for RB=%d GB=%d, %d parts", rb, gb, parts);
   hipLaunchKernelGGL(fn, grid, block, 0, stream, a);
   HIP_CHECK(hipGetLastError());
-  return strf("gemm_kernel<%d, %d>", rb, gb);
+  return parts == 1 ? strf("gemm_kernel<%d, %d, f16>", rb, gb) : strf("gemm_kernel<%d, %d>", rb, gb);
 }
 
 }  // namespace xtg::hip

@@ -59,6 +59,7 @@ struct GemvCall {
   const void* x = nullptr;   // raw rows [m][k] (x_dtype) in place of a prepared operand: the GEMV builds its own
   int x_dtype = 0;
   int k = 0;
+  int parts = 2;   // the GEMM's activation parts (prefill chunks): 2, high and low f16; 1, the high part alone
 };
 // The launch shape: R row-blocks and T k-tiles per wave, S waves per work-group along k.
 struct GemvShape {
