@@ -89,7 +89,9 @@ int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* 
  * projections of the device input x ([m][k], FP32 or BF16 per x_dtype) into consecutive [m][n_out_i] blocks of
  * the device output y starting at y_offset floats. Queued; 1 <= m <= 4096 (1-8 rows: the GEMV, which reads the rows
  * as they are; more: the GEMM on a prepared operand), n_w <= 4 per call (the fused q/k/v/g and gate/up of the Dory
- * sublayers). x must be 16-byte aligned. */
+ * sublayers). x must be 16-byte aligned. The GEMM keeps ~22 bits of each activation (two f16 parts); with
+ * XTG_GEMM_PARTS=1 in the environment (read at each call) it takes one f16 part, about 1.4-1.6x faster at ~2e-4
+ * relative error, the precision class of the reference's FP16 GPU prefill GEMM (opencl.cpp:232-269). */
 int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
                              size_t y_offset, char* err, int err_len);
 
