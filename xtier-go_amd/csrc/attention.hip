@@ -1512,15 +1512,16 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
     p.tile_lo = int(lo / kTile);
     p.tiles = hi > lo ? int((hi + kTile - 1) / kTile - lo / kTile) : 0;
   }
-  // about 128 work-groups over the KV heads and row blocks, at least two tiles per wave on a cache by position
+  // about 192 work-groups over the KV heads and row blocks, at least two tiles per wave on a cache by position
   // and one on a ring, at most one split per tile. Measured on the 4B-shaped decode step: every split adds a
-  // partial record that the gate kernel merges, and at 8K and 32K contexts 128 work-groups (16 splits on the
-  // global layers) beat 256 by 1.2-2.4 % (96: equal at 8K, 1.6 % slower at 32K; 64 and 512 slower still); one
-  // tile per wave on the 1088-slot rings (9 splits instead of 5) takes 1-1.3 % off the 8-row step, while on the
-  // global layers it doubles the partials at 4K and costs 2 %.
+  // partial record that the gate merges; with the gate's merge in one round of loads, 192 work-groups (24 splits on
+  // the global layers) take 1.6 % off the one-token step at 32K and 0.7 % at 8K against 128 (the 8-row step: 0.6 %
+  // faster at 32K, 0.4 % slower at 8K), 256 and 384 are slower; one tile per wave on the 1088-slot rings (9 splits
+  // instead of 5) takes 1-1.3 % off the 8-row step, while on the global layers it doubles the partials at 4K and
+  // costs 2 %.
   // (XTG_ATTN_SPLITS=n fixes the count, for experiments)
   if (p.tiles > 0) {
-    const int want = std::max(1, 128 / (c.kv_heads * p.blocks));   // about 128 work-groups over all blocks
+    const int want = std::max(1, 192 / (c.kv_heads * p.blocks));   // about 192 work-groups over all blocks
     const int mt = c.ring ? 1 : 2;
     p.splits = std::max(1, std::min(want, (p.tiles + mt * kWaves - 1) / (mt * kWaves)));
     if (const char* env = std::getenv("XTG_ATTN_SPLITS")) p.splits = std::max(1, std::atoi(env));
