@@ -1563,6 +1563,21 @@ void* attn_scratch_ptr(int device) {
 
 // ------------------------------------------------------------------------------------------------- launchers
 
+// The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks, as does a
+// wide GEMV on raw rows: raise the kernel's limit once.
+void allow_lds(const void* fn, size_t lds) {
+  if (lds <= 65536) return;
+  static thread_local const void* raised[128] = {};
+  for (const void* f : raised)
+    if (f == fn) return;
+  HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  for (const void*& f : raised)
+    if (!f) {
+      f = fn;
+      return;
+    }
+}
+
 namespace {
 
 using ScanFn = void (*)(const ScanArgs);
@@ -1586,20 +1601,6 @@ size_t scan_lds_bytes(int d, int qb, bool rawq) {
   fail("attention: no scan for head_dim %d and %d column blocks", d, qb);
 }
 
-// The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks (gfx950
-// has 160 KiB per CU): raise the kernel's limit once.
-void allow_lds(const void* fn, size_t lds) {
-  if (lds <= 65536) return;
-  static thread_local const void* raised[32] = {};
-  for (const void* f : raised)
-    if (f == fn) return;
-  HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-  for (const void*& f : raised)
-    if (!f) {
-      f = fn;
-      return;
-    }
-}
 
 size_t blk_records(const AttnPlan& p) { return size_t(p.kv_heads) * size_t(p.splits + 1) * size_t(p.qpad); }
 

@@ -43,6 +43,12 @@ inline std::string strf(const char* fmt, ...) {
     if (!(cond)) ::xtg::hip::fail(__VA_ARGS__); \
   } while (0)
 
+namespace xtg::hip {
+// A kernel that needs more than the default 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU): raise its limit
+// once (defined in attention.hip).
+void allow_lds(const void* fn, size_t lds);
+}  // namespace xtg::hip
+
 #define HIP_CHECK(expr)                                                                        \
   do {                                                                                         \
     hipError_t e_ = (expr);                                                                    \

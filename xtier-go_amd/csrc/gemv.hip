@@ -223,47 +223,82 @@ __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int 
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// The operand's entries of one k-tile built in the lane that consumes them, from raw BF16 rows: lane (c, g) holds
-// row c / 2's inputs 32 g .. 32 g + 31 of the tile (w4: 16 BF16 pairs), scaled by the power of two 2^e that brings
-// the tile's largest magnitude in that row to [2^14, 2^15) (prep_x_kernel's rule, per 128 inputs instead of per
-// row; the four lane groups holding the row's tile agree on it through two xor shuffles). Returns 2^-e, the factor
-// the tile's products take. Built in 16-bit integer steps on the bit pairs (2.5 VALU operations per input).
-// BF16 carries 8 significant bits, so f16(x * 2^e) is exact wherever it is a normal f16 and the low part is zero:
-// the odd (low-part) columns get +-0. An input whose scaled value falls below f16's normal range (at
-// least 2^28 times smaller than the tile's largest) is flushed, an error below 2^-28 of that largest magnitude;
-// e is capped at 112 so the exponent shift stays a subtraction (tiles whose largest magnitude is under 2^-98 keep
-// at least 6 of f16's 11 bits above their largest value, still more than BF16's 8). With the abs bits
-// a = [E:8][M:7], the f16 of x * 2^e is [E - 112 + e : 5][M : 7][000]: a saturating subtraction of (112 - e) << 7
-// (0 when the result would be below the normal range), a shift by 3 and the sign put back. A row whose tile holds
-// an infinity or NaN gets NaN operands (NaN outputs, as the prepared operand gives).
-__device__ inline float bf16_operand(const uint4 (&w4)[4], bool hi, uint4 (&xb)[4]) {
-  uint32_t w[16];
-  u16x2 m2 = {0, 0};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[4 * i] = w4[i].x, w[4 * i + 1] = w4[i].y, w[4 * i + 2] = w4[i].z, w[4 * i + 3] = w4[i].w;
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
-  uint32_t mx = m2.x > m2.y ? m2.x : m2.y;
-  mx = max(mx, uint32_t(__shfl_xor(int(mx), 16)));
-  mx = max(mx, uint32_t(__shfl_xor(int(mx), 32)));
+// Lanes of one wave passing values through LDS: a wave's LDS operations execute in issue order, so keeping the
+// compiler's order is enough.
+__device__ inline void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The operand of one k-tile from raw BF16 rows, converted by all 64 lanes and staged through LDS. Lane (j, i) =
+// (lane / 16, lane % 16) holds inputs 8 i .. 8 i + 7 of row j's k-tile in w[0] and of row j + 4's in w[1] (zeros
+// for rows past m). Each row's inputs are scaled by the power of two 2^e that brings the tile's largest magnitude in
+// that row to [2^14, 2^15) (prep_x_kernel's rule, per 128 inputs instead of per row; the row's 16 lanes agree on it
+// through DPP within their row of lanes). BF16 carries 8 significant bits, so f16(x * 2^e) is exact wherever it is
+// a normal f16 and the low part is zero (the odd operand columns read zeros). An input whose scaled value falls
+// below f16's normal range (at least 2^28 times smaller than the tile's largest) is flushed, an error below 2^-28 of
+// that largest magnitude; e is capped at 112 so the exponent shift stays a subtraction (tiles whose largest
+// magnitude is under 2^-98 keep at least 6 of f16's 11 bits above their largest value, still more than BF16's 8).
+// With the abs bits a = [E:8][M:7], the f16 of x * 2^e is [E - 112 + e : 5][M : 7][000]: a saturating subtraction
+// of (112 - e) << 7 (0 when the result would be below the normal range), a shift by 3 and the sign put back. A row
+// whose tile holds an infinity or NaN gets NaN operands (NaN outputs, as the prepared operand gives). The staged
+// tile [8 rows][16][8 f16] and the rows' factors 2^-e then go to the lanes that consume them: lane (c, g) of the
+// matrix op's operand takes row c / 2's inputs 32 g .. 32 g + 31 (four steps of 8) for even c < 2 m, zeros else.
+constexpr int kStageVecs = 8 * 16 + 2;   // one wave's staging, in 16-byte units: the rows' tiles, then 8 factors
+
+__device__ inline uint32_t row16_max(uint32_t v) {
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppXor1, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppXor2, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppHalfMirror, 0xF, 0xF, false)));
+  return max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppMirror, 0xF, 0xF, false)));
+}
+
+// 8 BF16 inputs of one row (a lane's share) to their f16 at the row's 2^e; returns e
+__device__ inline int bf16_to_f16_row(uint4& w4) {
+  uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+  u16x2 m2 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu),
+                                       __builtin_bit_cast(u16x2, w[1] & 0x7fff7fffu));
+  m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[2] & 0x7fff7fffu),
+                                                               __builtin_bit_cast(u16x2, w[3] & 0x7fff7fffu)));
+  const uint32_t mx = row16_max(m2.x > m2.y ? uint32_t(m2.x) : uint32_t(m2.y));
   const int e = mx == 0 || mx >= 0x7f80u ? 0 : min(141 - int(mx >> 7), 112);
-  const unsigned short c = hi ? (unsigned short)((112 - e) << 7) : (unsigned short)0x7f80u;   // low columns: all 0
+  const unsigned short c = (unsigned short)((112 - e) << 7);
   const u16x2 c2 = {c, c};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu), c2);
     const u16x2 f = d << (unsigned short)3;
-    w[i] = (w[i] & 0x80008000u) | __builtin_bit_cast(uint32_t, f);
+    w[i] = mx >= 0x7f80u ? 0x7e007e00u : (w[i] & 0x80008000u) | __builtin_bit_cast(uint32_t, f);
   }
-  if (__any(mx >= 0x7f80u)) {   // an infinity or NaN in a lane's tile: that row's products become NaN
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = mx >= 0x7f80u ? 0x7e007e00u : w[i];
+  w4 = make_uint4(w[0], w[1], w[2], w[3]);
+  return e;
+}
+
+// the k-tile's operand columns of lane (col, grp) and their factor 2^-e, from the rows in w (lane layout above);
+// stage: this wave's kStageVecs, free on entry and again on return
+__device__ inline float bf16_operand(uint4 (&w)[2], int m, int lane, uint4* stage, uint4 (&xb)[4]) {
+  const int j = lane >> 4, i = lane & 15, col = lane & 15, grp = lane >> 4;
+  float* fac = reinterpret_cast<float*>(stage + 128);
+  const int e0 = bf16_to_f16_row(w[0]);
+  stage[j * 16 + i] = w[0];
+  if (i == 0) fac[j] = ldexpf(1.f, -e0);
+  if (m > 4) {   // uniform: the second half of the rows
+    const int e1 = bf16_to_f16_row(w[1]);
+    stage[(j + 4) * 16 + i] = w[1];
+    if (i == 0) fac[j + 4] = ldexpf(1.f, -e1);
   }
+  wave_lds_order();
+  const int r = col >> 1;
+  const bool live = (col & 1) == 0 && r < m;
+  const int rc = live ? r : 0;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) xb[t] = make_uint4(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3]);
-  return ldexpf(1.f, -e);
+  for (int t = 0; t < 4; ++t) {
+    const uint4 v = stage[rc * 16 + 4 * grp + t];
+    xb[t] = live ? v : make_uint4(0, 0, 0, 0);
+  }
+  const float xs = fac[rc];
+  wave_lds_order();   // read before the next k-tile's staging
+  return live ? xs : 1.f;
 }
 
 // XR: false = a prepared operand (xop / xinv); true = raw BF16 rows (the kernel builds the operand per k-tile in
@@ -288,25 +323,25 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   uint4 xb[T][4];
   uint4 cw[T][R];
   uint32_t sw[T][R];
-  // raw rows: the lane's 32 inputs of each k-tile (8 BF16 per load; k is a multiple of 16, so a load is wholly
-  // inside the row or wholly past its end)
-  uint4 xr[XR ? T : 1][4];
+  // raw rows: lane (j, i) = (lane / 16, lane % 16) loads inputs 8 i .. 8 i + 7 of each k-tile of rows j and j + 4
+  // (8 BF16 per load; k is a multiple of 16, so a load is wholly inside the row or wholly past its end)
+  uint4 xr[XR ? T : 1][2];
   if constexpr (XR) {
     // the raw rows first, so they are turned into the operand while the weights are in flight; buffer loads
     // return zeros past the rows (absent rows, k-tiles past k), so no load sits behind a branch
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(a.x), (short)0, a.m * a.k * 2, 0x00020000);
-    const uint32_t xrow = uint32_t(col >> 1) * uint32_t(a.k) * 2u;
+    const int j = lane >> 4, i = lane & 15;
 #pragma unroll
     for (int u = 0; u < T; ++u) {
       const int kt = kt0 + u;
-      const int k0 = kt * kTileK + 32 * grp;
+      const int ki = kt * kTileK + 8 * i;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ki = k0 + i * 8;
-        const bool in = kt < KT && live_col && ki < a.k;
-        const uint32_t off = in ? xrow + uint32_t(ki) * 2u : 0x80000000u;
-        xr[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, int(off), 0, 0));
+      for (int h = 0; h < 2; ++h) {
+        const int row = j + 4 * h;
+        const bool in = kt < KT && row < a.m && ki < a.k;
+        const uint32_t off = in ? (uint32_t(row) * uint32_t(a.k) + uint32_t(ki)) * 2u : 0x80000000u;
+        xr[u][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, int(off), 0, 0));
       }
     }
   }
@@ -347,10 +382,12 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   }
   float xs[T];   // raw rows: each k-tile's factor 2^-e for the lane's column
   if constexpr (XR) __builtin_amdgcn_sched_barrier(0);   // every load issued before the conversion waits on x
+  // raw rows: this wave's staging area, after the cross-wave sums' region
+  uint4* stage = reinterpret_cast<uint4*>(red) + (S > 1 ? S * R * kMaxRows * 4 : 0) + wave * kStageVecs;
 #pragma unroll
   for (int u = 0; u < T; ++u) {
     xs[u] = 1.f;
-    if constexpr (XR) xs[u] = bf16_operand(xr[u], (col & 1) == 0, xb[u]);
+    if constexpr (XR) xs[u] = bf16_operand(xr[u], a.m, lane, stage, xb[u]);
   }
   f32x4 acc[R];
 #pragma unroll
@@ -415,9 +452,9 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
 namespace {
 using GemvFn = void (*)(const GemvArgs);
 
-// Raw BF16 rows hold 32 inputs (16 VGPRs) per k-tile until the tile's operand is built. Kernels that would exceed
-// a 1024-thread group's 128 VGPRs (spill) or take more than 4 k-tiles per wave are not made: those calls take the
-// prepared operand.
+// Raw BF16 rows hold 16 inputs (8 VGPRs) per lane and k-tile until the tile's operand is built. Kernels that would
+// exceed a 1024-thread group's 128 VGPRs or take more than 4 k-tiles per wave are not made (those calls take the
+// prepared operand), nor two row-blocks of four k-tiles in 1024-thread groups (measured slower than one).
 template <int R, int T>
 GemvFn pick_fn(int threads, bool xr) {
   if (xr) {
@@ -458,9 +495,9 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw) {
     }
   }
   if (raw) {
-    // raw BF16 rows (measured the same way): each wave converts its k-tiles of x once for all its row-blocks, so
-    // more row-blocks per wave pay: four with many row-blocks, two with few, and four k-tiles per wave only where
-    // K needs them (16 waves at most per work-group)
+    // raw BF16 rows (measured the same way, rotated cold weights, launch-shape sweeps over the decode projections
+    // at M = 1, 2, 4, 8): four row-blocks per wave with many row-blocks, two with few, and four k-tiles per wave
+    // (with one row-block) only where K needs them (16 waves at most per work-group)
     int nb = 0;
     for (int i = 0; i < nw; ++i) nb += nbs[i];
     const int r = nb >= 512 ? 4 : 2, t = (kt + 1) / 2 <= 16 ? 2 : 4;
@@ -538,7 +575,9 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   const int threads = sh.s * 64;
   GemvFn fn = gemv_fn(sh.r, sh.t, threads, xr);
   XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d%s", sh.r, sh.t, xr ? " on raw rows" : "");
-  const size_t lds = sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * kMaxRows * 4 * sizeof(f32x4) : 0;
+  const size_t lds = (sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * kMaxRows * 4 * sizeof(f32x4) : 0) +
+                     (xr ? size_t(sh.s) * kStageVecs * sizeof(uint4) : 0);
+  allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, threads <= 512 ? 512 : 1024)
@@ -594,13 +633,6 @@ __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// Lanes of one wave passing values through LDS: a wave's LDS operations execute in issue order, so keeping the
-// compiler's order is enough.
-__device__ inline void wave_lds_order() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
 }
 
 // The row values one lane reads for the kInNorm operand of a k-tile: inputs l and l + 64 of the tile; indices
@@ -1023,20 +1055,7 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   FusedFn fn = fused_fn(sh.r, sh.t, threads, f.in, f.out);
   XTG_CHECK(fn != nullptr, "fused gemv: no kernel for R=%d T=%d (in %d, out %d)", sh.r, sh.t, f.in, f.out);
   const size_t lds = size_t(FusedLds(sh.s, sh.r, f.in).total) * sizeof(float);
-  if (lds > 65536) {
-    static thread_local const void* raised[64] = {};
-    bool done = false;
-    for (const void* p : raised) done = done || p == reinterpret_cast<const void*>(fn);
-    if (!done) {
-      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    int(lds)));
-      for (const void*& p : raised)
-        if (!p) {
-          p = reinterpret_cast<const void*>(fn);
-          break;
-        }
-    }
-  }
+  allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   static const char* kIn[] = {"op", "slerp", "norm"};
