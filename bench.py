@@ -918,8 +918,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "NVFP4 skinny GEMM over one 4B-shaped layer's projections: QKV N=5120 K=3072, fused gate/up "
-                        "2x8192 K=3072, down N=3072 K=8192, each at M=1 and M=8 (6 calls per step, one GEMV launch each that builds its operand from the rows; "
-                        "BF16 unit-row activations, FP32 out); weights rotated over %d copies (%.2f GiB) so each "
+                        "2x8192 K=3072, down N=3072 K=8192, each at M=1 and M=8 (6 calls per step, one GEMV launch "
+                        "each that builds its operand from the rows; BF16 unit-row activations, FP32 out); weights "
+                        "rotated over %d copies (%.2f GiB) so each "
                         "call reads HBM; steps replayed from HIP graphs" % (copies, copies * set_bytes / 2 ** 30),
             "step_bytes": step_bytes,
             "gemv_gbs_by_rows": by_m,
