@@ -236,7 +236,7 @@ struct ScanArgs {
   int tile_lo, tiles;      // the key tiles to scan: tile_lo .. tile_lo + tiles - 1
   int pos0;                // positions are below 2^31 (the slot-position array is int32)
   float scale2;            // scale * log2(e)
-  const float* inv_freq;   // raw q rows only (the decode step's fused launch): the RoPE table [d / 2]
+  const float2* rope;      // raw q rows only (the decode step's fused launch): the RoPE rows [pos][d / 2]
   const float* qscale;     //   and the per-dim q scale [heads * d] (NULL: none)
 };
 
@@ -615,7 +615,7 @@ constexpr int scan_merge_floats() {
 template <int D>
 constexpr int sq_stride() { return D + 4; }
 template <int D, int QB, bool RAWQ>
-constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * sq_stride<D>() + 2 * kProdRows * (D / 2) : 0; }
+constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * sq_stride<D>() : 0; }
 template <int D, int QB>
 constexpr int scan_sq_offset() { return q_in_lds<D>() ? scan_qop_floats<D, QB>() : scan_merge_floats<D, QB>(); }
 template <int D, int QB, bool RAWQ>
@@ -626,10 +626,9 @@ constexpr int scan_lds_floats() {
 
 // One scan work-group (KV head, split) of a row block. RAWQ: q arrives as the projection wrote it, and the work-group
 // applies the producer's RoPE, justnorm and qscale itself (packs/dory/dory.cpp:482-490) before the scale, once per
-// q-col: the rows' angles FP32(pos) * inv_freq[i] go into a cosine / sine table in LDS (at most kProdRows rows, one
-// entry per thread); then 16 / QB threads per q-col take d / 2 * QB / 16 consecutive RoPE pairs (i, i + d/2) each,
-// rotate them, add their squares over those lanes, scale, and leave the processed q-col in LDS, from which every
-// lane takes its operand dims.
+// q-col: 16 / QB threads per q-col take d / 2 * QB / 16 consecutive RoPE pairs (i, i + d/2) each with their
+// angles' cosines and sines from the position's row of the RoPE table, rotate them, add their squares over those
+// lanes, scale, and leave the processed q-col in LDS, from which every lane takes its operand dims.
 template <int D, int QB, bool F8, bool RAWQ>
 __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   constexpr int NC = D / 32, ND = D / 16;
@@ -705,23 +704,22 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     constexpr int HALF = D / 2;
     constexpr int TPV = 16 / QB;          // threads per q-col
     constexpr int PP = HALF / TPV;        // RoPE pairs per thread
-    constexpr int kAngles = (kProdRows * HALF + kWaves * 64 - 1) / (kWaves * 64);
     static_assert(PP % 2 == 0 && TPV * QB * 16 == kWaves * 64, "q-col split");
     constexpr int SQS = sq_stride<D>();
     float* sq = lds + scan_sq_offset<D, QB>();   // processed q-cols [QB * 16][SQS]
-    float* scos = sq + QB * 16 * SQS;
-    float* ssin = scos + kProdRows * HALF;
-    const int nrows = min(a.rpb, a.n_q - row0);
     const int v = int(threadIdx.x) / TPV, p0 = (int(threadIdx.x) % TPV) * PP;
     const bool vlive = v < qcols;
     const int vrow = vlive ? v / a.group : 0;
     const int vh = kvh * a.group + (vlive ? v % a.group : 0);
-    // every load first: the table's frequencies, the q-col's pairs and their scales
-    float fr[kAngles];
-#pragma unroll
-    for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[(int(threadIdx.x) + u * kWaves * 64) % HALF];
-    float x1[PP], x2[PP], s1[PP], s2[PP];
+    // every load first: the q-col's pairs, their scales and their angles' (cos, sin) from the position's row
+    float x1[PP], x2[PP], s1[PP], s2[PP], cs[PP], sn[PP];
     const float* qp = qrows + (size_t(vrow) * size_t(a.heads) + size_t(vh)) * D;
+    const float2* rp = a.rope + size_t(a.pos0 + row0 + vrow) * HALF + p0;
+#pragma unroll
+    for (int e = 0; e < PP; e += 2) {   // PP consecutive pairs at a multiple of PP: 16-byte loads
+      const float4 r = *reinterpret_cast<const float4*>(rp + e);
+      cs[e] = r.x, sn[e] = r.y, cs[e + 1] = r.z, sn[e + 1] = r.w;
+    }
 #pragma unroll
     for (int e = 0; e < PP; e += 2) {   // PP consecutive floats at a multiple of PP: 8-byte loads at least
       const float2 t1 = *reinterpret_cast<const float2*>(qp + p0 + e);
@@ -739,21 +737,10 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
       }
     }
     load(A, min(t, t_last));
-#pragma unroll
-    for (int u = 0; u < kAngles; ++u) {
-      const int e = int(threadIdx.x) + u * kWaves * 64;
-      if (e < nrows * HALF) {
-        const float ang = float(a.pos0 + row0 + e / HALF) * fr[u];
-        scos[e] = cosf(ang);
-        ssin[e] = sinf(ang);
-      }
-    }
-    __syncthreads();
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < PP; ++e) {
-      const float cs = scos[vrow * HALF + p0 + e], sn = ssin[vrow * HALF + p0 + e];
-      const float o1 = x1[e] * cs - x2[e] * sn, o2 = x2[e] * cs + x1[e] * sn;
+      const float o1 = x1[e] * cs[e] - x2[e] * sn[e], o2 = x2[e] * cs[e] + x1[e] * sn[e];
       x1[e] = o1;
       x2[e] = o2;
       ss += o1 * o1 + o2 * o2;
@@ -1100,7 +1087,7 @@ struct ProduceArgs {
   int m, heads, kv_heads, group, window, rpb, splits, splits1, qpad, store;
   long long pos0;
   float scale;
-  const float* inv_freq;   // [d / 2]
+  const float2* rope;      // (cos, sin) of FP32(pos) * inv_freq[i] [pos][d / 2] (launch_rope_table)
   const float* qscale;     // [heads * d] or NULL
   void* ck;                // the cache (BF16, or FP8 codes with the scales below)
   void* cv;
@@ -1116,9 +1103,9 @@ struct ProduceArgs {
   int write_q;             // write the processed q rows back in place
 };
 
-// LDS of one producer work-group: row r's processed q heads, the k and v rows it attends to, their RoPE table.
+// LDS of one producer work-group: row r's processed q heads, the k and v rows it attends to.
 template <int D>
-constexpr int prod_lds_floats() { return (kProdGroup + 2 * kProdRows) * D + 2 * kProdRows * (D / 2); }
+constexpr int prod_lds_floats() { return (kProdGroup + 2 * kProdRows) * D; }
 
 // One work-group per (KV head, query row r). It takes RoPE + justnorm of row r's q heads of this KV head (times
 // qscale, written back in place) and of the k rows j0 .. r that row r attends to: each work-group recomputes
@@ -1135,8 +1122,6 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
   float* sq = lds;
   float* sk = sq + kProdGroup * D;
   float* sv = sk + kProdRows * D;
-  float* scos = sv + kProdRows * D;
-  float* ssin = scos + kProdRows * HALF;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool on = lane < HALF;
   const int l = lane & (HALF - 1);
@@ -1145,8 +1130,11 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
   const int nv = a.group + nk;                                   // row r's q heads, then those k rows
   const long long slot_r = a.ring ? (a.pos0 + r) % a.slots : a.pos0 + r;
 
-  // every load first, each at an index clamped into its buffer (no load behind a branch)
+  // every load first, each at an index clamped into its buffer (no load behind a branch): the rows' pairs, their
+  // scales, and their angles' (cos, sin) from the RoPE table's row of the row's position (engine/src/kernels.cpp:
+  // 203-222: the angle FP32(pos0 + row) * inv_freq[i])
   float x1[VPW][PR], x2[VPW][PR], s1[VPW][PR], s2[VPW][PR];
+  float2 cs[VPW][PR];
 #pragma unroll
   for (int it = 0; it < VPW; ++it) {
     const int idx = min(wave + it * kWaves, nv - 1);
@@ -1154,8 +1142,11 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
     const int h = kvh * a.group + (is_q ? idx : 0);
     const float* p = is_q ? a.q + (size_t(r) * size_t(a.heads) + size_t(h)) * D
                           : a.k + (size_t(j0 + idx - a.group) * size_t(a.kv_heads) + size_t(kvh)) * D;
+    const int t = is_q ? nk - 1 : idx - a.group;   // table row: row r for q, row j0 + t for k
+    const float2* rp = a.rope + size_t(a.pos0 + j0 + t) * HALF;
 #pragma unroll
     for (int u = 0; u < PR; ++u) {
+      cs[it][u] = rp[l + 64 * u];
       x1[it][u] = p[l + 64 * u];
       x2[it][u] = p[l + 64 * u + HALF];
       s1[it][u] = s2[it][u] = 1.f;
@@ -1165,27 +1156,14 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
       }
     }
   }
-  constexpr int kAngles = (kProdRows * HALF + kT - 1) / kT;
   constexpr int kVals = (kProdRows * D + kT - 1) / kT;
-  float fr[kAngles], vv[kVals];
-#pragma unroll
-  for (int u = 0; u < kAngles; ++u) fr[u] = a.inv_freq[min(tid + u * kT, nk * HALF - 1) % HALF];
+  float vv[kVals];
 #pragma unroll
   for (int u = 0; u < kVals; ++u) {
     const int e = min(tid + u * kT, nk * D - 1);
     vv[u] = a.v[(size_t(j0 + e / D) * size_t(a.kv_heads) + size_t(kvh)) * D + size_t(e % D)];
   }
-  // the rows' rotation angles FP32(pos0 + row) * inv_freq[i] (engine/src/kernels.cpp:203-222); v rows into LDS,
-  // row r's into the cache
-#pragma unroll
-  for (int u = 0; u < kAngles; ++u) {
-    const int e = tid + u * kT;
-    if (e < nk * HALF) {
-      const float ang = float(a.pos0 + j0 + e / HALF) * fr[u];
-      scos[e] = cosf(ang);
-      ssin[e] = sinf(ang);
-    }
-  }
+  // v rows into LDS, row r's into the cache
 #pragma unroll
   for (int u = 0; u < kVals; ++u) {
     const int e = tid + u * kT;
@@ -1208,7 +1186,7 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
     float o1[PR], o2[PR], ss = 0.f;
 #pragma unroll
     for (int u = 0; u < PR; ++u) {
-      const float c = scos[t * HALF + l + 64 * u], s = ssin[t * HALF + l + 64 * u];
+      const float c = cs[it][u].x, s = cs[it][u].y;
       o1[u] = x1[it][u] * c - x2[it][u] * s;
       o2[u] = x2[it][u] * c + x1[it][u] * s;
       ss += o1[u] * o1[u] + o2[u] * o2[u];
@@ -1563,6 +1541,27 @@ void* attn_scratch_ptr(int device) {
 
 // ------------------------------------------------------------------------------------------------- launchers
 
+// The RoPE rows of positions 0 .. n_pos - 1: (cos, sin) of the angle FP32(pos) * inv_freq[i] (engine/src/
+// kernels.cpp:203-222), [pos][d / 2], the same expression the row kernels evaluate, so a table entry is the value
+// they compute for that position.
+__global__ void __launch_bounds__(256) rope_table_kernel(const float* __restrict__ inv_freq, int half, long long n_pos,
+                                                         float2* __restrict__ out) {
+  const long long n = n_pos * half;
+  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long long)gridDim.x * 256) {
+    const float ang = float(e / half) * inv_freq[e % half];
+    out[e] = make_float2(cosf(ang), sinf(ang));
+  }
+}
+
+std::string launch_rope_table(const float* inv_freq, int d, long long n_pos, float2* out, hipStream_t stream) {
+  XTG_CHECK(d % 2 == 0 && d > 0 && n_pos > 0, "rope table: head_dim %d, %lld positions", d, n_pos);
+  const long long n = n_pos * (d / 2);
+  const unsigned blocks = unsigned(std::min<long long>((n + 255) / 256, 65536));
+  hipLaunchKernelGGL(rope_table_kernel, dim3(blocks), dim3(256), 0, stream, inv_freq, d / 2, n_pos, out);
+  HIP_CHECK(hipGetLastError());
+  return "rope_table_kernel";
+}
+
 // The wave merge of a scan needs more than the default 64 KiB of LDS for 128-dim heads and two q-blocks, as does a
 // wide GEMV on raw rows: raise the kernel's limit once.
 void allow_lds(const void* fn, size_t lds) {
@@ -1652,7 +1651,7 @@ ScanArgs scan_args(const DevKv& c, const AttnPlan& p, int b0, const float* q, in
 }
 
 ProduceArgs produce_args(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
-                         int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
+                         int m, int heads, long long pos0, int window, float scale, const float2* rope,
                          const float* qscale, bool store, float* part) {
   XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
   XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
@@ -1674,7 +1673,7 @@ ProduceArgs produce_args(const DevKv& c, const AttnPlan& p, float* q, const floa
   a.store = store ? 1 : 0;
   a.pos0 = pos0;
   a.scale = scale;
-  a.inv_freq = inv_freq;
+  a.rope = rope;
   a.qscale = qscale;
   a.ck = c.k;
   a.cv = c.v;
@@ -1768,10 +1767,10 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
 }
 
 std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
-                              int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
+                              int m, int heads, long long pos0, int window, float scale, const float2* rope,
                               const float* qscale, bool store, float* part, hipStream_t stream) {
-  const ProduceArgs a =
-      produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, inv_freq, qscale, store, part);
+  XTG_CHECK(rope, "producer: no RoPE table");
+  const ProduceArgs a = produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, rope, qscale, store, part);
   const int vpw = produce_vpw(p, m, window);
   const dim3 grid{unsigned(c.kv_heads * m)}, block{unsigned(kWaves * 64)};
 #define XTG_PROD(D, V) \
@@ -1789,8 +1788,9 @@ bool attn_step_fuses(const AttnPlan& p, int m) {
 
 std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
                              float* kout, int m, int heads, long long pos0, int window, float scale,
-                             const float* inv_freq, const float* qscale, bool store, float* part,
+                             const float2* rope, const float* qscale, bool store, float* part,
                              hipStream_t stream) {
+  XTG_CHECK(rope, "attention step: no RoPE table");
   XTG_CHECK(attn_step_fuses(p, m), "attention step: %d rows in %d blocks, %d splits: no fused launch", m, p.blocks,
             p.splits);
   XTG_CHECK(p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
@@ -1798,9 +1798,9 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
   XTG_CHECK(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(qscale) % 16 == 0,
             "attention step: q and qscale must be 16-byte aligned");
   ScanArgs a = scan_args(c, p, 0, q, m, heads, pos0, window, scale, part);
-  a.inv_freq = inv_freq;
+  a.rope = rope;
   a.qscale = qscale;
-  ProduceArgs pa = produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, inv_freq, qscale, store, part);
+  ProduceArgs pa = produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, rope, qscale, store, part);
   pa.write_q = 0;   // the scan work-groups read q raw while the producers run
   const int vpw = produce_vpw(p, m, window);
   const int qb = (m * p.group + 15) / 16;

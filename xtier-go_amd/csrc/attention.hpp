@@ -73,13 +73,16 @@ void* attn_scratch_ptr(int device);
 
 constexpr int kProdRows = 8, kProdGroup = 8;   // the producer's rows per call and q heads per KV head
 
+// The RoPE rows of positions 0 .. n_pos - 1 into out [n_pos][d / 2]: (cos, sin) of FP32(pos) * inv_freq[i]
+// (engine/src/kernels.cpp:203-222). The producer and the decode step's scan read their rows' angles from it.
+std::string launch_rope_table(const float* inv_freq, int d, long long n_pos, float2* out, hipStream_t stream);
 // The decode step's producer (packs/dory/dory.cpp:482-490 and the cache store of :507): in one launch per
-// call (m <= 8 rows), RoPE + justnorm of q and k (q *= qscale, q written back in place; k read only, the
-// processed rows also written to kout when it is not NULL), the own-key partials from the FP32 rows, and -- when
-// store is set -- k, v stored into the cache. Storing before the scan is exact when no key the scan should see is
+// call (m <= 8 rows), RoPE (angles from the table rope, covering positions pos0 .. pos0 + m - 1) + justnorm of
+// q and k (q *= qscale, q written back in place; k read only, the processed rows also written to kout when it is
+// not NULL), the own-key partials from the FP32 rows, and -- when store is set -- k, v stored into the cache. Storing before the scan is exact when no key the scan should see is
 // overwritten: a linear cache, or a ring of at least window + m - 1 slots.
 std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v, float* kout,
-                              int m, int heads, long long pos0, int window, float scale, const float* inv_freq,
+                              int m, int heads, long long pos0, int window, float scale, const float2* rope,
                               const float* qscale, bool store, float* part, hipStream_t stream);
 // The producer and the scan in one launch (same arguments and results as launch_qk_produce followed by
 // launch_attn_scan, except that q is not written back): for a call of one row block with cached keys to scan
@@ -88,7 +91,7 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const
 bool attn_step_fuses(const AttnPlan& p, int m);
 std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
                              float* kout, int m, int heads, long long pos0, int window, float scale,
-                             const float* inv_freq, const float* qscale, bool store, float* part,
+                             const float2* rope, const float* qscale, bool store, float* part,
                              hipStream_t stream);
 // The decode step's finish (dory.cpp:509-515): every row's merge, times sigmoid(g * gscale), justnorm over the
 // heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).

@@ -42,6 +42,7 @@ Backend::~Backend() {
     delete c;
   }
   for (auto& f : inv_freq_) (void)hipFree(f.second);
+  for (auto& t : rope_) (void)hipFree(t.p);
   for (const Pending& p : pending_) {
     (void)hipEventDestroy(p.a);
     (void)hipEventDestroy(p.b);
@@ -568,8 +569,8 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
   const AttnPlan p = attn_plan(*c, m, heads, pos0, window);
   ensure(part_, part_size_, p.part_floats() * sizeof(float));
   float* part = static_cast<float*>(part_);
-  const float* f = inv_freq(theta, c->head_dim);
   if (m > kProdRows) {
+    const float* f = inv_freq(theta, c->head_dim);
     // a prefill chunk (the reference's order, dory.cpp:481-515): RoPE + norms in place, the attention over the
     // read-only cache and the chunk's own keys (matrix-core own-key tiles), the store of the chunk's k / v, then
     // the merge with the gate and norm
@@ -590,14 +591,15 @@ void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, 
     ensure(kproc_, kproc_size_, size_t(m) * size_t(c->kv_heads) * size_t(c->head_dim) * sizeof(float));
     kout = static_cast<float*>(kproc_);
   }
+  const float2* rt = rope_table(theta, c->head_dim, pos0 + m);
   if (attn_step_fuses(p, m) && !std::getenv("XTG_ATTN_UNFUSED")) {
     timed([&] {
-      return launch_attn_step(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
+      return launch_attn_step(*c, p, q, k, v, kout, m, heads, pos0, window, scale, rt, qscale, store_first, part,
                               stream_);
     });
   } else {
     timed([&] {
-      return launch_qk_produce(*c, p, q, k, v, kout, m, heads, pos0, window, scale, f, qscale, store_first, part,
+      return launch_qk_produce(*c, p, q, k, v, kout, m, heads, pos0, window, scale, rt, qscale, store_first, part,
                                stream_);
     });
     if (p.splits > 0)
@@ -622,6 +624,29 @@ const float* Backend::inv_freq(float theta, int d) {
   HIP_CHECK(hipMalloc(&p, h.size() * sizeof(float)));
   HIP_CHECK(hipMemcpy(p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
   inv_freq_.push_back({{theta, d}, p});
+  return p;
+}
+
+const float2* Backend::rope_table(float theta, int d, long long n_pos) {
+  XTG_CHECK(n_pos > 0 && n_pos <= (1LL << 31), "rope: a table of %lld positions", n_pos);
+  RopeTable* t = nullptr;
+  for (auto& r : rope_)
+    if (r.theta == theta && r.d == d) t = &r;
+  if (t && t->n >= n_pos) return t->p;
+  XTG_CHECK(!capturing_, "rope: the table for theta %g, head_dim %d must cover position %lld before a graph capture",
+            theta, d, n_pos - 1);
+  const float* f = inv_freq(theta, d);
+  const long long n = std::min(std::max({n_pos, t ? 2 * t->n : 0LL, 4096LL}), 1LL << 31);
+  float2* p = nullptr;
+  HIP_CHECK(hipMalloc(&p, size_t(n) * size_t(d / 2) * sizeof(float2)));
+  timed([&] { return launch_rope_table(f, d, n, p, stream_); });
+  if (t) {
+    dev_free(t->p);
+    t->p = p;
+    t->n = n;
+  } else {
+    rope_.push_back({theta, d, n, p});
+  }
   return p;
 }
 

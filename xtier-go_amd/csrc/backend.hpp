@@ -110,6 +110,10 @@ class Backend {
               const double* u, int* out);
   // 1 / theta^(2i/d) in FP32 computed on the host as engine/src/kernels.cpp:191-201 does, kept on the device
   const float* inv_freq(float theta, int d);
+  // the RoPE rows (cos, sin) of positions 0 .. n - 1 for (theta, d), n >= n_pos (launch_rope_table): made on the
+  // device once and grown by doubling when a call needs more positions (not during a graph capture; a table a graph
+  // holds is retired until no graph exists). The decode step's producer and scan read their angles from it.
+  const float2* rope_table(float theta, int d, long long n_pos);
 
   // opencl.h:40-45
   void* alloc(size_t bytes);
@@ -203,6 +207,13 @@ class Backend {
   size_t sample_size_ = 0;
   std::unordered_set<DevKv*> kvs_;
   std::vector<std::pair<std::pair<float, int>, float*>> inv_freq_;
+  struct RopeTable {
+    float theta;
+    int d;
+    long long n;
+    float2* p;
+  };
+  std::vector<RopeTable> rope_;
   void* hx_ = nullptr;
   size_t hx_size_ = 0;
   void* stage_ = nullptr;   // a weight's checkpoint arrays on their way to the tile layout

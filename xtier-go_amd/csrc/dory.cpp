@@ -110,7 +110,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
         caches_.push_back(i < inst ? b_.kv_create(c.kv_heads, c.head_dim, c.context,
                                                    L.w.kind == XTG_DORY_SLIDING ? c.ring_slots : 0, c.kv_dtype)
                                    : nullptr);
-      b_.inv_freq(L.w.kind == XTG_DORY_SLIDING ? c.theta_sliding : c.theta_full, c.head_dim);
+      // the RoPE rows of every position the session can reach, made before any capture
+      b_.rope_table(L.w.kind == XTG_DORY_SLIDING ? c.theta_sliding : c.theta_full, c.head_dim, c.context);
     }
   }
   if (head_.codes) {   // else a BF16 head comes with set_head_bf16
