@@ -256,8 +256,9 @@ typedef struct xtg_hip_dory xtg_hip_dory;
 /* Replaces the DoryModel constructor's weight preparation (dory.cpp:365-371) and the GpuDorySession constructor
  * (dory.cpp:1043-1084): prepares every weight and the NVFP4 LM head [vocab][hidden] (head may be NULL when a BF16
  * head follows through xtg_hip_dory_head_bf16), uploads the vectors and logit_scale [vocab], creates the caches
- * (kv_dtype; sliding sublayers: rings of ring_slots). NULL on failure. The host weights must stay alive and
- * unchanged while the session exists (they key the prepared copies). */
+ * (kv_dtype; sliding sublayers: rings of ring_slots) and, per RoPE theta, the cosines and sines of every position
+ * below context (context x head_dim / 2 x 8 bytes of device memory each). NULL on failure. The host weights must
+ * stay alive and unchanged while the session exists (they key the prepared copies). */
 xtg_hip_dory* xtg_hip_dory_create(xtg_hip* h, const xtg_dory_config* c, const xtg_dory_layer* layers,
                                   const xtg_nvfp4* head, const float* logit_scale, char* err, int err_len);
 void xtg_hip_dory_destroy(xtg_hip_dory* d);
