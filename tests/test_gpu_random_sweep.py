@@ -76,19 +76,20 @@ def test_random_sweep(hip, pkg, orc, wl):
 @pytest.mark.gpu
 def test_random_dory_configs(hip, orc, wl):
     """The decode-step composition over random small configurations -- widths, head layouts (4/2, 8/2, 2/1, 4/4,
-    8/1 of 64 or 128), windows of 8-48 in rings of 4-64 slots more (some too short to store before the scan), one
-    or two loops, BF16 or FP8 caches -- through random calls: chunks of up to 40 rows, then steps of 1-8. Every
-    call's logits against the oracle's composition: rel-L2 <= 1e-3 and the same argmax per row."""
+    8/1 of 64, 128 or 256), windows of 8-48 in rings of 4-64 slots more (some too short to store before the scan),
+    one or two loops, BF16 or FP8 caches, per_loop or last_loop KV mode -- through random calls: chunks of up to 40
+    rows, then steps of 1-8. Every call's logits against the oracle's composition: rel-L2 <= 1e-3 and the same
+    argmax per row."""
     rng = np.random.default_rng(20261203)
     fails = []
-    for _ in range(25):
+    for _ in range(40):
         heads, kvh = [(4, 2), (8, 2), (2, 1), (4, 4), (8, 1)][int(rng.integers(0, 5))]
         window = int(rng.choice([8, 16, 48]))
         cfg = dict(hidden=int(rng.choice([128, 256, 384])), ffn=int(rng.choice([256, 384, 512])), heads=heads,
-                   kv_heads=kvh, head_dim=int(rng.choice([64, 128])), vocab=int(rng.choice([500, 1000, 3000])),
+                   kv_heads=kvh, head_dim=int(rng.choice([64, 128, 256])), vocab=int(rng.choice([500, 1000, 3000])),
                    n_in=2, n_rec=int(rng.choice([2, 4])), n_out=2, loops=int(rng.integers(1, 3)), window=window,
                    ring_slots=window + int(rng.choice([4, 16, 64])), theta_sliding=1e4, theta_full=1e6,
-                   kv_dtype=int(rng.integers(0, 2)))
+                   kv_dtype=int(rng.integers(0, 2)), kv_mode=int(rng.integers(0, 2)))
         context = 192
         w = wl.DoryWeights(cfg, seed=int(rng.integers(0, 1 << 30)), context=context)
         ref = orc.Dory(w, wl)
