@@ -831,7 +831,7 @@ def main():
     for name, m in calls:
         hip.profile(True)
         hip.matmul_dev(sets[0][name], dx[(name, m)], pkg.X_BF16, m, dy)
-        names = [k for k in hip.profile_report() if k.startswith("gemv_kernel")]
+        names = [k for k in hip.profile_report() if k.startswith(("gemv_kernel", "gemv_mx_kernel"))]
         hip.profile(False)
         kernel_of["%s_m%d" % (name, m)] = names[0]
     tot_bytes, tot_s = 0, 0.0

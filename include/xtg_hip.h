@@ -91,7 +91,9 @@ int xtg_hip_matmul_nvfp4(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const float* 
  * as they are; more: the GEMM on a prepared operand), n_w <= 4 per call (the fused q/k/v/g and gate/up of the Dory
  * sublayers). x must be 16-byte aligned. The GEMM keeps ~22 bits of each activation (two f16 parts); with
  * XTG_GEMM_PARTS=1 in the environment (read at each call) it takes one f16 part, about 1.4-1.6x faster at ~2e-4
- * relative error, the precision class of the reference's FP16 GPU prefill GEMM (opencl.cpp:232-269). */
+ * relative error, the precision class of the reference's FP16 GPU prefill GEMM (opencl.cpp:232-269). One or two
+ * BF16 rows run on the block-scaled FP4 x FP8 matrix op (no dequantisation; each BF16 input split exactly into two
+ * E4M3 parts); XTG_GEMV_MX=0 in the environment (read once) keeps them on the f16 matrix op, for comparison. */
 int xtg_hip_matmul_nvfp4_dev(xtg_hip* h, const xtg_nvfp4* ws, int n_w, const void* x, int x_dtype, int m, float* y,
                              size_t y_offset, char* err, int err_len);
 

@@ -449,6 +449,174 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   }
 }
 
+// ------------------------------------------------------------- one or two BF16 rows on the block-scaled FP4 op
+//
+// gfx950's v_mfma_scale_f32_16x16x128_f8f6f4 multiplies E2M1 codes as they are stored (A: 16 weight rows x 128
+// inputs, lane l = row l % 16 holding inputs 32 (l / 16) .. + 31 as 16 bytes, low nibble first: exactly a lane's
+// share of a weight tile) with an FP8 E4M3 operand B whose lanes (column l % 16, q = l / 16) hold inputs 16 q .. + 15
+// in bytes 0..15 and 64 + 16 q .. + 15 in bytes 16..31, each column scaled by a power of two (E8M0). So no
+// dequantisation runs on the vector ALUs. The NVFP4 group scale (E4M3, per 16 inputs) is not a power of two, so
+// the group sums are kept apart: column c of the operand holds activation row j's group g = c % 8 of the k-tile
+// (zeros elsewhere) as part p = c / 8 -- a BF16 input x (8 significant bits) is hi + lo / 16 exactly, hi = E4M3 of
+// x 2^e (the group's largest magnitude brought to [2^7, 2^8)) and lo = E4M3 of (x 2^e - hi) 16, the remainder
+// having at most 4 significant bits -- with column scale 2^-e (hi) or 2^-(e + 4) (lo). Output (row n, column c)
+// is then the exact-product FP32 sum over one group and part; each lane multiplies its four rows by their E4M3
+// group scale and accumulates over the k-tiles, and the 16 columns are added by DPP at the end.
+// Inputs whose scaled magnitude falls below E4M3's subnormal range (2^-20 of the group's largest) lose bits below
+// 2^-13 of that scale. A group holding an infinity or NaN gets NaN codes (NaN outputs).
+// Lane layout of the staging: lane l converts inputs 2 l, 2 l + 1 of each row (one 32-bit load), its group being
+// the 8 lanes l / 8 (largest magnitude by DPP within the half-row), and writes the two planes (hi, lo) [MR][128]
+// bytes and the groups' exponents to LDS; lane (c, q) then reads group c % 8 of plane c / 8 (16 bytes).
+constexpr int kMxStageVecs = (2 * 2 * 128 + 2 * 8 * 4) / 16;   // two rows: [2 planes][2 rows][128 B] + [2][8] ints
+
+template <int R, int T, int MAXT, int MR>
+__global__ void __launch_bounds__(MAXT) gemv_mx_kernel(const GemvArgs a) {
+  extern __shared__ f32x4 red[];
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  int wi = 0;
+  while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+  const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * R;
+  const int nb = a.nb[wi], KT = a.kt;
+  const uint8_t* __restrict__ tiles = a.tiles[wi];
+  const int kt0 = wave * T;
+  const int col = lane & 15, q = lane >> 4, g = col & 7, p = col >> 3;
+
+  // every load first: each row's two inputs of every k-tile (zeros for absent rows and k-tiles past k), then the
+  // weight tiles (clamped: an absent tile is a tile of the same weight, its results unstored or met by zeros) with
+  // the 8 scale bytes this lane's output rows need (rows 4 q .. 4 q + 3, group g)
+  uint32_t xr[T][MR];
+  const __amdgpu_buffer_rsrc_t xres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), (short)0, a.m * a.k * 2, 0x00020000);
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    const int ki = (kt0 + u) * kTileK + 2 * lane;
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+      const bool in = kt0 + u < KT && j < a.m && ki < a.k;
+      const uint32_t off = in ? (uint32_t(j) * uint32_t(a.k) + uint32_t(ki)) * 2u : 0x80000000u;
+      xr[u][j] = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(xres, int(off), 0, 0));
+    }
+  }
+  u32x4 cw[T][R];
+  u32x2 sw[T][R];
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint8_t* tile =
+          tiles + (size_t(min(rb0 + r, nb - 1)) * size_t(KT) + size_t(min(kt0 + u, KT - 1))) * kTileBytes;
+      cw[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + 16 * lane));
+      sw[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(tile + 1024 + 32 * (g >> 1) + 8 * q));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint8_t* stage = reinterpret_cast<uint8_t*>(reinterpret_cast<uint4*>(red) + (S > 1 ? S * R * kMaxRows * 4 : 0) +
+                                              wave * kMxStageVecs);
+  int* gexp = reinterpret_cast<int*>(stage + 2 * MR * 128);
+  f32x4 acc[R][MR];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < MR; ++j) acc[r][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    i32x8 B[MR];
+    int sb[MR];
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+      const uint32_t w = xr[u][j];
+      uint32_t am = max(w & 0x7fffu, (w >> 16) & 0x7fffu);
+      am = max(am, uint32_t(__builtin_amdgcn_update_dpp(0, int(am), kDppXor1, 0xF, 0xF, false)));
+      am = max(am, uint32_t(__builtin_amdgcn_update_dpp(0, int(am), kDppXor2, 0xF, 0xF, false)));
+      am = max(am, uint32_t(__builtin_amdgcn_update_dpp(0, int(am), kDppHalfMirror, 0xF, 0xF, false)));
+      const bool fin = am < 0x7f80u;
+      const int e = am == 0u || !fin ? 0 : min(134 - int(am >> 7), 123);
+      const float v0 = ldexpf(__uint_as_float(w << 16), e), v1 = ldexpf(__uint_as_float(w & 0xffff0000u), e);
+      uint32_t hi = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false)) & 0xffffu;
+      const float l0 = (v0 - __builtin_amdgcn_cvt_f32_fp8(hi, 0)) * 16.f;
+      const float l1 = (v1 - __builtin_amdgcn_cvt_f32_fp8(hi, 1)) * 16.f;
+      uint32_t lo = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(l0, l1, 0, false)) & 0xffffu;
+      if (!fin) hi = 0x7f7fu, lo = 0u;
+      *reinterpret_cast<uint16_t*>(stage + j * 128 + 2 * lane) = uint16_t(hi);
+      *reinterpret_cast<uint16_t*>(stage + (MR + j) * 128 + 2 * lane) = uint16_t(lo);
+      if ((lane & 7) == 0) gexp[j * 8 + (lane >> 3)] = e;
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+      const uint4 b = *reinterpret_cast<const uint4*>(stage + (p * MR + j) * 128 + 16 * g);
+      const bool first = g == q, second = g == q + 4;
+      B[j] = i32x8{int(first ? b.x : 0u), int(first ? b.y : 0u), int(first ? b.z : 0u), int(first ? b.w : 0u),
+                   int(second ? b.x : 0u), int(second ? b.y : 0u), int(second ? b.z : 0u), int(second ? b.w : 0u)};
+      sb[j] = 127 - gexp[j * 8 + g] - 4 * p;
+    }
+    wave_lds_order();   // read before the next k-tile's staging
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const i32x8 A = {int(cw[u][r][0]), int(cw[u][r][1]), int(cw[u][r][2]), int(cw[u][r][3]), 0, 0, 0, 0};
+      const uint32_t s0 = sw[u][r][0] >> (8 * (g & 1)), s1 = sw[u][r][1] >> (8 * (g & 1));
+      const f32x4 s = f32x4{__builtin_amdgcn_cvt_f32_fp8(s0, 0), __builtin_amdgcn_cvt_f32_fp8(s0, 2),
+                            __builtin_amdgcn_cvt_f32_fp8(s1, 0), __builtin_amdgcn_cvt_f32_fp8(s1, 2)};
+#pragma unroll
+      for (int j = 0; j < MR; ++j) {
+        const f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B[j], f32x4{0.f, 0.f, 0.f, 0.f}, 4, 0,
+                                                                          0, 127, 0, sb[j]);
+        acc[r][j] += c * s;
+      }
+    }
+  }
+  // the 16 columns (8 groups x hi / lo) of each output row added within each row of lanes; lane (c, q) with c = 2 j
+  // then holds activation row j's sums for output rows 4 q .. 4 q + 3, the layout of gemv_kernel's epilogue
+  f32x4 v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = acc[r][j][e];
+        t += dpp<kDppXor1>(t);
+        t += dpp<kDppXor2>(t);
+        t += dpp<kDppHalfMirror>(t);
+        t += dpp<kDppMirror>(t);
+        acc[r][j][e] = t;
+      }
+    }
+    v[r] = acc[r][0];
+    if constexpr (MR > 1) v[r] = col >= 2 ? acc[r][1] : acc[r][0];
+  }
+  const bool store_lane = (col & 1) == 0 && (col >> 1) < min(a.m, MR);
+  if (S == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (store_lane && rb0 + r < nb) store_rows(a, wi, rb0 + r, q, col >> 1, v[r]);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (store_lane) red[((wave * R + r) * kMaxRows + (col >> 1)) * 4 + q] = v[r];
+  __syncthreads();
+  for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
+    const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7;
+    if (rb0 + r >= nb || jj >= min(a.m, MR)) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w0 = 0; w0 < 16; w0 += 4) {
+      if (w0 >= S) break;
+      f32x4 t[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = red[(((w0 + i < S ? w0 + i : S - 1) * R + r) * kMaxRows + jj) * 4 + gg];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (w0 + i < S) sum += t[i];
+    }
+    store_rows(a, wi, rb0 + r, gg, jj, sum);
+  }
+}
+
 namespace {
 using GemvFn = void (*)(const GemvArgs);
 
@@ -483,6 +651,30 @@ bool shape_ok(int r, int t, int s, bool raw = false) {
   if (r * t > 12) return false;
   if (s > 8 && t > 4) return false;   // 1024-thread groups get 128 VGPRs per lane: T > 4 spills there
   return gemv_fn(r, t, s * 64, raw) != nullptr;
+}
+
+template <int R, int T, int MR>
+GemvFn mx_pick(int threads) {
+  if (threads <= 512) return gemv_mx_kernel<R, T, 512, MR>;
+  return gemv_mx_kernel<R, T, 1024, MR>;
+}
+
+// the block-scaled FP4 kernel for one or two raw BF16 rows, at the shapes the raw-row kernel takes
+GemvFn gemv_mx_fn(int r, int t, int threads, int m) {
+#define XTG_CASE(R, T)                                             \
+  if (r == R && t == T) return m == 1 ? mx_pick<R, T, 1>(threads) : mx_pick<R, T, 2>(threads);
+  XTG_CASE(1, 2) XTG_CASE(1, 4) XTG_CASE(2, 2) XTG_CASE(2, 4) XTG_CASE(4, 2) XTG_CASE(4, 4)
+#undef XTG_CASE
+  return nullptr;
+}
+
+// XTG_GEMV_MX=0 keeps one and two BF16 rows on the f16 matrix op (for comparison)
+bool mx_enabled() {
+  static const bool on = [] {
+    const char* env = std::getenv("XTG_GEMV_MX");
+    return !(env && env[0] == '0');
+  }();
+  return on;
 }
 }  // namespace
 
@@ -573,15 +765,17 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.y = c.y;
   XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
   const int threads = sh.s * 64;
-  GemvFn fn = gemv_fn(sh.r, sh.t, threads, xr);
+  GemvFn mx = xr && c.m <= 2 && mx_enabled() ? gemv_mx_fn(sh.r, sh.t, threads, c.m) : nullptr;
+  GemvFn fn = mx ? mx : gemv_fn(sh.r, sh.t, threads, xr);
   XTG_CHECK(fn != nullptr, "gemv: no kernel for shape R=%d T=%d%s", sh.r, sh.t, xr ? " on raw rows" : "");
   const size_t lds = (sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * kMaxRows * 4 * sizeof(f32x4) : 0) +
-                     (xr ? size_t(sh.s) * kStageVecs * sizeof(uint4) : 0);
+                     (xr ? size_t(sh.s) * (mx ? kMxStageVecs : kStageVecs) * sizeof(uint4) : 0);
   allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
-  return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, threads <= 512 ? 512 : 1024)
-            : strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, threads <= 512 ? 512 : 1024);
+  const int mt = threads <= 512 ? 512 : 1024;
+  if (mx) return strf("gemv_mx_kernel<%d, %d, %d, %d>", sh.r, sh.t, mt, c.m);
+  return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, mt) : strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, mt);
 }
 
 }  // namespace xtg::hip
