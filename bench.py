@@ -709,6 +709,43 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     return results
 
 
+def decode_eager_pass(pkg, wl, hip, ctx, kv_fp8, reps):
+    """The decode step run eagerly (no graph capture), for a kernel trace of it: the 4B-shaped model over BF16 or
+    FP8 caches holding a synthetic context of ctx unit-norm rows, `reps` one-row steps at position ctx, each
+    launch on the backend's stream; prints the wall-clock milliseconds per step (launch overheads included)."""
+    w = wl.DoryWeights(wl.DORY_4B, seed=11, context=ctx + 64)
+    if kv_fp8:
+        w.cfg = dict(w.cfg, kv_dtype=1)
+    dev = hip.dory(w)
+    c = w.cfg
+    kvh, d, ring, H, V = c["kv_heads"], c["head_dim"], c["ring_slots"], c["hidden"], c["vocab"]
+    rng = np.random.default_rng(12)
+    dK, dV = hip.array(wl.unit_heads(rng, (ctx, kvh), d)), hip.array(wl.unit_heads(rng, (ctx, kvh), d))
+    row = kvh * d * 4
+    x = rng.standard_normal((1, H)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    dx, dl = hip.array(x), hip.array(shape=(1, V))
+    kinds = [k for k in w.kinds if k != wl.MLP]
+    for a, kind in enumerate(kinds):
+        if kind == wl.FULL:
+            dev.cache(a).store(0, ctx, dK, dV)
+        else:
+            dev.cache(a).store(ctx - ring, ring, dK.ptr + (ctx - ring) * row, dV.ptr + (ctx - ring) * row)
+    dev.forward(dx, 1, ctx, dl)
+    hip.finish()
+    t = time.perf_counter()
+    for _ in range(reps):
+        dev.forward(dx, 1, ctx, dl)
+    hip.finish()
+    ms = (time.perf_counter() - t) / reps * 1e3
+    log("eager decode step, %s caches, ctx %d: %.3f ms per step (wall clock, %d steps)"
+        % ("FP8" if kv_fp8 else "BF16", ctx, ms, reps))
+    for a in (dK, dV, dx, dl):
+        a.free()
+    dev.destroy()
+    return ms
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -729,6 +766,9 @@ def main():
                          "or also the FP8 caches of the reference Dory's default (M=1; the default)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step measurement (for profiling it); prints its own JSON line")
+    ap.add_argument("--decode-eager", default="",
+                    help="KV,CTX (e.g. fp8,4096): only the decode step run eagerly, without graph capture, for a "
+                         "kernel trace of it (--decode-reps steps); prints its own JSON line")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
                          "left out of the JSON line")
@@ -743,6 +783,15 @@ def main():
 
     if args.pmc_pass:
         pmc_pass(pkg, wl)
+        return
+
+    if args.decode_eager:
+        kvs, ctx = args.decode_eager.split(",")
+        hip = pkg.HipBackend(0)
+        ms = decode_eager_pass(pkg, wl, hip, int(ctx), kvs == "fp8", args.decode_reps)
+        print(json.dumps({"metric": "eager decode step ms (%s caches, ctx %s)" % (kvs, ctx), "value": round(ms, 4),
+                          "unit": "ms", "higher_is_better": False}))
+        hip.close()
         return
 
     if args.decode_only:
