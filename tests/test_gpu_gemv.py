@@ -210,6 +210,59 @@ def test_raw_bf16_tiny_and_nonfinite_rows(hip, pkg, orc, wl):
     assert np.isnan(y[4]).all()
 
 
+@pytest.mark.parametrize("m", [1, 2])
+def test_block_scaled_rows_edge_cases(hip, pkg, orc, wl, m):
+    """One and two BF16 rows take the block-scaled FP4 x FP8 matrix op (each input split into two E4M3 parts at its
+    16-input group's power of two). Rows built against that split: magnitudes from 2^-60 to 2^60 alternating within
+    every group (the small half far below E4M3's range at the group's exponent: its contribution is below 2^-100 of
+    the output), BF16 subnormals (the exponent cap), one group of exact zeros in an otherwise normal row, values
+    whose 8 significant bits need both parts (128 + odd), magnitudes near 2^100, and -- in the last row of the
+    two-row case -- an infinity and a NaN in separate groups (that row's outputs are NaN, the other row's are not).
+    Against the oracle at rel-L2 1e-5 and the FP64 closed form at max |err| / RMS 3e-5."""
+    rng = np.random.default_rng(31 + m)
+    n, k = 272, 768
+    w = kt_weight(rng, n, k)
+    rows = []
+    x = rng.standard_normal(k).astype(np.float32)
+    x[::2] *= np.float32(2.0 ** 60)
+    x[1::2] *= np.float32(2.0 ** -60)
+    rows.append(x)
+    rows.append((rng.standard_normal(k) * 2.0 ** -128).astype(np.float32))   # BF16 subnormals
+    x = rng.standard_normal(k).astype(np.float32)
+    x[32:48] = 0.0
+    rows.append(x)
+    rows.append(((rng.integers(0, 2, k) * 2 - 1) * (128 + 2 * rng.integers(0, 64, k) + 1)).astype(np.float32))
+    rows.append((rng.standard_normal(k) * 2.0 ** 100).astype(np.float32))   # large, the FP32 sums stay finite
+    for i, x in enumerate(rows):
+        xs = [x] if m == 1 else [x, rows[(i + 1) % len(rows)]]
+        xb = wl.f32_to_bf16(np.stack(xs))
+        x32 = wl.bf16_to_f32(xb)
+        dx, dy = hip.array(xb), hip.array(shape=(m, n))
+        hip.matmul_dev([pkg.Weight(*w)], dx, pkg.X_BF16, m, dy)
+        y = dy.numpy()
+        dx.free()
+        dy.free()
+        (r,) = orc.matmul_nvfp4([w], x32)
+        exact = x32.astype(np.float64) @ wl.decode_nvfp4(*w).astype(np.float64).T
+        for j in range(m):
+            assert np.isfinite(y[j]).all(), (i, j)
+            assert rel_l2(y[j], r[j]) <= 1e-5, (i, j)
+            assert err_over_rms(y[j], exact[j]) <= 3e-5, (i, j)
+    if m == 2:
+        x = rng.standard_normal((2, k)).astype(np.float32)
+        x[1, 100] = np.inf
+        x[1, 300] = np.nan
+        xb = wl.f32_to_bf16(x)
+        dx, dy = hip.array(xb), hip.array(shape=(2, n))
+        hip.matmul_dev([pkg.Weight(*w)], dx, pkg.X_BF16, 2, dy)
+        y = dy.numpy()
+        dx.free()
+        dy.free()
+        (r,) = orc.matmul_nvfp4([w], wl.bf16_to_f32(xb[:1]))
+        assert rel_l2(y[0], r[0]) <= 1e-5
+        assert np.isnan(y[1]).all()
+
+
 def tiles_np(codes, scales):
     """The documented tile layout: tile (rb, kt) holds lane l = 16 g + r's 16 code bytes (row rb * 16 + r, inputs
     kt * 128 + 32 g .. + 32) at 16 l and its two scale bytes at 1024 + 2 l; zeros past n and k."""
