@@ -692,7 +692,12 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw) {
     // (with one row-block) only where K needs them (16 waves at most per work-group)
     int nb = 0;
     for (int i = 0; i < nw; ++i) nb += nbs[i];
-    const int r = nb >= 512 ? 4 : 2, t = (kt + 1) / 2 <= 16 ? 2 : 4;
+    int r = nb >= 512 ? 4 : 2;
+    const int t = (kt + 1) / 2 <= 16 ? 2 : 4;
+    // one or two rows on the block-scaled op (measured the same way over configs 0 and 1): one row-block per wave
+    // while the launch fits one work-group per CU, four where two would leave the CUs unevenly loaded (512 < nb <
+    // 1024), two otherwise (two work-groups per CU at 1024)
+    if (m <= 2 && mx_enabled()) r = nb <= 256 ? 1 : (nb <= 512 || nb >= 1024) ? 2 : 4;
     if (shape_ok(r, t, (kt + t - 1) / t, true)) return {r, t, (kt + t - 1) / t};
     if (shape_ok(1, 4, (kt + 3) / 4, true)) return {1, 4, (kt + 3) / 4};
   }
