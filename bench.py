@@ -11,14 +11,14 @@ streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed 
 rotation phase), so host launch cost does not set the pace.
 
 value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
-roofline: the dominant kernel, the GEMV instantiation that moves the largest share of the step's bytes (each call
-is one launch; the launch shape follows the call's shape, so the calls map onto three instantiations; the fused
-gate/up one carries 55 % of the bytes). For each
-(shape, rows) a graph of one call per weight copy is replayed between two HIP events on the backend's stream;
-achieved = algorithmic bytes of the dominant kernel's launches / their time, against the 8 TB/s HBM peak
-(all_calls_*: the same over all 6 calls). traffic: that kernel's HBM bytes per launch from rocprofv3 FETCH_SIZE /
-WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known size
-(profiles/gemv_layer_projections_traffic_pmc.md).
+roofline: the dominant kernel launch, the call (one GEMV launch: a kernel instantiation at one weight shape and row
+count) that moves the most bytes of the step -- an instantiation can serve calls of different sizes (QKV and
+gate/up at M=1 share one), and a roofline over a mixture of launch sizes describes none of them; by_kernel gives
+the same figures grouped by instantiation. For each (shape, rows) a graph of one call per weight copy is replayed
+between two HIP events on the backend's stream; achieved = the dominant call's algorithmic bytes per launch / its
+launch time, against the 8 TB/s HBM peak (all_calls_*: the same over all 6 calls). traffic: that call's HBM bytes
+per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --pmc-pass`, calibrated on a copy of known
+size (profiles/gemv_layer_projections_traffic_pmc.md).
 cpu_baseline: the reference engine's own CPU matmul_nvfp4 (oracle/_ref, compiled from the reference sources)
 on the same shapes and inputs on this host's cores, or the oracle restatement when that library is absent.
 """
@@ -900,8 +900,9 @@ def main():
         kb["s"] += t["ms"] / 1e3
         kb["calls"].append(key)
     all_achieved = tot_bytes / tot_s / 1e9
-    dominant = max(by_kernel, key=lambda k: by_kernel[k]["bytes"])
-    achieved = by_kernel[dominant]["bytes"] / by_kernel[dominant]["s"] / 1e9
+    dom_call = max(per_call, key=lambda k: per_call[k]["bytes"])   # the launch that moves the most bytes
+    dominant = per_call[dom_call]["kernel"]
+    achieved = per_call[dom_call]["gbs"]
     traffic = measured_traffic()
     if traffic:
         for key, v in per_call.items():
@@ -912,10 +913,10 @@ def main():
         keys = ["%s_m%d" % (name, m) for name, _ in SHAPES]
         by_m["m%d" % m] = round(sum(per_call[k]["bytes"] for k in keys) /
                                 sum(per_call[k]["us_per_launch"] for k in keys) / 1e3, 1)
-    log("GEMV: dominant kernel %s (%s, %.0f%% of the step's bytes, %.0f%% of its kernel time) %.1f GB/s (%.1f%% "
+    log("GEMV: dominant launch %s (%s, %.0f%% of the step's bytes, %.0f%% of its kernel time) %.1f GB/s (%.1f%% "
         "of HBM peak); all 6 calls %.1f GB/s (%.1f%%); M=1 %.1f, M=8 %.1f GB/s"
-        % (dominant, " + ".join(by_kernel[dominant]["calls"]), 100 * by_kernel[dominant]["bytes"] / tot_bytes,
-           100 * by_kernel[dominant]["s"] / tot_s, achieved,
+        % (dominant, dom_call, 100 * per_call[dom_call]["bytes"] / step_bytes,
+           100 * per_call[dom_call]["us_per_launch"] / sum(v["us_per_launch"] for v in per_call.values()), achieved,
            achieved / HBM_PEAK_GBS * 100, all_achieved, all_achieved / HBM_PEAK_GBS * 100, by_m["m1"], by_m["m8"]))
     for k, v in per_call.items():
         log("  %-22s %7.3f us  %7.1f GB/s" % (k, v["us_per_launch"], v["gbs"]))
@@ -977,14 +978,15 @@ def main():
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     # the dominant kernel's HBM bytes per launch (the mean over its calls, as achieved is);
-                     # per-call values in config.per_call
-                     "traffic": (int(sum(per_call[k]["traffic"] for k in by_kernel[dominant]["calls"]) /
-                                     len(by_kernel[dominant]["calls"]))
-                                 if all("traffic" in per_call[k] for k in by_kernel[dominant]["calls"]) else None),
-                     "kernel": dominant, "kernel_calls": by_kernel[dominant]["calls"],
-                     "kernel_byte_share": round(by_kernel[dominant]["bytes"] / tot_bytes, 4),
-                     "kernel_time_share": round(by_kernel[dominant]["s"] / tot_s, 4),
+                     # the dominant launch's HBM bytes (per-call values in config.per_call)
+                     "traffic": per_call[dom_call].get("traffic"),
+                     "kernel": dominant, "call": dom_call, "bytes_per_launch": per_call[dom_call]["bytes"],
+                     "us_per_launch": per_call[dom_call]["us_per_launch"],
+                     "byte_share": round(per_call[dom_call]["bytes"] / step_bytes, 4),
+                     "by_kernel": {k: {"calls": v["calls"], "gbs": round(v["bytes"] / v["s"] / 1e9, 1),
+                                       "frac": round(v["bytes"] / v["s"] / 1e9 / HBM_PEAK_GBS, 4),
+                                       "byte_share": round(v["bytes"] / tot_bytes, 4)}
+                                   for k, v in by_kernel.items()},
                      "all_calls_achieved": round(all_achieved, 1),
                      "all_calls_frac": round(all_achieved / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
