@@ -692,7 +692,9 @@ GemvShape gemv_shape(int kt, const int* nbs, int nw, int m, bool raw) {
     // (with one row-block) only where K needs them (16 waves at most per work-group)
     int nb = 0;
     for (int i = 0; i < nw; ++i) nb += nbs[i];
-    int r = nb >= 512 ? 4 : 2;
+    // (one row-block per wave where the launch fits one work-group per CU: 3072 x 3072 at M = 4 / 8, 4.96 / 5.46
+    // -> 4.42 / 4.74 us)
+    int r = nb <= 256 ? 1 : nb >= 512 ? 4 : 2;
     const int t = (kt + 1) / 2 <= 16 ? 2 : 4;
     // one or two rows on the block-scaled op (measured the same way over configs 0 and 1): one row-block per wave
     // while the launch fits one work-group per CU, four where two would leave the CUs unevenly loaded (512 < nb <
