@@ -7,10 +7,12 @@ fused gate/up (2 x N=8192, K=3072, one launch) and down (N=3072, K=8192) -- each
 builds its matrix-core operand from the rows itself. Weights follow the
 benchmark distributions (uniform E2M1 codes, |N(0,1)|*0.05 E4M3 scales, tensor scale 1.0); activations are unit
 BF16 rows. Consecutive calls read different copies of their weights, rotating over >= 1 GiB, so every launch
-streams from HBM rather than from the 256 MB Infinity Cache. Steps are replayed from HIP graphs (one per
-rotation phase), so host launch cost does not set the pace.
+streams from HBM rather than from the 256 MB Infinity Cache. The steps are replayed from a HIP graph, so host launch
+cost does not set the pace.
 
-value: whole-step algorithmic bytes / wall time per step (GB/s), inputs resident in HBM.
+value: whole-step algorithmic bytes / device time per step (GB/s), inputs resident in HBM: the K timed steps are one
+graph launch bracketed by HIP events on the backend's stream (host_ms_per_step: the wall clock of that launch through
+the final synchronisation, host latency included).
 roofline: the dominant kernel launch, the call (one GEMV launch: a kernel instantiation at one weight shape and row
 count) that moves the most bytes of the step -- an instantiation can serve calls of different sizes (QKV and
 gate/up at M=1 share one), and a roofline over a mixture of launch sizes describes none of them; by_kernel gives
@@ -562,6 +564,91 @@ def prefill_run(pkg, hip, dev, w, rng, prompts):
     return out
 
 
+def nvfp4_bytes(n, k):
+    """Codes, E4M3 scales and the tensor scale of an n x k NVFP4 weight."""
+    return n * k // 2 + n * k // 16 + 4
+
+
+def attn_splits(c, ctx, ring):
+    """The key splits the attention step's plan takes for one row (attn_plan in csrc/attention.hip: about 192
+    work-groups, four waves of 32-slot tiles each, at least two tiles per wave on a cache by position and one on a
+    ring)."""
+    tiles = -(-ring // 32) if ring else -(-ctx // 32)
+    mt = 1 if ring else 2
+    want = max(1, 192 // c["kv_heads"])
+    return max(1, min(want, -(-tiles // (mt * 4)), tiles))
+
+
+def decode_launches(w, wl, launches, ctx, fp8=False):
+    """Per-launch algorithmic bytes and GB/s of one eager one-row step, from its launches in queue order (the fused
+    one-token path: the input row's operand, then per attention sublayer the q/k/v/g projection, the attention step
+    (producer and scan), the gate by heads and the o-projection, per MLP sublayer gate/up and down, then the head).
+    Bytes per launch: the NVFP4 weights a projection streams plus its FP32 rows in and out; the attention step, the
+    keys and values it must read (every position of a global cache, the window's of a ring) plus q / k / v in and its
+    split partials out; the gate, those partials plus the gate rows in and the heads out."""
+    c = w.cfg
+    H, F, V = c["hidden"], c["ffn"], c["vocab"]
+    d, kvh, heads = c["head_dim"], c["kv_heads"], c["heads"]
+    Q, KV = heads * d, kvh * d
+    per_key = kvh * ((2 * d + 8 + 4) if fp8 else (2 * d * 2 + 4))   # K, V (and FP8 scales), slot position
+    roles = []   # (role, bytes) per launch
+    li = 0
+    seq = list(launches)
+    i = 0
+
+    def take(prefix):
+        nonlocal i
+        assert i < len(seq) and seq[i][0].startswith(prefix), (i, prefix, seq[i:i + 3])
+        i += 1
+        return seq[i - 1]
+
+    def add(role, b):
+        roles.append((role, b, seq[i - 1][0], seq[i - 1][1]))
+
+    if seq and seq[0][0].startswith("prep_x"):
+        take("prep_x")
+        add("input operand", 4 * H * 2)
+    for kind in w.kinds:
+        if kind == wl.MLP:
+            take("gemv")
+            add("gate/up", 2 * nvfp4_bytes(F, H) + 4 * H * 4 + 4 * F)
+            take("gemv")
+            add("down", nvfp4_bytes(H, F) + 4 * F + 4 * H * 2)
+            continue
+        take("gemv")
+        add("q/k/v/g", nvfp4_bytes(2 * Q + 2 * KV, H) + 4 * H * 4 + 4 * (2 * Q + 2 * KV))
+        ring = c["ring_slots"] if kind == wl.SLIDING else 0
+        visible = min(ctx, c["window"]) if ring else ctx
+        part = (attn_splits(c, ctx, ring) + 1) * heads * (d + 2) * 4
+        while i < len(seq) and not seq[i][0].startswith(("attn_gate", "gemv")):
+            name = seq[i][0]
+            take("")
+            add("attention (global)" if not ring else "attention (ring)",
+                visible * per_key + 4 * (Q + 2 * KV) + part if name.startswith("attn_step") else 0)
+        take("attn_gate")
+        add("gate", part + 4 * Q * 2)
+        take("gemv")
+        add("o", nvfp4_bytes(H, Q) + 4 * Q + 4 * H * 2)
+    take("gemv")
+    add("head", nvfp4_bytes(V, H) + 4 * H * 4 + 4 * V * 2)
+    assert i == len(seq), seq[i:]
+    out = {}
+    for role, b, name, ms in roles:
+        r = out.setdefault(role, {"launches": 0, "us": 0.0, "bytes": 0, "kernels": []})
+        r["launches"] += 1
+        r["us"] += ms * 1e3
+        r["bytes"] += b
+        if name not in r["kernels"]:
+            r["kernels"].append(name)
+    for r in out.values():
+        r["us_per_launch"] = round(r["us"] / r["launches"], 3)
+        r["bytes_per_launch"] = r["bytes"] // r["launches"]
+        r["gbs"] = round(r["bytes"] / r["us"] / 1e3, 1) if r["us"] > 0 else None
+        r["frac"] = round(r["bytes"] / r["us"] / 1e3 / HBM_PEAK_GBS, 4) if r["us"] > 0 else None
+        r["us"] = round(r["us"], 1)
+    return out
+
+
 def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
     """The synthetic 4B-shaped looped-nGPT decode step (random-init NVFP4 weights, BF16 KV), one decode
     row (M=1) and one 8-row verify step per context, each captured as a HIP graph and replayed. The caches hold a
@@ -622,10 +709,21 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
                               "hbm_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1)}
         res["tok_s"] = res["m1"]["rows_per_s"]
         res["step_bytes_m1"] = w.weight_bytes() + kv_step[ctx]
+        # one eager one-row step with every launch timed by events: per-launch bytes and GB/s by role
+        dev.forward(dx, 1, ctx, dl)
+        hip.finish()
+        hip.profile(True, launches=True)
+        dev.forward(dx, 1, ctx, dl)
+        _, seq = hip.profile_report(launches=True)
+        hip.profile(False)
+        res["launches_m1"] = decode_launches(w, wl, seq, ctx)
         results["ctx%d" % ctx] = res
         log("decode ctx %5d: M=1 %.3f ms/token (%.0f tok/s, %.0f GB/s), M=8 verify %.3f ms/step (%.0f rows/s)"
             % (ctx, res["m1"]["ms_per_step"], res["tok_s"], res["m1"]["hbm_gbs"], res["m8"]["ms_per_step"],
                res["m8"]["rows_per_s"]))
+        log("  eager step by launch: " + ", ".join(
+            "%s %d x %.2f us %.0f GB/s" % (r, v["launches"], v["us_per_launch"], v["gbs"] or 0)
+            for r, v in res["launches_m1"].items()))
     # per-kernel breakdown of one eager step at the largest context (events around every launch)
     hip.profile(True)
     dev.forward(dx, 1, ctx_max, dl)
@@ -665,6 +763,11 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
         kv8 = kv_step[ctx] // 2 + kv_step[ctx] // (2 * d) * 4   # 1-byte codes + a 4-byte scale per (row, head)
         fp8["ctx%d" % ctx] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1), "kv_bytes": kv8,
                               "hbm_gbs": round((w.weight_bytes() + kv8) / (ms / 1e3) / 1e9, 1)}
+        hip.profile(True, launches=True)
+        dev8.forward(dx, 1, ctx, dl)
+        _, seq = hip.profile_report(launches=True)
+        hip.profile(False)
+        fp8["ctx%d" % ctx]["launches_m1"] = decode_launches(w8, wl, seq, ctx, fp8=True)
         log("decode ctx %5d, FP8 caches: M=1 %.3f ms/token (%.0f tok/s)" % (ctx, ms, 1e3 / ms))
     if dev8:
         # per-kernel breakdown of one eager FP8 step at the largest context (events around every launch)
@@ -834,29 +937,39 @@ def main():
     calls = [(name, m) for m in ROWS for name, _ in SHAPES]
     step_bytes = sum(call_bytes(dict(SHAPES)[name], m) for name, m in calls)
 
-    # one graph per rotation phase p: call i of the step reads copy (6 p + i) mod copies
+    # The timed steps as one HIP graph: step s's call i reads weight copy (6 s + i) mod copies, so consecutive
+    # launches stream different copies; the warm-up steps are a graph of their own, the same way.
     for name, m in calls:   # size the scratch before capturing
         hip.matmul_dev(sets[0][name], dx[(name, m)], pkg.X_BF16, m, dy)
     hip.finish()
-    phases = []
-    for p in range(copies):
-        hip.graph_begin()
-        for i, (name, m) in enumerate(calls):
-            hip.matmul_dev(sets[(len(calls) * p + i) % copies][name], dx[(name, m)], pkg.X_BF16, m, dy)
-        phases.append(hip.graph_end("step_phase%d" % p))
 
-    for s in range(args.warmup):
-        hip.graph_launch(phases[s % copies])
+    def steps_graph(first, n, label):
+        hip.graph_begin()
+        for st in range(first, first + n):
+            for i, (name, m) in enumerate(calls):
+                hip.matmul_dev(sets[(len(calls) * st + i) % copies][name], dx[(name, m)], pkg.X_BF16, m, dy)
+        return hip.graph_end(label)
+
+    warm = steps_graph(0, max(1, args.warmup), "warmup_steps")
+    timed = steps_graph(max(1, args.warmup), args.steps, "timed_steps")
+    hip.graph_launch(warm)
     hip.finish()
+    # device time: events on the backend's stream around the one launch of the K steps (launch gaps between the
+    # step's kernels included; host launch and synchronisation latency not); the wall clock of the same launch
+    # through hip.finish() beside it
+    hip.profile(True)
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        hip.graph_launch(phases[s % copies])
+    hip.graph_launch(timed)
     hip.finish()
-    el = time.perf_counter() - t0
+    el_host = time.perf_counter() - t0
+    el = hip.profile_report()["timed_steps"]["ms"] / 1e3
+    hip.profile(False)
+    hip.graph_destroy(warm)
+    hip.graph_destroy(timed)
     ms_per_step = el / args.steps * 1e3
     value = step_bytes / (el / args.steps) / 1e9
-    log("timed %d steps: %.4f ms/step, %.1f GB/s whole-step (%.1f%% of HBM peak)"
-        % (args.steps, ms_per_step, value, value / HBM_PEAK_GBS * 100))
+    log("timed %d steps: %.4f ms/step by device events (%.4f ms/step wall clock), %.1f GB/s whole-step (%.1f%% of "
+        "HBM peak)" % (args.steps, ms_per_step, el_host / args.steps * 1e3, value, value / HBM_PEAK_GBS * 100))
 
     # roofline: per-call graphs (one GEMV launch per weight copy, the step's own kernel), timed by events
     per_call = {}
@@ -961,6 +1074,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "host_ms_per_step": round(el_host / args.steps * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -971,7 +1085,7 @@ def main():
                         "2x8192 K=3072, down N=3072 K=8192, each at M=1 and M=8 (6 calls per step, one GEMV launch "
                         "each that builds its operand from the rows; BF16 unit-row activations, FP32 out); weights "
                         "rotated over %d copies (%.2f GiB) so each "
-                        "call reads HBM; steps replayed from HIP graphs" % (copies, copies * set_bytes / 2 ** 30),
+                        "call reads HBM; the timed steps one HIP graph, timed by device events" % (copies, copies * set_bytes / 2 ** 30),
             "step_bytes": step_bytes,
             "gemv_gbs_by_rows": by_m,
             "per_call": per_call,

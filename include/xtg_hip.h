@@ -170,15 +170,17 @@ typedef struct xtg_attn_args {
 /* Replaces xtg::attention(ThreadPool&, const AttnArgs&) (kv.h:79, kv.cpp:166-286): causal GQA attention of the
  * call's n_q rows over the cached positions before pos0 plus the call's own keys; window > 0 limits a row at t to
  * keys t - window + 1 .. t. The cache is read only; which slots a row sees is decided from the positions stored
- * in them (for a ring: npu/xtg_npu.cpp:236-258). Queued. head_dim 64 or 128, at most 8 q heads per KV head. */
+ * in them (for a ring: npu/xtg_npu.cpp:236-258). Queued. head_dim 64, 128 or 256, at most 8 q heads per KV head. */
 int xtg_hip_attention(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len);
 /* No counterpart in the reference: xtg_hip_attention for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and results; it
  * allocates nothing: the split partials go to one fixed device array of XTG_HIP_ATTN_SCRATCH_BYTES per device, held
- * from the library's load until the process ends, and no profiling events are made. A call whose partials exceed it
- * fails (-1, the sizes in err) before anything is queued: decode and verify calls fit (8 rows over 8 KV heads of 128
- * take about 2 MB), long prefill chunks may not. Every such call on a device shares that array, so calls that overlap
- * on one device (two backends' streams) race; calls queued on one backend's stream run in order. */
+ * from the library's load until the process ends (profiling events are made only while xtg_hip_profile is on). A
+ * call whose partials exceed the array fails (-1, the sizes in err) before anything is queued: decode and verify
+ * calls fit (8 rows over 8 KV heads of 128 take about 2 MB), long prefill chunks may not. The array belongs to the
+ * first backend (xtg_hip handle) that calls this on the device, until that backend is closed; a call from another
+ * backend on the same device meanwhile fails (-1), since their calls would race on the one array. Calls queued on
+ * the owning backend's stream run in order; each rewrites every partial it reads. */
 #define XTG_HIP_ATTN_SCRATCH_BYTES (16u << 20)
 int xtg_hip_attention_noalloc(xtg_hip* h, const xtg_attn_args* a, char* err, int err_len);
 
@@ -326,11 +328,13 @@ void xtg_hip_graph_destroy(xtg_hip* h, xtg_hip_graph* g);
 /* ---------------------------------------------------------------------------------------------- profiling */
 
 /* Replaces the XTG_GPU_PROFILE switch of the OpenCL backend (opencl.cpp:293-315, :391-392): with enable != 0
- * every kernel the backend queues is bracketed by two events on its stream. */
+ * every kernel the backend queues is bracketed by two events on its stream; enable == 2 also keeps every launch's
+ * time in queue order for the report. */
 int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len);
 /* Waits for queued work and writes {"kernels": {name: {"calls": n, "ms": total}}} for the launches recorded since
- * the last report (names as rocprof prints them, without the namespace), then starts over. Returns the length
- * (without the NUL), or -1. */
+ * the last report (names as rocprof prints them, without the namespace), with "launches": [[name, ms], ...] in
+ * queue order after enable == 2, then starts over. Returns the length (without the NUL), or -1; a report longer
+ * than out_len is cut (and its records are gone). */
 int xtg_hip_profile_report(xtg_hip* h, char* out, int out_len);
 
 #ifdef __cplusplus

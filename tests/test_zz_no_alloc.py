@@ -4,8 +4,10 @@ the C ABI. Bar: equal bit for bit (integer-exact agreement is expected: the same
 
 - Two calls in a row, the second smaller (a global cache at a 4K context with an 8-row verify step, then a 1088-slot
   ring read by one row), so the second runs on what the first left in the shared array; FP8 caches as well.
-- A fresh backend, whose own attention scratch was never sized, captures the call into a HIP graph and replays it.
-- A call whose partials exceed the array is refused before anything is queued.
+- A fresh backend, whose own attention scratch was never sized, captures the call into a HIP graph and replays it
+  (first in this file: the array then belongs to that backend until it is closed).
+- A call whose partials exceed the array is refused before anything is queued; so is a call from a second open
+  backend on the device while the first holds the array (their calls would race on it).
 """
 import numpy as np
 import pytest
@@ -41,26 +43,8 @@ def run(b, fn, case, ctx, n_q, window):
     return out.numpy()
 
 
-@pytest.mark.parametrize("dtype", [0, 1])
-def test_noalloc_matches_attention_two_calls(hip, dtype):
-    rng = np.random.default_rng(700 + dtype)
-    big = make_case(hip, rng, 4096, 8, dtype=dtype)
-    small = make_case(hip, rng, 40000, 1, ring=1088, dtype=dtype)
-    got_big = run(hip, hip.attention_noalloc, big, 4096, 8, 0)
-    got_small = run(hip, hip.attention_noalloc, small, 40000, 1, 1024)   # right after, on the same array
-    want_big = run(hip, hip.attention, big, 4096, 8, 0)
-    want_small = run(hip, hip.attention, small, 40000, 1, 1024)
-    assert np.isfinite(got_big).all() and np.isfinite(got_small).all()
-    np.testing.assert_array_equal(got_big, want_big)
-    np.testing.assert_array_equal(got_small, want_small)
-    for cache, arrays in (big, small):
-        cache.destroy()
-        for a in arrays:
-            a.free()
-
-
 def test_noalloc_under_graph_capture(pkg):
-    b = pkg.HipBackend(0)   # its attention scratch has never been sized
+    b = pkg.HipBackend(0)   # its attention scratch has never been sized; it holds the device's array until closed
     try:
         rng = np.random.default_rng(701)
         case = make_case(b, rng, 2048, 8)
@@ -82,6 +66,24 @@ def test_noalloc_under_graph_capture(pkg):
         b.close()
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_noalloc_matches_attention_two_calls(hip, dtype):
+    rng = np.random.default_rng(700 + dtype)
+    big = make_case(hip, rng, 4096, 8, dtype=dtype)
+    small = make_case(hip, rng, 40000, 1, ring=1088, dtype=dtype)
+    got_big = run(hip, hip.attention_noalloc, big, 4096, 8, 0)
+    got_small = run(hip, hip.attention_noalloc, small, 40000, 1, 1024)   # right after, on the same array
+    want_big = run(hip, hip.attention, big, 4096, 8, 0)
+    want_small = run(hip, hip.attention, small, 40000, 1, 1024)
+    assert np.isfinite(got_big).all() and np.isfinite(got_small).all()
+    np.testing.assert_array_equal(got_big, want_big)
+    np.testing.assert_array_equal(got_small, want_small)
+    for cache, arrays in (big, small):
+        cache.destroy()
+        for a in arrays:
+            a.free()
+
+
 def test_noalloc_refuses_more_than_its_scratch(hip, pkg):
     """512 rows over 8 KV heads of 128 (64 row blocks) need about 17 MB of partials: more than the 16 MiB array."""
     rng = np.random.default_rng(702)
@@ -92,3 +94,28 @@ def test_noalloc_refuses_more_than_its_scratch(hip, pkg):
     cache.destroy()
     for a in (q, k, v, out):
         a.free()
+
+
+def test_noalloc_refuses_a_second_backend(hip, pkg):
+    """While the session's backend holds the device's array (its call claims it), a second open backend's call is
+    refused before anything is queued; the holder's calls still run and match xtg_hip_attention."""
+    rng = np.random.default_rng(703)
+    mine = make_case(hip, rng, 1024, 1)
+    got = run(hip, hip.attention_noalloc, mine, 1024, 1, 0)
+    b = pkg.HipBackend(0)
+    try:
+        other = make_case(b, rng, 1024, 1)
+        cache, (q, k, v, out) = other
+        with pytest.raises(pkg.XtgError, match="another open backend"):
+            b.attention_noalloc(cache, q, k, v, out, 1, 1024, HEADS)
+        np.testing.assert_array_equal(run(hip, hip.attention_noalloc, mine, 1024, 1, 0), got)
+        np.testing.assert_array_equal(run(hip, hip.attention, mine, 1024, 1, 0), got)
+        cache.destroy()
+        for a in other[1]:
+            a.free()
+    finally:
+        b.close()
+    for c, arrays in (mine,):
+        c.destroy()
+        for a in arrays:
+            a.free()

@@ -352,17 +352,22 @@ class HipBackend:
     def graph_destroy(self, g):
         lib().xtg_hip_graph_destroy(self.h, g)
 
-    def profile(self, enable=True):
+    def profile(self, enable=True, launches=False):
+        """Per-kernel event timing on (launches: also every launch's time in queue order) or off."""
         err = _errbuf()
-        _check(lib().xtg_hip_profile(self.h, 1 if enable else 0, err, len(err)), err)
+        _check(lib().xtg_hip_profile(self.h, (2 if launches else 1) if enable else 0, err, len(err)), err)
 
-    def profile_report(self):
-        """{kernel name: {"calls": n, "ms": total}} since the last report (waits for queued work)."""
-        buf = ctypes.create_string_buffer(1 << 16)
+    def profile_report(self, launches=False):
+        """{kernel name: {"calls": n, "ms": total}} since the last report (waits for queued work); with launches,
+        also the list [(name, ms), ...] of every launch in queue order (profiling turned on with launches=True)."""
+        buf = ctypes.create_string_buffer(1 << 22)
         n = lib().xtg_hip_profile_report(self.h, buf, len(buf))
         if n < 0 or n >= len(buf):
             raise XtgError("profile report failed")
-        return json.loads(buf.value.decode())["kernels"]
+        rep = json.loads(buf.value.decode())
+        if launches:
+            return rep["kernels"], [tuple(x) for x in rep.get("launches", [])]
+        return rep["kernels"]
 
     def array(self, a=None, shape=None, dtype=np.float32):
         """A device buffer owned by this backend, filled from the numpy array a (or left unset)."""

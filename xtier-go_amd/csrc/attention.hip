@@ -1539,6 +1539,27 @@ void* attn_scratch_ptr(int device) {
   return ptrs[size_t(device)];
 }
 
+namespace {
+std::mutex scratch_mu;
+std::vector<const void*> scratch_owner;   // per device: the backend holding the array, or NULL
+}  // namespace
+
+bool attn_scratch_claim(int device, const void* owner) {
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  XTG_CHECK(device >= 0 && owner, "attention scratch: device %d", device);
+  if (size_t(device) >= scratch_owner.size()) scratch_owner.resize(size_t(device) + 1, nullptr);
+  const void*& o = scratch_owner[size_t(device)];
+  if (o && o != owner) return false;
+  o = owner;
+  return true;
+}
+
+void attn_scratch_let_go(int device, const void* owner) {
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (device >= 0 && size_t(device) < scratch_owner.size() && scratch_owner[size_t(device)] == owner)
+    scratch_owner[size_t(device)] = nullptr;
+}
+
 // ------------------------------------------------------------------------------------------------- launchers
 
 // The RoPE rows of positions 0 .. n_pos - 1: (cos, sin) of the angle FP32(pos) * inv_freq[i] (engine/src/

@@ -70,6 +70,11 @@ std::string launch_attn_merge(const AttnPlan& p, int n_q, int heads, const float
 // is its device address on `device`, which must be the current device; the first call per device looks it up.
 constexpr size_t kAttnScratchBytes = size_t(16) << 20;
 void* attn_scratch_ptr(int device);
+// The array of a device belongs to one backend at a time: the first that claims it keeps it until it lets go (at
+// its close), and a claim from another backend on that device is refused (false), since their calls would race on
+// the one array. Claiming again from the holder succeeds.
+bool attn_scratch_claim(int device, const void* owner);
+void attn_scratch_let_go(int device, const void* owner);
 
 constexpr int kProdRows = 8, kProdGroup = 8;   // the producer's rows per call and q heads per KV head
 

@@ -22,6 +22,7 @@ Backend::Backend(int device) : device_(device) {
 Backend::~Backend() {
   // teardown: errors cannot be reported from a destructor; every release is still attempted
   (void)hipSetDevice(device_);
+  attn_scratch_let_go(device_, this);
   if (capturing_) {
     hipGraph_t g = nullptr;
     (void)hipStreamEndCapture(stream_, &g);
@@ -537,10 +538,15 @@ void Backend::attention_noalloc(const DevKv* c, int n_q, long long pos0, int hea
             "attention_noalloc: %d rows over %d KV heads (%d key splits) need %zu bytes of partials; the fixed scratch "
             "holds %zu",
             n_q, c->kv_heads, p.splits, need, kAttnScratchBytes);
+  XTG_CHECK(attn_scratch_claim(device_, this),
+            "attention_noalloc: another open backend on device %d uses the device's fixed scratch (calls from two "
+            "backends would race on it); close that backend first",
+            device_);
   float* part = static_cast<float*>(attn_scratch_);
-  launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_);
-  if (p.splits > 0) launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_);
-  launch_attn_merge(p, n_q, heads, part, out, stream_);
+  timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_); });
+  if (p.splits > 0)
+    timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_); });
+  timed([&] { return launch_attn_merge(p, n_q, heads, part, out, stream_); });
 }
 
 void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
@@ -711,10 +717,11 @@ hipEvent_t Backend::event() {
   return e;
 }
 
-void Backend::set_profile(bool on) {
+void Backend::set_profile(int mode) {
   XTG_CHECK(!capturing_, "profile: not during graph capture");
-  if (!on && profile_) profile_report();   // settle what was recorded
-  profile_ = on;
+  XTG_CHECK(mode >= 0 && mode <= 2, "profile: mode %d (0 off, 1 totals, 2 totals and the launch sequence)", mode);
+  if (profile_ && mode != profile_) profile_report();   // settle what was recorded
+  profile_ = mode;
 }
 
 void Backend::graph_begin() {
@@ -769,15 +776,27 @@ std::string Backend::profile_report() {
     if (it == totals_.end()) it = totals_.insert(totals_.end(), {p.name, Total{}});
     it->second.calls += 1;
     it->second.ms += ms;
-    free_events_.push_back(p.a);
-    free_events_.push_back(p.b);
   }
-  pending_.clear();
   std::string s = "{\"kernels\": {";
   for (size_t i = 0; i < totals_.size(); ++i)
     s += strf("%s\"%s\": {\"calls\": %ld, \"ms\": %.6f}", i ? ", " : "", totals_[i].first.c_str(),
               totals_[i].second.calls, totals_[i].second.ms);
-  s += "}}";
+  s += "}";
+  if (profile_ == 2) {   // every launch in queue order
+    s += ", \"launches\": [";
+    for (size_t i = 0; i < pending_.size(); ++i) {
+      float ms = 0;
+      HIP_CHECK(hipEventElapsedTime(&ms, pending_[i].a, pending_[i].b));
+      s += strf("%s[\"%s\", %.6f]", i ? ", " : "", pending_[i].name.c_str(), ms);
+    }
+    s += "]";
+  }
+  s += "}";
+  for (const Pending& p : pending_) {
+    free_events_.push_back(p.a);
+    free_events_.push_back(p.b);
+  }
+  pending_.clear();
   totals_.clear();
   return s;
 }

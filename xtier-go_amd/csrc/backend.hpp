@@ -78,8 +78,9 @@ class Backend {
   // attention(pool, AttnArgs) (kv.h:64-79) over a device cache; q / k / v / out are device memory
   void attention(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                  const float* k, const float* v, float* out);
-  // The same with the split partials in the device's fixed scratch (attn_scratch_ptr): allocates nothing, creates no
-  // profiling events; refuses a call whose partials exceed kAttnScratchBytes.
+  // The same with the split partials in the device's fixed scratch (attn_scratch_ptr): allocates nothing (profiling
+  // events only while profiling is on); refuses a call whose partials exceed kAttnScratchBytes, and calls while
+  // another open backend on the device holds the array (attn_scratch_claim: the first caller keeps it until closed).
   void attention_noalloc(const DevKv* c, int n_q, long long pos0, int heads, int window, float scale, const float* q,
                          const float* k, const float* v, float* out);
   // The attention half of a Dory sublayer (packs/dory/dory.cpp:482-515) on device rows q [m][heads][d],
@@ -128,10 +129,10 @@ class Backend {
   std::string info_json() const;
   size_t weight_bytes() const { return weight_bytes_; }
 
-  // Per-kernel device time (the reference's XTG_GPU_PROFILE, opencl.cpp:293-315): with profiling on, every
-  // launch is bracketed by two events on the stream; report() waits, sums the durations per kernel name and
-  // starts over.
-  void set_profile(bool on);
+  // Per-kernel device time (the reference's XTG_GPU_PROFILE, opencl.cpp:293-315): with profiling on (mode 1, or 2
+  // to list every launch in queue order as well), every launch is bracketed by two events on the stream; report()
+  // waits, sums the durations per kernel name and starts over.
+  void set_profile(int mode);
   std::string profile_report();
 
   // HIP graphs over the backend's stream: begin/end capture every launch queued in between into one graph,
@@ -178,7 +179,7 @@ class Backend {
     std::string name;
     hipEvent_t a, b;
   };
-  bool profile_ = false;
+  int profile_ = 0;
   bool capturing_ = false;
   std::unordered_map<hipGraphExec_t, std::string> graphs_;
   std::vector<Pending> pending_;

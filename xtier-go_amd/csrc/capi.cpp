@@ -427,7 +427,7 @@ void xtg_hip_graph_destroy(xtg_hip* h, xtg_hip_graph* g) {
 int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h, "profile: NULL handle");
-    h->b->set_profile(enable != 0);
+    h->b->set_profile(enable == 2 ? 2 : enable != 0 ? 1 : 0);
   });
 }
 

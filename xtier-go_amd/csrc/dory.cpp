@@ -132,8 +132,9 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
   part_h_ = scratch(size_t(kMaxFusedGroups));
   part_a_ = scratch(size_t(c.heads));
   att_ = scratch(size_t(c.heads) * size_t(c.head_dim));
-  // XTG_DECODE_UNFUSED=1 runs one-token steps on the separate norm launches (the prefill path's), for comparison
-  fused_ = !std::getenv("XTG_DECODE_UNFUSED");
+  // XTG_DECODE_UNFUSED=1 runs one-token steps on the separate norm launches (the prefill path's), for comparison;
+  // so do models whose shapes some fused projection is not made for
+  fused_ = !std::getenv("XTG_DECODE_UNFUSED") && fused_unsupported().empty();
   input_ = scratch(R * H);
   state_ = scratch(R * H);
   proj_ = scratch(R * size_t(2 * Q + 2 * KV));
@@ -152,6 +153,52 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
     const std::vector<uint8_t> zeros(xop_bytes(H), 0);
     b_.write(op_lin_, 0, zeros.data(), zeros.size());
   }
+}
+
+std::string DorySession::fused_unsupported() {
+  // every launch sublayer_decode and head can make, with the most records any producer of a slerp leaves (the o and
+  // down projections), checked before the first step rather than thrown on it
+  auto desc = [&](const xtg_nvfp4* ws, int nw, int in, int out, int groups) {
+    FusedGemv f;
+    f.c.nw = nw;
+    for (int i = 0; i < nw; ++i) f.c.w[i] = &b_.prepare(ws[i]);
+    f.c.m = 1;
+    f.c.k = ws[0].k;
+    f.in = in;
+    f.out = out;
+    f.in_groups = groups;
+    return f;
+  };
+  int slerp_groups = 1;
+  for (const Layer& L : layers_) {
+    const bool mlp = L.w.kind == XTG_DORY_MLP;
+    const FusedGemv p = desc(mlp ? &L.w.down : &L.w.o, 1, kInNorm, kOutSlerp, 1);
+    slerp_groups = std::max(slerp_groups, fused_gemv_groups(p));
+  }
+  std::string why;
+  auto check = [&](const FusedGemv& f, const char* what) {
+    if (!why.empty()) return;
+    const std::string w = fused_gemv_unsupported(f);
+    if (!w.empty()) why = strf("%s: %s", what, w.c_str());
+  };
+  for (const Layer& L : layers_) {
+    if (L.w.kind == XTG_DORY_MLP) {
+      const xtg_nvfp4 gu[2] = {L.w.gate, L.w.up};
+      int groups = 0;
+      for (int in : {kInOp, kInSlerp}) {   // the first projection of a step, or one after a slerp
+        const FusedGemv f = desc(gu, 2, in, kOutSwiglu, in == kInSlerp ? slerp_groups : 0);
+        check(f, "gate/up");
+        groups = std::max(groups, fused_gemv_groups(f));
+      }
+      check(desc(&L.w.down, 1, kInNorm, kOutSlerp, groups), "down");
+    } else {
+      const xtg_nvfp4 qkvg[4] = {L.w.q, L.w.k, L.w.v, L.w.g};   // after a prepared operand: the plain GEMV
+      check(desc(qkvg, 4, kInSlerp, kOutPlain, slerp_groups), "q/k/v/g");
+      check(desc(&L.w.o, 1, kInNorm, kOutSlerp, c_.heads), "o");
+    }
+  }
+  if (head_.codes) check(desc(&head_, 1, kInSlerp, kOutPlain, slerp_groups), "head");
+  return why;
 }
 
 void DorySession::release_all() {

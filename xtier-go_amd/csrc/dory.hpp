@@ -4,6 +4,7 @@
 // can be captured into one HIP graph.
 #pragma once
 
+#include <string>
 #include <vector>
 
 #include "backend.hpp"
@@ -61,6 +62,9 @@ class DorySession {
   float* upload(const float* v, size_t n);
   void build(const xtg_dory_layer* layers, const float* logit_scale);
   void prepare(const xtg_nvfp4& w);
+  // why some projection of a one-token step has no fused launch for this model's shapes ("" when all have one): such
+  // a model's one-token steps take the separate norm launches
+  std::string fused_unsupported();
   void release_all();
 
   Backend& b_;

@@ -1190,25 +1190,44 @@ int fused_gemv_groups(const FusedGemv& f) {
   return wgs;
 }
 
+std::string fused_gemv_unsupported(const FusedGemv& f) {
+  const GemvCall& c = f.c;
+  if (c.nw < 1 || c.nw > 4) return strf("%d weights (1..4)", c.nw);
+  if (c.m != 1) return strf("%d rows (one)", c.m);
+  const int kt = c.w[0]->kt;
+  for (int i = 0; i < c.nw; ++i)
+    if (c.w[i]->kt != kt) return "input widths differ";
+  if (f.out == kOutSwiglu && (c.nw != 2 || c.w[0]->n != c.w[1]->n)) return "SwiGLU pairs two weights of one shape";
+  if (f.out == kOutSlerp && c.nw != 1) return "slerp records come from one weight";
+  if (f.in != kInOp && (f.in_groups < 1 || f.in_groups > kMaxFusedGroups))
+    return strf("records of %d work-groups (1..%d)", f.in_groups, kMaxFusedGroups);
+  const GemvShape sh = fused_shape(f);
+  if (sh.t != 2 && sh.t != 4) return strf("%d k-tiles per wave (2 or 4)", sh.t);
+  if (sh.s > 16 || sh.s * sh.t < kt)
+    return strf("%d k-tiles at %d per wave need %d waves (at most 16)", kt, sh.t, (kt + sh.t - 1) / sh.t);
+  const int wgs = fused_gemv_groups(f);
+  if (f.in == kInSlerp && (c.k + wgs - 1) / wgs > 64)
+    return strf("x_new of %d inputs over %d work-groups (at most 64 each)", c.k, wgs);
+  if (f.out != kOutPlain && wgs > kMaxFusedGroups)
+    return strf("%d work-groups' records (at most %d)", wgs, kMaxFusedGroups);
+  if (!fused_fn(sh.r, sh.t, sh.s * 64, f.in, f.out))
+    return strf("no kernel for R=%d T=%d (in %d, out %d)", sh.r, sh.t, f.in, f.out);
+  return std::string();
+}
+
 std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   const GemvCall& c = f.c;
-  XTG_CHECK(c.nw >= 1 && c.nw <= 4, "gemv: %d weights (1..4)", c.nw);
-  XTG_CHECK(c.m == 1, "fused gemv: %d rows (one)", c.m);
+  const std::string why = fused_gemv_unsupported(f);
+  XTG_CHECK(why.empty(), "fused gemv: %s", why.c_str());
   XTG_CHECK(f.in == kInNorm || c.xop, "fused gemv: no operand");
-  XTG_CHECK(f.in == kInOp || (f.in_x && f.in_part && f.in_groups > 0 && c.k > 0 && c.k % 16 == 0 &&
-                              (f.in == kInNorm || (f.in_o && f.in_lr))),
+  XTG_CHECK(f.in == kInOp || (f.in_x && f.in_part && c.k > 0 && c.k % 16 == 0 && (f.in == kInNorm || (f.in_o && f.in_lr))),
             "fused gemv: rows, records and width for the input side");
-  XTG_CHECK(f.out != kOutSwiglu || (c.nw == 2 && c.w[0]->n == c.w[1]->n && f.out_sg && f.out_su && f.out_part),
-            "fused gemv: SwiGLU pairs two weights of one shape");
-  XTG_CHECK(f.out != kOutSlerp || (c.nw == 1 && f.out_x && f.out_lr && f.out_part && !c.col_scale[0]),
-            "fused gemv: slerp records come from one weight");
-  XTG_CHECK(f.in == kInOp || f.in_groups <= kMaxFusedGroups, "fused gemv: records of %d work-groups (at most %d)",
-            f.in_groups, kMaxFusedGroups);
+  XTG_CHECK(f.out != kOutSwiglu || (f.out_sg && f.out_su && f.out_part), "fused gemv: SwiGLU scales and records");
+  XTG_CHECK(f.out != kOutSlerp || (f.out_x && f.out_lr && f.out_part && !c.col_scale[0]),
+            "fused gemv: slerp rows and records");
   FusedArgs a{};
   const int kt = c.w[0]->kt;
-  for (int i = 0; i < c.nw; ++i) XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
   const GemvShape sh = fused_shape(f);
-  XTG_CHECK(sh.t == 2 || sh.t == 4, "fused gemv: %d k-tiles per wave", sh.t);
   const int rb = f.out == kOutSwiglu ? sh.r / 2 : sh.r;
   int wgs = 0;
   for (int i = 0; i < c.nw; ++i) {
@@ -1247,14 +1266,8 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   a.out_su = f.out_su;
   a.out_part = f.out_part;
   XTG_CHECK(wgs == fused_gemv_groups(f), "fused gemv: %d work-groups", wgs);
-  XTG_CHECK(f.in != kInSlerp || (c.k + wgs - 1) / wgs <= 64, "fused gemv: x_new of %d inputs over %d work-groups",
-            c.k, wgs);
-  XTG_CHECK(f.out == kOutPlain || wgs <= kMaxFusedGroups, "fused gemv: %d work-groups' records (at most %d)", wgs,
-            kMaxFusedGroups);
-  XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
   const int threads = sh.s * 64;
   FusedFn fn = fused_fn(sh.r, sh.t, threads, f.in, f.out);
-  XTG_CHECK(fn != nullptr, "fused gemv: no kernel for R=%d T=%d (in %d, out %d)", sh.r, sh.t, f.in, f.out);
   const size_t lds = size_t(FusedLds(sh.s, sh.r, f.in).total) * sizeof(float);
   allow_lds(reinterpret_cast<const void*>(fn), lds);
   hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);

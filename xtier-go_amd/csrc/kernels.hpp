@@ -119,6 +119,9 @@ struct FusedGemv {
   float out_ea = 1.f, out_eb = 1.f;  // its factors 2^ea, 2^eb
 };
 int fused_gemv_groups(const FusedGemv& f);
+// Why launch_gemv_fused cannot take f's weights, rows, kinds and record count (no kernel made for the launch shape,
+// more waves or records than a launch holds), or "" when it can; pointers are not looked at.
+std::string fused_gemv_unsupported(const FusedGemv& f);
 constexpr int kMaxFusedGroups = 1024;   // work-groups of a launch whose records a consumer takes
 std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream);
 
