@@ -58,6 +58,44 @@ def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
+# rocprofv3 sets ROCPROF_<domain>=1 in the environment of the program it traces. In a traced process the bench
+# captures no HIP graph: twice a traced run died (host SIGSEGV) inside hipGraphLaunch, both times after graph execs
+# had been destroyed and new ones instantiated and replayed in the same process, and never without the tracer.
+TRACED = any(os.environ.get("ROCPROF_" + d) == "1" for d in (
+    "KERNEL_TRACE", "HIP_RUNTIME_API_TRACE", "HIP_COMPILER_API_TRACE", "HSA_CORE_API_TRACE", "HSA_AMD_EXT_API_TRACE",
+    "MEMORY_COPY_TRACE", "MEMORY_ALLOCATION_TRACE", "SCRATCH_MEMORY_TRACE"))
+
+
+class Replay:
+    """The launches fn() queues, replayable: captured into a HIP graph, or in a traced process (TRACED) fn itself
+    run again on each replay. With profiling on, a graph replay is one entry under its label; eager launches are
+    entries under their kernels' names (time() adds them up)."""
+
+    def __init__(self, hip, label, fn):
+        self.hip, self.label, self.fn, self.g = hip, label, fn, None
+        if not TRACED:
+            hip.graph_begin()
+            fn()
+            self.g = hip.graph_end(label)
+
+    def launch(self):
+        if self.g is not None:
+            self.hip.graph_launch(self.g)
+        else:
+            self.fn()
+
+    def time(self, rep, replays):
+        """(ms, replays) of this replayable's launches in a profile report covering `replays` replays of it."""
+        if self.g is not None:
+            return rep[self.label]["ms"], rep[self.label]["calls"]
+        return sum(v["ms"] for v in rep.values()), replays
+
+    def destroy(self):
+        if self.g is not None:
+            self.hip.graph_destroy(self.g)
+            self.g = None
+
+
 def call_bytes(ws, m):
     """Algorithmic HBM bytes of one call: codes + scales + tensor scale per weight, BF16 x once, FP32 y."""
     k = ws[0][1]
@@ -140,20 +178,17 @@ def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
         for m in SWEEP_ROWS:
             hip.matmul_dev(sets[0], dx, pkg.X_BF16, m, dy)   # sizes what the call needs before the capture
             hip.finish()
-            hip.graph_begin()
-            for ws in sets:
-                hip.matmul_dev(ws, dx, pkg.X_BF16, m, dy)
-            label = "sweep_%s_m%d" % (name, m)
-            g = hip.graph_end(label)
-            hip.graph_launch(g)
+            g = Replay(hip, "sweep_%s_m%d" % (name, m),
+                       lambda: [hip.matmul_dev(ws, dx, pkg.X_BF16, m, dy) for ws in sets])
+            g.launch()
             hip.finish()
             hip.profile(True)
             for _ in range(reps):
-                hip.graph_launch(g)
-            t = hip.profile_report()[label]
+                g.launch()
+            ms, n = g.time(hip.profile_report(), reps)
             hip.profile(False)
-            hip.graph_destroy(g)
-            us = t["ms"] * 1e3 / (t["calls"] * copies)
+            g.destroy()
+            us = ms * 1e3 / (n * copies)
             b = call_bytes(shapes, m)
             out["%s_m%d" % (name, m)] = {"us_per_launch": round(us, 3), "bytes": b, "gbs": round(b / us / 1e3, 1),
                                          "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -692,18 +727,16 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
         for m in (1, 8):
             dev.forward(dx, m, ctx, dl)   # eager once (scratch sized), then capture
             hip.finish()
-            hip.graph_begin()
-            dev.forward(dx, m, ctx, dl)
-            g = hip.graph_end("dory_step_ctx%d_m%d" % (ctx, m))
+            g = Replay(hip, "dory_step_ctx%d_m%d" % (ctx, m), lambda: dev.forward(dx, m, ctx, dl))
             for _ in range(3):
-                hip.graph_launch(g)
+                g.launch()
             hip.finish()
             t = time.perf_counter()
             for _ in range(reps):
-                hip.graph_launch(g)
+                g.launch()
             hip.finish()
             ms = (time.perf_counter() - t) / reps * 1e3
-            hip.graph_destroy(g)
+            g.destroy()
             step_bytes = w.weight_bytes() + kv_step[ctx]
             res["m%d" % m] = {"ms_per_step": round(ms, 4), "rows_per_s": round(m * 1e3 / ms, 1),
                               "hbm_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1)}
@@ -748,18 +781,16 @@ def decode_bench(pkg, wl, hip, contexts, reps, cpu_seconds, kv="both"):
         hip.finish()
         dev8.forward(dx, 1, ctx, dl)
         hip.finish()
-        hip.graph_begin()
-        dev8.forward(dx, 1, ctx, dl)
-        g = hip.graph_end("dory_step_fp8_ctx%d" % ctx)
+        g = Replay(hip, "dory_step_fp8_ctx%d" % ctx, lambda: dev8.forward(dx, 1, ctx, dl))
         for _ in range(3):
-            hip.graph_launch(g)
+            g.launch()
         hip.finish()
         t = time.perf_counter()
         for _ in range(reps):
-            hip.graph_launch(g)
+            g.launch()
         hip.finish()
         ms = (time.perf_counter() - t) / reps * 1e3
-        hip.graph_destroy(g)
+        g.destroy()
         kv8 = kv_step[ctx] // 2 + kv_step[ctx] // (2 * d) * 4   # 1-byte codes + a 4-byte scale per (row, head)
         fp8["ctx%d" % ctx] = {"ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1), "kv_bytes": kv8,
                               "hbm_gbs": round((w.weight_bytes() + kv8) / (ms / 1e3) / 1e9, 1)}
@@ -943,29 +974,28 @@ def main():
         hip.matmul_dev(sets[0][name], dx[(name, m)], pkg.X_BF16, m, dy)
     hip.finish()
 
-    def steps_graph(first, n, label):
-        hip.graph_begin()
+    def steps(first, n):
         for st in range(first, first + n):
             for i, (name, m) in enumerate(calls):
                 hip.matmul_dev(sets[(len(calls) * st + i) % copies][name], dx[(name, m)], pkg.X_BF16, m, dy)
-        return hip.graph_end(label)
 
-    warm = steps_graph(0, max(1, args.warmup), "warmup_steps")
-    timed = steps_graph(max(1, args.warmup), args.steps, "timed_steps")
-    hip.graph_launch(warm)
+    warm = Replay(hip, "warmup_steps", lambda: steps(0, max(1, args.warmup)))
+    timed = Replay(hip, "timed_steps", lambda: steps(max(1, args.warmup), args.steps))
+    warm.launch()
     hip.finish()
     # device time: events on the backend's stream around the one launch of the K steps (launch gaps between the
     # step's kernels included; host launch and synchronisation latency not); the wall clock of the same launch
-    # through hip.finish() beside it
-    hip.profile(True)
+    # through hip.finish() beside it. In a traced process (no graph) the steps run eagerly and the wall clock is
+    # the figure.
+    hip.profile(not TRACED)
     t0 = time.perf_counter()
-    hip.graph_launch(timed)
+    timed.launch()
     hip.finish()
     el_host = time.perf_counter() - t0
-    el = hip.profile_report()["timed_steps"]["ms"] / 1e3
+    el = hip.profile_report()["timed_steps"]["ms"] / 1e3 if not TRACED else el_host
     hip.profile(False)
-    hip.graph_destroy(warm)
-    hip.graph_destroy(timed)
+    warm.destroy()
+    timed.destroy()
     ms_per_step = el / args.steps * 1e3
     value = step_bytes / (el / args.steps) / 1e9
     log("timed %d steps: %.4f ms/step by device events (%.4f ms/step wall clock), %.1f GB/s whole-step (%.1f%% of "
@@ -975,19 +1005,29 @@ def main():
     per_call = {}
     gemv_graphs = {}
     for name, m in calls:
-        hip.graph_begin()
-        for c in range(copies):
-            hip.matmul_dev(sets[c][name], dx[(name, m)], pkg.X_BF16, m, dy)
-        gemv_graphs[(name, m)] = hip.graph_end("gemv_%s_m%d" % (name, m))
+        gemv_graphs[(name, m)] = Replay(hip, "gemv_%s_m%d" % (name, m), lambda name=name, m=m: [
+            hip.matmul_dev(sets[c][name], dx[(name, m)], pkg.X_BF16, m, dy) for c in range(copies)])
     for g in gemv_graphs.values():   # warm
-        hip.graph_launch(g)
+        g.launch()
     hip.finish()
-    hip.profile(True)
-    for _ in range(args.roofline_reps):
-        for g in gemv_graphs.values():
-            hip.graph_launch(g)
-    rep = hip.profile_report()
-    hip.profile(False)
+    timing = {}   # (ms, replays) per call: the calls' replays interleaved, or one call at a time when traced
+    if not TRACED:
+        hip.profile(True)
+        for _ in range(args.roofline_reps):
+            for g in gemv_graphs.values():
+                g.launch()
+        rep = hip.profile_report()
+        hip.profile(False)
+        timing = {key: g.time(rep, args.roofline_reps) for key, g in gemv_graphs.items()}
+    else:
+        for key, g in gemv_graphs.items():
+            hip.profile(True)
+            for _ in range(args.roofline_reps):
+                g.launch()
+            timing[key] = g.time(hip.profile_report(), args.roofline_reps)
+            hip.profile(False)
+    for g in gemv_graphs.values():
+        g.destroy()
     # the kernel that serves each call: one eager call each, named by the profile report
     kernel_of = {}
     for name, m in calls:
@@ -999,18 +1039,18 @@ def main():
     tot_bytes, tot_s = 0, 0.0
     by_kernel = {}
     for name, m in calls:
-        t = rep["gemv_%s_m%d" % (name, m)]
-        launches = t["calls"] * copies
-        us = t["ms"] * 1e3 / launches
+        ms, replays = timing[(name, m)]
+        launches = replays * copies
+        us = ms * 1e3 / launches
         b = call_bytes(dict(SHAPES)[name], m)
         key = "%s_m%d" % (name, m)
         per_call[key] = {"kernel": kernel_of[key], "us_per_launch": round(us, 3), "bytes": b,
                          "gbs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         tot_bytes += b * launches
-        tot_s += t["ms"] / 1e3
+        tot_s += ms / 1e3
         kb = by_kernel.setdefault(kernel_of[key], {"bytes": 0.0, "s": 0.0, "calls": []})
         kb["bytes"] += b * launches
-        kb["s"] += t["ms"] / 1e3
+        kb["s"] += ms / 1e3
         kb["calls"].append(key)
     all_achieved = tot_bytes / tot_s / 1e9
     dom_call = max(per_call, key=lambda k: per_call[k]["bytes"])   # the launch that moves the most bytes

@@ -230,21 +230,24 @@ __device__ inline void wave_lds_order() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// The operand of one k-tile from raw BF16 rows, converted by all 64 lanes and staged through LDS. Lane (j, i) =
-// (lane / 16, lane % 16) holds inputs 8 i .. 8 i + 7 of row j's k-tile in w[0] and of row j + 4's in w[1] (zeros
-// for rows past m). Each row's inputs are scaled by the power of two 2^e that brings the tile's largest magnitude in
-// that row to [2^14, 2^15) (prep_x_kernel's rule, per 128 inputs instead of per row; the row's 16 lanes agree on it
-// through DPP within their row of lanes). BF16 carries 8 significant bits, so f16(x * 2^e) is exact wherever it is
-// a normal f16 and the low part is zero (the odd operand columns read zeros). An input whose scaled value falls
-// below f16's normal range (at least 2^28 times smaller than the tile's largest) is flushed, an error below 2^-28 of
-// that largest magnitude; e is capped at 112 so the exponent shift stays a subtraction (tiles whose largest
-// magnitude is under 2^-98 keep at least 6 of f16's 11 bits above their largest value, still more than BF16's 8).
-// With the abs bits a = [E:8][M:7], the f16 of x * 2^e is [E - 112 + e : 5][M : 7][000]: a saturating subtraction
-// of (112 - e) << 7 (0 when the result would be below the normal range), a shift by 3 and the sign put back. A row
-// whose tile holds an infinity or NaN gets NaN operands (NaN outputs, as the prepared operand gives). The staged
-// tile [8 rows][16][8 f16] and the rows' factors 2^-e then go to the lanes that consume them: lane (c, g) of the
-// matrix op's operand takes row c / 2's inputs 32 g .. 32 g + 31 (four steps of 8) for even c < 2 m, zeros else.
-constexpr int kStageVecs = 8 * 16 + 2;   // one wave's staging, in 16-byte units: the rows' tiles, then 8 factors
+// The operand of a wave's T k-tiles from raw BF16 rows, converted by all 64 lanes and staged through LDS one k-tile
+// at a time. Lane (j, i) = (lane / 16, lane % 16) holds inputs 8 i .. 8 i + 7 of each k-tile of row j in xr[u][0]
+// and of row j + 4 in xr[u][1] (zeros for rows past m). Each row's inputs are scaled by the power of two 2^e that
+// brings the row's largest magnitude over the wave's k-tiles to [2^14, 2^15) (prep_x_kernel's rule, per wave's
+// share of the row instead of per row; the row's 16 lanes agree on it through DPP within their row of lanes), so
+// the matrix ops accumulate across the wave's k-tiles and one multiply by 2^-e per column follows. BF16 carries 8
+// significant bits, so f16(x * 2^e) is exact wherever it is a normal f16 and the low part is zero (the odd operand
+// columns read zeros). An input whose scaled value falls below f16's normal range (at least 2^28 times smaller than
+// that largest magnitude) is flushed, an error below 2^-28 of it; e is capped at 112 so the exponent shift stays a
+// subtraction (rows whose largest magnitude is under 2^-98 keep at least 6 of f16's 11 bits above their largest
+// value, still more than BF16's 8). With the abs bits a = [E:8][M:7], the f16 of x * 2^e is [E - 112 + e : 5][M : 7]
+// [000]: a saturating subtraction of (112 - e) << 7 (0 when the result would be below the normal range), a shift by 3
+// and the sign put back. A row holding an infinity or NaN gets the factor NaN (NaN outputs, as the prepared operand
+// gives). Each staged k-tile [8 rows][16][8 f16] then goes to the lanes that consume it: lane (c, g) of the matrix
+// op's operand takes row c / 2's inputs 32 g .. 32 g + 31 (four steps of 8) for even c < 2 m, zeros else. One
+// exponent per wave instead of per k-tile halves the conversion's instructions (the largest magnitude is reduced
+// across lanes once): the 8-row calls of the 4B layer's projections took 0.14-0.65 us less per launch.
+constexpr int kStageVecs = 8 * 16 + 2;   // one wave's staging, in 16-byte units: the rows' k-tile, then 8 factors
 
 __device__ inline uint32_t row16_max(uint32_t v) {
   v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppXor1, 0xF, 0xF, false)));
@@ -253,52 +256,57 @@ __device__ inline uint32_t row16_max(uint32_t v) {
   return max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppMirror, 0xF, 0xF, false)));
 }
 
-// 8 BF16 inputs of one row (a lane's share) to their f16 at the row's 2^e; returns e
-__device__ inline int bf16_to_f16_row(uint4& w4) {
-  uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-  u16x2 m2 = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[0] & 0x7fff7fffu),
-                                       __builtin_bit_cast(u16x2, w[1] & 0x7fff7fffu));
-  m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(__builtin_bit_cast(u16x2, w[2] & 0x7fff7fffu),
-                                                               __builtin_bit_cast(u16x2, w[3] & 0x7fff7fffu)));
-  const uint32_t mx = row16_max(m2.x > m2.y ? uint32_t(m2.x) : uint32_t(m2.y));
-  const int e = mx == 0 || mx >= 0x7f80u ? 0 : min(141 - int(mx >> 7), 112);
-  const unsigned short c = (unsigned short)((112 - e) << 7);
-  const u16x2 c2 = {c, c};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu), c2);
-    const u16x2 f = d << (unsigned short)3;
-    w[i] = mx >= 0x7f80u ? 0x7e007e00u : (w[i] & 0x80008000u) | __builtin_bit_cast(uint32_t, f);
-  }
-  w4 = make_uint4(w[0], w[1], w[2], w[3]);
-  return e;
-}
-
-// the k-tile's operand columns of lane (col, grp) and their factor 2^-e, from the rows in w (lane layout above);
-// stage: this wave's kStageVecs, free on entry and again on return
-__device__ inline float bf16_operand(uint4 (&w)[2], int m, int lane, uint4* stage, uint4 (&xb)[4]) {
+// The operand entries xb[u][step] of lane (col, grp) for the wave's T k-tiles and the lane's column factor 2^-e (1
+// for dead columns), from the rows in xr (lane layout above); stage: this wave's kStageVecs, free on entry and again
+// on return.
+template <int T>
+__device__ inline float bf16_operands(uint4 (&xr)[T][2], int m, int lane, uint4* stage, uint4 (&xb)[T][4]) {
   const int j = lane >> 4, i = lane & 15, col = lane & 15, grp = lane >> 4;
   float* fac = reinterpret_cast<float*>(stage + 128);
-  const int e0 = bf16_to_f16_row(w[0]);
-  stage[j * 16 + i] = w[0];
-  if (i == 0) fac[j] = ldexpf(1.f, -e0);
-  if (m > 4) {   // uniform: the second half of the rows
-    const int e1 = bf16_to_f16_row(w[1]);
-    stage[(j + 4) * 16 + i] = w[1];
-    if (i == 0) fac[j + 4] = ldexpf(1.f, -e1);
+  u16x2 c2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {   // rows j and j + 4: the largest magnitude over the wave's k-tiles
+    u16x2 m2 = {0, 0};
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+      const uint32_t w[4] = {xr[u][h].x, xr[u][h].y, xr[u][h].z, xr[u][h].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[q] & 0x7fff7fffu));
+    }
+    const uint32_t mx = row16_max(m2.x > m2.y ? uint32_t(m2.x) : uint32_t(m2.y));
+    const int e = mx == 0 || mx >= 0x7f80u ? 0 : min(141 - int(mx >> 7), 112);
+    const unsigned short c = (unsigned short)((112 - e) << 7);
+    c2[h] = u16x2{c, c};
+    if (i == 0 && (h == 0 || m > 4)) fac[j + 4 * h] = mx >= 0x7f80u ? __builtin_nanf("") : ldexpf(1.f, -e);
   }
-  wave_lds_order();
   const int r = col >> 1;
   const bool live = (col & 1) == 0 && r < m;
   const int rc = live ? r : 0;
+  float xs = 1.f;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint4 v = stage[rc * 16 + 4 * grp + t];
-    xb[t] = live ? v : make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < T; ++u) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && m <= 4) break;   // uniform: the second half of the rows
+      uint32_t w[4] = {xr[u][h].x, xr[u][h].y, xr[u][h].z, xr[u][h].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w[q] & 0x7fff7fffu), c2[h]);
+        const u16x2 f = d << (unsigned short)3;
+        w[q] = (w[q] & 0x80008000u) | __builtin_bit_cast(uint32_t, f);
+      }
+      stage[(j + 4 * h) * 16 + i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint4 v = stage[rc * 16 + 4 * grp + t];
+      xb[u][t] = live ? v : make_uint4(0, 0, 0, 0);
+    }
+    if (u == 0) xs = live ? fac[rc] : 1.f;
+    wave_lds_order();   // read before the next k-tile's staging
   }
-  const float xs = fac[rc];
-  wave_lds_order();   // read before the next k-tile's staging
-  return live ? xs : 1.f;
+  return xs;
 }
 
 // XR: false = a prepared operand (xop / xinv); true = raw BF16 rows (the kernel builds the operand per k-tile in
@@ -380,14 +388,12 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
       }
     }
   }
-  float xs[T];   // raw rows: each k-tile's factor 2^-e for the lane's column
-  if constexpr (XR) __builtin_amdgcn_sched_barrier(0);   // every load issued before the conversion waits on x
-  // raw rows: this wave's staging area, after the cross-wave sums' region
-  uint4* stage = reinterpret_cast<uint4*>(red) + (S > 1 ? S * R * kMaxRows * 4 : 0) + wave * kStageVecs;
-#pragma unroll
-  for (int u = 0; u < T; ++u) {
-    xs[u] = 1.f;
-    if constexpr (XR) xs[u] = bf16_operand(xr[u], a.m, lane, stage, xb[u]);
+  float xs = 1.f;   // raw rows: the wave's factor 2^-e for the lane's column
+  if constexpr (XR) {
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the conversion waits on x
+    // this wave's staging area, after the cross-wave sums' region
+    uint4* stage = reinterpret_cast<uint4*>(red) + (S > 1 ? S * R * kMaxRows * 4 : 0) + wave * kStageVecs;
+    xs = bf16_operands<T>(xr, a.m, lane, stage, xb);
   }
   f32x4 acc[R];
 #pragma unroll
@@ -398,19 +404,16 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     for (int r = 0; r < R; ++r) {
       const f16x2 s0 = scale_pair(sw[u][r], 0), s1 = scale_pair(sw[u][r], 1);
       const uint32_t words[4] = {cw[u][r].x, cw[u][r].y, cw[u][r].z, cw[u][r].w};
-      f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const f16x8 A = dequant8(words[t], t < 2 ? s0 : s1);
-        const f16x8 B = __builtin_bit_cast(f16x8, xb[u][t]);
-        if constexpr (!XR)
-          acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[r], 0, 0, 0);
-        else
-          part = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, part, 0, 0, 0);
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(f16x8, xb[u][t]), acc[r], 0, 0, 0);
       }
-      if constexpr (XR) acc[r] += part * xs[u];   // a power of two: exact
     }
   }
+  if constexpr (XR)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] *= xs;   // a power of two: exact
   if (S == 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
