@@ -225,6 +225,49 @@ def gemv_sweep(pkg, wl, hip, reps, cpu_seconds):
     return out
 
 
+# Sizes of the read floor: the 6-call step's launches (QKV 5120, down 3072x8192, gate/up 2x8192 at M=8), a global
+# layer's attention at 32K (BF16 K and V, 8 KV heads of 128) and the NVFP4 LM head (131072 x 3072).
+READ_SIZES = [("qkv5120_m8", 9060352), ("down3072x8192_m8", 14385152), ("gateup2x8192_m8", 28885008),
+              ("attention_ctx32768", 134217728), ("head131072x3072", 226492416)]
+POOL_BYTES = 2 << 30
+
+
+def read_floor(pkg, hip, reps):
+    """The device's streaming-read roofline at the hot path's sizes (xtg_hip_read_probe, the reference's readsum
+    probe): for each size, a graph of one read per slice of a 2 GiB pool (so every launch streams from HBM, not from
+    the 256 MB Infinity Cache) replayed between events on the backend's stream; per launch us, GB/s and fraction of
+    the 8 TB/s peak."""
+    pool = hip.alloc(POOL_BYTES)
+    out = {}
+    for name, size in READ_SIZES:
+        size = size // 16 * 16
+        copies = max(2, POOL_BYTES // size)
+        parts = hip.array(shape=(copies * hip.read_probe_partials(size),), dtype=np.uint32)
+        per = hip.read_probe_partials(size) * 4
+
+        def reads():
+            for c in range(copies):
+                hip.read_probe(pool + c * size, size, parts.ptr + c * per)
+
+        g = Replay(hip, "read_%s" % name, reads)
+        g.launch()
+        hip.finish()
+        hip.profile(True)
+        for _ in range(reps):
+            g.launch()
+        ms, n = g.time(hip.profile_report(), reps)
+        hip.profile(False)
+        g.destroy()
+        parts.free()
+        us = ms * 1e3 / (n * copies)
+        out[name] = {"bytes": size, "us": round(us, 3), "gbs": round(size / us / 1e3, 1),
+                     "frac": round(size / us / 1e3 / HBM_PEAK_GBS, 4), "copies": copies}
+        log("read floor %-20s %10d B: %.2f us, %.0f GB/s (%.1f%% of HBM peak)"
+            % (name, size, us, size / us / 1e3, size / us / 1e3 / HBM_PEAK_GBS * 100))
+    hip.release(pool)
+    return out
+
+
 def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
     """Decode attention over global caches and sliding rings through xtg_hip_attention (own-key, scan and merge
     launches, each between events on the backend's stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
@@ -903,6 +946,9 @@ def main():
     ap.add_argument("--decode-eager", default="",
                     help="KV,CTX (e.g. fp8,4096): only the decode step run eagerly, without graph capture, for a "
                          "kernel trace of it (--decode-reps steps); prints its own JSON line")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only the streaming-read roofline at the hot path's sizes (for profiling it); prints its own "
+                         "JSON line")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
                          "left out of the JSON line")
@@ -925,6 +971,14 @@ def main():
         ms = decode_eager_pass(pkg, wl, hip, int(ctx), kvs == "fp8", args.decode_reps)
         print(json.dumps({"metric": "eager decode step ms (%s caches, ctx %s)" % (kvs, ctx), "value": round(ms, 4),
                           "unit": "ms", "higher_is_better": False}))
+        hip.close()
+        return
+
+    if args.read_floor:
+        hip = pkg.HipBackend(0)
+        floor = read_floor(pkg, hip, 10)
+        print(json.dumps({"metric": "streaming read GB/s", "value": floor["gateup2x8192_m8"]["gbs"], "unit": "GB/s",
+                          "higher_is_better": True, "read_floor": floor}))
         hip.close()
         return
 
@@ -1074,6 +1128,15 @@ def main():
     for k, v in per_call.items():
         log("  %-22s %7.3f us  %7.1f GB/s" % (k, v["us_per_launch"], v["gbs"]))
 
+    # the plain streaming read of each call's bytes (the same rotation over HBM): each call's time against it
+    floor = read_floor(pkg, hip, 10)
+    floor_by_bytes = sorted((v["bytes"], v["us"]) for v in floor.values())
+    for key, v in per_call.items():
+        near = min(floor_by_bytes, key=lambda bu: abs(bu[0] - v["bytes"]))
+        if abs(near[0] - v["bytes"]) <= 0.05 * v["bytes"]:
+            v["read_floor_us"] = near[1]
+            v["of_read_floor"] = round(near[1] / v["us_per_launch"], 4)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(base, xs, args.cpu_seconds)
@@ -1144,6 +1207,7 @@ def main():
                      "all_calls_achieved": round(all_achieved, 1),
                      "all_calls_frac": round(all_achieved / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
+        "read_floor": floor,
         "gemv_sweep": sweep,
         "decode_attention": attention,
         "bf16_lm_head": bf16_head,

@@ -337,6 +337,16 @@ int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len);
  * than out_len is cut (and its records are gone). */
 int xtg_hip_profile_report(xtg_hip* h, char* out, int out_len);
 
+/* ------------------------------------------------------------------------------------------------ probes */
+
+/* The device probe's streaming read (tests/gpu_probe.cpp:59-66, readsum: a buffer summed in 16-byte loads, one
+ * partial per work-group): every byte of src (device, 16-byte aligned, a multiple of 16 bytes) read once and
+ * XOR-folded into out (device, xtg_hip_read_probe_partials(bytes) uint32 partials, one per work-group of 256 threads
+ * with 8 loads each). Queued. Profiled by xtg_hip_profile like any kernel: the read roofline of this device at a
+ * given size. */
+size_t xtg_hip_read_probe_partials(size_t bytes);
+int xtg_hip_read_probe(xtg_hip* h, const void* src, size_t bytes, uint32_t* out, char* err, int err_len);
+
 #ifdef __cplusplus
 }
 #endif

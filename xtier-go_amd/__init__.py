@@ -116,6 +116,8 @@ SIGNATURES = [
     ("xtg_hip_graph_end", _I, [_P, ctypes.c_char_p, ctypes.POINTER(_P)] + _ERR),
     ("xtg_hip_graph_launch", _I, [_P, _P] + _ERR),
     ("xtg_hip_graph_destroy", None, [_P, _P]),
+    ("xtg_hip_read_probe_partials", _SZ, [_SZ]),
+    ("xtg_hip_read_probe", _I, [_P, _P, _SZ, _P] + _ERR),
     ("xtg_hip_profile", _I, [_P, _I] + _ERR),
     ("xtg_hip_profile_report", _I, [_P, ctypes.c_char_p, _I]),
 ]
@@ -420,6 +422,16 @@ class HipBackend:
     def add_norm(self, a, b, out, rows, width):
         err = _errbuf()
         _check(lib().xtg_hip_add_norm(self.h, _ptr(a), _ptr(b), _ptr(out), rows, width, err, len(err)), err)
+
+    def read_probe(self, src, nbytes, out):
+        """The streaming-read probe: out (device uint32, read_probe_partials(nbytes)) gets the XOR partials of the
+        nbytes at src (device)."""
+        err = _errbuf()
+        _check(lib().xtg_hip_read_probe(self.h, _ptr(src), nbytes, _ptr(out), err, len(err)), err)
+
+    @staticmethod
+    def read_probe_partials(nbytes):
+        return int(lib().xtg_hip_read_probe_partials(nbytes))
 
     def argmax(self, logits, rows, n, out):
         """out[r] (device int32) = the first index of the largest of logits[r][:n] (device)."""

@@ -232,6 +232,10 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
     timed([&] { return launch_gemm(c, stream_); });
 }
 
+void Backend::read_probe(const void* src, size_t bytes, uint32_t* out) {
+  timed([&] { return launch_read_probe(src, bytes, out, stream_); });
+}
+
 int Backend::matmul_fused(const xtg_nvfp4* ws, int nw, FusedGemv f, const void* op, int m, float* y) {
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
   XTG_CHECK(m == 1, "fused matmul: %d rows (one)", m);

@@ -116,6 +116,10 @@ class Backend {
   // holds is retired until no graph exists). The decode step's producer and scan read their angles from it.
   const float2* rope_table(float theta, int d, long long n_pos);
 
+  // the streaming-read probe (tests/gpu_probe.cpp:59-66's readsum): out (device) gets read_probe_groups(bytes)
+  // XOR partials of src's bytes; queued
+  void read_probe(const void* src, size_t bytes, uint32_t* out);
+
   // opencl.h:40-45
   void* alloc(size_t bytes);
   void release(void* p);

@@ -424,6 +424,15 @@ void xtg_hip_graph_destroy(xtg_hip* h, xtg_hip_graph* g) {
   if (h && g) guarded(nullptr, 0, [&] { h->b->graph_destroy(reinterpret_cast<hipGraphExec_t>(g)); });
 }
 
+size_t xtg_hip_read_probe_partials(size_t bytes) { return xtg::hip::read_probe_groups(bytes); }
+
+int xtg_hip_read_probe(xtg_hip* h, const void* src, size_t bytes, uint32_t* out, char* err, int err_len) {
+  return guarded(err, err_len, [&] {
+    XTG_CHECK(h, "read probe: NULL handle");
+    h->b->read_probe(src, bytes, out);
+  });
+}
+
 int xtg_hip_profile(xtg_hip* h, int enable, char* err, int err_len) {
   return guarded(err, err_len, [&] {
     XTG_CHECK(h, "profile: NULL handle");

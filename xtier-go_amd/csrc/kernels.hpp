@@ -154,6 +154,12 @@ GemvShape gemv_bf16_shape(int kt, int nb, int m);
 std::string launch_gemv_bf16(const PackedBf16& w, const void* xop, int m, float* y, const float* col_scale,
                              hipStream_t stream);
 
+// ---- the streaming-read probe (probe.hip) ----
+// XOR fold of bytes (a multiple of 16) of device memory in 16-byte loads: one uint32 partial per work-group into out
+// (read_probe_groups(bytes) of them).
+size_t read_probe_groups(size_t bytes);
+std::string launch_read_probe(const void* src, size_t bytes, uint32_t* out, hipStream_t stream);
+
 // ---- sampling (sample.hip) ----
 constexpr int kMaxSampleRows = 8;
 // xtg::Sampler::sample for rows of device logits [rows][n] with the caller's uniform draws u[rows] (host, [0, 1)),
