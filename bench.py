@@ -59,8 +59,9 @@ def log(msg):
 
 
 # rocprofv3 sets ROCPROF_<domain>=1 in the environment of the program it traces. In a traced process the bench
-# captures no HIP graph: twice a traced run died (host SIGSEGV) inside hipGraphLaunch, both times after graph execs
-# had been destroyed and new ones instantiated and replayed in the same process, and never without the tracer.
+# destroys no graph exec and captures graphs only for the 6-call step and the per-call GEMV launches: twice a traced
+# run died (host SIGSEGV) inside hipGraphLaunch, both times after graph execs had been destroyed and new ones
+# instantiated and replayed in the same process, and never without the tracer; the other sections run eagerly there.
 TRACED = any(os.environ.get("ROCPROF_" + d) == "1" for d in (
     "KERNEL_TRACE", "HIP_RUNTIME_API_TRACE", "HIP_COMPILER_API_TRACE", "HSA_CORE_API_TRACE", "HSA_AMD_EXT_API_TRACE",
     "MEMORY_COPY_TRACE", "MEMORY_ALLOCATION_TRACE", "SCRATCH_MEMORY_TRACE"))
@@ -69,11 +70,15 @@ TRACED = any(os.environ.get("ROCPROF_" + d) == "1" for d in (
 class Replay:
     """The launches fn() queues, replayable: captured into a HIP graph, or in a traced process (TRACED) fn itself
     run again on each replay. With profiling on, a graph replay is one entry under its label; eager launches are
-    entries under their kernels' names (time() adds them up)."""
+    entries under their kernels' names (time() adds them up). keep_in_trace: the 6-call step's and the per-call
+    GEMV graphs stay graphs in a traced process too (the configuration traced runs have replayed without failure: no
+    graph exec is destroyed there before the process ends), so the trace times the launches the untraced run
+    times."""
 
-    def __init__(self, hip, label, fn):
+    def __init__(self, hip, label, fn, keep_in_trace=False):
         self.hip, self.label, self.fn, self.g = hip, label, fn, None
-        if not TRACED:
+        self.keep = keep_in_trace and TRACED
+        if not TRACED or self.keep:
             hip.graph_begin()
             fn()
             self.g = hip.graph_end(label)
@@ -91,7 +96,7 @@ class Replay:
         return sum(v["ms"] for v in rep.values()), replays
 
     def destroy(self):
-        if self.g is not None:
+        if self.g is not None and not self.keep:   # a traced process destroys no graph exec before it ends
             self.hip.graph_destroy(self.g)
             self.g = None
 
@@ -1033,20 +1038,20 @@ def main():
             for i, (name, m) in enumerate(calls):
                 hip.matmul_dev(sets[(len(calls) * st + i) % copies][name], dx[(name, m)], pkg.X_BF16, m, dy)
 
-    warm = Replay(hip, "warmup_steps", lambda: steps(0, max(1, args.warmup)))
-    timed = Replay(hip, "timed_steps", lambda: steps(max(1, args.warmup), args.steps))
+    warm = Replay(hip, "warmup_steps", lambda: steps(0, max(1, args.warmup)), keep_in_trace=True)
+    timed = Replay(hip, "timed_steps", lambda: steps(max(1, args.warmup), args.steps), keep_in_trace=True)
     warm.launch()
     hip.finish()
     # device time: events on the backend's stream around the one launch of the K steps (launch gaps between the
     # step's kernels included; host launch and synchronisation latency not); the wall clock of the same launch
     # through hip.finish() beside it. In a traced process (no graph) the steps run eagerly and the wall clock is
     # the figure.
-    hip.profile(not TRACED)
+    hip.profile(True)
     t0 = time.perf_counter()
     timed.launch()
     hip.finish()
     el_host = time.perf_counter() - t0
-    el = hip.profile_report()["timed_steps"]["ms"] / 1e3 if not TRACED else el_host
+    el = timed.time(hip.profile_report(), 1)[0] / 1e3
     hip.profile(False)
     warm.destroy()
     timed.destroy()
@@ -1060,12 +1065,13 @@ def main():
     gemv_graphs = {}
     for name, m in calls:
         gemv_graphs[(name, m)] = Replay(hip, "gemv_%s_m%d" % (name, m), lambda name=name, m=m: [
-            hip.matmul_dev(sets[c][name], dx[(name, m)], pkg.X_BF16, m, dy) for c in range(copies)])
+            hip.matmul_dev(sets[c][name], dx[(name, m)], pkg.X_BF16, m, dy) for c in range(copies)],
+            keep_in_trace=True)
     for g in gemv_graphs.values():   # warm
         g.launch()
     hip.finish()
-    timing = {}   # (ms, replays) per call: the calls' replays interleaved, or one call at a time when traced
-    if not TRACED:
+    timing = {}   # (ms, replays) per call: the calls' replays interleaved (graphs), or one call at a time (eager)
+    if all(g.g is not None for g in gemv_graphs.values()):
         hip.profile(True)
         for _ in range(args.roofline_reps):
             for g in gemv_graphs.values():
