@@ -652,13 +652,13 @@ def nvfp4_bytes(n, k):
     return n * k // 2 + n * k // 16 + 4
 
 
-def attn_splits(c, ctx, ring):
+def attn_splits(c, ctx, ring, fp8=False):
     """The key splits the attention step's plan takes for one row (attn_plan in csrc/attention.hip: about 192
-    work-groups, four waves of 32-slot tiles each, at least two tiles per wave on a cache by position and one on a
-    ring)."""
+    work-groups, 512 on an FP8 cache by position, four waves of 32-slot tiles each, at least two tiles per wave on a
+    cache by position and one on a ring)."""
     tiles = -(-ring // 32) if ring else -(-ctx // 32)
     mt = 1 if ring else 2
-    want = max(1, 192 // c["kv_heads"])
+    want = max(1, (512 if fp8 and not ring else 192) // c["kv_heads"])
     return max(1, min(want, -(-tiles // (mt * 4)), tiles))
 
 
@@ -702,7 +702,7 @@ def decode_launches(w, wl, launches, ctx, fp8=False):
         add("q/k/v/g", nvfp4_bytes(2 * Q + 2 * KV, H) + 4 * H * 4 + 4 * (2 * Q + 2 * KV))
         ring = c["ring_slots"] if kind == wl.SLIDING else 0
         visible = min(ctx, c["window"]) if ring else ctx
-        part = (attn_splits(c, ctx, ring) + 1) * heads * (d + 2) * 4
+        part = (attn_splits(c, ctx, ring, fp8) + 1) * heads * (d + 2) * 4
         while i < len(seq) and not seq[i][0].startswith(("attn_gate", "gemv")):
             name = seq[i][0]
             take("")

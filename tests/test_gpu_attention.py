@@ -204,10 +204,11 @@ def test_decode_sharp_softmax(hip, orc, qmul):
 @pytest.mark.parametrize("qmul,n_q,fp8", [(200.0, 1, False), (200.0, 8, False), (2000.0, 1, False),
                                            (2000.0, 8, False), (2000.0, 1, True), (2000.0, 8, True)])
 def test_decode_sharp_softmax_32k(hip, orc, qmul, n_q, fp8):
-    """The config-2 global cache at 32768 positions (the plan's 24 key splits, merged across splits) under a peaked
-    softmax: unit q scaled by 200 (scores of std ~1.6 over the keys) and by 2000 (std ~16: the largest scores ~70,
-    a few keys carry the weight, as Dory's scores in the hundreds do); BF16 and FP8 caches, 1 and 8 rows. Against the
-    oracle at 5e-5 and against an FP64 softmax of what the cache holds at 3x the oracle's own error."""
+    """The 4B model's global cache at 32768 positions (the plan's 24 key splits, 64 for one row of an FP8 cache,
+    merged across splits) under a peaked softmax: unit q scaled by 200 (scores of std ~1.6 over the keys) and by 2000
+    (std ~16: the largest scores ~70, a few keys carry the weight, as Dory's scores in the hundreds do); BF16 and FP8
+    caches, 1 and 8 rows. Against the oracle at 5e-5 and against an FP64 softmax of what the cache holds at 3x the
+    oracle's own error."""
     rng = np.random.default_rng(int(qmul) + n_q + 7 * fp8)
     out, ref, exact = run_case(hip, orc, 32768, n_q, 0, 32, 8, 128, None, rng, unit=True, qmul=qmul, fp8=fp8)
     assert exact is not None
@@ -217,7 +218,7 @@ def test_decode_sharp_softmax_32k(hip, orc, qmul, n_q, fp8):
 
 
 @pytest.mark.parametrize("window,fp8", [(1024, False), (1088, False), (1024, True)])
-def test_ring_wrapped_config3(hip, orc, wl, window, fp8):
+def test_ring_wrapped_1088_slots(hip, orc, wl, window, fp8):
     """The sliding-window ring: a 1088-slot ring after 40000 positions (holding 38912..39999), 8 rows at
     40000..40007, q and k produced by RoPE (theta 1e6) -> per-head norm -> q * qscale ~ U(0.5, 1.5); the mask is rebuilt from the stored
     slot positions. Compared with the oracle's position form and its slot form."""

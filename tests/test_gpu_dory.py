@@ -510,6 +510,71 @@ def test_4b_decode_step_fp8(hip, orc, wl, model_4b):
     assert (got.argmax(1) == want.argmax(1)).all()
 
 
+def test_fp8_global_gate_waves(hip, orc, wl, monkeypatch):
+    """The one-token step's gate by heads over the global layer's split partials of an FP8 cache: 16, 32 and 64 key
+    splits per KV head (17, 33 and 65 records per column at 4K, 8K and 32K positions) take one, two and four waves
+    per head. An 8-sublayer model with the 4B attention shape (32 q / 8 KV heads of 128, one global layer, three
+    1088-slot rings), the global cache filled to 32768 and the rings with the positions before each one-token step,
+    at 4096, 8192 and 32768: the fused session's launches name the gate's wave count, and its logits agree with the
+    separate norm launches' (XTG_DECODE_UNFUSED=1, whose gate merges all records in one work-group per row) within
+    1e-4 and with the oracle's within 1e-3, same argmax."""
+    cfg = dict(wl.DORY_4B, n_in=2, n_rec=4, n_out=2, vocab=4096, kv_dtype=1)
+    ctx = 32768
+    w = wl.DoryWeights(cfg, seed=91, context=ctx + 64)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    ref = orc.Dory(w, wl)
+    fused = hip.dory(w)
+    monkeypatch.setenv("XTG_DECODE_UNFUSED", "1")
+    separate = hip.dory(w)
+    monkeypatch.delenv("XTG_DECODE_UNFUSED")
+    rng = np.random.default_rng(92)
+    K = wl_unit(rng, (ctx, cfg["kv_heads"]), cfg["head_dim"])
+    Vv = wl_unit(rng, (ctx, cfg["kv_heads"]), cfg["head_dim"])
+
+    def store(kind, lo, hi):   # positions lo .. hi - 1 into every cache of that kind, in all three sessions
+        a = 0
+        for k in w.kinds:
+            if k == 0:
+                continue
+            if k == kind:
+                for p in range(lo, hi, 1024):
+                    q = min(hi, p + 1024)
+                    ref.cache(a, 0).store(p, K[p:q], Vv[p:q])
+                    fused.cache(a, 0).store_host(p, K[p:q], Vv[p:q])
+                    separate.cache(a, 0).store_host(p, K[p:q], Vv[p:q])
+            a += 1
+
+    store(2, 0, ctx)   # the global cache: a step at pos reads positions below pos only
+    dx = hip.array(shape=(1, H))
+    dl = hip.array(shape=(1, V))
+    try:
+        for pos, waves in ((4096, 1), (8192, 2), (32768, 4)):
+            store(1, pos - cfg["ring_slots"], pos)   # the rings: the slots' worth of positions before the step
+            x = unit_rows(rng, 1, H)
+            dx.upload(x)
+            hip.profile(True, launches=True)
+            fused.forward(dx, 1, pos, dl)
+            _, launches = hip.profile_report(launches=True)
+            hip.profile(False)
+            got = dl.numpy().copy()
+            separate.forward(dx, 1, pos, dl)
+            sep = dl.numpy().copy()
+            want = ref.forward(x, pos, threads=16)
+            names = {n for n, _ in launches if n.startswith("attn_gate_heads_kernel")}
+            assert "attn_gate_heads_kernel<128, %d>" % waves in names, (pos, sorted(names))
+            e_sep, e_ref = rel_l2(got, sep), rel_l2(got, want)
+            print("FP8 global gate at %d: %s; fused vs separate %.2e, vs oracle %.2e" % (pos, sorted(names), e_sep,
+                                                                                     e_ref))
+            assert e_sep <= 1e-4, pos
+            assert e_ref <= 1e-3, pos
+            assert (got.argmax(1) == want.argmax(1)).all() and (sep.argmax(1) == want.argmax(1)).all(), pos
+    finally:
+        dx.free()
+        dl.free()
+        fused.destroy()
+        separate.destroy()
+
+
 def test_bf16_head_and_fp8_caches(hip, orc, wl):
     """The BF16 checkpoint's configuration (dory.cpp:141, 325, 1203): a BF16 LM head over FP8 caches, the tiny
     model over 24 positions in chunks of 8 and single rows; logits against the oracle with the same head."""

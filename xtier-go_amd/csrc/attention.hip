@@ -1414,12 +1414,15 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
   if (xop) emit_operand_mx<kMergeThreads, U>(t, Q, row, xop, xinv, ostride, mx * f);
 }
 
-// The one-token step's gate with its norm left to the o-projection: one wave per head. Lane l = (part p, chunk c)
-// with CH = D / 8 chunks of 8 dims and P = 64 / CH parts: part p merges the head's records s = p, p + P, ... (up to
-// 8 of them per batch, all loads in flight together), the parts' states are combined across lanes (exchanges of
-// lanes l ^ CH, l ^ 2 CH, ...: the same order every call), and part 0 applies a * sigmoid(g * gs)
-// (dory.cpp:509-512), writes the gated head to y and its sum of squares to rec[head], from which the o-projection's
-// operand takes the justnorm (dory.cpp:513-515).
+// The one-token step's gate with its norm left to the o-projection: W waves per head. Lane l of wave w = (part p,
+// chunk c) with CH = D / 8 chunks of 8 dims, P = 64 / CH parts per wave and p = w P + l / CH: part p merges the
+// head's records s = p, p + W P, ... (up to 8 of them per batch, all loads in flight together; the host takes W so
+// that one batch holds them all where it can, since every further batch is one more round trip of dependent loads:
+// 65 records per column, the 32K global layers of an FP8 cache, took three on one wave). Waves 1 .. W - 1 hand
+// their lanes' states to wave 0 through LDS, which takes them in wave order; the parts' states are then combined
+// across lanes (exchanges of lanes l ^ CH, l ^ 2 CH, ...): the same order every call. Part 0 applies
+// a * sigmoid(g * gs) (dory.cpp:509-512), writes the gated head to y and its sum of squares to rec[head], from which
+// the o-projection's operand takes the justnorm (dory.cpp:513-515).
 template <int CH>
 __device__ inline float xor_parts_max(float v) {
   if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
@@ -1433,17 +1436,43 @@ __device__ inline float xor_parts_sum(float v) {
   return xor32_sum(v);
 }
 
-template <int D>
-__global__ void __launch_bounds__(64) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
-                                                             const float* __restrict__ gs, float* __restrict__ y,
-                                                             float* __restrict__ rec) {
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
+                                                                 const float* __restrict__ gs, float* __restrict__ y,
+                                                                 float* __restrict__ rec) {
   constexpr int CH = D / 8, P = 64 / CH;
   static_assert(CH >= 8 && CH <= 32, "8 to 32 chunks per head");
-  const int h = blockIdx.x, lane = threadIdx.x, c = h * CH + lane % CH, p = lane / CH;
+  __shared__ float hand[W > 1 ? (W - 1) * 10 * 64 : 1];   // waves 1 .. W - 1: [wave][M, L, o[8]][lane]
+  const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = h * CH + lane % CH, p = wave * P + lane / CH;
+  // the gate's inputs first (every wave: no load behind a branch; wave 0 uses them)
   const float4 g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
   const float4 s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
   float M, L, o[8];
-  merge8_state<D, 8>(a.acc, a.ml, chunk_rec0<D>(a, 0, c), a.qpad, p, P, a.splits1, (8 * c) % D, M, L, o);
+  merge8_state<D, 8>(a.acc, a.ml, chunk_rec0<D>(a, 0, c), a.qpad, p, W * P, a.splits1, (8 * c) % D, M, L, o);
+  if constexpr (W > 1) {
+    if (wave > 0) {
+      float* hp = hand + (wave - 1) * 10 * 64 + lane;
+      hp[0] = M;
+      hp[64] = L;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hp[(2 + e) * 64] = o[e];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w) {
+      const float* hp = hand + w * 10 * 64 + lane;
+      const float M2 = hp[0];
+      const float mn = fmaxf(M, M2);
+      if (mn == -INFINITY) continue;
+      const float f1 = exp2_fast(M - mn), f2 = exp2_fast(M2 - mn);   // -inf: 0
+      L = L * f1 + hp[64] * f2;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = o[e] * f1 + hp[(2 + e) * 64] * f2;
+      M = mn;
+    }
+  }
   const float Mh = xor_parts_max<CH>(M);
   const float f = M == -INFINITY ? 0.f : exp2_fast(M - Mh);
   const float Lh = xor_parts_sum<CH>(L * f);
@@ -1498,10 +1527,13 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
   // the global layers) take 1.6 % off the one-token step at 32K and 0.7 % at 8K against 128 (the 8-row step: 0.6 %
   // faster at 32K, 0.4 % slower at 8K), 256 and 384 are slower; one tile per wave on the 1088-slot rings (9 splits
   // instead of 5) takes 1-1.3 % off the 8-row step, while on the global layers it doubles the partials at 4K and
-  // costs 2 %.
+  // costs 2 %. A one-row scan of an E4M3 cache by position is bound by the codes' conversion, not by the merge: 512
+  // work-groups there take 1.2 % off the one-token step at 32K (1.098 -> 1.085 ms; 0.2 % at 8K), while at 8 rows
+  // they cost 4 %.
   // (XTG_ATTN_SPLITS=n fixes the count, for experiments)
   if (p.tiles > 0) {
-    const int want = std::max(1, 192 / (c.kv_heads * p.blocks));   // about 192 work-groups over all blocks
+    const int wgs = c.fp8 && !c.ring && n_q == 1 ? 512 : 192;
+    const int want = std::max(1, wgs / (c.kv_heads * p.blocks));   // about wgs work-groups over all blocks
     const int mt = c.ring ? 1 : 2;
     p.splits = std::max(1, std::min(want, (p.tiles + mt * kWaves - 1) / (mt * kWaves)));
     if (const char* env = std::getenv("XTG_ATTN_SPLITS")) p.splits = std::max(1, std::atoi(env));
@@ -1883,17 +1915,20 @@ std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* pa
   auto al = [](const void* x) { return reinterpret_cast<uintptr_t>(x) % 16 == 0; };
   XTG_CHECK(g && gs && y && rec && al(g) && al(gs) && al(y), "attention gate by heads: 16-byte aligned rows");
   const MergeArgs a = merge_args(p, heads, part);
-  const dim3 grid{unsigned(heads)}, block{64u};
-  if (p.d == 64)
-    hipLaunchKernelGGL((attn_gate_heads_kernel<64>), grid, block, 0, stream, a, g, gs, y, rec);
-  else if (p.d == 128)
-    hipLaunchKernelGGL((attn_gate_heads_kernel<128>), grid, block, 0, stream, a, g, gs, y, rec);
-  else if (p.d == 256)
-    hipLaunchKernelGGL((attn_gate_heads_kernel<256>), grid, block, 0, stream, a, g, gs, y, rec);
-  else
-    XTG_CHECK(false, "attention gate by heads: head_dim %d", p.d);
+  XTG_CHECK(p.d == 64 || p.d == 128 || p.d == 256, "attention gate by heads: head_dim %d", p.d);
+  // waves per head: enough parts (64 / (d / 8) per wave) for the records to fit one batch of 8 each, at most 4
+  const int parts = (a.splits1 + 7) / 8, per_wave = 64 / (p.d / 8);
+  const int need = (parts + per_wave - 1) / per_wave;
+  const int w = need <= 1 ? 1 : need <= 2 ? 2 : 4;
+  const dim3 grid{unsigned(heads)}, block{unsigned(64 * w)};
+#define XTG_GATE_HEADS(D, W)                                                                       \
+  if (p.d == D && w == W) hipLaunchKernelGGL((attn_gate_heads_kernel<D, W>), grid, block, 0, stream, a, g, gs, y, rec);
+  XTG_GATE_HEADS(64, 1) XTG_GATE_HEADS(64, 2) XTG_GATE_HEADS(64, 4)
+  XTG_GATE_HEADS(128, 1) XTG_GATE_HEADS(128, 2) XTG_GATE_HEADS(128, 4)
+  XTG_GATE_HEADS(256, 1) XTG_GATE_HEADS(256, 2) XTG_GATE_HEADS(256, 4)
+#undef XTG_GATE_HEADS
   HIP_CHECK(hipGetLastError());
-  return strf("attn_gate_heads_kernel<%d>", p.d);
+  return strf("attn_gate_heads_kernel<%d, %d>", p.d, w);
 }
 
 }  // namespace xtg::hip
