@@ -85,7 +85,8 @@ def test_noalloc_matches_attention_two_calls(hip, dtype):
 
 
 def test_noalloc_refuses_more_than_its_scratch(hip, pkg):
-    """512 rows over 8 KV heads of 128 (64 row blocks) need about 17 MB of partials: more than the 16 MiB array."""
+    """512 rows over 8 KV heads of 128 (64 row blocks, one key split and four own-key chunks) need about 43 MB of
+    partials: more than the 16 MiB array."""
     rng = np.random.default_rng(702)
     cache, (q, k, v, out) = make_case(hip, rng, 4096, 512)
     with pytest.raises(pkg.XtgError, match="fixed scratch holds"):

@@ -958,7 +958,10 @@ __device__ inline void write_partial(float* acc, float* ml, size_t rec, float M,
 }
 
 // Own keys on the matrix cores (FP32 MFMA 16x16x4), for calls of many rows: one wave per tile of 16 q-cols of a
-// row block, over every own key any of its columns sees, 16 keys a step.
+// row block and chunk of kOwnChunk keys of the range any of its columns sees (from the range's first key), 16 keys
+// a step; each chunk leaves its own partial record (own-key record `splits + chunk`), an empty chunk the record of
+// no key (max -inf, sum 0), which the merges skip. Chunks put several waves on a SIMD where one wave per column
+// tile had every step wait for its loads.
 //   S^T (16 keys x 16 q-cols) = K Q^T: at step s lane group g (lane / 16) feeds dim (D / 4) g + s of key / q-col
 //   lane % 16, so each lane's K and Q values are D / 4 contiguous floats; lane (g, j) gets S^T[key 4 g + r][col j].
 //   O^T (D x 16 q-cols) += V^T P^T: step r sums keys 4 g + r over the lane groups, so P^T comes straight from the
@@ -973,6 +976,7 @@ struct OwnArgs {
   float* ml;
   size_t blk_records;
   int b0, nblocks, rpb, n_own, heads, kv_heads, group, window, splits, splits1, qpad, tiles;   // tiles per block
+  int own;                 // key chunks per column tile
   float scale2;
 };
 
@@ -981,10 +985,11 @@ __global__ void __launch_bounds__(256) attn_own_mfma_kernel(const OwnArgs a) {
   constexpr int S = D / 4, T = D / 16;
   const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
   const int w = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
-  const int per_blk = a.kv_heads * a.tiles;
+  const int per_blk = a.kv_heads * a.tiles * a.own;
   if (w >= per_blk * a.nblocks) return;   // no barriers below: a spare wave just leaves
-  // the last (longest) blocks first
-  const int blk = a.b0 + a.nblocks - 1 - w / per_blk, kvh = (w % per_blk) / a.tiles, tile = w % a.tiles;
+  // the last (longest) blocks first; a tile's chunks in consecutive waves (one work-group shares its q loads)
+  const int blk = a.b0 + a.nblocks - 1 - w / per_blk, ct = (w % per_blk) / a.own, chunk = w % a.own;
+  const int kvh = ct / a.tiles, tile = ct % a.tiles;
   const int row0 = blk * a.rpb, n_rows = min(a.rpb, a.n_own - row0), cols = n_rows * a.group;
   const int qc = tile * 16 + j;
   if (tile * 16 >= cols) return;           // a padding tile of the block
@@ -993,7 +998,8 @@ __global__ void __launch_bounds__(256) attn_own_mfma_kernel(const OwnArgs a) {
   const int lo = a.window > 0 ? max(0, i - a.window + 1) : 0;
   // the tile's key range: its rows run from the first column's to the last live column's
   const int i_first = row0 + (tile * 16) / a.group, i_last = row0 + (min(tile * 16 + 15, cols - 1)) / a.group;
-  const int kmin = a.window > 0 ? max(0, i_first - a.window + 1) : 0, kmax = i_last + 1;
+  const int k0 = a.window > 0 ? max(0, i_first - a.window + 1) : 0;
+  const int kmin = k0 + chunk * kOwnChunk, kmax = min(i_last + 1, kmin + kOwnChunk);   // this chunk's keys
 
   float qv[S];
   {
@@ -1069,7 +1075,7 @@ __global__ void __launch_bounds__(256) attn_own_mfma_kernel(const OwnArgs a) {
   L += __shfl_xor(L, 16);
   L += __shfl_xor(L, 32);
   if (!live) return;
-  const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(a.splits)) * size_t(a.qpad) + size_t(qc);
+  const size_t rec = (size_t(kvh) * size_t(a.splits1) + size_t(a.splits + chunk)) * size_t(a.qpad) + size_t(qc);
   float* acc = a.acc + size_t(blk) * a.blk_records * D + rec * D;
   if (g == 0) *reinterpret_cast<float2*>(a.ml + (size_t(blk) * a.blk_records + rec) * 2) = make_float2(M, L);
 #pragma unroll
@@ -1541,6 +1547,11 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
   } else {
     p.splits = 0;
   }
+  // own keys: a column tile's key range is at most the call's rows, or with a window the window and the block's
+  // other rows; the matrix-core own-key kernel takes it in chunks of kOwnChunk keys, a wave each (the producer of a
+  // call of up to kProdRows rows writes the one record itself)
+  const int own_range = window > 0 ? int(std::min<long long>(n_q, (long long)window + p.rpb - 1)) : n_q;
+  p.own = std::max(1, (own_range + kOwnChunk - 1) / kOwnChunk);
   return p;
 }
 
@@ -1654,7 +1665,7 @@ size_t scan_lds_bytes(int d, int qb, bool rawq) {
 }
 
 
-size_t blk_records(const AttnPlan& p) { return size_t(p.kv_heads) * size_t(p.splits + 1) * size_t(p.qpad); }
+size_t blk_records(const AttnPlan& p) { return size_t(p.kv_heads) * size_t(p.splits + p.own) * size_t(p.qpad); }
 
 MergeArgs merge_args(const AttnPlan& p, int heads, const float* part) {
   MergeArgs a;
@@ -1664,7 +1675,7 @@ MergeArgs merge_args(const AttnPlan& p, int heads, const float* part) {
   a.group = p.group;
   a.rpb = p.rpb;
   a.kv_heads = p.kv_heads;
-  a.splits1 = p.splits + 1;
+  a.splits1 = p.splits + p.own;
   a.qpad = p.qpad;
   return a;
 }
@@ -1693,7 +1704,7 @@ ScanArgs scan_args(const DevKv& c, const AttnPlan& p, int b0, const float* q, in
   a.group = p.group;
   a.window = window;
   a.splits = p.splits;
-  a.splits1 = p.splits + 1;
+  a.splits1 = p.splits + p.own;
   a.qpad = p.qpad;
   a.slots_pad = c.slots_pad;
   a.tile_lo = p.tile_lo;
@@ -1709,6 +1720,7 @@ ProduceArgs produce_args(const DevKv& c, const AttnPlan& p, float* q, const floa
   XTG_CHECK(m >= 1 && m <= kProdRows, "producer: %d rows (1..%d)", m, kProdRows);
   XTG_CHECK(p.group <= kProdGroup, "producer: %d query heads per KV head", p.group);
   XTG_CHECK(!store || !c.ring || c.slots >= m, "producer: %d rows into a %lld-slot ring", m, c.slots);
+  XTG_CHECK(p.own == 1, "producer: %d own-key records (one)", p.own);
   ProduceArgs a{};
   a.q = q;
   a.k = k;
@@ -1721,7 +1733,7 @@ ProduceArgs produce_args(const DevKv& c, const AttnPlan& p, float* q, const floa
   a.window = window;
   a.rpb = p.rpb;
   a.splits = p.splits;
-  a.splits1 = p.splits + 1;
+  a.splits1 = p.splits + p.own;
   a.qpad = p.qpad;
   a.store = store ? 1 : 0;
   a.pos0 = pos0;
@@ -1790,11 +1802,12 @@ std::string launch_attn_own(const AttnPlan& p, int b0, int nblocks, const float*
   a.group = p.group;
   a.window = window;
   a.splits = p.splits;
-  a.splits1 = p.splits + 1;
+  a.splits1 = p.splits + p.own;
   a.qpad = p.qpad;
   a.tiles = p.qpad / 16;
+  a.own = p.own;
   a.scale2 = scale * kLog2e;
-  const long long waves = (long long)p.kv_heads * a.tiles * nblocks;
+  const long long waves = (long long)p.kv_heads * a.tiles * p.own * nblocks;
   const dim3 grid{unsigned((waves + 3) / 4)}, block{256};
   if (p.d == 64)
     hipLaunchKernelGGL(attn_own_mfma_kernel<64>, grid, block, 0, stream, a);

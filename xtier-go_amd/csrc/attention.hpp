@@ -39,18 +39,21 @@ std::string launch_kv_store(const DevKv& c, long long pos, int n, const float* k
                             hipStream_t stream);
 
 // How one attention call (n_q query rows at pos0) is cut up. Query rows go in blocks of rpb rows (at most 32
-// (row, head) columns per KV head); each block's key tiles go to `splits` work-groups per KV head, plus one more
-// partial per (block, KV head) for this call's own keys. Partials: acc [blocks][kv_heads][splits + 1][qpad][d]
-// then (max, sum) [blocks][kv_heads][splits + 1][qpad][2]; q-col (row r of the block, head g of the group) is
+// (row, head) columns per KV head); each block's key tiles go to `splits` work-groups per KV head, plus `own`
+// partials per (block, KV head) for this call's own keys (one per chunk of kOwnChunk keys of a column tile's key
+// range; chunks with no key leave an empty record, sum 0). Partials: acc [blocks][kv_heads][splits + own][qpad][d]
+// then (max, sum) [blocks][kv_heads][splits + own][qpad][2]; q-col (row r of the block, head g of the group) is
 // r * group + g.
+constexpr int kOwnChunk = 128;
 struct AttnPlan {
   int group = 1;               // q heads per KV head
   int rpb = 1, blocks = 1;     // rows per block, blocks
   int qpad = 16;               // q-cols per block, padded to 16
   int tile_lo = 0, tiles = 0;  // the 32-slot tiles to scan
   int splits = 0;              // work-groups per KV head over the tiles (0: no cached key is visible)
+  int own = 1;                 // own-key records per (block, KV head, q-col), after the splits'
   int kv_heads = 1, d = 64;
-  size_t records() const { return size_t(blocks) * size_t(kv_heads) * size_t(splits + 1) * size_t(qpad); }
+  size_t records() const { return size_t(blocks) * size_t(kv_heads) * size_t(splits + own) * size_t(qpad); }
   size_t part_floats() const { return records() * size_t(d + 2); }
 };
 AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int window);
