@@ -274,8 +274,9 @@ def read_floor(pkg, hip, reps):
 
 
 def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
-    """Decode attention over global caches and sliding rings through xtg_hip_attention (own-key, scan and merge
-    launches, each between events on the backend's stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
+    """Decode attention over global caches and sliding rings through xtg_hip_attention (a call of one row block: its
+    own keys and the scan in one launch, then the merge by heads; each launch between events on the backend's
+    stream), 32 q / 8 KV heads of 128, unit-norm K / V / q:
     - global caches of 4K / 8K / 32K positions, 1 and 8 new rows at positions ctx ..;
     - a 1088-slot ring after 40000 decoded positions (slots hold 38912 .. 39999), window 1024, 1 and 8
       rows at 40000 ..; the q / k producer (RoPE, per-head norm, qscale) timed beside it (xtg_hip_qk_rope_norm).
@@ -283,7 +284,8 @@ def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
     every call streams the cache from HBM. Algorithmic bytes: the visible K and V (ctx positions, or the whole ring)
     at 2 bytes (BF16) or 1 byte plus a 4-byte scale per (position, head) for each of K and V (FP8), plus q, the new k
     and v, and out in FP32; the roofline fraction is that over the scan launch's time (the launch that streams the
-    cache). The reference's CPU attention (oracle/_ref) on the same inputs beside it."""
+    cache: the scan, or the own keys and scan in one launch). The reference's CPU attention (oracle/_ref) on the
+    same inputs beside it."""
     heads, kvh, d = 32, 8, 128
     rng = np.random.default_rng(61)
     out = {}
@@ -325,7 +327,7 @@ def decode_attention_bench(pkg, wl, hip, reps, cpu_seconds):
                 hip.profile(False)
                 calls = reps * copies
                 kern = {kk: round(v["ms"] * 1e3 / v["calls"], 3) for kk, v in rep.items()}
-                scan = [kk for kk in rep if kk.startswith("attn_scan_kernel")][0]
+                scan = [kk for kk in rep if kk.startswith(("attn_scan_kernel", "attn_step_kernel"))][0]
                 attn_us = sum(v["ms"] for kk, v in rep.items() if kk.startswith("attn_")) * 1e3 / calls
                 visible = ring if ring else ctx
                 b = visible * per_pos + 4 * d * (2 * heads * n_q + 2 * kvh * n_q)

@@ -125,6 +125,37 @@ def test_decode_global_cache_fp8(hip, orc, ctx, n_q):
     assert rel_l2(out, ref) <= 1e-5
 
 
+# Calls of one row block with cached keys take their own keys and the scan in one launch and the merge by heads;
+# XTG_ATTN_UNFUSED=1 takes the own-key, scan and merge launches. (heads, kv_heads, d, cached, n_q, window, fp8)
+ONE_BLOCK = [(32, 8, 128, 4096, 1, 0, 0), (32, 8, 128, 4096, 8, 0, 1), (32, 8, 128, 3000, 5, 1024, 0),
+             (16, 4, 256, 700, 5, 64, 1), (8, 2, 64, 500, 3, 0, 0), (16, 2, 128, 700, 4, 0, 1),
+             (32, 8, 128, 0, 8, 0, 0)]
+
+
+@pytest.mark.parametrize("heads,kvh,d,cached,n_q,window,fp8", ONE_BLOCK)
+def test_one_block_call_fused_and_three_launches(hip, orc, monkeypatch, heads, kvh, d, cached, n_q, window, fp8):
+    """The same call both ways on the same inputs: the launches name the path taken (one launch for the own keys
+    and the scan, then attn_merge_heads_kernel; with nothing cached the three launches either way), the two outputs
+    agree within 2e-6 and each is within the oracle bar of 1e-5."""
+    outs = []
+    for unfused in (False, True):
+        if unfused:
+            monkeypatch.setenv("XTG_ATTN_UNFUSED", "1")
+        rng = np.random.default_rng(900 + heads + d + cached + n_q + window + fp8)
+        hip.profile(True, launches=True)
+        out, ref, _ = run_case(hip, orc, cached, n_q, window, heads, kvh, d, None, rng, unit=True, fp8=bool(fp8))
+        _, launches = hip.profile_report(launches=True)
+        hip.profile(False)
+        names = [n for n, _ in launches]
+        fused = any(n.startswith("attn_step_kernel") for n in names)
+        assert fused == (cached > 0 and not unfused), names
+        assert any(n.startswith("attn_merge_heads_kernel") for n in names) == fused, names
+        assert rel_l2(out, ref) <= 1e-5
+        outs.append(out)
+    monkeypatch.delenv("XTG_ATTN_UNFUSED")
+    assert rel_l2(outs[0], outs[1]) <= 2e-6
+
+
 # The real Dory 4B's attention (docs/dory.md:13): 16 q heads over 4 KV heads of 256. (cached, n_q, window, FP8):
 # decode and verify steps over global caches, a prefill chunk, sliding windows over rings of window + 16 slots
 # (the CPU session's ring, packs/dory/dory.cpp:43, 449), a call with nothing cached.

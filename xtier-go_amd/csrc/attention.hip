@@ -238,6 +238,8 @@ struct ScanArgs {
   float scale2;            // scale * log2(e)
   const float2* rope;      // raw q rows only (the decode step's fused launch): the RoPE rows [pos][d / 2]
   const float* qscale;     //   and the per-dim q scale [heads * d] (NULL: none)
+  int plain;               // raw q rows used as they are (the attention call's fused launch): rope is one identity
+                           //   row (cos 1, sin 0), read for every position, and no norm
 };
 
 // FP32 -> BF16 on the vector ALU (v_cvt_pk_bf16_f32, round to nearest even) and back (exact).
@@ -714,7 +716,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     // every load first: the q-col's pairs, their scales and their angles' (cos, sin) from the position's row
     float x1[PP], x2[PP], s1[PP], s2[PP], cs[PP], sn[PP];
     const float* qp = qrows + (size_t(vrow) * size_t(a.heads) + size_t(vh)) * D;
-    const float2* rp = a.rope + size_t(a.pos0 + row0 + vrow) * HALF + p0;
+    const float2* rp = a.rope + (a.plain ? size_t(0) : size_t(a.pos0 + row0 + vrow) * HALF) + p0;
 #pragma unroll
     for (int e = 0; e < PP; e += 2) {   // PP consecutive pairs at a multiple of PP: 16-byte loads
       const float4 r = *reinterpret_cast<const float4*>(rp + e);
@@ -750,7 +752,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     ss += dpp<kDppXor2>(ss);
     ss += dpp<kDppHalfMirror>(ss);
     if constexpr (TPV == 16) ss += dpp<kDppMirror>(ss);
-    const float f = inv_norm_of(ss);
+    const float f = a.plain ? 1.f : inv_norm_of(ss);
 #pragma unroll
     for (int e = 0; e < PP; e += 2) {
       *reinterpret_cast<float2*>(sq + v * SQS + p0 + e) = make_float2((x1[e] * f) * s1[e], (x1[e + 1] * f) * s1[e + 1]);
@@ -1107,6 +1109,8 @@ struct ProduceArgs {
   float* ml;
   size_t blk_records;      // records per row block
   int write_q;             // write the processed q rows back in place
+  int plain;               // q, k used as they are (the attention call's fused launch; no store, kout or write_q):
+                           //   rope is one identity row, read for every position, and no norm
 };
 
 // LDS of one producer work-group: row r's processed q heads, the k and v rows it attends to.
@@ -1149,7 +1153,7 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
     const float* p = is_q ? a.q + (size_t(r) * size_t(a.heads) + size_t(h)) * D
                           : a.k + (size_t(j0 + idx - a.group) * size_t(a.kv_heads) + size_t(kvh)) * D;
     const int t = is_q ? nk - 1 : idx - a.group;   // table row: row r for q, row j0 + t for k
-    const float2* rp = a.rope + size_t(a.pos0 + j0 + t) * HALF;
+    const float2* rp = a.rope + (a.plain ? size_t(0) : size_t(a.pos0 + j0 + t) * HALF);
 #pragma unroll
     for (int u = 0; u < PR; ++u) {
       cs[it][u] = rp[l + 64 * u];
@@ -1197,7 +1201,7 @@ __device__ inline void produce_row(const ProduceArgs& a, int kvh, int r, float* 
       o2[u] = x2[it][u] * c + x1[it][u] * s;
       ss += o1[u] * o1[u] + o2[u] * o2[u];
     }
-    const float f = inv_norm_of(wave_sum(on ? ss : 0.f));
+    const float f = a.plain ? 1.f : inv_norm_of(wave_sum(on ? ss : 0.f));
 #pragma unroll
     for (int u = 0; u < PR; ++u) {
       o1[u] *= f;
@@ -1428,7 +1432,9 @@ __global__ void __launch_bounds__(kMergeThreads) attn_gate_kernel(const MergeArg
 // their lanes' states to wave 0 through LDS, which takes them in wave order; the parts' states are then combined
 // across lanes (exchanges of lanes l ^ CH, l ^ 2 CH, ...): the same order every call. Part 0 applies
 // a * sigmoid(g * gs) (dory.cpp:509-512), writes the gated head to y and its sum of squares to rec[head], from which
-// the o-projection's operand takes the justnorm (dory.cpp:513-515).
+// the o-projection's operand takes the justnorm (dory.cpp:513-515). Without GATE the same merge is the attention
+// call's (kv.cpp:262-285) for a call of one row block: head blockIdx.x of row blockIdx.y, merged, into y
+// [rows][heads * D].
 template <int CH>
 __device__ inline float xor_parts_max(float v) {
   if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
@@ -1442,20 +1448,23 @@ __device__ inline float xor_parts_sum(float v) {
   return xor32_sum(v);
 }
 
-template <int D, int W>
-__global__ void __launch_bounds__(64 * W) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
-                                                                 const float* __restrict__ gs, float* __restrict__ y,
-                                                                 float* __restrict__ rec) {
+template <int D, int W, bool GATE>
+__device__ inline void merge_heads(const MergeArgs& a, const float* __restrict__ g, const float* __restrict__ gs,
+                                   float* __restrict__ y, float* __restrict__ rec) {
   constexpr int CH = D / 8, P = 64 / CH;
   static_assert(CH >= 8 && CH <= 32, "8 to 32 chunks per head");
   __shared__ float hand[W > 1 ? (W - 1) * 10 * 64 : 1];   // waves 1 .. W - 1: [wave][M, L, o[8]][lane]
   const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = GATE ? 0 : int(blockIdx.y);
   const int c = h * CH + lane % CH, p = wave * P + lane / CH;
   // the gate's inputs first (every wave: no load behind a branch; wave 0 uses them)
-  const float4 g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
-  const float4 s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
+  float4 g0, g1, s0, s1;
+  if constexpr (GATE) {
+    g0 = *reinterpret_cast<const float4*>(g + 8 * c), g1 = *reinterpret_cast<const float4*>(g + 8 * c + 4);
+    s0 = *reinterpret_cast<const float4*>(gs + 8 * c), s1 = *reinterpret_cast<const float4*>(gs + 8 * c + 4);
+  }
   float M, L, o[8];
-  merge8_state<D, 8>(a.acc, a.ml, chunk_rec0<D>(a, 0, c), a.qpad, p, W * P, a.splits1, (8 * c) % D, M, L, o);
+  merge8_state<D, 8>(a.acc, a.ml, chunk_rec0<D>(a, row, c), a.qpad, p, W * P, a.splits1, (8 * c) % D, M, L, o);
   if constexpr (W > 1) {
     if (wave > 0) {
       float* hp = hand + (wave - 1) * 10 * 64 + lane;
@@ -1483,20 +1492,44 @@ __global__ void __launch_bounds__(64 * W) attn_gate_heads_kernel(const MergeArgs
   const float f = M == -INFINITY ? 0.f : exp2_fast(M - Mh);
   const float Lh = xor_parts_sum<CH>(L * f);
   const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
-  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  float t[8], ss = 0.f;
+  float t[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    t[e] = (xor_parts_sum<CH>(o[e] * f) * inv) * (1.f / (1.f + expf(-gv[e] * sv[e])));
-    ss += t[e] * t[e];
+  for (int e = 0; e < 8; ++e) t[e] = xor_parts_sum<CH>(o[e] * f) * inv;
+  if constexpr (!GATE) {
+    float* yr = y + size_t(row) * size_t(gridDim.x) * D;
+    if (p == 0) {
+      *reinterpret_cast<float4*>(yr + 8 * c) = make_float4(t[0], t[1], t[2], t[3]);
+      *reinterpret_cast<float4*>(yr + 8 * c + 4) = make_float4(t[4], t[5], t[6], t[7]);
+    }
+    return;
+  } else {
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      t[e] *= 1.f / (1.f + expf(-gv[e] * sv[e]));
+      ss += t[e] * t[e];
+    }
+    if (p == 0) {
+      *reinterpret_cast<float4*>(y + 8 * c) = make_float4(t[0], t[1], t[2], t[3]);
+      *reinterpret_cast<float4*>(y + 8 * c + 4) = make_float4(t[4], t[5], t[6], t[7]);
+    }
+    ss = wave_sum(p == 0 ? ss : 0.f);
+    if (lane == 0) rec[h] = ss;
   }
-  if (p == 0) {
-    *reinterpret_cast<float4*>(y + 8 * c) = make_float4(t[0], t[1], t[2], t[3]);
-    *reinterpret_cast<float4*>(y + 8 * c + 4) = make_float4(t[4], t[5], t[6], t[7]);
-  }
-  ss = wave_sum(p == 0 ? ss : 0.f);
-  if (lane == 0) rec[h] = ss;
+}
+
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W) attn_gate_heads_kernel(const MergeArgs a, const float* __restrict__ g,
+                                                                 const float* __restrict__ gs, float* __restrict__ y,
+                                                                 float* __restrict__ rec) {
+  merge_heads<D, W, true>(a, g, gs, y, rec);
+}
+
+template <int D, int W>
+__global__ void __launch_bounds__(64 * W) attn_merge_heads_kernel(const MergeArgs a, float* __restrict__ out) {
+  merge_heads<D, W, false>(a, nullptr, nullptr, out, nullptr);
 }
 
 // ------------------------------------------------------------------------------------------------------- plan
@@ -1855,8 +1888,9 @@ bool attn_step_fuses(const AttnPlan& p, int m) {
 std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
                              float* kout, int m, int heads, long long pos0, int window, float scale,
                              const float2* rope, const float* qscale, bool store, float* part,
-                             hipStream_t stream) {
+                             hipStream_t stream, bool plain) {
   XTG_CHECK(rope, "attention step: no RoPE table");
+  XTG_CHECK(!plain || (!store && !kout && !qscale), "attention step: q and k as they are take no store, kout or qscale");
   XTG_CHECK(attn_step_fuses(p, m), "attention step: %d rows in %d blocks, %d splits: no fused launch", m, p.blocks,
             p.splits);
   XTG_CHECK(p.splits <= p.tiles, "attention: %d splits over %d tiles", p.splits, p.tiles);
@@ -1868,6 +1902,7 @@ std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const 
   a.qscale = qscale;
   ProduceArgs pa = produce_args(c, p, q, k, v, kout, m, heads, pos0, window, scale, rope, qscale, store, part);
   pa.write_q = 0;   // the scan work-groups read q raw while the producers run
+  a.plain = pa.plain = plain ? 1 : 0;
   const int vpw = produce_vpw(p, m, window);
   const int qb = (m * p.group + 15) / 16;
   const dim3 grid{unsigned(c.kv_heads * p.splits + c.kv_heads * m)}, block{unsigned(kWaves * 64)};
@@ -1922,6 +1957,14 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
   return strf("attn_gate_kernel<%d, %d>", p.d, u);
 }
 
+// waves per head of a merge by heads: enough parts (64 / (d / 8) per wave) for a column's records to fit one batch of
+// 8 each, at most 4
+int merge_heads_waves(const AttnPlan& p, int records) {
+  const int parts = (records + 7) / 8, per_wave = 64 / (p.d / 8);
+  const int need = (parts + per_wave - 1) / per_wave;
+  return need <= 1 ? 1 : need <= 2 ? 2 : 4;
+}
+
 std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* part, const float* g, const float* gs,
                                    float* y, float* rec, hipStream_t stream) {
   XTG_CHECK(p.blocks == 1, "attention gate by heads: one query row");
@@ -1929,19 +1972,37 @@ std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* pa
   XTG_CHECK(g && gs && y && rec && al(g) && al(gs) && al(y), "attention gate by heads: 16-byte aligned rows");
   const MergeArgs a = merge_args(p, heads, part);
   XTG_CHECK(p.d == 64 || p.d == 128 || p.d == 256, "attention gate by heads: head_dim %d", p.d);
-  // waves per head: enough parts (64 / (d / 8) per wave) for the records to fit one batch of 8 each, at most 4
-  const int parts = (a.splits1 + 7) / 8, per_wave = 64 / (p.d / 8);
-  const int need = (parts + per_wave - 1) / per_wave;
-  const int w = need <= 1 ? 1 : need <= 2 ? 2 : 4;
+  const int w = merge_heads_waves(p, a.splits1);
   const dim3 grid{unsigned(heads)}, block{unsigned(64 * w)};
-#define XTG_GATE_HEADS(D, W)                                                                       \
-  if (p.d == D && w == W) hipLaunchKernelGGL((attn_gate_heads_kernel<D, W>), grid, block, 0, stream, a, g, gs, y, rec);
+#define XTG_GATE_HEADS(D, W)                                                                                  \
+  if (p.d == D && w == W)                                                                                     \
+    hipLaunchKernelGGL((attn_gate_heads_kernel<D, W>), grid, block, 0, stream, a, g, gs, y, rec);
   XTG_GATE_HEADS(64, 1) XTG_GATE_HEADS(64, 2) XTG_GATE_HEADS(64, 4)
   XTG_GATE_HEADS(128, 1) XTG_GATE_HEADS(128, 2) XTG_GATE_HEADS(128, 4)
   XTG_GATE_HEADS(256, 1) XTG_GATE_HEADS(256, 2) XTG_GATE_HEADS(256, 4)
 #undef XTG_GATE_HEADS
   HIP_CHECK(hipGetLastError());
   return strf("attn_gate_heads_kernel<%d, %d>", p.d, w);
+}
+
+std::string launch_attn_merge_heads(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
+                                    hipStream_t stream) {
+  XTG_CHECK(p.blocks == 1 && n_q >= 1 && n_q <= p.rpb, "attention merge by heads: %d rows in %d blocks", n_q,
+            p.blocks);
+  XTG_CHECK(p.d == 64 || p.d == 128 || p.d == 256, "attention merge by heads: head_dim %d", p.d);
+  XTG_CHECK(reinterpret_cast<uintptr_t>(out) % 16 == 0, "attention merge by heads: 16-byte aligned out");
+  const MergeArgs a = merge_args(p, heads, part);
+  const int w = merge_heads_waves(p, a.splits1);
+  const dim3 grid{unsigned(heads), unsigned(n_q)}, block{unsigned(64 * w)};
+#define XTG_MERGE_HEADS(D, W)                                                                                 \
+  if (p.d == D && w == W)                                                                                     \
+    hipLaunchKernelGGL((attn_merge_heads_kernel<D, W>), grid, block, 0, stream, a, out);
+  XTG_MERGE_HEADS(64, 1) XTG_MERGE_HEADS(64, 2) XTG_MERGE_HEADS(64, 4)
+  XTG_MERGE_HEADS(128, 1) XTG_MERGE_HEADS(128, 2) XTG_MERGE_HEADS(128, 4)
+  XTG_MERGE_HEADS(256, 1) XTG_MERGE_HEADS(256, 2) XTG_MERGE_HEADS(256, 4)
+#undef XTG_MERGE_HEADS
+  HIP_CHECK(hipGetLastError());
+  return strf("attn_merge_heads_kernel<%d, %d>", p.d, w);
 }
 
 }  // namespace xtg::hip

@@ -96,11 +96,13 @@ std::string launch_qk_produce(const DevKv& c, const AttnPlan& p, float* q, const
 // launch_attn_scan, except that q is not written back): for a call of one row block with cached keys to scan
 // (attn_step_fuses). The store may run concurrently with the scan only under the store-first condition above;
 // otherwise pass store = false and kout, and store after.
+// plain: q and k as they are (no RoPE, norms, qscale, store or kout; rope one identity row, cos 1 and sin 0): the
+// attention call's own keys and scan in one launch, for a call that attn_step_fuses.
 bool attn_step_fuses(const AttnPlan& p, int m);
 std::string launch_attn_step(const DevKv& c, const AttnPlan& p, float* q, const float* k, const float* v,
                              float* kout, int m, int heads, long long pos0, int window, float scale,
                              const float2* rope, const float* qscale, bool store, float* part,
-                             hipStream_t stream);
+                             hipStream_t stream, bool plain = false);
 // The decode step's finish (dory.cpp:509-515): every row's merge, times sigmoid(g * gscale), justnorm over the
 // heads, written to out (optional) and as a GEMV operand (optional, Backend::op_bytes(heads * d) bytes).
 std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* part, const float* g, const float* gs,
@@ -109,5 +111,9 @@ std::string launch_attn_gate(const AttnPlan& p, int m, int heads, const float* p
 // rec [heads] = each head's sum of squares (the records a kInNorm projection takes, kernels.hpp FusedGemv).
 std::string launch_attn_gate_heads(const AttnPlan& p, int heads, const float* part, const float* g, const float* gs,
                                    float* y, float* rec, hipStream_t stream);
+// The attention call's merge (launch_attn_merge) for a call of one row block, by heads: one work-group per (head,
+// row) merges that head's records with one to four waves, out [n_q][heads][d] (16-byte aligned).
+std::string launch_attn_merge_heads(const AttnPlan& p, int n_q, int heads, const float* part, float* out,
+                                    hipStream_t stream);
 
 }  // namespace xtg::hip

@@ -17,6 +17,9 @@ Backend::Backend(int device) : device_(device) {
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   attn_scratch_ = attn_scratch_ptr(device);   // with the device current, once per device
+  const std::vector<float2> ident(128, make_float2(1.f, 0.f));   // head_dim up to 256
+  HIP_CHECK(hipMalloc(&ident_rope_, ident.size() * sizeof(float2)));
+  HIP_CHECK(hipMemcpy(ident_rope_, ident.data(), ident.size() * sizeof(float2), hipMemcpyHostToDevice));
 }
 
 Backend::~Backend() {
@@ -33,7 +36,7 @@ Backend::~Backend() {
   for (auto& kv : weights_) (void)hipFree(kv.second.tiles);
   for (auto& kv : bf16_weights_) (void)hipFree(kv.second.tiles);
   for (void* p : allocs_) (void)hipFree(p);
-  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_, sample_})
+  for (void* p : {op_, opb_, hx_, hy_, part_, kproc_, stage_, sample_, static_cast<void*>(ident_rope_)})
     if (p) (void)hipFree(p);
   for (void* p : retired_) (void)hipFree(p);
   for (DevKv* c : kvs_) {
@@ -546,7 +549,21 @@ void Backend::attention_noalloc(const DevKv* c, int n_q, long long pos0, int hea
             "attention_noalloc: another open backend on device %d uses the device's fixed scratch (calls from two "
             "backends would race on it); close that backend first",
             device_);
-  float* part = static_cast<float*>(attn_scratch_);
+  attention_launches(c, p, n_q, pos0, heads, window, scale, q, k, v, out, static_cast<float*>(attn_scratch_));
+}
+
+void Backend::attention_launches(const DevKv* c, const AttnPlan& p, int n_q, long long pos0, int heads, int window,
+                                 float scale, const float* q, const float* k, const float* v, float* out,
+                                 float* part) {
+  if (attn_step_fuses(p, n_q) && !std::getenv("XTG_ATTN_UNFUSED")) {
+    // the producer's work-groups take the own keys from q and k as they are (write_q off: q is only read)
+    timed([&] {
+      return launch_attn_step(*c, p, const_cast<float*>(q), k, v, nullptr, n_q, heads, pos0, window, scale,
+                              ident_rope_, nullptr, false, part, stream_, true);
+    });
+    timed([&] { return launch_attn_merge_heads(p, n_q, heads, part, out, stream_); });
+    return;
+  }
   timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_); });
   if (p.splits > 0)
     timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_); });
@@ -558,12 +575,8 @@ void Backend::attention(const DevKv* c, int n_q, long long pos0, int heads, int 
   check_attention(c, n_q, pos0, q, k, v, out);
   const AttnPlan p = attn_plan(*c, n_q, heads, pos0, window);
   ensure(part_, part_size_, p.part_floats() * sizeof(float));
-  float* part = static_cast<float*>(part_);
   // every row block in one launch each (the last block may be partial: its q-cols past the rows are masked)
-  timed([&] { return launch_attn_own(p, 0, p.blocks, q, k, v, n_q, heads, window, scale, part, stream_); });
-  if (p.splits > 0)
-    timed([&] { return launch_attn_scan(*c, p, 0, p.blocks, q, n_q, heads, pos0, window, scale, part, stream_); });
-  timed([&] { return launch_attn_merge(p, n_q, heads, part, out, stream_); });
+  attention_launches(c, p, n_q, pos0, heads, window, scale, q, k, v, out, static_cast<float*>(part_));
 }
 
 void Backend::attn_step(DevKv* c, int m, long long pos0, int heads, int window, float scale, float theta, float* q,

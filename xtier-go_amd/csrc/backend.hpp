@@ -166,7 +166,13 @@ class Backend {
   void ensure(void*& buf, size_t& size, size_t need);
   void check_attention(const DevKv* c, int n_q, long long pos0, const float* q, const float* k, const float* v,
                        const float* out) const;
+  // the attention call's launches on partials `part`: for a call of one row block with cached keys to scan, its own
+  // keys and the scan in one launch and the merge by heads (XTG_ATTN_UNFUSED=1: the three launches below); else
+  // the own keys, the scan and the merge
+  void attention_launches(const DevKv* c, const AttnPlan& p, int n_q, long long pos0, int heads, int window,
+                          float scale, const float* q, const float* k, const float* v, float* out, float* part);
   void* attn_scratch_ = nullptr;   // this device's fixed attention scratch (device address)
+  float2* ident_rope_ = nullptr;   // one RoPE row of 128 identity pairs (cos 1, sin 0): q and k taken as they are
   // frees device memory now (after queued work), or retires it until no graph exists
   void dev_free(void* p);
   void drop_weight(const void* key);
