@@ -1566,9 +1566,10 @@ AttnPlan attn_plan(const DevKv& c, int n_q, int heads, long long pos0, int windo
   // the global layers) take 1.6 % off the one-token step at 32K and 0.7 % at 8K against 128 (the 8-row step: 0.6 %
   // faster at 32K, 0.4 % slower at 8K), 256 and 384 are slower; one tile per wave on the 1088-slot rings (9 splits
   // instead of 5) takes 1-1.3 % off the 8-row step, while on the global layers it doubles the partials at 4K and
-  // costs 2 %. A one-row scan of an E4M3 cache by position is bound by the codes' conversion, not by the merge: 512
-  // work-groups there take 1.2 % off the one-token step at 32K (1.098 -> 1.085 ms; 0.2 % at 8K), while at 8 rows
-  // they cost 4 %.
+  // costs 2 %. A one-row scan of an E4M3 cache by position has half the bytes per tile for the same conversion
+  // work: at 192 work-groups (under one wave per SIMD) its waves issued VALU for 39 % of their cycles and waited for
+  // 8 %, and 512 work-groups take 1.5 % off the one-token step at 32K (1.099 -> 1.082 ms, with the gate's merge on
+  // more waves; 0.2 % at 8K; 768 and 1024: 1.109 and 1.105 ms), while at 8 rows they cost 4 %.
   // (XTG_ATTN_SPLITS=n fixes the count, for experiments)
   if (p.tiles > 0) {
     const int wgs = c.fp8 && !c.ring && n_q == 1 ? 512 : 192;
