@@ -956,6 +956,9 @@ def main():
     ap.add_argument("--read-floor", action="store_true",
                     help="only the streaming-read roofline at the hot path's sizes (for profiling it); prints its own "
                          "JSON line")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the decode-attention calls through xtg_hip_attention (for profiling them); prints "
+                         "its own JSON line")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
                          "left out of the JSON line")
@@ -978,6 +981,15 @@ def main():
         ms = decode_eager_pass(pkg, wl, hip, int(ctx), kvs == "fp8", args.decode_reps)
         print(json.dumps({"metric": "eager decode step ms (%s caches, ctx %s)" % (kvs, ctx), "value": round(ms, 4),
                           "unit": "ms", "higher_is_better": False}))
+        hip.close()
+        return
+
+    if args.attention_only:
+        hip = pkg.HipBackend(0)
+        att = decode_attention_bench(pkg, wl, hip, 3, 0)
+        print(json.dumps({"metric": "decode attention call us (bf16 ring1088, one row)",
+                          "value": att["bf16_ring1088_q1"]["attention_us"], "unit": "us", "higher_is_better": False,
+                          "decode_attention": att}))
         hip.close()
         return
 
