@@ -304,8 +304,11 @@ __device__ inline void load_tile(KvTile<D>& T, const uint4* __restrict__ kb, con
 }
 
 // The q operand of a scan, B of the score products: column block qb, 32-dim chunk c, BF16 term t (split3). Heads of
-// up to 128 dims keep it in registers; larger heads keep it in the work-group's LDS, where all 4 waves read it (they
-// scan the same q-cols), as [qb][c][t][64 lanes] x 16 bytes.
+// more than 128 dims, and 128-dim heads in the decode step's fused launch (raw q rows), keep it in the work-group's
+// LDS, where all 4 waves read it (they scan the same q-cols), as [qb][c][t][64 lanes] x 16 bytes; other scans in
+// registers. For the fused launch that frees 48 registers per lane (the one-row FP8 kernel 218 -> 173): 0.7 % off
+// the one-token step with BF16 caches and 1.4 % with FP8 (4K-32K, the 8-row steps 0.3-1 %), while the prefill
+// scan, 16 q-cols x 2 blocks over thousands of keys, ran 10 % slower with it.
 template <int D, int QB>
 struct QRegs {
   bf16x8 q[QB][D / 32][3];
@@ -317,8 +320,8 @@ struct QLds {
   int lane;
   __device__ bf16x8 get(int qb, int c, int t) const { return base[((qb * (D / 32) + c) * 3 + t) * 64 + lane]; }
 };
-template <int D>
-constexpr bool q_in_lds() { return D > 128; }
+template <int D, bool RAWQ>
+constexpr bool q_in_lds() { return D > 128 || (RAWQ && D == 128); }
 
 // The online-softmax state of the lane's column in each q-block (the same in the 4 lanes of a column).
 template <int D, int QB>
@@ -601,13 +604,13 @@ __device__ inline void scan_tile(KvTile8<D>& T, const QS& qop, const int (&lo)[Q
   next_v(T);
 }
 
-// LDS of a scan work-group. Heads of up to 128 dims: the wave merge, then (raw q rows) the processed q-cols and the
-// rows' RoPE cosines and sines. Larger heads: the q operand first, then one region that holds the processed q-cols
-// and the RoPE table before the scan and the wave merge after it; the merge runs in passes of 128 dims.
+// LDS of a scan work-group. The q operand in registers: the wave merge, then (raw q rows) the processed q-cols and
+// the rows' RoPE cosines and sines. The q operand in LDS: the operand first, then one region that holds the processed
+// q-cols and the RoPE table before the scan and the wave merge after it; the merge runs in passes of 128 dims.
 template <int D>
 constexpr int scan_merge_passes() { return D > 128 ? D / 128 : 1; }
-template <int D, int QB>
-constexpr int scan_qop_floats() { return q_in_lds<D>() ? QB * (D / 32) * 3 * 64 * 4 : 0; }
+template <int D, int QB, bool RAWQ>
+constexpr int scan_qop_floats() { return q_in_lds<D, RAWQ>() ? QB * (D / 32) * 3 * 64 * 4 : 0; }
 template <int D, int QB>
 constexpr int scan_merge_floats() {
   return kWaves * QB * 2 * 16 + kWaves * QB * (D / 16 / scan_merge_passes<D>()) * 64 * 4;
@@ -618,12 +621,15 @@ template <int D>
 constexpr int sq_stride() { return D + 4; }
 template <int D, int QB, bool RAWQ>
 constexpr int scan_rawq_floats() { return RAWQ ? QB * 16 * sq_stride<D>() : 0; }
-template <int D, int QB>
-constexpr int scan_sq_offset() { return q_in_lds<D>() ? scan_qop_floats<D, QB>() : scan_merge_floats<D, QB>(); }
+template <int D, int QB, bool RAWQ>
+constexpr int scan_sq_offset() {
+  return q_in_lds<D, RAWQ>() ? scan_qop_floats<D, QB, RAWQ>() : scan_merge_floats<D, QB>();
+}
 template <int D, int QB, bool RAWQ>
 constexpr int scan_lds_floats() {
-  return q_in_lds<D>() ? scan_qop_floats<D, QB>() + std::max(scan_merge_floats<D, QB>(), scan_rawq_floats<D, QB, RAWQ>())
-                       : scan_merge_floats<D, QB>() + scan_rawq_floats<D, QB, RAWQ>();
+  return q_in_lds<D, RAWQ>()
+             ? scan_qop_floats<D, QB, RAWQ>() + std::max(scan_merge_floats<D, QB>(), scan_rawq_floats<D, QB, RAWQ>())
+             : scan_merge_floats<D, QB>() + scan_rawq_floats<D, QB, RAWQ>();
 }
 
 // One scan work-group (KV head, split) of a row block. RAWQ: q arrives as the projection wrote it, and the work-group
@@ -676,7 +682,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
 
   // q operands: column j of q-block qb is q-col qb * 16 + j = (row, head in the group); times scale * log2(e),
   // three terms. lo: the first stored position the column sees.
-  constexpr bool QL = q_in_lds<D>();
+  constexpr bool QL = q_in_lds<D, RAWQ>();
   std::conditional_t<QL, QLds<D, QB>, QRegs<D, QB>> qop;
   bf16x8* qlds = reinterpret_cast<bf16x8*>(lds);   // QL: the operand's LDS region
   // QL: each wave builds the chunks c = wave (mod 4) of every q-block into LDS; else every wave all of them
@@ -708,7 +714,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
     constexpr int PP = HALF / TPV;        // RoPE pairs per thread
     static_assert(PP % 2 == 0 && TPV * QB * 16 == kWaves * 64, "q-col split");
     constexpr int SQS = sq_stride<D>();
-    float* sq = lds + scan_sq_offset<D, QB>();   // processed q-cols [QB * 16][SQS]
+    float* sq = lds + scan_sq_offset<D, QB, RAWQ>();   // processed q-cols [QB * 16][SQS]
     const int v = int(threadIdx.x) / TPV, p0 = (int(threadIdx.x) % TPV) * PP;
     const bool vlive = v < qcols;
     const int vrow = vlive ? v / a.group : 0;
@@ -836,7 +842,7 @@ __device__ inline void scan_split(const ScanArgs& a, int bx, float* lds) {
   // merge the 4 waves' states in LDS: (max, sum) as [wave][qb][2][16 cols], then accumulators
   // [wave][qb][dd][64 lanes][4], NDP dim blocks at a time (one pass for heads of up to 128 dims)
   constexpr int MP = scan_merge_passes<D>(), NDP = ND / MP;
-  float* ml = lds + scan_qop_floats<D, QB>();
+  float* ml = lds + scan_qop_floats<D, QB, RAWQ>();
   float* accs = ml + kWaves * QB * 2 * 16;   // QL: the region the q-cols were processed in (read before the barrier
                                              // that completed the operand)
 #pragma unroll
