@@ -584,8 +584,8 @@ def bf16_head_bench(pkg, wl, hip, reps):
 
 def sampling_bench(pkg, hip, reps):
     """The device sampler on 131072-wide logits (the vocabulary), 1 and 8 rows: greedy (argmax), temperature only
-    (walk in index order), top_k 40 and top_p 0.9 (sorted candidates), each call (all its launches) bracketed by
-    events on the backend's stream."""
+    (walk in index order), top_k 40 and top_p 0.9 (sorted candidates); events on the backend's stream around each
+    call (its launches timed as one, under the name of the last: `kernel`)."""
     n = 131072
     rng = np.random.default_rng(51)
     x = (rng.standard_normal((8, n)) * 3).astype(np.float32)
@@ -959,6 +959,8 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="only the decode-attention calls through xtg_hip_attention (for profiling them); prints "
                          "its own JSON line")
+    ap.add_argument("--sampling-only", action="store_true",
+                    help="only the device sampler on 131072-wide logits (for profiling it); prints its own JSON line")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
                          "left out of the JSON line")
@@ -990,6 +992,15 @@ def main():
         print(json.dumps({"metric": "decode attention call us (bf16 ring1088, one row)",
                           "value": att["bf16_ring1088_q1"]["attention_us"], "unit": "us", "higher_is_better": False,
                           "decode_attention": att}))
+        hip.close()
+        return
+
+    if args.sampling_only:
+        hip = pkg.HipBackend(0)
+        samp = sampling_bench(pkg, hip, 20)
+        print(json.dumps({"metric": "top_k 40 sampling call us (one row of 131072)",
+                          "value": samp["top_k40_m1"]["us"], "unit": "us", "higher_is_better": False,
+                          "sampling": samp}))
         hip.close()
         return
 

@@ -18,16 +18,19 @@
 //
 // Design: three launches. Slices of 2048 logits (a work-group of 256 each): their maxima; then, with the row's max,
 // their weights, sums (fixed order), min_p counts and, with a filter, every thread's two most likely pairs (the
-// slice's 64 largest thread maxima sorted in LDS, and the largest second). Then
+// slice's 64 largest thread maxima in candidate order, and the largest second). Then
 // one work-group of 1024 threads per row: the slice sums in order give the total and, without a filter, the slice
 // where the running sum passes r, walked by hierarchical running sums (16 wave segments, 16 parts, tiles of 64).
 // With a filter, a threshold tau that the kept prefix cannot go below comes from the sorted union of the slices'
 // lists -- its top_k-th value for top_k, the value where its running mass first reaches total * top_p * (1 + 1e-6)
 // for top_p, the floor for min_p (max(floor, that) with both): the union is a subset of the row, so the row holds at
 // least as much above tau. When in every slice the 64th listed maximum and every thread's second lie below tau,
-// the union holds every weight >= tau, and the candidates are its sorted prefix; otherwise they are gathered from the row (at most 4096, sorted in LDS), or, past
-// that, the whole row is sorted by a stable LSD radix sort in scratch memory (8 passes of 4 bits): slower, the same
-// result. Greedy rows take the slices' first maxima (argmax_pick_kernel).
+// the union holds every weight >= tau, and the candidates are its sorted prefix; otherwise they are gathered from
+// the row (at most 4096, sorted in LDS), or, past that, the whole row is sorted by a stable LSD radix sort in scratch
+// memory (8 passes of 4 bits): slower, the same result. Sorts in LDS are merges of sorted runs of 64 (the slices'
+// lists as they come; gathered pairs sorted by the waves in registers first), one barrier per doubling of the run
+// instead of one per stage of a bitonic network over the whole set (78 for 4096 pairs). Greedy rows take the
+// slices' first maxima (argmax_pick_kernel).
 #include <cfloat>
 #include <climits>
 #include <cmath>
@@ -213,25 +216,157 @@ __device__ inline int first_crossing(WF wf, int len, double r, bool strict, doub
   return first;
 }
 
-// Bitonic sort of n2 (a power of two, <= kCand) pairs in LDS into candidate order; every thread of the work-group.
-__device__ inline void sort_pairs(float* cw, int* ci, int n2) {
-  for (int k = 2; k <= n2; k <<= 1)
+// Candidate order over (weight, index) pairs is total for distinct indices (the padding pairs (-1, INT_MAX) are
+// equal to each other), so every sort below gives the one order a sort of the reference's comparator gives.
+
+// One wave's pair (w, id) in lane l of a run of 64 sorted in registers into candidate order (lane 0 most likely):
+// a bitonic network over the lanes (partner l ^ j by shuffle), every run of 2k ascending where l & k is clear, the
+// last level all ascending. Pairs that compare equal stay where they are.
+__device__ inline void wave_sort64(float& w, int& id) {
+  const int l = int(threadIdx.x) & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      __syncthreads();
-      for (int p = int(threadIdx.x); p < n2 / 2; p += kSampleThreads) {
-        const int lo = 2 * p - (p & (j - 1)), hi = lo + j;   // lo has bit j clear
-        const bool up = (lo & k) == 0;                        // this run ascends in candidate order
-        const float wl = cw[lo], wh = cw[hi];
-        const int il = ci[lo], ih = ci[hi];
-        if (more_likely(wh, ih, wl, il) == up) {
-          cw[lo] = wh;
-          cw[hi] = wl;
-          ci[lo] = ih;
-          ci[hi] = il;
+      const float wp = __shfl_xor(w, j);
+      const int ip = __shfl_xor(id, j);
+      const bool up = k == 64 || (l & k) == 0;   // this run ascends in candidate order
+      const bool first = (l & j) == 0;            // the lower place of the pair
+      // the lower place of an ascending run (the upper of a descending one) takes the more likely pair
+      const bool take = up == first ? more_likely(wp, ip, w, id) : more_likely(w, id, wp, ip);
+      if (take) w = wp, id = ip;
+    }
+}
+
+// n2 (a power of two) pairs in LDS whose runs of `run` pairs (a power of two) are each in candidate order, merged
+// into candidate order by pairwise merges of the runs, one level per doubling. Each thread makes E = n2 / NT
+// consecutive outputs of its pair of runs (A, B), at least one: it finds by binary search on its diagonal how many
+// of A's pairs come before its first output (merge path), then merges E pairs in order; of two equal pairs A's goes
+// first. tw / ti: scratch for n2 pairs. The result is in cw / ci; every thread of the work-group (NT) takes part.
+template <int NT>
+__device__ inline void merge_runs(float* cw, int* ci, float* tw, int* ti, int n2, int run) {
+  const int E = n2 > NT ? n2 / NT : 1;
+  float* sw = cw;
+  int* si = ci;
+  float* dw = tw;
+  int* di = ti;
+  for (int L = run; L < n2; L <<= 1) {
+    __syncthreads();
+    const int o0 = int(threadIdx.x) * E;
+    if (o0 < n2) {
+      const int base = o0 & ~(2 * L - 1), d = o0 - base;
+      const float* aw = sw + base;
+      const int* ai = si + base;
+      const float* bw = aw + L;
+      const int* bi = ai + L;
+      int lo = d > L ? d - L : 0, hi = d < L ? d : L;
+      while (lo < hi) {   // A's pairs among the first d outputs: A[mid] goes first unless B[d - 1 - mid] is more likely
+        const int mid = (lo + hi) >> 1;
+        if (more_likely(bw[d - 1 - mid], bi[d - 1 - mid], aw[mid], ai[mid]))
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      int x = lo, y = d - lo;
+      float wa = x < L ? aw[x] : 0.f, wb = y < L ? bw[y] : 0.f;
+      int ia = x < L ? ai[x] : 0, ib = y < L ? bi[y] : 0;
+      for (int e = 0; e < E; ++e) {
+        const bool take_a = y >= L || (x < L && !more_likely(wb, ib, wa, ia));
+        dw[o0 + e] = take_a ? wa : wb;
+        di[o0 + e] = take_a ? ia : ib;
+        if (take_a) {
+          ++x;
+          wa = x < L ? aw[x] : 0.f;
+          ia = x < L ? ai[x] : 0;
+        } else {
+          ++y;
+          wb = y < L ? bw[y] : 0.f;
+          ib = y < L ? bi[y] : 0;
         }
       }
     }
+    float* tf = sw;
+    sw = dw;
+    dw = tf;
+    int* tn = si;
+    si = di;
+    di = tn;
+  }
   __syncthreads();
+  if (sw != cw) {   // an odd number of levels: the result back into cw / ci
+    for (int q = int(threadIdx.x); q < n2; q += NT) {
+      cw[q] = sw[q];
+      ci[q] = si[q];
+    }
+    __syncthreads();
+  }
+}
+
+// The R most likely of nr runs of R pairs each in candidate order (nr and R powers of two), in order, into cw / ci
+// [0, R): pairwise merges that keep each pair's first R, one level per halving of the runs (output d of a pair by
+// merge path on diagonal d, A's pair first of two equal ones). tw / ti: scratch for nr R / 2 pairs. Every thread of
+// the work-group (NT) takes part.
+template <int NT>
+__device__ inline void merge_top(float* cw, int* ci, float* tw, int* ti, int nr, int R) {
+  float* sw = cw;
+  int* si = ci;
+  float* dw = tw;
+  int* di = ti;
+  for (int m = nr; m > 1; m >>= 1) {
+    __syncthreads();
+    for (int q = int(threadIdx.x); q < (m >> 1) * R; q += NT) {
+      const int pr = q / R, d = q - pr * R;
+      const float* aw = sw + 2 * pr * R;
+      const int* ai = si + 2 * pr * R;
+      const float* bw = aw + R;
+      const int* bi = ai + R;
+      int lo = 0, hi = d;   // d < R: both runs can supply all d
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (more_likely(bw[d - 1 - mid], bi[d - 1 - mid], aw[mid], ai[mid]))
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      const int x = lo, y = d - lo;   // x, y < R
+      const bool take_a = !more_likely(bw[y], bi[y], aw[x], ai[x]);
+      dw[q] = take_a ? aw[x] : bw[y];
+      di[q] = take_a ? ai[x] : bi[y];
+    }
+    float* tf = sw;
+    sw = dw;
+    dw = tf;
+    int* tn = si;
+    si = di;
+    di = tn;
+  }
+  __syncthreads();
+  if (sw != cw) {
+    for (int q = int(threadIdx.x); q < R; q += NT) {
+      cw[q] = sw[q];
+      ci[q] = si[q];
+    }
+    __syncthreads();
+  }
+}
+
+// n2 (a power of two, <= kCand) pairs in LDS in any order into candidate order: runs of 64 sorted by the waves in
+// registers, then merged. tw / ti: scratch for n2 pairs. Every thread of the work-group (NT threads).
+template <int NT>
+__device__ inline void sort_pairs(float* cw, int* ci, float* tw, int* ti, int n2) {
+  const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
+  __syncthreads();   // the pairs are in
+  for (int r = wave; r * 64 < n2; r += NT / 64) {
+    const int q = r * 64 + lane;
+    float w = q < n2 ? cw[q] : -1.f;   // a run shorter than 64 (n2 < 64): padding that sorts last
+    int id = q < n2 ? ci[q] : INT_MAX;
+    wave_sort64(w, id);
+    if (q < n2) {
+      cw[q] = w;
+      ci[q] = id;
+    }
+  }
+  merge_runs<NT>(cw, ci, tw, ti, n2, n2 < 64 ? n2 : 64);
 }
 }  // namespace
 
@@ -333,8 +468,8 @@ __global__ void __launch_bounds__(64) argmax_pick_kernel(const SampleArgs a) {
 // most likely pairs: the 64 largest of the threads' first ones in candidate order (256 sorted in LDS) and the
 // largest of their second ones. Any weight of the slice at or above a threshold above both is one of those 64.
 __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const SampleArgs a) {
-  __shared__ float cw[kSliceThreads];
-  __shared__ int ci[kSliceThreads];
+  __shared__ float cw[kSliceThreads], tw[kSliceThreads];
+  __shared__ int ci[kSliceThreads], ti[kSliceThreads];
   __shared__ double dred[kSliceThreads / 64][2];
   __shared__ int ired[kSliceThreads / 64];
   __shared__ float m2red[kSliceThreads / 64];
@@ -379,25 +514,13 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
   if ((t & 63) == 0) dred[t >> 6][0] = s, dred[t >> 6][1] = sf, ired[t >> 6] = nf, m2red[t >> 6] = m2;
   const size_t so = size_t(row) * a.slices + sl;
   if (a.lists) {
-    cw[t] = w1;
-    ci[t] = i1;
-    for (int k = 2; k <= kSliceThreads; k <<= 1)
-      for (int jj = k >> 1; jj > 0; jj >>= 1) {
-        __syncthreads();
-        if (t < kSliceThreads / 2) {
-          const int lo = 2 * t - (t & (jj - 1)), hi = lo + jj;
-          const bool up = (lo & k) == 0;
-          const float wl = cw[lo], wh = cw[hi];
-          const int il = ci[lo], ih = ci[hi];
-          if (more_likely(wh, ih, wl, il) == up) {
-            cw[lo] = wh;
-            cw[hi] = wl;
-            ci[lo] = ih;
-            ci[hi] = il;
-          }
-        }
-      }
-    __syncthreads();
+    // the threads' first pairs in candidate order: each wave's 64 in registers, then merged
+    float wq = w1;
+    int iq = i1;
+    wave_sort64(wq, iq);
+    cw[t] = wq;
+    ci[t] = iq;
+    merge_runs<kSliceThreads>(cw, ci, tw, ti, kSliceThreads, 64);
     if (t < kSliceTop) {
       a.sw[so * kSliceTop + t] = cw[t];
       a.si[so * kSliceTop + t] = ci[t];
@@ -423,9 +546,11 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
 __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const SampleArgs a) {
   __shared__ double red[kSampleThreads / 64 + 4];   // >= 20
   __shared__ uint32_t ured[kSampleThreads / 64 + 1];
-  __shared__ uint32_t hist[16 * kSampleThreads];   // the whole-row sort's digit counts
+  __shared__ uint32_t hist[16 * kSampleThreads];   // the whole-row sort's digit counts, or the merges' scratch
   __shared__ float cw[kCand];
   __shared__ int ci[kCand];
+  float* tw = reinterpret_cast<float*>(hist);
+  int* ti = reinterpret_cast<int*>(hist + kCand);
   __shared__ int sel, ccount, slices_ok;
   __shared__ float tau_s;
   __shared__ double base_s;
@@ -480,7 +605,14 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
       cw[q] = q < U ? a.sw[so * kSliceTop + q] : -1.f;
       ci[q] = q < U ? a.si[so * kSliceTop + q] : INT_MAX;
     }
-    sort_pairs(cw, ci, n2);
+    // every slice's list (and the padding) is a run of kSliceTop in candidate order; top_k up to kSliceTop needs
+    // only the union's first kSliceTop (the filters never look past the first top_k candidates)
+    const bool top_only = topk && a.top_k <= kSliceTop;
+    const int sorted = top_only ? kSliceTop : U;   // the union's leading pairs in candidate order in cw / ci
+    if (top_only)
+      merge_top<kSampleThreads>(cw, ci, tw, ti, n2 / kSliceTop, kSliceTop);
+    else
+      merge_runs<kSampleThreads>(cw, ci, tw, ti, n2, kSliceTop);
     int qp = -1;   // top_p: the union's first position whose running mass reaches total * top_p * (1 + 1e-6)
     if (!topk && a.top_p < 1.f) {
       double at_unused;
@@ -515,9 +647,9 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
       }
     __syncthreads();
     if (tau >= 0.f && slices_ok) {   // the candidates: the union's prefix at or above tau, already in order
-      if (t == 0) sel = U;
+      if (t == 0) sel = sorted;
       __syncthreads();
-      for (int q = t; q < U; q += kSampleThreads)
+      for (int q = t; q < sorted; q += kSampleThreads)
         if (!(cw[q] >= tau)) atomicMin(&sel, q);
       __syncthreads();
       nc = sel;
@@ -536,18 +668,39 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     if (t == 0) ccount = 0;
     __syncthreads();
     if (tau >= 0.f) {
-      for (int i0 = t; i0 < n; i0 += 8 * kSampleThreads) {
-        float v[8];
+      // rounds of kGather weights per thread, all loads in flight (the row was written by other work-groups: its
+      // lines come from beyond this XCD's L2); a wave takes its places with one atomic, each lane its share by a
+      // prefix over the wave's counts (the order is free: the pairs are sorted next)
+      constexpr int kGather = 32;
+      const int lane = t & 63;
+      for (int r0 = 0; r0 < n; r0 += kGather * kSampleThreads) {   // the same rounds in every thread
+        float v[kGather];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = i0 + u * kSampleThreads < n ? w[i0 + u * kSampleThreads] : -1.f;
+        for (int u = 0; u < kGather; ++u) {
+          const int i = r0 + u * kSampleThreads + t;
+          v[u] = i < n ? w[i] : -1.f;
+        }
+        int c = 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < kGather; ++u) c += v[u] >= tau ? 1 : 0;
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o);
+          if (lane >= o) incl += y;
+        }
+        const int wtot = __shfl(incl, 63);
+        int wb = 0;
+        if (lane == 0 && wtot > 0) wb = atomicAdd(&ccount, wtot);
+        int pos = __shfl(wb, 0) + incl - c;
+#pragma unroll
+        for (int u = 0; u < kGather; ++u)
           if (v[u] >= tau) {
-            const int pos = atomicAdd(&ccount, 1);
             if (pos < kCand) {
               cw[pos] = v[u];
-              ci[pos] = i0 + u * kSampleThreads;
+              ci[pos] = r0 + u * kSampleThreads + t;
             }
+            ++pos;
           }
       }
     }
@@ -561,7 +714,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
         cw[q] = -1.f;
         ci[q] = INT_MAX;
       }
-      sort_pairs(cw, ci, n2);
+      sort_pairs<kSampleThreads>(cw, ci, tw, ti, n2);
       L = nc;
     } else {
       // the whole row, stably sorted by (~bits(w), index), 4 bits a pass, contiguous chunks per thread
