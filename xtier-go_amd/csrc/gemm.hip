@@ -271,7 +271,8 @@ std::string launch_gemm(const GemvCall& c, hipStream_t stream) {
   // single part (blocks of 16 rows), measured likewise (512 / 2048 rows): four row-blocks and four pairs on the
   // wide projections at 2048 rows and gate/up at 512 (198 / 319 / 76 us), four and two on o and down at 2048
   // (85 / 152 us), two and two below that (q/k/v/g 62 us, o 35 us, down 61 us at 512 rows); eight pairs were 2-4x
-  // slower at every size
+  // slower at every size (the compiler keeps an 8-block XTile in scratch memory; eight two-part groups without
+  // that, as two 4-group halves, were still 13-40 % slower than the shapes above)
   if (parts == 1) {
     gb = tiles_for(4, 4) >= 512 ? 4 : 2;
     rb = gb == 4 || tiles_for(4, 2) >= 768 ? 4 : 2;
