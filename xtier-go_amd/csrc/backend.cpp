@@ -207,8 +207,9 @@ void Backend::prep_x(const void* x, int x_dtype, int m, int k, void* op, float* 
   timed([&] { return launch_prep_x(x, x_dtype, m, k, op, stream_, copy); });
 }
 
-void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
-                        const float* col_scale) {
+int Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
+                       const float* col_scale, int ksplit) {
+  XTG_CHECK(ksplit == 1 || ksplit == 2, "matmul: a K split in %d parts (1 or 2)", ksplit);
   XTG_CHECK(nw >= 1 && nw <= 4, "matmul: %d weights (1..4 per call)", nw);
   XTG_CHECK(!col_scale || nw == 1, "matmul: a column scale applies to a single weight");
   XTG_CHECK(m >= 1 && m <= kMaxDeviceRows, "matmul: %d rows (1..%d per device call)", m, kMaxDeviceRows);
@@ -229,10 +230,16 @@ void Backend::matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, floa
   c.xinv = reinterpret_cast<const float*>(static_cast<const char*>(op) + xop_bytes(k));
   c.col_scale[0] = col_scale;
   // up to 8 rows: the bandwidth-bound GEMV; more (a prefill chunk): the matrix-core GEMM over 8-row groups
-  if (m <= kMaxRows)
-    timed([&] { return launch_gemv(c, stream_); });
-  else
+  if (m > kMaxRows) {
     timed([&] { return launch_gemm(c, stream_); });
+    return 1;
+  }
+  if (ksplit == 2 && m >= 2) {
+    c.ksplit = 2;
+    c.y_part = off - y_off;   // one output set: m rows of every weight
+  }
+  timed([&] { return launch_gemv(c, stream_); });
+  return c.ksplit;
 }
 
 void Backend::read_probe(const void* src, size_t bytes, uint32_t* out) {
@@ -680,15 +687,15 @@ void Backend::qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, i
   timed([&] { return launch_qk_rope_norm(q, k, m, heads, kv_heads, d, pos0, f, qscale, stream_); });
 }
 
-void Backend::slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op) {
+void Backend::slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op, size_t part) {
   XTG_CHECK(x && o && lr && rows >= 1 && w >= 1, "slerp: bad arguments");
-  timed([&] { return launch_slerp_norm(x, o, lr, rows, w, op, stream_); });
+  timed([&] { return launch_slerp_norm(x, o, lr, rows, w, op, stream_, part); });
 }
 
 void Backend::swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
-                          float* out, void* op) {
+                          float* out, void* op, size_t part) {
   XTG_CHECK(g && u && sg && su && rows >= 1 && w >= 1, "swiglu: bad arguments");
-  timed([&] { return launch_swiglu_norm(g, u, sg, su, rows, w, out, op, stream_); });
+  timed([&] { return launch_swiglu_norm(g, u, sg, su, rows, w, out, op, stream_, part); });
 }
 
 void Backend::gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op) {

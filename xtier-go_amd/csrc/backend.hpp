@@ -48,8 +48,11 @@ class Backend {
   // the two halves of matmul_dev: the activation operand ([xop][8 row scales], op_bytes(k)) and the GEMV on it
   static size_t op_bytes(int k) { return op_group_bytes(k); }   // per 8 rows
   void prep_x(const void* x, int x_dtype, int m, int k, void* op, float* copy = nullptr);   // copy: FP32 rows too
-  void matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
-                 const float* col_scale = nullptr);   // col_scale (device, single weight): y[.][n] *= col_scale[n]
+  // col_scale (device, single weight): y[.][n] *= col_scale[n]. ksplit = 2 (2..8 rows; kernels.hpp GemvCall): the
+  // GEMV's K in two halves, the second half's outputs one output set later (m times the weights' total n floats);
+  // returns the output sets written (1 or 2: more rows than 8 take the GEMM, whole)
+  int matmul_op(const xtg_nvfp4* ws, int nw, const void* op, int m, float* y, size_t y_off,
+                const float* col_scale = nullptr, int ksplit = 1);
   // The one-token decode step's projections with its norms riding on them (kernels.hpp FusedGemv; m = 1): the weights,
   // m and the output y (consecutive [m][n_i] blocks; one [m][n] block for a SwiGLU pair) go into f.c; with kInOp,
   // op is the prepared operand. Returns the launch's work-group count: the records a consumer takes.
@@ -98,9 +101,10 @@ class Backend {
   // GEMV / GEMM operand of ceil(rows / 8) groups of op_bytes(w) bytes.
   void qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0, float theta,
                     const float* qscale);
-  void slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op = nullptr);
+  // part (floats, optional): the second output set of a K-split matmul_op to add to o (to g and u)
+  void slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op = nullptr, size_t part = 0);
   void swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w, float* out,
-                   void* op = nullptr);
+                   void* op = nullptr, size_t part = 0);
   void gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op = nullptr);
   void add_norm(const float* a, const float* b, float* out, int rows, int w, void* op = nullptr);
   // greedy decoding's token (xtg::argmax, sampler.cpp:8-13) of each of `rows` rows of n logits; device out int32

@@ -135,6 +135,8 @@ void DorySession::build(const xtg_dory_layer* layers, const float* logit_scale) 
   // XTG_DECODE_UNFUSED=1 runs one-token steps on the separate norm launches (the prefill path's), for comparison;
   // so do models whose shapes some fused projection is not made for
   fused_ = !std::getenv("XTG_DECODE_UNFUSED") && fused_unsupported().empty();
+  // XTG_VERIFY_WHOLE_K=1: steps of several rows keep the whole K in their projections (for comparison)
+  ksplit_ = !std::getenv("XTG_VERIFY_WHOLE_K");
   input_ = scratch(R * H);
   state_ = scratch(R * H);
   proj_ = scratch(R * size_t(2 * Q + 2 * KV));
@@ -265,12 +267,16 @@ void DorySession::set_head_bf16(const xtg_bf16& head) {
 void DorySession::sublayer(Layer& L, int m, long long pos0, int inst, bool store) {
   // packs/dory/dory.cpp:467-518; x's GEMV operand is in op_h_ on entry and on exit
   const int H = c_.hidden, Q = c_.heads * c_.head_dim, KV = c_.kv_heads * c_.head_dim, F = c_.ffn;
+  // steps of 2..8 rows: the gate/up, down and o projections split K in two (GemvCall::ksplit), and the norm launch
+  // that reads their outputs adds the halves; prompt chunks (the GEMM) and single rows keep one output set
+  const int ks = ksplit_ && m >= 2 ? 2 : 1;
   if (L.w.kind == XTG_DORY_MLP) {
     const xtg_nvfp4 gu[2] = {L.w.gate, L.w.up};
-    b_.matmul_op(gu, 2, op_h_, m, gu_, 0);                                      // gate rows [m][F], then up rows
-    b_.swiglu_norm(gu_, gu_ + size_t(m) * F, L.sg, L.su, m, F, nullptr, op_f_);  // justnorm(silu(g sg) (u su))
-    b_.matmul_op(&L.w.down, 1, op_f_, m, o_, 0);
-    b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
+    const int gp = b_.matmul_op(gu, 2, op_h_, m, gu_, 0, nullptr, ks);  // gate rows [m][F], then up rows
+    b_.swiglu_norm(gu_, gu_ + size_t(m) * F, L.sg, L.su, m, F, nullptr, op_f_,
+                   gp == 2 ? size_t(m) * 2 * F : 0);   // justnorm(silu(g sg) (u su))
+    const int dp = b_.matmul_op(&L.w.down, 1, op_f_, m, o_, 0, nullptr, ks);
+    b_.slerp_norm(x_, o_, L.lr, m, H, op_h_, dp == 2 ? size_t(m) * H : 0);
     return;
   }
   const xtg_nvfp4 qkvg[4] = {L.w.q, L.w.k, L.w.v, L.w.g};
@@ -283,8 +289,8 @@ void DorySession::sublayer(Layer& L, int m, long long pos0, int inst, bool store
   const float scale = 1.f / std::sqrt(float(c_.head_dim));
   b_.attn_step(this->cache(L.attn, inst), m, pos0, c_.heads, sliding ? c_.window : 0, scale,
                sliding ? c_.theta_sliding : c_.theta_full, q, k, v, L.qscale, g, L.gscale, nullptr, op_q_, store);
-  b_.matmul_op(&L.w.o, 1, op_q_, m, o_, 0);
-  b_.slerp_norm(x_, o_, L.lr, m, H, op_h_);
+  const int op = b_.matmul_op(&L.w.o, 1, op_q_, m, o_, 0, nullptr, ks);
+  b_.slerp_norm(x_, o_, L.lr, m, H, op_h_, op == 2 ? size_t(m) * H : 0);
 }
 
 void DorySession::materialize(int m) {

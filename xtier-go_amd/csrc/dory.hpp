@@ -88,6 +88,7 @@ class DorySession {
   float *part_s_ = nullptr, *part_h_ = nullptr;
   float *part_a_ = nullptr, *att_ = nullptr;   // the attention gate's per-head records and gated heads
   bool fused_ = true, pend_ = false;
+  bool ksplit_ = true;   // steps of 2..8 rows split K in two in gate/up, down and o (GemvCall::ksplit)
   const float* pend_lr_ = nullptr;
   float pend_a_ = 1.f, pend_b_ = 1.f;   // its linear-form operand's factors, the operand in op_lin_
   int pend_groups_ = 0;

@@ -205,6 +205,7 @@ struct GemvArgs {
   const void* x;       // raw rows [m][k] (FP32 or BF16) when the kernel builds its own operand
   int k;
   float* y;
+  long long y_part;    // with a K split in two: the floats from one output set to the next (blockIdx.y)
 };
 
 // Output of one accumulator fragment: for activation row j, rows 4 g .. 4 g + 3 of the row-block (high and low
@@ -214,7 +215,7 @@ __device__ inline void store_rows(const GemvArgs& a, int wi, int rb, int g, int 
   const int n = a.n[wi];
   const int n0 = rb * kTileRows + 4 * g;
   const float f = a.xinv ? a.global[wi] * a.xinv[j] : a.global[wi];
-  float* yp = a.y + a.y_off[wi] + (long long)j * n;
+  float* yp = a.y + a.y_off[wi] + (long long)blockIdx.y * a.y_part + (long long)j * n;
   const float* cs = a.col_scale[wi];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -321,7 +322,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * R;
   const int nb = a.nb[wi], KT = a.kt;
   const uint8_t* __restrict__ tiles = a.tiles[wi];
-  const int kt0 = wave * T;
+  const int kt0 = (int(blockIdx.y) * S + wave) * T;   // with a K split, blockIdx.y's half of the k-tiles
 
   // every load of the wave first (T k-tiles of activations, R x T weight tiles), then the math; operand columns
   // of absent activation rows are not loaded (their accumulator columns are never stored)
@@ -751,8 +752,19 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   GemvArgs a{};
   const int kt = c.w[0]->kt;
   for (int i = 0; i < c.nw; ++i) XTG_CHECK(c.w[i]->kt == kt, "gemv: input widths differ");
-  const GemvShape sh = call_shape(c);
   const bool xr = raw_kind(c);
+  XTG_CHECK(c.ksplit == 1 || (c.ksplit == 2 && !xr && c.m >= 2 && c.y_part > 0),
+            "gemv: a K split takes a prepared operand of 2..8 rows and a second output set");
+  const int ks = c.ksplit;
+  GemvShape sh = call_shape(c);
+  if (ks == 2) {
+    // half of K, two row-blocks per wave (down / o / gate 3072..8192 wide at 8 rows, measured on MI355X: 1.7 / 0.6 /
+    // 1.5 us per launch faster than the whole K, against 0.4 us slower / no gain at one row-block)
+    int nbs[4];
+    for (int i = 0; i < c.nw; ++i) nbs[i] = c.w[i]->nb;
+    sh = gemv_shape((kt + 1) / 2, nbs, c.nw, c.m, false);
+    if (shape_ok(2, sh.t, sh.s)) sh.r = 2;
+  }
   int wgs = 0;
   for (int i = 0; i < c.nw; ++i) {
     a.tiles[i] = c.w[i]->tiles;
@@ -773,7 +785,8 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.x = c.x;
   a.k = c.k;
   a.y = c.y;
-  XTG_CHECK(sh.s * sh.t >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
+  a.y_part = ks == 2 ? (long long)c.y_part : 0;
+  XTG_CHECK(sh.s * sh.t * ks >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
   const int threads = sh.s * 64;
   GemvFn mx = xr && c.m <= 2 && mx_enabled() ? gemv_mx_fn(sh.r, sh.t, threads, c.m) : nullptr;
   GemvFn fn = mx ? mx : gemv_fn(sh.r, sh.t, threads, xr);
@@ -781,11 +794,12 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   const size_t lds = (sh.s > 1 ? size_t(sh.s) * size_t(sh.r) * kMaxRows * 4 * sizeof(f32x4) : 0) +
                      (xr ? size_t(sh.s) * (mx ? kMxStageVecs : kStageVecs) * sizeof(uint4) : 0);
   allow_lds(reinterpret_cast<const void*>(fn), lds);
-  hipLaunchKernelGGL(fn, dim3(unsigned(wgs)), dim3(unsigned(threads)), lds, stream, a);
+  hipLaunchKernelGGL(fn, dim3(unsigned(wgs), unsigned(ks)), dim3(unsigned(threads)), lds, stream, a);
   HIP_CHECK(hipGetLastError());
   const int mt = threads <= 512 ? 512 : 1024;
   if (mx) return strf("gemv_mx_kernel<%d, %d, %d, %d>", sh.r, sh.t, mt, c.m);
-  return xr ? strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, mt) : strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, mt);
+  if (xr) return strf("gemv_kernel<%d, %d, %d, bf16>", sh.r, sh.t, mt);
+  return ks == 2 ? strf("gemv_kernel<%d, %d, %d> (K / 2)", sh.r, sh.t, mt) : strf("gemv_kernel<%d, %d, %d>", sh.r, sh.t, mt);
 }
 
 }  // namespace xtg::hip

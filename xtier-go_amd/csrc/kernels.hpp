@@ -60,6 +60,12 @@ struct GemvCall {
   int x_dtype = 0;
   int k = 0;
   int parts = 2;   // the GEMM's activation parts (prefill chunks): 2, high and low f16; 1, the high part alone
+  // the GEMV on a prepared operand (2..8 rows): 2 splits K in two halves whose partial outputs go to y (the first
+  // k-tiles) and to y + y_part (the rest), each laid out as y_off says; the consumer adds them, first + second.
+  // Each work-group then reads half of the rows' operand (the bytes its k-range needs), the share of a launch that
+  // grows with the rows. 1: one output set.
+  int ksplit = 1;
+  size_t y_part = 0;
 };
 // The launch shape: R row-blocks and T k-tiles per wave, S waves per work-group along k.
 struct GemvShape {

@@ -89,17 +89,30 @@ __device__ inline void finish_row(float (&t)[U][8], float sumsq, int w, bool vec
   if (xop) emit_operand_mx<kNormThreads, U>(t, w, int(blockIdx.x), xop, xinv, ostride, mx * f);
 }
 
+// A second part of a row split in two along K (GemvCall::ksplit): r += that part, element by element (first part +
+// second, the one order).
+template <int U>
+__device__ inline void add_part(const float* row, int w, int vec, float (&r)[U][8]) {
+  float p[U][8];
+  load_row<kNormThreads, U>(row, w, vec, p);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[u][e] += p[u][e];
+}
+
 template <int U>
 __global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
-                                                                   const float* __restrict__ lr, int w, int vec,
-                                                                   f16x8* __restrict__ xop, float* __restrict__ xinv,
-                                                                   size_t ostride) {
+                                                                   size_t part, const float* __restrict__ lr, int w,
+                                                                   int vec, f16x8* __restrict__ xop,
+                                                                   float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float* xr = x + size_t(blockIdx.x) * w;
   float a[U][8], b[U][8], l[U][8];
   load_row<kNormThreads, U>(xr, w, vec, a);
   load_row<kNormThreads, U>(o + size_t(blockIdx.x) * w, w, vec, b);
   load_row<kNormThreads, U>(lr, w, vec, l);
+  if (part) add_part<U>(o + part + size_t(blockIdx.x) * w, w, vec, b);
   float sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -124,7 +137,7 @@ __global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restr
 
 template <int U>
 __global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* g,
-                                                                    const float* __restrict__ u_,
+                                                                    const float* __restrict__ u_, size_t part,
                                                                     const float* __restrict__ sg,
                                                                     const float* __restrict__ su, int w, int vec,
                                                                     float* out, f16x8* __restrict__ xop,
@@ -135,6 +148,10 @@ __global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* 
   load_row<kNormThreads, U>(u_ + size_t(blockIdx.x) * w, w, vec, b);
   load_row<kNormThreads, U>(sg, w, vec, s1);
   load_row<kNormThreads, U>(su, w, vec, s2);
+  if (part) {
+    add_part<U>(g + part + size_t(blockIdx.x) * w, w, vec, a);
+    add_part<U>(u_ + part + size_t(blockIdx.x) * w, w, vec, b);
+  }
   float s = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -301,17 +318,18 @@ std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_hea
 }
 
 std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op,
-                              hipStream_t stream) {
+                              hipStream_t stream, size_t part) {
   const Operand p = operand_of(op, rows, w);
-  const int vec = rows_vec(w, {x, o, lr});
-  XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, lr, w, vec, p.xop, p.xinv, p.stride);
+  const int vec = rows_vec(w, {x, o, lr, o + part});
+  XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, part, lr, w, vec, p.xop, p.xinv, p.stride);
 }
 
 std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
-                               float* out, void* op, hipStream_t stream) {
+                               float* out, void* op, hipStream_t stream, size_t part) {
+  XTG_CHECK(!part || (out != g && out != u), "swiglu_norm: a split input is not written in place");
   const Operand p = operand_of(op, rows, w);
-  const int vec = rows_vec(w, {g, u, sg, su, out});
-  XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, sg, su, w, vec, out, p.xop, p.xinv, p.stride);
+  const int vec = rows_vec(w, {g, u, sg, su, out, g + part, u + part});
+  XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, part, sg, su, w, vec, out, p.xop, p.xinv, p.stride);
 }
 
 std::string launch_gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op,

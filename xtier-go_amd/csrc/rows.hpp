@@ -11,12 +11,14 @@ namespace xtg::hip {
 
 std::string launch_qk_rope_norm(float* q, float* k, int m, int heads, int kv_heads, int d, long long pos0,
                                 const float* inv_freq, const float* qscale, hipStream_t stream);
-// x = justnorm(slerp) in place
+// x = justnorm(slerp) in place; part (floats, optional): o is the sum of o and o + part (a K-split GEMV's two
+// output sets, added in that order)
 std::string launch_slerp_norm(float* x, const float* o, const float* lr, int rows, int w, void* op,
-                              hipStream_t stream);
-// out (optional, may be g) = justnorm(silu(g sg) (u su))
+                              hipStream_t stream, size_t part = 0);
+// out (optional, may be g) = justnorm(silu(g sg) (u su)); part as for slerp_norm, for g and u alike (out then may
+// not be g or u)
 std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, const float* su, int rows, int w,
-                               float* out, void* op, hipStream_t stream);
+                               float* out, void* op, hipStream_t stream, size_t part = 0);
 // out (optional, may be a) = justnorm(a sigmoid(gate gs))
 std::string launch_gate_norm(const float* a, const float* gate, const float* gs, int rows, int w, float* out, void* op,
                              hipStream_t stream);
