@@ -584,15 +584,16 @@ def bf16_head_bench(pkg, wl, hip, reps):
 
 def sampling_bench(pkg, hip, reps):
     """The device sampler on 131072-wide logits (the vocabulary), 1 and 8 rows: greedy (argmax), temperature only
-    (walk in index order), top_k 40 and top_p 0.9 (sorted candidates); events on the backend's stream around each
-    call (its launches timed as one, under the name of the last: `kernel`)."""
+    (walk in index order), top_k 40, top_k 300 and top_p 0.9 (sorted candidates); events on the backend's stream
+    around each call (its launches timed as one, under the name of the last: `kernel`)."""
     n = 131072
     rng = np.random.default_rng(51)
     x = (rng.standard_normal((8, n)) * 3).astype(np.float32)
     dx, dout = hip.array(x), hip.array(shape=(8,), dtype=np.int32)
     out = {"n": n}
     for label, p in (("greedy", dict(temperature=0.0)), ("temperature", dict(temperature=0.8)),
-                     ("top_k40", dict(temperature=0.8, top_k=40)), ("top_p0.9", dict(temperature=0.8, top_p=0.9))):
+                     ("top_k40", dict(temperature=0.8, top_k=40)), ("top_k300", dict(temperature=0.8, top_k=300)),
+                     ("top_p0.9", dict(temperature=0.8, top_p=0.9))):
         for m in (1, 8):
             u = rng.random(m)
             hip.sample(dx, m, n, u, dout, **p)

@@ -107,14 +107,16 @@ def test_argmax(hip, orc, rows, n):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 37, 1000, 5000, 131072])
+@pytest.mark.parametrize("n", [1, 37, 1000, 5000, 131072, 150001])
 def test_sample(hip, orc, n):
     """xtg::Sampler::sample (sampler.cpp:40-94) on the device with the same draws as the oracle (itself pinned
-    against the reference's Sampler): every filter combination over 8 rows at a time, ties planted, greedy rows
-    routed to argmax; top_k up to the slices' 64 listed weights (the union's first 64 only), just past them, past
-    the 4096 the union holds (the whole row sorted), and the whole row. The weights are FP32 exp values on both sides, so a token may differ only where r (or the
-    top_p target) lies within a rounding step of a running-sum boundary: a mismatch counts as one only if the
-    oracle's margin there exceeds 1e-6 of the total."""
+    against the reference's Sampler): every filter combination over 8 rows at a time, greedy rows routed to argmax;
+    ties planted among the most likely, and logits on a grid of 1/4 (exact ties through the kept candidates, which
+    must come out in index order); top_k up to the slices' 64 listed weights (the union's first 64 only), just past
+    them, past the 4096 the union holds (the whole row sorted), and the whole row; a row of 150001 (more than 4096
+    listed weights, not a multiple of 4). The weights are FP32 exp values on both sides, so a token may differ only
+    where r (or the top_p target) lies within a rounding step of a running-sum boundary: a mismatch counts as one
+    only if the oracle's margin there exceeds 1e-6 of the total."""
     rng = np.random.default_rng(n)
     dout = hip.array(shape=(8,), dtype=np.int32)
     checked = 0
@@ -123,6 +125,8 @@ def test_sample(hip, orc, n):
         x = (rng.standard_normal((rows, n)) * rng.choice([0.5, 2.0, 8.0])).astype(np.float32)
         if trial % 3 == 0 and n > 3:
             x[0, rng.integers(0, n, 3)] = x[0].max()   # ties among the most likely
+        if trial % 4 == 1:
+            x = np.round(x * 4) / 4   # ties everywhere
         params = dict(temperature=float(rng.choice([0.0, 0.3, 1.0, 2.0])),
                       top_p=float(rng.choice([1.0, 0.9, 0.5, 0.05])),
                       top_k=int(rng.choice([0, 1, 5, 40, 64, 65, 300, 5000, n])),

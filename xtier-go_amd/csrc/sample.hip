@@ -21,11 +21,13 @@
 // slice's 64 largest thread maxima in candidate order, and the largest second). Then
 // one work-group of 1024 threads per row: the slice sums in order give the total and, without a filter, the slice
 // where the running sum passes r, walked by hierarchical running sums (16 wave segments, 16 parts, tiles of 64).
-// With a filter, a threshold tau that the kept prefix cannot go below comes from the sorted union of the slices'
-// lists -- its top_k-th value for top_k, the value where its running mass first reaches total * top_p * (1 + 1e-6)
-// for top_p, the floor for min_p (max(floor, that) with both): the union is a subset of the row, so the row holds at
-// least as much above tau. When in every slice the 64th listed maximum and every thread's second lie below tau,
-// the union holds every weight >= tau, and the candidates are its sorted prefix; otherwise they are gathered from
+// With a filter, a threshold tau that the kept prefix cannot go below comes from the union of the slices' lists --
+// for top_k up to 64 its top_k-th pair (merges that keep the first 64); for a larger top_k, and for top_p, the lower
+// edge of the 24-bit bucket of weight bits where the union's running count reaches top_k, or its mass total * top_p
+// * (1 + 1e-6) (a radix select, three passes of 256 counters; masses in fixed point, so exact and order-free); the
+// floor for min_p (max(floor, that) with both): the union is a subset of the row, so the row holds at least as much
+// at or above tau. When in every slice the 64th listed maximum and every thread's second lie below tau, the union
+// holds every weight >= tau, and the candidates are its pairs at or above tau; otherwise they are gathered from
 // the row (at most 4096, sorted in LDS), or, past that, the whole row is sorted by a stable LSD radix sort in scratch
 // memory (8 passes of 4 bits): slower, the same result. Sorts in LDS are merges of sorted runs of 64 (the slices'
 // lists as they come; gathered pairs sorted by the waves in registers first), one barrier per doubling of the run
@@ -45,7 +47,8 @@ namespace {
 constexpr int kSampleThreads = 1024;
 
 // Exclusive prefix of v over the work-group in thread order; every thread gets its own prefix and *all the total.
-// A wave scan by shuffles, then the 16 wave totals in order. red: at least kSampleThreads / 64 + 1 entries.
+// A wave scan by shuffles, then every thread adds the 16 wave totals before its wave (in order) itself. red: at
+// least kSampleThreads / 64 entries.
 template <typename T>
 __device__ inline T block_exclusive(T v, T* red, T* all) {
   const int t = int(threadIdx.x), lane = t & 63, wave = t >> 6;
@@ -58,18 +61,15 @@ __device__ inline T block_exclusive(T v, T* red, T* all) {
   __syncthreads();   // red may still be read by a previous call
   if (lane == 63) red[wave] = x;
   __syncthreads();
-  if (t == 0) {
-    T s = T(0);
-    for (int i = 0; i < kSampleThreads / 64; ++i) {
-      const T c = red[i];
-      red[i] = s;
-      s += c;
-    }
-    red[kSampleThreads / 64] = s;
+  T before = T(0), tot = T(0);
+#pragma unroll
+  for (int i = 0; i < kSampleThreads / 64; ++i) {
+    const T c = red[i];
+    before += i < wave ? c : T(0);
+    tot += c;
   }
-  __syncthreads();
-  *all = red[kSampleThreads / 64];
-  return red[wave] + x - v;
+  *all = tot;
+  return before + x - v;
 }
 
 // Double sums across a wave on the vector ALUs: DPP within rows of 16 on the two 32-bit halves, then the gfx950
@@ -368,6 +368,74 @@ __device__ inline void sort_pairs(float* cw, int* ci, float* tw, int* ti, int n2
   }
   merge_runs<NT>(cw, ci, tw, ti, n2, n2 < 64 ? n2 : 64);
 }
+
+// A weight that the kept prefix cannot go below, from the U pairs of the slices' lists (weights in [0, 1]; below 0:
+// padding): an MSD radix select over the weights' bits, 8 a pass for three passes, finds the bucket of 24 leading
+// bits in which the running count (mass = false) or mass of the union from its most likely side first reaches
+// `target` (<= U; a mass target < U), and returns the bucket's lower edge; -1 when the union never reaches it. Masses are fixed point
+// at 2^-F with U <= 2^(62 - F): the sums are exact and order-free, each weight's share is rounded down and the
+// target up. The row holds the union, so its own count or mass at or above that edge is at least as large. h: 256
+// LDS counters; sel, above: LDS words. Every thread of the work-group.
+__device__ inline float union_select(const float* __restrict__ uw, int U, bool mass, double target,
+                                     unsigned long long* h, int* sel, unsigned long long* above_s) {
+  const int t = int(threadIdx.x), lane = t & 63, wave = t >> 6;
+  const double scale = ldexp(1.0, 62 - (32 - __clz(U)));
+  const unsigned long long tgt = mass ? (unsigned long long)ceil(target * scale) : (unsigned long long)target;
+  uint32_t prefix = 0u;
+  unsigned long long above = 0ull;
+  for (int p = 0; p < 3; ++p) {
+    const int sh = 24 - 8 * p;
+    if (t < 256) h[t] = 0ull;
+    __syncthreads();
+    for (int e = t; e < U; e += kSampleThreads) {
+      const float x = uw[e];
+      const uint32_t b = __float_as_uint(x);
+      if (x >= 0.f && (p == 0 || (b >> (sh + 8)) == prefix))
+        atomicAdd(&h[(b >> sh) & 255u], mass ? (unsigned long long)(double(x) * scale) : 1ull);
+    }
+    __syncthreads();
+    if (wave == 0) {   // digits from the most likely: lane l holds 255 - 4 l .. 252 - 4 l
+      unsigned long long c[4], s = 0ull;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c[q] = h[255 - 4 * lane - q];
+        s += c[q];
+      }
+      unsigned long long x = s;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      const unsigned long long m = __ballot(above + x >= tgt);
+      const int l = m ? __ffsll(m) - 1 : 0;
+      if (lane == l) {
+        int d = -1;
+        unsigned long long run = above + x - s;
+        if (m) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (d < 0) {
+              if (run + c[q] >= tgt)
+                d = 255 - 4 * lane - q;
+              else
+                run += c[q];
+            }
+          }
+        }
+        *sel = d;
+        *above_s = run;
+      }
+    }
+    __syncthreads();
+    const int d = *sel;
+    above = *above_s;
+    __syncthreads();   // sel, above_s and h are written again by the next pass or the caller
+    if (d < 0) return -1.f;
+    prefix = (prefix << 8) | uint32_t(d);
+  }
+  return __uint_as_float(prefix << 8);
+}
 }  // namespace
 
 // Per-row scratch (floats / ints / doubles laid out by SampleScratch): the weights, and per slice of kSlice logits
@@ -551,8 +619,9 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   __shared__ int ci[kCand];
   float* tw = reinterpret_cast<float*>(hist);
   int* ti = reinterpret_cast<int*>(hist + kCand);
+  __shared__ unsigned long long selh[256];
   __shared__ int sel, ccount, slices_ok;
-  __shared__ float tau_s;
+  __shared__ unsigned long long above_s;
   __shared__ double base_s;
   const int row = int(blockIdx.x), t = int(threadIdx.x), n = a.n, S = a.slices;
   const float* w = a.w + size_t(row) * size_t(n);
@@ -594,80 +663,94 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     return;
   }
 
-  // tau from the slices' 64 most likely (their union, sorted): the kept prefix lies at or above it
+  // tau, a weight that the kept prefix cannot go below, from the union of the slices' lists (S * 64 pairs): for
+  // top_k up to 64 the union's top_k-th pair, from merges that keep each pair of runs' first 64; otherwise
+  // union_select's bucket edge where the union's count reaches top_k, or where its mass reaches total * top_p *
+  // (1 + 1e-6); the floor for min_p (the larger of the two with top_p). The union is a subset of the row, so the row
+  // holds at least as much at or above tau.
   const int U = S * kSliceTop;
-  int nc = INT_MAX;
+  const float* uw = a.sw + so * kSliceTop;
+  const int* ui = a.si + so * kSliceTop;
+  const bool top_only = topk && a.top_k <= kSliceTop && U <= kCand;
+  int nc = INT_MAX;        // candidates in cw / ci (INT_MAX: none yet)
+  bool in_order = false;   // in candidate order already
   float tau = -1.f;
-  if (U <= kCand) {
+  if (top_only) {
     int n2 = 1;
     while (n2 < U) n2 <<= 1;
     for (int q = t; q < n2; q += kSampleThreads) {
-      cw[q] = q < U ? a.sw[so * kSliceTop + q] : -1.f;
-      ci[q] = q < U ? a.si[so * kSliceTop + q] : INT_MAX;
+      cw[q] = q < U ? uw[q] : -1.f;
+      ci[q] = q < U ? ui[q] : INT_MAX;
     }
     // every slice's list (and the padding) is a run of kSliceTop in candidate order; top_k up to kSliceTop needs
     // only the union's first kSliceTop (the filters never look past the first top_k candidates)
-    const bool top_only = topk && a.top_k <= kSliceTop;
-    const int sorted = top_only ? kSliceTop : U;   // the union's leading pairs in candidate order in cw / ci
-    if (top_only)
-      merge_top<kSampleThreads>(cw, ci, tw, ti, n2 / kSliceTop, kSliceTop);
-    else
-      merge_runs<kSampleThreads>(cw, ci, tw, ti, n2, kSliceTop);
-    int qp = -1;   // top_p: the union's first position whose running mass reaches total * top_p * (1 + 1e-6)
-    if (!topk && a.top_p < 1.f) {
-      double at_unused;
-      const double target = total * double(a.top_p) * (1.0 + 1e-6);
-      qp = first_crossing([&](int j) { return fmaxf(cw[j], 0.f); }, U, target, false, red, &sel, &at_unused);
+    merge_top<kSampleThreads>(cw, ci, tw, ti, n2 / kSliceTop, kSliceTop);
+    tau = cw[a.top_k - 1] >= 0.f ? cw[a.top_k - 1] : -1.f;
+  } else if (topk) {
+    tau = a.top_k <= U ? union_select(uw, U, false, double(a.top_k), selh, &sel, &above_s) : -1.f;
+  } else {
+    if (a.top_p < 1.f) {
+      const double target = total * double(a.top_p) * (1.0 + 1e-6);   // the union's mass is at most U
+      tau = target < double(U) ? union_select(uw, U, true, target, selh, &sel, &above_s) : -1.f;
     }
-    if (t == 0) {
-      float tv = 0.f;
-      bool ok = true;
-      if (topk) {
-        ok = a.top_k <= U && cw[a.top_k - 1] >= 0.f;
-        tv = ok ? cw[a.top_k - 1] : 0.f;
-      } else {
-        if (a.top_p < 1.f) {
-          ok = qp < U && cw[qp] >= 0.f;
-          tv = ok ? cw[qp] : 0.f;
-        }
-        if (a.min_p > 0.f) tv = fmaxf(tv, floor_w);
-      }
-      tau_s = ok ? tv : -1.f;
-      slices_ok = 1;
+    if (a.min_p > 0.f) tau = fmaxf(tau, floor_w);   // min_p keeps nothing below its floor
+  }
+  // every weight >= tau is a listed thread maximum when, in every slice, the 64th listed maximum and every thread's
+  // second most likely lie below tau
+  if (t == 0) slices_ok = 1;
+  __syncthreads();
+  if (tau >= 0.f)
+    for (int q = t; q < S; q += kSampleThreads) {
+      const float last = uw[size_t(q) * kSliceTop + kSliceTop - 1];
+      const float m2 = a.sm2[so + q];
+      if (!(last < tau) || !(m2 < tau)) atomicAnd(&slices_ok, 0);   // ties or runs at tau may continue past the lists
     }
+  __syncthreads();
+  if (tau >= 0.f && slices_ok && top_only) {   // the union's prefix at or above tau, already in order
+    if (t == 0) sel = kSliceTop;
     __syncthreads();
-    tau = tau_s;
-    // every weight >= tau is a listed thread maximum when, in every slice, the 64th listed maximum and every
-    // thread's second most likely lie below tau
-    if (tau >= 0.f)
-      for (int q = t; q < S; q += kSampleThreads) {
-        const float last = a.sw[(so + q) * kSliceTop + kSliceTop - 1];
-        const float m2 = a.sm2[so + q];
-        if (!(last < tau) || !(m2 < tau)) atomicAnd(&slices_ok, 0);   // ties or runs at tau may continue past the lists
-      }
+    for (int q = t; q < kSliceTop; q += kSampleThreads)
+      if (!(cw[q] >= tau)) atomicMin(&sel, q);
     __syncthreads();
-    if (tau >= 0.f && slices_ok) {   // the candidates: the union's prefix at or above tau, already in order
-      if (t == 0) sel = sorted;
-      __syncthreads();
-      for (int q = t; q < sorted; q += kSampleThreads)
-        if (!(cw[q] >= tau)) atomicMin(&sel, q);
-      __syncthreads();
-      nc = sel;
-      __syncthreads();
+    nc = sel;
+    in_order = true;
+    __syncthreads();
+  } else if (tau >= 0.f && slices_ok && U <= kCand) {   // the union's pairs at or above tau (sorted next)
+    constexpr int PT = kCand / kSampleThreads;
+    float x[PT];
+    int xi[PT];
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < PT; ++r) {
+      const int e = PT * t + r;
+      x[r] = e < U ? uw[e] : -1.f;
+      xi[r] = e < U ? ui[e] : 0;
+      c += x[r] >= tau ? 1 : 0;
     }
+    uint32_t tot;
+    int at = int(block_exclusive<uint32_t>(uint32_t(c), ured, &tot));
+#pragma unroll
+    for (int r = 0; r < PT; ++r)
+      if (x[r] >= tau) {
+        cw[at] = x[r];
+        ci[at] = xi[r];
+        ++at;
+      }
+    nc = int(tot);
   }
   const float* sw_l = cw;
   const int* si_l = ci;
   const uint32_t* ksrc = nullptr;
   const int* isrc = nullptr;
   int L;   // candidates available in order
-  if (nc != INT_MAX) {
+  if (in_order) {
     L = nc;
   } else {
-    // gather every weight >= tau from the row (order-free, then sorted), or sort the whole row
+    // gather every weight >= tau from the row (order-free, then sorted) unless the union supplied them, or sort the
+    // whole row
     if (t == 0) ccount = 0;
     __syncthreads();
-    if (tau >= 0.f) {
+    if (nc == INT_MAX && tau >= 0.f) {
       // rounds of kGather weights per thread, all loads in flight (the row was written by other work-groups: its
       // lines come from beyond this XCD's L2); a wave takes its places with one atomic, each lane its share by a
       // prefix over the wave's counts (the order is free: the pairs are sorted next)
@@ -705,7 +788,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
       }
     }
     __syncthreads();
-    nc = tau >= 0.f ? ccount : INT_MAX;
+    if (nc == INT_MAX) nc = tau >= 0.f ? ccount : INT_MAX;
     __syncthreads();
     if (nc <= kCand) {
       int n2 = 1;
