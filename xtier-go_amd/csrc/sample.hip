@@ -217,156 +217,136 @@ __device__ inline int first_crossing(WF wf, int len, double r, bool strict, doub
 }
 
 // Candidate order over (weight, index) pairs is total for distinct indices (the padding pairs (-1, INT_MAX) are
-// equal to each other), so every sort below gives the one order a sort of the reference's comparator gives.
+// equal to each other), so every sort below gives the one order a sort of the reference's comparator gives. In LDS
+// a pair is one 64-bit key whose ascending order is candidate order: above, the weight's bits mapped so that larger
+// weights give smaller values (desc_key); below, the index. Weights >= 0 sort before the padding's -1.
+__device__ inline uint32_t desc_key(float w) {
+  const uint32_t u = __float_as_uint(w);
+  return ~(u ^ ((u >> 31) ? 0xffffffffu : 0x80000000u));
+}
+__device__ inline unsigned long long pair_key(float w, int id) {
+  return (static_cast<unsigned long long>(desc_key(w)) << 32) | uint32_t(id);
+}
+constexpr unsigned long long kPadKey = 0xbf8000007fffffffull;   // pair_key(-1, INT_MAX)
+__device__ inline float key_w(unsigned long long k) {
+  const uint32_t y = ~uint32_t(k >> 32);
+  return __uint_as_float((y & 0x80000000u) ? (y ^ 0x80000000u) : ~y);
+}
+__device__ inline int key_id(unsigned long long k) { return int(uint32_t(k)); }
 
-// One wave's pair (w, id) in lane l of a run of 64 sorted in registers into candidate order (lane 0 most likely):
-// a bitonic network over the lanes (partner l ^ j by shuffle), every run of 2k ascending where l & k is clear, the
-// last level all ascending. Pairs that compare equal stay where they are.
-__device__ inline void wave_sort64(float& w, int& id) {
+// One wave's key in lane l of a run of 64 sorted in registers into ascending order (lane 0 most likely): a bitonic
+// network over the lanes (partner l ^ j by shuffle), every run of 2k ascending where l & k is clear, the last level
+// all ascending. Equal keys stay where they are.
+__device__ inline void wave_sort64(unsigned long long& k) {
   const int l = int(threadIdx.x) & 63;
 #pragma unroll
-  for (int k = 2; k <= 64; k <<= 1)
+  for (int r = 2; r <= 64; r <<= 1)
 #pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const float wp = __shfl_xor(w, j);
-      const int ip = __shfl_xor(id, j);
-      const bool up = k == 64 || (l & k) == 0;   // this run ascends in candidate order
+    for (int j = r >> 1; j > 0; j >>= 1) {
+      const unsigned long long kp = __shfl_xor(k, j);
+      const bool up = r == 64 || (l & r) == 0;   // this run ascends
       const bool first = (l & j) == 0;            // the lower place of the pair
-      // the lower place of an ascending run (the upper of a descending one) takes the more likely pair
-      const bool take = up == first ? more_likely(wp, ip, w, id) : more_likely(w, id, wp, ip);
-      if (take) w = wp, id = ip;
+      // the lower place of an ascending run (the upper of a descending one) takes the smaller key
+      const bool take = up == first ? kp < k : k < kp;
+      if (take) k = kp;
     }
 }
 
-// n2 (a power of two) pairs in LDS whose runs of `run` pairs (a power of two) are each in candidate order, merged
-// into candidate order by pairwise merges of the runs, one level per doubling. Each thread makes E = n2 / NT
-// consecutive outputs of its pair of runs (A, B), at least one: it finds by binary search on its diagonal how many
-// of A's pairs come before its first output (merge path), then merges E pairs in order; of two equal pairs A's goes
-// first. tw / ti: scratch for n2 pairs. The result is in cw / ci; every thread of the work-group (NT) takes part.
+// n2 (a power of two) keys in LDS whose runs of `run` keys (a power of two) are each ascending, merged into ascending
+// order by pairwise merges of the runs, one level per doubling. Each thread makes E = n2 / NT consecutive outputs
+// of its pair of runs (A, B), at least one: it finds by binary search on its diagonal how many of A's keys come
+// before its first output (merge path), then merges E keys in order; of two equal keys A's goes first. tk: scratch
+// for n2 keys. The result is in ck; every thread of the work-group (NT) takes part.
 template <int NT>
-__device__ inline void merge_runs(float* cw, int* ci, float* tw, int* ti, int n2, int run) {
+__device__ inline void merge_runs(unsigned long long* ck, unsigned long long* tk, int n2, int run) {
   const int E = n2 > NT ? n2 / NT : 1;
-  float* sw = cw;
-  int* si = ci;
-  float* dw = tw;
-  int* di = ti;
+  unsigned long long* src = ck;
+  unsigned long long* dst = tk;
   for (int L = run; L < n2; L <<= 1) {
     __syncthreads();
     const int o0 = int(threadIdx.x) * E;
     if (o0 < n2) {
       const int base = o0 & ~(2 * L - 1), d = o0 - base;
-      const float* aw = sw + base;
-      const int* ai = si + base;
-      const float* bw = aw + L;
-      const int* bi = ai + L;
+      const unsigned long long* A = src + base;
+      const unsigned long long* B = A + L;
       int lo = d > L ? d - L : 0, hi = d < L ? d : L;
-      while (lo < hi) {   // A's pairs among the first d outputs: A[mid] goes first unless B[d - 1 - mid] is more likely
+      while (lo < hi) {   // A's keys among the first d outputs: A[mid] goes first unless B[d - 1 - mid] is smaller
         const int mid = (lo + hi) >> 1;
-        if (more_likely(bw[d - 1 - mid], bi[d - 1 - mid], aw[mid], ai[mid]))
+        if (B[d - 1 - mid] < A[mid])
           hi = mid;
         else
           lo = mid + 1;
       }
       int x = lo, y = d - lo;
-      float wa = x < L ? aw[x] : 0.f, wb = y < L ? bw[y] : 0.f;
-      int ia = x < L ? ai[x] : 0, ib = y < L ? bi[y] : 0;
+      unsigned long long ka = x < L ? A[x] : ~0ull, kb = y < L ? B[y] : ~0ull;
       for (int e = 0; e < E; ++e) {
-        const bool take_a = y >= L || (x < L && !more_likely(wb, ib, wa, ia));
-        dw[o0 + e] = take_a ? wa : wb;
-        di[o0 + e] = take_a ? ia : ib;
-        if (take_a) {
-          ++x;
-          wa = x < L ? aw[x] : 0.f;
-          ia = x < L ? ai[x] : 0;
-        } else {
-          ++y;
-          wb = y < L ? bw[y] : 0.f;
-          ib = y < L ? bi[y] : 0;
-        }
+        const bool take_a = ka <= kb;   // an exhausted run reads as the largest key
+        dst[o0 + e] = take_a ? ka : kb;
+        if (take_a)
+          ka = ++x < L ? A[x] : ~0ull;
+        else
+          kb = ++y < L ? B[y] : ~0ull;
       }
     }
-    float* tf = sw;
-    sw = dw;
-    dw = tf;
-    int* tn = si;
-    si = di;
-    di = tn;
+    unsigned long long* tmp = src;
+    src = dst;
+    dst = tmp;
   }
   __syncthreads();
-  if (sw != cw) {   // an odd number of levels: the result back into cw / ci
-    for (int q = int(threadIdx.x); q < n2; q += NT) {
-      cw[q] = sw[q];
-      ci[q] = si[q];
-    }
+  if (src != ck) {   // an odd number of levels: the result back into ck
+    for (int q = int(threadIdx.x); q < n2; q += NT) ck[q] = src[q];
     __syncthreads();
   }
 }
 
-// The R most likely of nr runs of R pairs each in candidate order (nr and R powers of two), in order, into cw / ci
-// [0, R): pairwise merges that keep each pair's first R, one level per halving of the runs (output d of a pair by
-// merge path on diagonal d, A's pair first of two equal ones). tw / ti: scratch for nr R / 2 pairs. Every thread of
-// the work-group (NT) takes part.
+// The R smallest of nr ascending runs of R keys each (nr and R powers of two), in order, into ck[0, R): pairwise
+// merges that keep each pair's first R, one level per halving of the runs (output d of a pair by merge path on
+// diagonal d, A's key first of two equal ones). tk: scratch for nr R / 2 keys. Every thread of the work-group (NT).
 template <int NT>
-__device__ inline void merge_top(float* cw, int* ci, float* tw, int* ti, int nr, int R) {
-  float* sw = cw;
-  int* si = ci;
-  float* dw = tw;
-  int* di = ti;
+__device__ inline void merge_top(unsigned long long* ck, unsigned long long* tk, int nr, int R) {
+  unsigned long long* src = ck;
+  unsigned long long* dst = tk;
   for (int m = nr; m > 1; m >>= 1) {
     __syncthreads();
     for (int q = int(threadIdx.x); q < (m >> 1) * R; q += NT) {
       const int pr = q / R, d = q - pr * R;
-      const float* aw = sw + 2 * pr * R;
-      const int* ai = si + 2 * pr * R;
-      const float* bw = aw + R;
-      const int* bi = ai + R;
+      const unsigned long long* A = src + 2 * pr * R;
+      const unsigned long long* B = A + R;
       int lo = 0, hi = d;   // d < R: both runs can supply all d
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (more_likely(bw[d - 1 - mid], bi[d - 1 - mid], aw[mid], ai[mid]))
+        if (B[d - 1 - mid] < A[mid])
           hi = mid;
         else
           lo = mid + 1;
       }
-      const int x = lo, y = d - lo;   // x, y < R
-      const bool take_a = !more_likely(bw[y], bi[y], aw[x], ai[x]);
-      dw[q] = take_a ? aw[x] : bw[y];
-      di[q] = take_a ? ai[x] : bi[y];
+      const unsigned long long ka = A[lo], kb = B[d - lo];   // lo, d - lo < R
+      dst[q] = ka <= kb ? ka : kb;
     }
-    float* tf = sw;
-    sw = dw;
-    dw = tf;
-    int* tn = si;
-    si = di;
-    di = tn;
+    unsigned long long* tmp = src;
+    src = dst;
+    dst = tmp;
   }
   __syncthreads();
-  if (sw != cw) {
-    for (int q = int(threadIdx.x); q < R; q += NT) {
-      cw[q] = sw[q];
-      ci[q] = si[q];
-    }
+  if (src != ck) {
+    for (int q = int(threadIdx.x); q < R; q += NT) ck[q] = src[q];
     __syncthreads();
   }
 }
 
-// n2 (a power of two, <= kCand) pairs in LDS in any order into candidate order: runs of 64 sorted by the waves in
-// registers, then merged. tw / ti: scratch for n2 pairs. Every thread of the work-group (NT threads).
+// n2 (a power of two, <= kCand) keys in LDS in any order into ascending order: runs of 64 sorted by the waves in
+// registers, then merged. tk: scratch for n2 keys. Every thread of the work-group (NT threads).
 template <int NT>
-__device__ inline void sort_pairs(float* cw, int* ci, float* tw, int* ti, int n2) {
+__device__ inline void sort_pairs(unsigned long long* ck, unsigned long long* tk, int n2) {
   const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
-  __syncthreads();   // the pairs are in
+  __syncthreads();   // the keys are in
   for (int r = wave; r * 64 < n2; r += NT / 64) {
     const int q = r * 64 + lane;
-    float w = q < n2 ? cw[q] : -1.f;   // a run shorter than 64 (n2 < 64): padding that sorts last
-    int id = q < n2 ? ci[q] : INT_MAX;
-    wave_sort64(w, id);
-    if (q < n2) {
-      cw[q] = w;
-      ci[q] = id;
-    }
+    unsigned long long k = q < n2 ? ck[q] : kPadKey;   // a run shorter than 64 (n2 < 64): padding that sorts last
+    wave_sort64(k);
+    if (q < n2) ck[q] = k;
   }
-  merge_runs<NT>(cw, ci, tw, ti, n2, n2 < 64 ? n2 : 64);
+  merge_runs<NT>(ck, tk, n2, n2 < 64 ? n2 : 64);
 }
 
 // A weight that the kept prefix cannot go below, from the U pairs of the slices' lists (weights in [0, 1]; below 0:
@@ -536,8 +516,7 @@ __global__ void __launch_bounds__(64) argmax_pick_kernel(const SampleArgs a) {
 // most likely pairs: the 64 largest of the threads' first ones in candidate order (256 sorted in LDS) and the
 // largest of their second ones. Any weight of the slice at or above a threshold above both is one of those 64.
 __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const SampleArgs a) {
-  __shared__ float cw[kSliceThreads], tw[kSliceThreads];
-  __shared__ int ci[kSliceThreads], ti[kSliceThreads];
+  __shared__ unsigned long long ck[kSliceThreads], tk[kSliceThreads];
   __shared__ double dred[kSliceThreads / 64][2];
   __shared__ int ired[kSliceThreads / 64];
   __shared__ float m2red[kSliceThreads / 64];
@@ -583,15 +562,13 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
   const size_t so = size_t(row) * a.slices + sl;
   if (a.lists) {
     // the threads' first pairs in candidate order: each wave's 64 in registers, then merged
-    float wq = w1;
-    int iq = i1;
-    wave_sort64(wq, iq);
-    cw[t] = wq;
-    ci[t] = iq;
-    merge_runs<kSliceThreads>(cw, ci, tw, ti, kSliceThreads, 64);
+    unsigned long long kq = pair_key(w1, i1);
+    wave_sort64(kq);
+    ck[t] = kq;
+    merge_runs<kSliceThreads>(ck, tk, kSliceThreads, 64);
     if (t < kSliceTop) {
-      a.sw[so * kSliceTop + t] = cw[t];
-      a.si[so * kSliceTop + t] = ci[t];
+      a.sw[so * kSliceTop + t] = key_w(ck[t]);
+      a.si[so * kSliceTop + t] = key_id(ck[t]);
     }
   } else {
     __syncthreads();
@@ -614,11 +591,11 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
 __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const SampleArgs a) {
   __shared__ double red[kSampleThreads / 64 + 4];   // >= 20
   __shared__ uint32_t ured[kSampleThreads / 64 + 1];
-  __shared__ uint32_t hist[16 * kSampleThreads];   // the whole-row sort's digit counts, or the merges' scratch
-  __shared__ float cw[kCand];
-  __shared__ int ci[kCand];
-  float* tw = reinterpret_cast<float*>(hist);
-  int* ti = reinterpret_cast<int*>(hist + kCand);
+  // the whole-row sort's digit counts, or the merges' scratch keys
+  __shared__ __align__(16) uint32_t hist[16 * kSampleThreads];
+  static_assert(2 * kCand <= 16 * kSampleThreads, "scratch keys in hist");
+  __shared__ unsigned long long ck[kCand];   // candidates as pair keys
+  unsigned long long* tk = reinterpret_cast<unsigned long long*>(hist);
   __shared__ unsigned long long selh[256];
   __shared__ int sel, ccount, slices_ok;
   __shared__ unsigned long long above_s;
@@ -672,20 +649,18 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   const float* uw = a.sw + so * kSliceTop;
   const int* ui = a.si + so * kSliceTop;
   const bool top_only = topk && a.top_k <= kSliceTop && U <= kCand;
-  int nc = INT_MAX;        // candidates in cw / ci (INT_MAX: none yet)
+  int nc = INT_MAX;        // candidates in ck (INT_MAX: none yet)
   bool in_order = false;   // in candidate order already
   float tau = -1.f;
   if (top_only) {
     int n2 = 1;
     while (n2 < U) n2 <<= 1;
-    for (int q = t; q < n2; q += kSampleThreads) {
-      cw[q] = q < U ? uw[q] : -1.f;
-      ci[q] = q < U ? ui[q] : INT_MAX;
-    }
+    for (int q = t; q < n2; q += kSampleThreads) ck[q] = q < U ? pair_key(uw[q], ui[q]) : kPadKey;
     // every slice's list (and the padding) is a run of kSliceTop in candidate order; top_k up to kSliceTop needs
     // only the union's first kSliceTop (the filters never look past the first top_k candidates)
-    merge_top<kSampleThreads>(cw, ci, tw, ti, n2 / kSliceTop, kSliceTop);
-    tau = cw[a.top_k - 1] >= 0.f ? cw[a.top_k - 1] : -1.f;
+    merge_top<kSampleThreads>(ck, tk, n2 / kSliceTop, kSliceTop);
+    const float wk = key_w(ck[a.top_k - 1]);
+    tau = wk >= 0.f ? wk : -1.f;
   } else if (topk) {
     tau = a.top_k <= U ? union_select(uw, U, false, double(a.top_k), selh, &sel, &above_s) : -1.f;
   } else {
@@ -710,7 +685,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     if (t == 0) sel = kSliceTop;
     __syncthreads();
     for (int q = t; q < kSliceTop; q += kSampleThreads)
-      if (!(cw[q] >= tau)) atomicMin(&sel, q);
+      if (!(key_w(ck[q]) >= tau)) atomicMin(&sel, q);
     __syncthreads();
     nc = sel;
     in_order = true;
@@ -731,15 +706,9 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     int at = int(block_exclusive<uint32_t>(uint32_t(c), ured, &tot));
 #pragma unroll
     for (int r = 0; r < PT; ++r)
-      if (x[r] >= tau) {
-        cw[at] = x[r];
-        ci[at] = xi[r];
-        ++at;
-      }
+      if (x[r] >= tau) ck[at++] = pair_key(x[r], xi[r]);
     nc = int(tot);
   }
-  const float* sw_l = cw;
-  const int* si_l = ci;
   const uint32_t* ksrc = nullptr;
   const int* isrc = nullptr;
   int L;   // candidates available in order
@@ -779,10 +748,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
 #pragma unroll
         for (int u = 0; u < kGather; ++u)
           if (v[u] >= tau) {
-            if (pos < kCand) {
-              cw[pos] = v[u];
-              ci[pos] = r0 + u * kSampleThreads + t;
-            }
+            if (pos < kCand) ck[pos] = pair_key(v[u], r0 + u * kSampleThreads + t);
             ++pos;
           }
       }
@@ -793,11 +759,8 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     if (nc <= kCand) {
       int n2 = 1;
       while (n2 < nc) n2 <<= 1;
-      for (int q = nc + t; q < n2; q += kSampleThreads) {
-        cw[q] = -1.f;
-        ci[q] = INT_MAX;
-      }
-      sort_pairs<kSampleThreads>(cw, ci, tw, ti, n2);
+      for (int q = nc + t; q < n2; q += kSampleThreads) ck[q] = kPadKey;
+      sort_pairs<kSampleThreads>(ck, tk, n2);
       L = nc;
     } else {
       // the whole row, stably sorted by (~bits(w), index), 4 bits a pass, contiguous chunks per thread
@@ -866,8 +829,8 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
       L = n;
     }
   }
-  auto sw = [&](int j) { return ksrc ? __uint_as_float(~ksrc[j]) : sw_l[j]; };
-  auto sidx = [&](int j) { return ksrc ? isrc[j] : si_l[j]; };
+  auto sw = [&](int j) { return ksrc ? __uint_as_float(~ksrc[j]) : key_w(ck[j]); };
+  auto sidx = [&](int j) { return ksrc ? isrc[j] : key_id(ck[j]); };
 
   // the reference's filters over the candidates in order (sampler.cpp:63-91)
   int keep = n;
