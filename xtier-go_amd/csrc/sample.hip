@@ -363,16 +363,27 @@ __device__ inline float union_select(const float* __restrict__ uw, int U, bool m
   const unsigned long long tgt = mass ? (unsigned long long)ceil(target * scale) : (unsigned long long)target;
   uint32_t prefix = 0u;
   unsigned long long above = 0ull;
+  // the first 4 * kSampleThreads weights stay in registers over the passes (the lists were written on other XCDs:
+  // each read waits on memory); any beyond are read again by each pass
+  constexpr int KR = 4;
+  float xr[KR];
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    const int e = t + r * kSampleThreads;
+    xr[r] = e < U ? uw[e] : -1.f;
+  }
   for (int p = 0; p < 3; ++p) {
     const int sh = 24 - 8 * p;
     if (t < 256) h[t] = 0ull;
     __syncthreads();
-    for (int e = t; e < U; e += kSampleThreads) {
-      const float x = uw[e];
+    auto add = [&](float x) {
       const uint32_t b = __float_as_uint(x);
       if (x >= 0.f && (p == 0 || (b >> (sh + 8)) == prefix))
         atomicAdd(&h[(b >> sh) & 255u], mass ? (unsigned long long)(double(x) * scale) : 1ull);
-    }
+    };
+#pragma unroll
+    for (int r = 0; r < KR; ++r) add(xr[r]);
+    for (int e = t + KR * kSampleThreads; e < U; e += kSampleThreads) add(uw[e]);
     __syncthreads();
     if (wave == 0) {   // digits from the most likely: lane l holds 255 - 4 l .. 252 - 4 l
       unsigned long long c[4], s = 0ull;
@@ -524,8 +535,15 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
   const float* l = a.logits + size_t(row) * size_t(a.n);
   float* w = a.w + size_t(row) * size_t(a.n);
   const int b = sl * kSlice, e = min(a.n, b + kSlice);
+  // the row's max over the slices' maxima: loaded in parallel (they were written on other XCDs), then reduced
+  __shared__ float mred[kSliceThreads / 64];
   float mx = -INFINITY;
-  for (int s = 0; s < a.slices; ++s) mx = fmaxf(mx, a.smax[size_t(row) * a.slices + s]);
+  for (int s = t; s < a.slices; s += kSliceThreads) mx = fmaxf(mx, a.smax[size_t(row) * a.slices + s]);
+  mx = wave_max(mx);
+  if ((t & 63) == 0) mred[t >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kSliceThreads / 64; ++q) mx = fmaxf(mx, mred[q]);
   const float inv_t = 1.f / a.temperature;
   const float floor_w = a.min_p * 1.0f;
   float v[kSlice / kSliceThreads];
@@ -605,14 +623,33 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   const size_t so = size_t(row) * S;
   const float floor_w = a.min_p * 1.0f;
 
-  // totals over the row: slice by slice, in order
-  if (t == 0) {
+  // totals over the row: slice by slice, in order; the slices' figures (written on other XCDs) go through LDS in
+  // chunks of 1024, loaded in parallel, and one thread adds them in order
+  double* lsum = reinterpret_cast<double*>(hist);
+  double* lfl = lsum + kSampleThreads;
+  int* lnf = reinterpret_cast<int*>(lfl + kSampleThreads);
+  {
     double tot = 0.0, tf = 0.0;
     int nf = 0;
-    for (int q = 0; q < S; ++q) tot += a.ssum[so + q], tf += a.sfl[so + q], nf += a.snfl[so + q];
-    red[0] = tot;
-    red[1] = tf;
-    ccount = nf;
+    for (int b = 0; b < S; b += kSampleThreads) {
+      if (b + t < S) {
+        lsum[t] = a.ssum[so + b + t];
+        lfl[t] = a.sfl[so + b + t];
+        lnf[t] = a.snfl[so + b + t];
+      }
+      __syncthreads();
+      if (t == 0) {
+        const int m = min(kSampleThreads, S - b);
+#pragma unroll 8
+        for (int i = 0; i < m; ++i) tot += lsum[i], tf += lfl[i], nf += lnf[i];
+      }
+      __syncthreads();
+    }
+    if (t == 0) {
+      red[0] = tot;
+      red[1] = tf;
+      ccount = nf;
+    }
   }
   __syncthreads();
   double total = red[0];
@@ -623,10 +660,26 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   const bool topk = a.top_k > 0 && a.top_k < n;
   if (!topk && a.top_p >= 1.f && a.min_p <= 0.f) {   // no filter: the candidates in index order
     const double r = a.u[row] * total;
-    if (t == 0) {   // the slice where the running sum passes r, and the running sum before it
+    if (t == 0) {   // the slice where the running sum passes r, and the running sum before it (8 sums read at once)
       double c = 0.0;
       int q = 0;
-      while (q < S - 1 && !(c + a.ssum[so + q] > r)) c += a.ssum[so + q++];
+      bool done = false;
+      for (int q0 = 0; q0 < S && !done; q0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = q0 + i < S ? (S <= kSampleThreads ? lsum[q0 + i] : a.ssum[so + q0 + i]) : 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (!done) {
+            if (q0 + i >= S - 1 || c + v[i] > r) {
+              q = q0 + i;
+              done = true;
+            } else {
+              c += v[i];
+            }
+          }
+        }
+      }
       sel = q;
       base_s = c;
     }
@@ -649,6 +702,8 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   const float* uw = a.sw + so * kSliceTop;
   const int* ui = a.si + so * kSliceTop;
   const bool top_only = topk && a.top_k <= kSliceTop && U <= kCand;
+  const float last_p = t < S ? uw[size_t(t) * kSliceTop + kSliceTop - 1] : 0.f;
+  const float m2_p = t < S ? a.sm2[so + t] : 0.f;
   int nc = INT_MAX;        // candidates in ck (INT_MAX: none yet)
   bool in_order = false;   // in candidate order already
   float tau = -1.f;
@@ -671,13 +726,13 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     if (a.min_p > 0.f) tau = fmaxf(tau, floor_w);   // min_p keeps nothing below its floor
   }
   // every weight >= tau is a listed thread maximum when, in every slice, the 64th listed maximum and every thread's
-  // second most likely lie below tau
+  // second most likely lie below tau (the first 1024 slices' figures were loaded before tau was known)
   if (t == 0) slices_ok = 1;
   __syncthreads();
   if (tau >= 0.f)
     for (int q = t; q < S; q += kSampleThreads) {
-      const float last = uw[size_t(q) * kSliceTop + kSliceTop - 1];
-      const float m2 = a.sm2[so + q];
+      const float last = q == t ? last_p : uw[size_t(q) * kSliceTop + kSliceTop - 1];
+      const float m2 = q == t ? m2_p : a.sm2[so + q];
       if (!(last < tau) || !(m2 < tau)) atomicAnd(&slices_ok, 0);   // ties or runs at tau may continue past the lists
     }
   __syncthreads();
