@@ -451,6 +451,9 @@ struct SampleArgs {
   float* sw;             // [rows][slices][kSliceTop]: the slice's 64 largest thread maxima, in candidate order
   int* si;
   float* sm2;            // [rows][slices]: the largest second-most-likely weight of any thread of the slice
+  float* tmax;           // [rows][slices][kSliceThreads]: each slice thread's most likely weight (-1: none)
+  float* tsec;           // [rows][slices][kSliceThreads]: its second most likely (-1: none)
+  uint8_t* tu;           // [rows][slices][kSliceThreads]: the most likely one's place u (index b + t + 256 u)
   int lists;             // a filter applies: make the lists
   uint32_t* keys;        // [rows][2][n] (the whole-row sort)
   int* idx;
@@ -579,6 +582,11 @@ __global__ void __launch_bounds__(kSliceThreads) slice_weights_kernel(const Samp
   if ((t & 63) == 0) dred[t >> 6][0] = s, dred[t >> 6][1] = sf, ired[t >> 6] = nf, m2red[t >> 6] = m2;
   const size_t so = size_t(row) * a.slices + sl;
   if (a.lists) {
+    // the thread's summary: the gather of candidates at or above a threshold reads it instead of the row
+    const size_t th = so * kSliceThreads + size_t(t);
+    a.tmax[th] = w1;
+    a.tsec[th] = w2;
+    a.tu[th] = uint8_t(i1 == INT_MAX ? 0 : (i1 - b - t) / kSliceThreads);
     // the threads' first pairs in candidate order: each wave's 64 in registers, then merged
     unsigned long long kq = pair_key(w1, i1);
     wave_sort64(kq);
@@ -615,7 +623,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
   __shared__ unsigned long long ck[kCand];   // candidates as pair keys
   unsigned long long* tk = reinterpret_cast<unsigned long long*>(hist);
   __shared__ unsigned long long selh[256];
-  __shared__ int sel, ccount, slices_ok;
+  __shared__ int sel, ccount, slices_ok, nread;
   __shared__ unsigned long long above_s;
   __shared__ double base_s;
   const int row = int(blockIdx.x), t = int(threadIdx.x), n = a.n, S = a.slices;
@@ -775,21 +783,41 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
     if (t == 0) ccount = 0;
     __syncthreads();
     if (nc == INT_MAX && tau >= 0.f) {
-      // rounds of kGather weights per thread, all loads in flight (the row was written by other work-groups: its
-      // lines come from beyond this XCD's L2); a wave takes its places with one atomic, each lane its share by a
-      // prefix over the wave's counts (the order is free: the pairs are sorted next)
-      constexpr int kGather = 32;
+      // from the slices' thread summaries, 16 slice threads a thread with every load in flight (they were written on
+      // other XCDs): a slice thread whose second most likely lies below tau holds at most its first, at b + t + 256 u;
+      // one whose second reaches tau is listed, and its weights are read from the row next. A wave takes places for
+      // the first kind with one atomic, each hit of the second kind one (the order is free: the pairs are sorted next).
+      constexpr int PT = 16;
+      constexpr int kReadCap = kCand / 2;   // slice threads to read from the row (each holds >= 2 candidates)
+      int* rlist = reinterpret_cast<int*>(hist);
+      if (t == 0) nread = 0;
+      __syncthreads();
       const int lane = t & 63;
-      for (int r0 = 0; r0 < n; r0 += kGather * kSampleThreads) {   // the same rounds in every thread
-        float v[kGather];
+      const int nth = S * kSliceThreads;   // a multiple of PT
+      const size_t tb = so * kSliceThreads;
+      for (int j0 = 0; j0 < nth; j0 += PT * kSampleThreads) {   // the same rounds in every thread
+        const int j = j0 + PT * t;
+        float fm[PT], fs[PT];
+        uint8_t fu[PT];
+        if (j < nth) {
 #pragma unroll
-        for (int u = 0; u < kGather; ++u) {
-          const int i = r0 + u * kSampleThreads + t;
-          v[u] = i < n ? w[i] : -1.f;
+          for (int q = 0; q < PT / 4; ++q) {
+            const float4 m4 = *reinterpret_cast<const float4*>(a.tmax + tb + j + 4 * q);
+            const float4 s4 = *reinterpret_cast<const float4*>(a.tsec + tb + j + 4 * q);
+            fm[4 * q] = m4.x, fm[4 * q + 1] = m4.y, fm[4 * q + 2] = m4.z, fm[4 * q + 3] = m4.w;
+            fs[4 * q] = s4.x, fs[4 * q + 1] = s4.y, fs[4 * q + 2] = s4.z, fs[4 * q + 3] = s4.w;
+          }
+          const uint4 u4 = *reinterpret_cast<const uint4*>(a.tu + tb + j);
+          const uint32_t uw4[4] = {u4.x, u4.y, u4.z, u4.w};
+#pragma unroll
+          for (int q = 0; q < PT; ++q) fu[q] = uint8_t(uw4[q >> 2] >> (8 * (q & 3)));
+        } else {
+#pragma unroll
+          for (int q = 0; q < PT; ++q) fm[q] = fs[q] = -1.f, fu[q] = 0;
         }
         int c = 0;
 #pragma unroll
-        for (int u = 0; u < kGather; ++u) c += v[u] >= tau ? 1 : 0;
+        for (int q = 0; q < PT; ++q) c += fs[q] < tau && fm[q] >= tau ? 1 : 0;
         int incl = c;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -801,12 +829,32 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
         if (lane == 0 && wtot > 0) wb = atomicAdd(&ccount, wtot);
         int pos = __shfl(wb, 0) + incl - c;
 #pragma unroll
-        for (int u = 0; u < kGather; ++u)
-          if (v[u] >= tau) {
-            if (pos < kCand) ck[pos] = pair_key(v[u], r0 + u * kSampleThreads + t);
+        for (int q = 0; q < PT; ++q) {
+          const int jj = j + q, sl = jj / kSliceThreads, tt = jj % kSliceThreads;
+          if (fs[q] < tau && fm[q] >= tau) {
+            if (pos < kCand) ck[pos] = pair_key(fm[q], sl * kSlice + tt + kSliceThreads * int(fu[q]));
             ++pos;
+          } else if (fs[q] >= tau) {
+            const int at = atomicAdd(&nread, 1);
+            if (at < kReadCap) rlist[at] = jj;
           }
+        }
       }
+      // the listed slice threads' weights from the row, 8 threads to each, all loads at once; more than kReadCap of
+      // them hold more than kCand candidates, which the whole-row sort takes
+      __syncthreads();
+      const int nr = min(nread, kReadCap);
+      constexpr int PU = kSlice / kSliceThreads;
+      for (int e = t; e < nr * PU; e += kSampleThreads) {
+        const int jj = rlist[e / PU], u = e % PU;
+        const int i = (jj / kSliceThreads) * kSlice + jj % kSliceThreads + u * kSliceThreads;
+        const float x = i < n ? w[i] : -1.f;
+        if (x >= tau) {
+          const int at = atomicAdd(&ccount, 1);
+          if (at < kCand) ck[at] = pair_key(x, i);
+        }
+      }
+      if (t == 0 && nread > kReadCap) atomicMax(&ccount, kCand + 1);
     }
     __syncthreads();
     if (nc == INT_MAX) nc = tau >= 0.f ? ccount : INT_MAX;
@@ -929,7 +977,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_pick_kernel(const Sampl
 
 namespace {
 struct SampleScratch {
-  size_t w, smax, sbest, sbi, ssum, sfl, snfl, sw, si, sm2, keys, idx, total;
+  size_t w, smax, sbest, sbi, ssum, sfl, snfl, sw, si, sm2, tmax, tsec, tu, keys, idx, total;
 };
 SampleScratch scratch_layout(int rows, int n) {
   const size_t S = size_t((n + kSlice - 1) / kSlice), R = size_t(rows), N = size_t(n);
@@ -950,6 +998,9 @@ SampleScratch scratch_layout(int rows, int n) {
   o.sw = take(R * S * kSliceTop * 4);
   o.si = take(R * S * kSliceTop * 4);
   o.sm2 = take(R * S * 4);
+  o.tmax = take(R * S * kSliceThreads * 4);
+  o.tsec = take(R * S * kSliceThreads * 4);
+  o.tu = take(R * S * kSliceThreads);
   o.keys = take(R * 2 * N * 4);
   o.idx = take(R * 2 * N * 4);
   o.total = at;
@@ -973,6 +1024,9 @@ SampleArgs sample_args(const float* logits, int rows, int n, void* scratch, int*
   a.sw = reinterpret_cast<float*>(base + o.sw);
   a.si = reinterpret_cast<int*>(base + o.si);
   a.sm2 = reinterpret_cast<float*>(base + o.sm2);
+  a.tmax = reinterpret_cast<float*>(base + o.tmax);
+  a.tsec = reinterpret_cast<float*>(base + o.tsec);
+  a.tu = reinterpret_cast<uint8_t*>(base + o.tu);
   a.keys = reinterpret_cast<uint32_t*>(base + o.keys);
   a.idx = reinterpret_cast<int*>(base + o.idx);
   a.out = out;
