@@ -84,6 +84,44 @@ def test_one_token_steps_fused_and_separate(hip, orc, wl, monkeypatch, loops):
     separate.destroy()
 
 
+def test_verify_steps_split_and_whole_k(hip, orc, wl, monkeypatch):
+    """Steps of 2..8 rows split the gate/up, down and o projections' K in two (two output sets, added by the norm
+    launch that reads them); XTG_VERIFY_WHOLE_K=1 keeps the whole K. A model wide enough that each half holds
+    several k-tiles (hidden 1024, FFN 2048, 8 q heads of 128): both against the oracle, and against each other over
+    the same calls (the halves' sum differs from the whole sum by rounding only); one-row steps between them."""
+    w = wl.DoryWeights(dict(wl.DORY_TINY, hidden=1024, ffn=2048, heads=8, kv_heads=2, head_dim=128), seed=15,
+                       context=128)
+    H, V = w.cfg["hidden"], w.cfg["vocab"]
+    ref = orc.Dory(w, wl)
+    split = hip.dory(w)
+    monkeypatch.setenv("XTG_VERIFY_WHOLE_K", "1")
+    whole = hip.dory(w)
+    monkeypatch.delenv("XTG_VERIFY_WHOLE_K")
+    rng = np.random.default_rng(16)
+    dx = hip.array(shape=(8, H))
+    dl = hip.array(shape=(8, V))
+    pos = 0
+    for step, m in enumerate([8, 2, 1, 5, 8, 3]):
+        x = unit_rows(rng, m, H)
+        dx.upload(np.concatenate([x, np.zeros((8 - m, H), np.float32)]))
+        outs = []
+        for dev in (split, whole):
+            dev.forward(dx, m, pos, dl)
+            outs.append(dl.numpy()[:m].copy())
+        want = ref.forward(x, pos)
+        for got in outs:
+            assert rel_l2(got, want) <= 1e-3, step
+            assert (got.argmax(1) == want.argmax(1)).all(), step
+        e = rel_l2(outs[0], outs[1])
+        print("step %d (%d rows): split against whole K %.2e" % (step, m, e))
+        assert e <= 1e-4, step
+        pos += m
+    dx.free()
+    dl.free()
+    split.destroy()
+    whole.destroy()
+
+
 def test_wide_model_one_token_steps(hip, orc, wl, monkeypatch):
     """hidden 5120 / FFN 9728 with 32 q heads of 128: the q/k/v/g launch (640 row-blocks, 40 k-tiles) and the down
     projection (76 k-tiles) take launch shapes no fused one-token kernel is made for, so the session runs its
