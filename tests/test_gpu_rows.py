@@ -143,3 +143,28 @@ def test_sample(hip, orc, n):
             checked += 1
     dout.free()
     assert checked > 0
+
+
+@pytest.mark.gpu
+def test_sample_past_1024_slices(hip, orc):
+    """A row of 1026 * 2048 - 3 logits: more slices (1026) than the pick kernel's 1024 threads, so the slices'
+    totals go through LDS in two chunks, the walk without a filter reads the sums past the first chunk from memory,
+    the threshold select reads lists past its registers and the gather from the thread summaries takes several
+    rounds; each filter kind against the oracle, two rows per call (ties planted in one)."""
+    n = 1026 * 2048 - 3
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((2, n)) * 3).astype(np.float32)
+    x[1, rng.integers(0, n, 4)] = x[1].max()
+    dx = hip.array(x)
+    dout = hip.array(shape=(2,), dtype=np.int32)
+    for params in (dict(temperature=0.8), dict(temperature=0.8, top_k=50), dict(temperature=0.8, top_k=3000),
+                   dict(temperature=0.8, top_p=0.9), dict(temperature=1.3, min_p=0.05, top_p=0.7)):
+        u = rng.random(2)
+        hip.sample(dx, 2, n, u, dout, **params)
+        got = dout.numpy()
+        want, margin = orc.sample(x, u, **params)
+        for r in range(2):
+            if got[r] != want[r]:
+                assert margin[r] < 1e-6, (params, r, int(got[r]), int(want[r]), float(margin[r]))
+    dx.free()
+    dout.free()
