@@ -101,18 +101,19 @@ __device__ inline void add_part(const float* row, int w, int vec, float (&r)[U][
     for (int e = 0; e < 8; ++e) r[u][e] += p[u][e];
 }
 
-template <int U>
-__global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
-                                                                   size_t part, const float* __restrict__ lr, int w,
-                                                                   int vec, f16x8* __restrict__ xop,
-                                                                   float* __restrict__ xinv, size_t ostride) {
+// PART: o holds two parts of a row split along K (the second at o + part), added as they load; its loads go out with
+// the others (a load behind a branch would wait for them).
+template <int U, bool PART>
+__device__ inline void slerp_norm_row(float* __restrict__ x, const float* __restrict__ o, size_t part,
+                                      const float* __restrict__ lr, int w, int vec, f16x8* __restrict__ xop,
+                                      float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float* xr = x + size_t(blockIdx.x) * w;
   float a[U][8], b[U][8], l[U][8];
   load_row<kNormThreads, U>(xr, w, vec, a);
   load_row<kNormThreads, U>(o + size_t(blockIdx.x) * w, w, vec, b);
   load_row<kNormThreads, U>(lr, w, vec, l);
-  if (part) add_part<U>(o + part + size_t(blockIdx.x) * w, w, vec, b);
+  if constexpr (PART) add_part<U>(o + part + size_t(blockIdx.x) * w, w, vec, b);
   float sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -136,19 +137,34 @@ __global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restr
 }
 
 template <int U>
-__global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* g,
-                                                                    const float* __restrict__ u_, size_t part,
-                                                                    const float* __restrict__ sg,
-                                                                    const float* __restrict__ su, int w, int vec,
-                                                                    float* out, f16x8* __restrict__ xop,
-                                                                    float* __restrict__ xinv, size_t ostride) {
+__global__ void __launch_bounds__(kNormThreads) slerp_norm_kernel(float* __restrict__ x, const float* __restrict__ o,
+                                                                   size_t part, const float* __restrict__ lr, int w,
+                                                                   int vec, f16x8* __restrict__ xop,
+                                                                   float* __restrict__ xinv, size_t ostride) {
+  slerp_norm_row<U, false>(x, o, part, lr, w, vec, xop, xinv, ostride);
+}
+
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) slerp_norm_part_kernel(float* __restrict__ x,
+                                                                        const float* __restrict__ o, size_t part,
+                                                                        const float* __restrict__ lr, int w, int vec,
+                                                                        f16x8* __restrict__ xop,
+                                                                        float* __restrict__ xinv, size_t ostride) {
+  slerp_norm_row<U, true>(x, o, part, lr, w, vec, xop, xinv, ostride);
+}
+
+// PART: g and u hold two parts of rows split along K (the second at + part), added as they load, with the other loads.
+template <int U, bool PART>
+__device__ inline void swiglu_norm_row(const float* g, const float* __restrict__ u_, size_t part,
+                                       const float* __restrict__ sg, const float* __restrict__ su, int w, int vec,
+                                       float* out, f16x8* __restrict__ xop, float* __restrict__ xinv, size_t ostride) {
   __shared__ float red[kNormRed];
   float a[U][8], b[U][8], s1[U][8], s2[U][8];
   load_row<kNormThreads, U>(g + size_t(blockIdx.x) * w, w, vec, a);
   load_row<kNormThreads, U>(u_ + size_t(blockIdx.x) * w, w, vec, b);
   load_row<kNormThreads, U>(sg, w, vec, s1);
   load_row<kNormThreads, U>(su, w, vec, s2);
-  if (part) {
+  if constexpr (PART) {
     add_part<U>(g + part + size_t(blockIdx.x) * w, w, vec, a);
     add_part<U>(u_ + part + size_t(blockIdx.x) * w, w, vec, b);
   }
@@ -162,6 +178,24 @@ __global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* 
       s += a[u][e] * a[u][e];
     }
   finish_row<U>(a, s, w, vec, out ? out + size_t(blockIdx.x) * w : nullptr, xop, xinv, ostride, red);
+}
+
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) swiglu_norm_kernel(const float* g, const float* __restrict__ u_,
+                                                                    size_t part, const float* __restrict__ sg,
+                                                                    const float* __restrict__ su, int w, int vec,
+                                                                    float* out, f16x8* __restrict__ xop,
+                                                                    float* __restrict__ xinv, size_t ostride) {
+  swiglu_norm_row<U, false>(g, u_, part, sg, su, w, vec, out, xop, xinv, ostride);
+}
+
+template <int U>
+__global__ void __launch_bounds__(kNormThreads) swiglu_norm_part_kernel(const float* g, const float* __restrict__ u_,
+                                                                         size_t part, const float* __restrict__ sg,
+                                                                         const float* __restrict__ su, int w, int vec,
+                                                                         float* out, f16x8* __restrict__ xop,
+                                                                         float* __restrict__ xinv, size_t ostride) {
+  swiglu_norm_row<U, true>(g, u_, part, sg, su, w, vec, out, xop, xinv, ostride);
 }
 
 template <int U>
@@ -321,6 +355,7 @@ std::string launch_slerp_norm(float* x, const float* o, const float* lr, int row
                               hipStream_t stream, size_t part) {
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {x, o, lr, o + part});
+  if (part) XTG_NORM_DISPATCH(slerp_norm_part_kernel, x, o, part, lr, w, vec, p.xop, p.xinv, p.stride);
   XTG_NORM_DISPATCH(slerp_norm_kernel, x, o, part, lr, w, vec, p.xop, p.xinv, p.stride);
 }
 
@@ -329,6 +364,7 @@ std::string launch_swiglu_norm(const float* g, const float* u, const float* sg, 
   XTG_CHECK(!part || (out != g && out != u), "swiglu_norm: a split input is not written in place");
   const Operand p = operand_of(op, rows, w);
   const int vec = rows_vec(w, {g, u, sg, su, out, g + part, u + part});
+  if (part) XTG_NORM_DISPATCH(swiglu_norm_part_kernel, g, u, part, sg, su, w, vec, out, p.xop, p.xinv, p.stride);
   XTG_NORM_DISPATCH(swiglu_norm_kernel, g, u, part, sg, su, w, vec, out, p.xop, p.xinv, p.stride);
 }
 
