@@ -122,9 +122,10 @@ __device__ inline double wave_range_sum(WF wf, int b, int e) {
 }
 
 // The first position i in [0, len) at which the running sum of wf(0 .. i) satisfies strict ? sum > r : sum >= r,
-// or len when none does; *at_sum: that running sum (the whole sum when none), both counted from base0. Three
-// levels: 16 segments (a wave each), the crossing segment's 16 parts (a wave each), then the crossing part's tiles
-// of 64 by one wave, the crossing tile scanned. The sums of each level run in order. red: >= 20 doubles, sel: LDS int.
+// or len when none does; *at_sum: that running sum (the whole sum when none), both counted from base0. Up to three
+// levels: 16 segments (a wave each), the crossing segment's 16 parts (a wave each) unless the segment holds at most
+// 512, then the crossing range's tiles of 64 by one wave, the crossing tile scanned. The sums of each level run in
+// order. red: >= 20 doubles, sel: LDS int.
 template <typename WF>
 __device__ inline int first_crossing(WF wf, int len, double r, bool strict, double* red, int* sel, double* at_sum,
                                      double base0 = 0.0) {
@@ -168,6 +169,7 @@ __device__ inline int first_crossing(WF wf, int len, double r, bool strict, doub
     const int nlo = min(hi, lo + found * part);
     hi = min(hi, nlo + part);
     lo = nlo;
+    if (hi - lo <= 512) break;   // few enough for the walk below (8 tiles of 64 loaded at once)
   }
   // level 3: one wave walks [lo, hi) (at most 8 tiles of 64 for rows up to 131072) in tiles, eight loaded at once
   if (wave == 0) {
