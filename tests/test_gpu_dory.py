@@ -84,13 +84,17 @@ def test_one_token_steps_fused_and_separate(hip, orc, wl, monkeypatch, loops):
     separate.destroy()
 
 
-def test_verify_steps_split_and_whole_k(hip, orc, wl, monkeypatch):
+@pytest.mark.parametrize("shape", [(1024, 2048, 8, 2), (1280, 2816, 10, 5)])
+def test_verify_steps_split_and_whole_k(hip, orc, wl, monkeypatch, shape):
     """Steps of 2..8 rows split the gate/up, down and o projections' K in two (two output sets, added by the norm
-    launch that reads them); XTG_VERIFY_WHOLE_K=1 keeps the whole K. A model wide enough that each half holds
-    several k-tiles (hidden 1024, FFN 2048, 8 q heads of 128): both against the oracle, and against each other over
-    the same calls (the halves' sum differs from the whole sum by rounding only); one-row steps between them."""
-    w = wl.DoryWeights(dict(wl.DORY_TINY, hidden=1024, ffn=2048, heads=8, kv_heads=2, head_dim=128), seed=15,
-                       context=128)
+    launch that reads them); XTG_VERIFY_WHOLE_K=1 keeps the whole K. Models wide enough that each half holds
+    several k-tiles of 256 (hidden 1024, FFN 2048, 8 q heads of 128), and with odd k-tile counts, whose second half
+    is a tile shorter (hidden 1280 and 10 q heads of 128: 5 tiles; FFN 2816: 11): both against the oracle, and
+    against each other over the same calls (the halves' sum differs from the whole sum by rounding only); one-row
+    steps between them."""
+    hidden, ffn, heads, kv_heads = shape
+    w = wl.DoryWeights(dict(wl.DORY_TINY, hidden=hidden, ffn=ffn, heads=heads, kv_heads=kv_heads, head_dim=128),
+                       seed=15, context=128)
     H, V = w.cfg["hidden"], w.cfg["vocab"]
     ref = orc.Dory(w, wl)
     split = hip.dory(w)
