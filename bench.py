@@ -931,6 +931,84 @@ def decode_eager_pass(pkg, wl, hip, ctx, kv_fp8, reps):
     return ms
 
 
+PHASES = ("entry", "loads issued", "first row load in", "operand built", "first weight tile in", "matrix ops done",
+          "work-group barrier passed", "stores issued")
+
+
+def gemv_phases(pkg, wl, reps):
+    """Per-wave phase stamps of the step's 8-row GEMV launches (gemv_kernel on raw BF16 rows), from the phase-stamp
+    build (xtier-go_amd/build.py --stamps, loaded through XTG_HIP_LIB): each wave records the constant-rate clock at
+    its entry, once its loads are issued, when its first row load and its first weight tile have arrived, once its
+    operand is built, after its matrix ops, after the work-group's barrier and after its stores. One launch at a
+    time on weights not touched for >= 1 GiB of other calls (cold), events around it; times are from the first
+    wave's entry (the earliest, median and latest wave to reach each point; medians over the repetitions)."""
+    import ctypes
+    setter = pkg.lib().xtg_hip_phase_stamps
+    setter.restype = ctypes.c_int
+    setter.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.POINTER(ctypes.c_int)]
+    rng = np.random.default_rng(20261201)
+    base = {name: [pkg.Weight(*wl.nvfp4_weight(rng, n, k)) for n, k in shapes] for name, shapes in SHAPES}
+    set_bytes = sum(w.codes.nbytes + w.scales.nbytes for ws in base.values() for w in ws)
+    copies = max(2, -(-(1 << 30) // set_bytes) + 1)
+    hip = pkg.HipBackend(0)
+    sets = []
+    for _ in range(copies):
+        s = {name: [pkg.Weight(w.codes.copy(), w.scales.copy(), w.glob) for w in ws] for name, ws in base.items()}
+        for ws in s.values():
+            for w in ws:
+                hip.prepare(w)
+        sets.append(s)
+    dx = {name: hip.array(wl.unit_rows_bf16(rng, 8, shapes[0][1])) for name, shapes in SHAPES}
+    dy = hip.array(shape=(8 * 16384 + 64,))
+    records = 2 * 1024 * 16
+    buf = hip.array(shape=(records, 8), dtype=np.uint64)
+    zeros = np.zeros((records, 8), dtype=np.uint64)
+    khz = ctypes.c_int(0)
+    if setter(ctypes.c_void_p(buf.ptr), records, ctypes.byref(khz)) != 0 or khz.value <= 0:
+        raise RuntimeError("xtg_hip_phase_stamps failed")
+    per_us = khz.value / 1e3   # clock ticks per microsecond
+    out = {"clock_mhz": khz.value / 1e3}
+    calls = [(name, 8) for name, _ in SHAPES]
+    for c in range(copies):   # every copy once, so each measured copy was last read >= 1 GiB of traffic ago
+        for name, m in calls:
+            hip.matmul_dev(sets[c][name], dx[name], pkg.X_BF16, m, dy)
+    hip.finish()
+    for i, (name, m) in enumerate(calls):
+        rows = []
+        launch_us = []
+        kernel = None
+        for r in range(reps):
+            c = (r * len(calls) + i) % copies
+            buf.upload(zeros)
+            hip.profile(True)
+            hip.matmul_dev(sets[c][name], dx[name], pkg.X_BF16, m, dy)
+            rep = hip.profile_report()
+            hip.profile(False)
+            kernel, v = next((k, v) for k, v in rep.items() if k.startswith("gemv_kernel"))
+            launch_us.append(v["ms"] * 1e3 / v["calls"])
+            st = buf.numpy().astype(np.int64)
+            st = st[st[:, 0] != 0]
+            rows.append((st - st[:, :1].min()) / per_us)
+        # stamp order in a record: entry, issued, operand, first weight, matrix done, barrier, stores, first row
+        order = (0, 1, 7, 2, 3, 4, 5, 6)
+        fast = np.median([[x[:, k].min() for k in order] for x in rows], axis=0)
+        med = np.median([[np.median(x[:, k]) for k in order] for x in rows], axis=0)
+        slow = np.median([[x[:, k].max() for k in order] for x in rows], axis=0)
+        waves = int(np.median([x.shape[0] for x in rows]))
+        key = "%s_m%d" % (name, m)
+        out[key] = {"kernel": kernel, "waves": waves, "launch_us_events": round(float(np.median(launch_us)), 3),
+                    "span_us": round(float(slow[-1]), 3),
+                    "phases_us": {p: {"first": round(float(f), 3), "median": round(float(a), 3),
+                                      "slowest": round(float(b), 3)} for p, f, a, b in zip(PHASES, fast, med, slow)}}
+        log("%s (%s, %d waves): launch %.2f us by events, first entry to last store %.2f us"
+            % (key, kernel, waves, out[key]["launch_us_events"], out[key]["span_us"]))
+        for p, f, a, b in zip(PHASES, fast, med, slow):
+            log("  %-26s first %6.2f  median %6.2f  slowest %6.2f us" % (p, f, a, b))
+    setter(None, 0, ctypes.byref(khz))
+    hip.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -965,7 +1043,15 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the 6-call GEMV step and its roofline (for profiling them); the other sections are "
                          "left out of the JSON line")
+    ap.add_argument("--gemv-phases", action="store_true",
+                    help="only the per-wave phase stamps of the step's 8-row GEMV launches, from the phase-stamp "
+                         "build (xtier-go_amd/build.py --stamps); prints its own JSON line")
     args = ap.parse_args()
+    if args.gemv_phases:   # the phase-stamp build of the library, before the package loads one
+        os.environ["XTG_HIP_LIB"] = os.path.join(PKG_DIR, "libxtg_hip_stamps.so")
+        if not os.path.exists(os.environ["XTG_HIP_LIB"]):
+            print("--gemv-phases needs the phase-stamp build: python xtier-go_amd/build.py --stamps", file=sys.stderr)
+            sys.exit(2)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels are one GPU's share of a "
               "sharded layer); run with --gpus 1", file=sys.stderr)
@@ -976,6 +1062,13 @@ def main():
 
     if args.pmc_pass:
         pmc_pass(pkg, wl)
+        return
+
+    if args.gemv_phases:
+        ph = gemv_phases(pkg, wl, 5)
+        print(json.dumps({"metric": "8-row GEMV launch phases (us from the first wave's entry)",
+                          "value": ph["gateup2x8192_m8"]["span_us"], "unit": "us", "higher_is_better": False,
+                          "gemv_phases": ph}))
         return
 
     if args.decode_eager:

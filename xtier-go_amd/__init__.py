@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libxtg_hip.so")
+# XTG_HIP_LIB: another build of the same library (the phase-stamp build that `bench.py --gemv-phases` loads)
+LIB_PATH = os.environ.get("XTG_HIP_LIB") or os.path.join(HERE, "libxtg_hip.so")
 
 X_F32, X_BF16 = 0, 1
 KV_BF16, KV_FP8 = 0, 1

@@ -206,7 +206,45 @@ struct GemvArgs {
   int k;
   float* y;
   long long y_part;    // with a K split in two: the floats from one output set to the next (blockIdx.y)
+#ifdef XTG_PHASE_STAMPS
+  unsigned long long* stamps;   // per-wave phase records (the phase-stamp build only)
+  long long stamp_records;
+#endif
 };
+
+// Phase stamps (the phase-stamp build only, build.py --stamps, -DXTG_PHASE_STAMPS): each wave of gemv_kernel reads
+// the constant-rate clock (s_memrealtime) at kernel entry [0], once its loads are issued [1], when its first row
+// load has arrived [7] (raw rows), once its operand is built [2], when its first weight tile has arrived [3], after
+// its matrix ops [4], after the work-group's barrier [5] and after its stores are issued [6]; lane 0 writes the 8
+// stamps as one record at ((blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave). A stamp that waits on a value (an empty asm statement taking
+// it) marks when that value is there; the loads themselves are issued as in the product build.
+#ifdef XTG_PHASE_STAMPS
+#define XTG_STAMPS_DECL unsigned long long st_[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#define XTG_STAMP(i) st_[i] = __builtin_amdgcn_s_memrealtime();
+#define XTG_STAMP_AFTER(i, v)        \
+  {                                  \
+    asm volatile("" ::"v"(v));       \
+    st_[i] = __builtin_amdgcn_s_memrealtime(); \
+  }
+#define XTG_STAMPS_WRITE                                                                                        \
+  {                                                                                                             \
+    st_[6] = __builtin_amdgcn_s_memrealtime();                                                                  \
+    const long long rec_ = ((long long)blockIdx.y * gridDim.x + blockIdx.x) * 16 + wave;                        \
+    if (a.stamps && lane == 0 && rec_ < a.stamp_records) {                                                      \
+      unsigned long long* d_ = a.stamps + rec_ * 8;                                                             \
+      for (int i_ = 0; i_ < 8; ++i_) d_[i_] = st_[i_];                                                          \
+    }                                                                                                           \
+  }
+namespace {
+unsigned long long* g_stamp_buf = nullptr;   // set by xtg_hip_phase_stamps (host side)
+long long g_stamp_records = 0;
+}  // namespace
+#else
+#define XTG_STAMPS_DECL
+#define XTG_STAMP(i)
+#define XTG_STAMP_AFTER(i, v)
+#define XTG_STAMPS_WRITE
+#endif
 
 // Output of one accumulator fragment: for activation row j, rows 4 g .. 4 g + 3 of the row-block (high and low
 // columns already added).
@@ -316,6 +354,8 @@ __device__ inline float bf16_operands(uint4 (&xr)[T][2], int m, int lane, uint4*
 template <int R, int T, int MAXT, bool XR>
 __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   extern __shared__ f32x4 red[];
+  XTG_STAMPS_DECL
+  XTG_STAMP(0)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
   int wi = 0;
   while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
@@ -390,12 +430,21 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     }
   }
   float xs = 1.f;   // raw rows: the wave's factor 2^-e for the lane's column
+#ifdef XTG_PHASE_STAMPS
+  __builtin_amdgcn_sched_barrier(0);
+  XTG_STAMP(1)
+#endif
   if constexpr (XR) {
+    XTG_STAMP_AFTER(7, xr[0][0].x)
     __builtin_amdgcn_sched_barrier(0);   // every load issued before the conversion waits on x
     // this wave's staging area, after the cross-wave sums' region
     uint4* stage = reinterpret_cast<uint4*>(red) + (S > 1 ? S * R * kMaxRows * 4 : 0) + wave * kStageVecs;
     xs = bf16_operands<T>(xr, a.m, lane, stage, xb);
   }
+  if constexpr (XR) {
+    XTG_STAMP_AFTER(2, xb[T - 1][3].x)
+  }
+  XTG_STAMP_AFTER(3, cw[0][0].x)
   f32x4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -415,7 +464,9 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   if constexpr (XR)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] *= xs;   // a power of two: exact
+  XTG_STAMP_AFTER(4, acc[R - 1][3])
   if (S == 1) {
+    XTG_STAMP(5)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       f32x4 v = acc[r];
@@ -423,6 +474,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
       for (int e = 0; e < 4; ++e) v[e] += dpp<kDppXor1>(v[e]);   // high + low column of the row
       if ((col & 1) == 0 && rb0 + r < nb) store_rows(a, wi, rb0 + r, grp, col >> 1, v);
     }
+    XTG_STAMPS_WRITE
     return;
   }
   // each wave adds its high and low columns (lanes l and l ^ 1) and stores row j's sums at [wave][r][j][gg]
@@ -434,6 +486,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     if ((col & 1) == 0 && (col >> 1) < a.m) red[((wave * R + r) * kMaxRows + (col >> 1)) * 4 + grp] = v;
   }
   __syncthreads();
+  XTG_STAMP(5)
   for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
     const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7;
     if (rb0 + r >= nb || jj >= a.m) continue;
@@ -451,6 +504,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
     }
     store_rows(a, wi, rb0 + r, gg, jj, sum);
   }
+  XTG_STAMPS_WRITE
 }
 
 // ------------------------------------------------------------- one or two BF16 rows on the block-scaled FP4 op
@@ -786,6 +840,10 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.k = c.k;
   a.y = c.y;
   a.y_part = ks == 2 ? (long long)c.y_part : 0;
+#ifdef XTG_PHASE_STAMPS
+  a.stamps = g_stamp_buf;
+  a.stamp_records = g_stamp_records;
+#endif
   XTG_CHECK(sh.s * sh.t * ks >= kt && sh.s <= 16, "gemv: shape R=%d T=%d S=%d for %d k-tiles", sh.r, sh.t, sh.s, kt);
   const int threads = sh.s * 64;
   GemvFn mx = xr && c.m <= 2 && mx_enabled() ? gemv_mx_fn(sh.r, sh.t, threads, c.m) : nullptr;
@@ -1296,3 +1354,17 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
 }
 
 }  // namespace xtg::hip
+
+#ifdef XTG_PHASE_STAMPS
+// The phase-stamp build's one extra export: every later gemv_kernel launch writes its records into buf (device
+// memory of records * 64 bytes; NULL: none); *clock_khz receives the rate of the clock the stamps read.
+extern "C" int xtg_hip_phase_stamps(void* buf, long long records, int* clock_khz) {
+  xtg::hip::g_stamp_buf = static_cast<unsigned long long*>(buf);
+  xtg::hip::g_stamp_records = buf ? records : 0;
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return -1;
+  *clock_khz = khz;
+  return 0;
+}
+#endif
