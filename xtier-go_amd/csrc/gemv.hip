@@ -190,22 +190,26 @@ std::string launch_prep_x(const void* x, int x_dtype, int m, int k, void* op, hi
 // ------------------------------------------------------------------------------------------------------ GEMV
 
 struct GemvArgs {
-  const uint8_t* tiles[4];
+  // what a work-group needs before its first load, in the first two 64-byte lines: the work-group -> weight choice
+  // reads wg_end and then nb / tiles from the same line
+  int wg_end[4];   // cumulative work-group counts per weight
   int nb[4];
+  const uint8_t* tiles[4];
+  int nw;
+  int kt;
+  int m;
+  int k;
+  int waves;           // waves per work-group (blockDim.x / 64)
+  const void* x;       // raw rows [m][k] (FP32 or BF16) when the kernel builds its own operand
+  const uint4* xop;
+  const float* xinv;   // the operand's row factors (NULL: the rows were taken raw)
+  float* y;
+  long long y_part;    // with a K split in two: the floats from one output set to the next (blockIdx.y)
+  // the epilogue's
   int n[4];
   float global[4];
   long long y_off[4];
   const float* col_scale[4];   // optional per-output-column factor (the LM head's logit scale)
-  int wg_end[4];   // cumulative work-group counts per weight
-  int nw;
-  int kt;
-  int m;
-  const uint4* xop;
-  const float* xinv;   // the operand's row factors (NULL: the rows were taken raw)
-  const void* x;       // raw rows [m][k] (FP32 or BF16) when the kernel builds its own operand
-  int k;
-  float* y;
-  long long y_part;    // with a K split in two: the floats from one output set to the next (blockIdx.y)
 #ifdef XTG_PHASE_STAMPS
   unsigned long long* stamps;   // per-wave phase records (the phase-stamp build only)
   long long stamp_records;
@@ -356,9 +360,9 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   extern __shared__ f32x4 red[];
   XTG_STAMPS_DECL
   XTG_STAMP(0)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = a.waves;
   int wi = 0;
-  while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+  while (wi < 3 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;   // wg_end past the last weight = the total
   const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * R;
   const int nb = a.nb[wi], KT = a.kt;
   const uint8_t* __restrict__ tiles = a.tiles[wi];
@@ -487,7 +491,7 @@ __global__ void __launch_bounds__(MAXT) gemv_kernel(const GemvArgs a) {
   }
   __syncthreads();
   XTG_STAMP(5)
-  for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
+  for (int item = threadIdx.x; item < R * 32; item += S * 64) {
     const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7;
     if (rb0 + r >= nb || jj >= a.m) continue;
     // the S <= 16 waves in order, the reads in batches of 4 with clamped indices (no wait between them)
@@ -532,9 +536,9 @@ __global__ void __launch_bounds__(MAXT) gemv_mx_kernel(const GemvArgs a) {
   extern __shared__ f32x4 red[];
   typedef int i32x8 __attribute__((ext_vector_type(8)));
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = a.waves;
   int wi = 0;
-  while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+  while (wi < 3 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;   // wg_end past the last weight = the total
   const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * R;
   const int nb = a.nb[wi], KT = a.kt;
   const uint8_t* __restrict__ tiles = a.tiles[wi];
@@ -657,7 +661,7 @@ __global__ void __launch_bounds__(MAXT) gemv_mx_kernel(const GemvArgs a) {
   for (int r = 0; r < R; ++r)
     if (store_lane) red[((wave * R + r) * kMaxRows + (col >> 1)) * 4 + q] = v[r];
   __syncthreads();
-  for (int item = threadIdx.x; item < R * 32; item += blockDim.x) {
+  for (int item = threadIdx.x; item < R * 32; item += S * 64) {
     const int r = item >> 5, l = item & 31, gg = l >> 3, jj = l & 7;
     if (rb0 + r >= nb || jj >= min(a.m, MR)) continue;
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -840,6 +844,7 @@ std::string launch_gemv(const GemvCall& c, hipStream_t stream) {
   a.k = c.k;
   a.y = c.y;
   a.y_part = ks == 2 ? (long long)c.y_part : 0;
+  a.waves = sh.s;
 #ifdef XTG_PHASE_STAMPS
   a.stamps = g_stamp_buf;
   a.stamp_records = g_stamp_records;
@@ -959,7 +964,7 @@ __global__ void __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(T == 
 gemv_fused_kernel(const FusedArgs f) {
   const GemvArgs& a = f.g;
   extern __shared__ f32x4 red[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, S = a.waves;
   constexpr bool PAIR = OUT == kOutSwiglu;
   constexpr int RB = PAIR ? R / 2 : R;   // row-blocks per weight: PAIR takes RB of gate and the same RB of up
   static_assert(!PAIR || R % 2 == 0, "paired row-blocks");
@@ -969,7 +974,7 @@ gemv_fused_kernel(const FusedArgs f) {
   constexpr int NI = Q == 5 ? 3 : 8;          // records per quantity a lane holds from the start (P <= 64 NI)
   int wi = 0;
   if constexpr (!PAIR)
-    while (wi < a.nw - 1 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;
+    while (wi < 3 && int(blockIdx.x) >= a.wg_end[wi]) ++wi;   // wg_end past the last weight = the total
   const int rb0 = (int(blockIdx.x) - (wi ? a.wg_end[wi - 1] : 0)) * RB;
   const int KT = a.kt, kt0 = wave * T;
   const FusedLds L(S, R, IN);
@@ -1323,6 +1328,7 @@ std::string launch_gemv_fused(const FusedGemv& f, hipStream_t stream) {
   a.g.xinv = c.xinv;
   a.g.k = c.k;
   a.g.y = c.y;
+  a.g.waves = sh.s;
   a.in_groups = f.in_groups;
   a.in_x = f.in_x;
   a.in_o = f.in_o;
